@@ -1,0 +1,99 @@
+/* rg HIP device backend: the C ABI of librg_hip.so.
+ *
+ * This is the drop-in replacement for rg's device layer. In the reference that layer is the
+ * `Exec` trait (src/plan.rs:29-41) implemented by `MetalExec` (src/metal.rs:728-750), built by
+ * `MetalProgram` (src/metal.rs:362-530), stubbed on other platforms by src/metal_stub.rs:6-40
+ * and selected in src/lib.rs:4-8. Each entry point below names the reference interface it
+ * replaces. Plans arrive as the flat descriptor of rg_plan.h.
+ *
+ * Ownership: a program owns the device kernels, the step list and a pool of slot frames; an
+ * exec owns one frame and returns it to the pool when freed (metal.rs:505-523, 565-571).
+ * Errors: construction reports a message through (err, err_len); execution errors are latched,
+ * the first one wins and later steps do nothing until the exec is freed (metal.rs:536-537,
+ * 584-590). Threading: a program may be shared; each exec is used by one thread at a time.
+ */
+#ifndef RG_HIP_H
+#define RG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rg_plan.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The device-resident step loop: the arguments of `run_loop` (src/validate.rs:289-363) after
+ * the engine has derived its swap and copy lists from the plan (validate.rs:303-318). */
+typedef struct rg_run_desc {
+  int64_t n_swaps;
+  const int64_t* swaps;        /* n_swaps pairs (input slot, output slot): buffers exchanged */
+  int64_t n_copies;
+  const int64_t* copies;       /* n_copies triples (input slot, output slot, elements) */
+  int64_t n_data;
+  const int64_t* data_slots;   /* slots of the data inputs */
+  const uint64_t* data_bytes;  /* bytes of each data input */
+  int64_t n_batches;           /* >1: batch k % n_batches is loaded before step k */
+  const void* const* batches;  /* host pointers, batches[b * n_data + j] */
+  int64_t n_history;
+  const int64_t* history_slots;/* scalar outputs recorded after every step */
+  int64_t steps;
+  double* history;             /* out: n_history rows of `steps` values */
+} rg_run_desc;
+
+typedef struct rg_run_result {
+  int64_t done;                /* completed steps */
+  int64_t nonfinite_step;      /* first step whose history held a non-finite value, or -1 */
+  double seconds;              /* time in the step loop, excluding one-time setup */
+} rg_run_result;
+
+/* metal.rs:58-60 `available()`: 1 when a gfx950 device is present. */
+int rg_hip_available(void);
+
+/* metal.rs:380-503 `MetalProgram::new(&Plan)`: builds the kernels for every plan step (JIT
+ * compiled fused groups plus precompiled instruction kernels). Refuses a slot larger than the
+ * device memory. Returns NULL with a message on failure (validate.rs:478-482 turns it into
+ * DEVICE_UNAVAILABLE). */
+void* rg_hip_program_new(const int64_t* plan_words, size_t n_words, const void* const_blob,
+                         size_t const_bytes, char* err, size_t err_len);
+void rg_hip_program_free(void* program);
+/* metal.rs:385-388 `allocated_bytes()`: device bytes this process holds, to catch leaks. */
+uint64_t rg_hip_program_allocated_bytes(void* program);
+/* metal.rs:525-529 `inject_failure_for_test()`: the next step fails as a device error would. */
+void rg_hip_program_inject_failure(void* program);
+
+/* metal.rs:505-523 `MetalProgram::exec`: a frame from the pool, or a new zeroed one with the
+ * constants written. */
+void* rg_hip_exec_new(void* program, char* err, size_t err_len);
+/* Drop of `MetalExec` (metal.rs:565-571): the frame goes back to the pool. */
+void rg_hip_exec_free(void* exec);
+/* `Exec::write_prefix` / `Exec::load` (plan.rs:33, 36): host bytes into the start of a slot. */
+int rg_hip_exec_write(void* exec, int64_t slot, const void* src, uint64_t bytes);
+/* `Exec::prefix` (plan.rs:35): the first bytes of a slot back to the host. */
+int rg_hip_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes);
+/* `Exec::scalar` (plan.rs:37): element 0 of a slot as a double. */
+double rg_hip_exec_scalar(void* exec, int64_t slot);
+/* `Exec::swap` (plan.rs:34): exchanges the buffers behind two slots. */
+void rg_hip_exec_swap(void* exec, int64_t a, int64_t b);
+/* `Exec::step` (plan.rs:32): runs every plan step once and waits for the device. */
+void rg_hip_exec_step(void* exec);
+/* Runs plan steps [begin, end) and waits: what the instrumented check needs between steps. */
+void rg_hip_exec_steps(void* exec, int64_t begin, int64_t end);
+/* `Exec::failure` (plan.rs:38-40): 1 and the message when the device failed, else 0. */
+int rg_hip_exec_failure(void* exec, char* buf, size_t len);
+/* metal.rs:690-698 `step_timed`: adds each plan step's device seconds to seconds[step]. */
+int rg_hip_exec_step_timed(void* exec, double* seconds);
+/* metal.rs:700-713 `breakdown`: whole steps, and where the time went, as JSON. */
+int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len);
+/* The device-resident `run_loop` (validate.rs:289-363): steps captured in HIP graphs and
+ * replayed, batches and history kept on the device, state handed off by buffer swaps and
+ * copies. Semantics equal the host loop: a non-finite history value stops the run after that
+ * step's state handoff. Returns 0, or -1 when the device failed (see rg_hip_exec_failure). */
+int rg_hip_exec_run(void* exec, const rg_run_desc* desc, rg_run_result* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RG_HIP_H */

@@ -1,0 +1,253 @@
+/* rg plan descriptor: the flat, C-ABI form of rg's `Plan` (reference src/plan.rs:75-164).
+ *
+ * A device backend receives a plan as one array of int64 words plus one byte blob holding the
+ * constant tensors. The words encode, in order:
+ *
+ *   header     RG_PLAN_MAGIC, RG_PLAN_VERSION
+ *   slots      n_slots, then per slot: dtype, capacity (elements), pinned (0/1)
+ *              (plan.rs:151-154: `slots`, `pinned`)
+ *   consts     n_consts, then per const: slot, n (elements), byte offset into the blob
+ *              (plan.rs:155 `consts`; values are row-major, native-endian, dtype sizes 4/8/4)
+ *   inputs     n_inputs, then per input: slot, n                (plan.rs:156-157)
+ *   outputs    n_outputs, then per output: slot, n, rank, dims  (plan.rs:142-147, 158)
+ *   steps      n_steps, then per step a tagged record:
+ *     RG_STEP_INSTR  op, dtype, dst, n, mode, node,
+ *                    rank, dims (output shape),
+ *                    n_args, per arg: slot, rank, dims,
+ *                    n_attr, attr words (op specific, below)   (plan.rs:127-140 `Instr`)
+ *     RG_STEP_FUSED  dtype, n, regs, rank, dims,
+ *                    n_in, per input: slot, kind, row_len, reg, rank, dims,
+ *                    n_ops, per micro-op: op, reg, n_args, per arg: is_reg, index,
+ *                    n_out, per output: reg, slot                (plan.rs:85-111 `Fused`)
+ *
+ * Attribute words per op:
+ *   MATMUL_T       ta, tb
+ *   REDUCE         kind, keepdims, n_axes, axes...
+ *   TRANSPOSE      perm...
+ *   BROADCAST_TO   shape...            RESHAPE  shape...
+ *   SLICE          rank, starts..., stops...
+ *   PAD            rank, starts..., shape...
+ *   CAST           target dtype
+ *   TAKE           axis                TAKE_GRAD  axis, shape...
+ *   TAKE_ALONG_GRAD shape...           CONCAT     axis
+ *   RAND_UNIFORM / RAND_NORMAL  dtype, shape...
+ *   KEY_SPLIT      n                   ARG_TOP_K  k          CUMSUM reverse
+ *
+ * Slot buffers hold at least `capacity` elements (at least 4 bytes) and start zeroed; a value
+ * is the row-major prefix of `n` elements of its slot.
+ */
+#ifndef RG_PLAN_H
+#define RG_PLAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define RG_PLAN_MAGIC 0x4c50475244ll /* "DRGPL" */
+#define RG_PLAN_VERSION 1
+
+enum rg_dtype { RG_F32 = 0, RG_F64 = 1, RG_I32 = 2 };
+
+/* Operation codes: the variants of `Op` (reference src/graph.rs:47-114) that can reach a plan. */
+enum rg_op {
+  RG_OP_INPUT = 0, RG_OP_CONST, RG_OP_NEG, RG_OP_EXP, RG_OP_LOG, RG_OP_SQRT, RG_OP_SIN, RG_OP_COS,
+  RG_OP_TANH, RG_OP_ABS, RG_OP_SIGN, RG_OP_ADD, RG_OP_SUB, RG_OP_MUL, RG_OP_DIV, RG_OP_POW,
+  RG_OP_MAX, RG_OP_MIN, RG_OP_GT, RG_OP_GE, RG_OP_WHERE, RG_OP_MATMUL, RG_OP_MATMUL_T,
+  RG_OP_REDUCE, RG_OP_RESHAPE, RG_OP_TRANSPOSE, RG_OP_BROADCAST_TO, RG_OP_SLICE, RG_OP_PAD,
+  RG_OP_CAST, RG_OP_STOP_GRADIENT, RG_OP_FLOOR, RG_OP_TAKE, RG_OP_TAKE_ALONG, RG_OP_TAKE_GRAD,
+  RG_OP_TAKE_ALONG_GRAD, RG_OP_CONCAT, RG_OP_ARGMAX, RG_OP_RAND_UNIFORM, RG_OP_RAND_NORMAL,
+  RG_OP_KEY_SPLIT, RG_OP_ARG_TOP_K, RG_OP_CUMSUM, RG_OP_SCAN, RG_OP_WHILE, RG_OP_COND,
+  RG_OP_OUTPUT, RG_OP_PLACEHOLDER, RG_OP_CUSTOM, RG_OP_COUNT
+};
+
+enum rg_reduce_kind { RG_REDUCE_SUM = 0, RG_REDUCE_MAX = 1, RG_REDUCE_MIN = 2 };
+/* Input kinds of a fused group (plan.rs:75-83). */
+enum rg_arg_kind { RG_ARG_FULL = 0, RG_ARG_SPLAT = 1, RG_ARG_ROW = 2, RG_ARG_BROADCAST = 3 };
+/* Binary broadcast modes of a single elementwise instruction (plan.rs:119-125). */
+enum rg_mode { RG_MODE_SAME = 0, RG_MODE_ASCALAR = 1, RG_MODE_BSCALAR = 2, RG_MODE_GENERAL = 3 };
+enum rg_step_kind { RG_STEP_INSTR = 0, RG_STEP_FUSED = 1 };
+
+#ifdef __cplusplus
+#include <stdexcept>
+#include <vector>
+
+namespace rgplan {
+
+struct Arg {
+  int64_t slot;
+  std::vector<int64_t> shape;
+};
+
+struct Instr {
+  int32_t op, dtype;
+  int64_t dst, n, mode, node;
+  std::vector<int64_t> shape;
+  std::vector<Arg> args;
+  std::vector<int64_t> attr;
+};
+
+struct FusedInput {
+  int64_t slot, kind, row_len, reg;
+  std::vector<int64_t> shape;
+};
+
+struct MicroOp {
+  int32_t op;
+  int64_t reg;
+  std::vector<std::pair<int64_t, int64_t>> args; /* (is_reg, index) */
+};
+
+struct Fused {
+  int32_t dtype;
+  int64_t n, regs;
+  std::vector<int64_t> shape;
+  std::vector<FusedInput> inputs;
+  std::vector<MicroOp> ops;
+  std::vector<std::pair<int64_t, int64_t>> outputs; /* (reg, slot) */
+};
+
+struct Step {
+  int32_t kind;
+  Instr instr;
+  Fused fused;
+};
+
+struct Slot {
+  int32_t dtype;
+  int64_t cap;
+  bool pinned;
+};
+
+struct Const {
+  int64_t slot, n, offset;
+};
+
+struct Output {
+  int64_t slot, n;
+  std::vector<int64_t> shape;
+};
+
+struct Plan {
+  std::vector<Slot> slots;
+  std::vector<Const> consts;
+  std::vector<std::pair<int64_t, int64_t>> inputs; /* (slot, n) */
+  std::vector<Output> outputs;
+  std::vector<Step> steps;
+};
+
+inline int64_t dtype_size(int32_t d) { return d == RG_F64 ? 8 : 4; }
+
+/* Parses the word array; throws std::runtime_error on a malformed descriptor. */
+inline Plan parse(const int64_t* w, size_t nw) {
+  size_t p = 0;
+  auto next = [&]() -> int64_t {
+    if (p >= nw) throw std::runtime_error("plan descriptor truncated");
+    return w[p++];
+  };
+  auto vec = [&](int64_t n) {
+    if (n < 0 || (size_t)n > nw) throw std::runtime_error("plan descriptor has a bad length");
+    std::vector<int64_t> v((size_t)n);
+    for (auto& x : v) x = next();
+    return v;
+  };
+  if (next() != RG_PLAN_MAGIC) throw std::runtime_error("not an rg plan descriptor");
+  if (next() != RG_PLAN_VERSION) throw std::runtime_error("unsupported plan descriptor version");
+  Plan pl;
+  int64_t ns = next();
+  for (int64_t i = 0; i < ns; i++) {
+    Slot s;
+    s.dtype = (int32_t)next();
+    s.cap = next();
+    s.pinned = next() != 0;
+    pl.slots.push_back(s);
+  }
+  int64_t nc = next();
+  for (int64_t i = 0; i < nc; i++) {
+    Const c;
+    c.slot = next();
+    c.n = next();
+    c.offset = next();
+    pl.consts.push_back(c);
+  }
+  int64_t ni = next();
+  for (int64_t i = 0; i < ni; i++) {
+    int64_t s = next();
+    int64_t n = next();
+    pl.inputs.push_back({s, n});
+  }
+  int64_t no = next();
+  for (int64_t i = 0; i < no; i++) {
+    Output o;
+    o.slot = next();
+    o.n = next();
+    o.shape = vec(next());
+    pl.outputs.push_back(o);
+  }
+  int64_t nst = next();
+  for (int64_t i = 0; i < nst; i++) {
+    Step st;
+    st.kind = (int32_t)next();
+    if (st.kind == RG_STEP_INSTR) {
+      Instr& in = st.instr;
+      in.op = (int32_t)next();
+      in.dtype = (int32_t)next();
+      in.dst = next();
+      in.n = next();
+      in.mode = next();
+      in.node = next();
+      in.shape = vec(next());
+      int64_t na = next();
+      for (int64_t a = 0; a < na; a++) {
+        Arg arg;
+        arg.slot = next();
+        arg.shape = vec(next());
+        in.args.push_back(arg);
+      }
+      in.attr = vec(next());
+    } else if (st.kind == RG_STEP_FUSED) {
+      Fused& f = st.fused;
+      f.dtype = (int32_t)next();
+      f.n = next();
+      f.regs = next();
+      f.shape = vec(next());
+      int64_t nin = next();
+      for (int64_t a = 0; a < nin; a++) {
+        FusedInput fi;
+        fi.slot = next();
+        fi.kind = next();
+        fi.row_len = next();
+        fi.reg = next();
+        fi.shape = vec(next());
+        f.inputs.push_back(fi);
+      }
+      int64_t nops = next();
+      for (int64_t a = 0; a < nops; a++) {
+        MicroOp m;
+        m.op = (int32_t)next();
+        m.reg = next();
+        int64_t nargs = next();
+        for (int64_t b = 0; b < nargs; b++) {
+          int64_t is_reg = next();
+          int64_t idx = next();
+          m.args.push_back({is_reg, idx});
+        }
+        f.ops.push_back(m);
+      }
+      int64_t nout = next();
+      for (int64_t a = 0; a < nout; a++) {
+        int64_t r = next();
+        int64_t s = next();
+        f.outputs.push_back({r, s});
+      }
+    } else {
+      throw std::runtime_error("unknown plan step kind");
+    }
+    pl.steps.push_back(std::move(st));
+  }
+  if (p != nw) throw std::runtime_error("plan descriptor has trailing words");
+  return pl;
+}
+
+}  // namespace rgplan
+#endif /* __cplusplus */
+
+#endif /* RG_PLAN_H */

@@ -1,0 +1,92 @@
+// Device backends behind the C ABI of include/rg_hip.h, loaded at run time.
+//
+// The engine is written against this table exactly as the reference's `Compiled` is written
+// against `Exec` (src/plan.rs:29-41). The product registers one backend, "hip" (librg_hip.so);
+// a test harness may register a second library with the same ABI under another name.
+#pragma once
+#include <memory>
+#include <mutex>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "../../../include/rg_hip.h"
+#include "plan.h"
+
+namespace rg {
+
+struct Backend {
+  std::string name, path, prefix;
+  void* lib = nullptr;
+  int (*available)() = nullptr;
+  void* (*program_new)(const int64_t*, size_t, const void*, size_t, char*, size_t) = nullptr;
+  void (*program_free)(void*) = nullptr;
+  uint64_t (*program_allocated_bytes)(void*) = nullptr;
+  void (*program_inject_failure)(void*) = nullptr;
+  void* (*exec_new)(void*, char*, size_t) = nullptr;
+  void (*exec_free)(void*) = nullptr;
+  int (*exec_write)(void*, int64_t, const void*, uint64_t) = nullptr;
+  int (*exec_read)(void*, int64_t, void*, uint64_t) = nullptr;
+  double (*exec_scalar)(void*, int64_t) = nullptr;
+  void (*exec_swap)(void*, int64_t, int64_t) = nullptr;
+  void (*exec_step)(void*) = nullptr;
+  void (*exec_steps)(void*, int64_t, int64_t) = nullptr;
+  int (*exec_failure)(void*, char*, size_t) = nullptr;
+  int (*exec_step_timed)(void*, double*) = nullptr;  // optional
+  int (*exec_breakdown)(void*, int64_t, char*, size_t) = nullptr;  // optional
+  int (*exec_run)(void*, const rg_run_desc*, rg_run_result*) = nullptr;  // optional
+};
+
+// Loads `path` and resolves `<prefix><entry point>` for every ABI function; throws a message.
+void register_backend(const std::string& name, const std::string& path, const std::string& prefix);
+// The backend registered under `name` whose device is present, or nullptr.
+Backend* find_backend(const std::string& name);
+std::vector<std::string> available_backends();
+// Where eager operations and constant folding run: "hip" when present, else the first other
+// registered backend; throws DEVICE_UNAVAILABLE when there is none.
+Backend* eager_backend();
+
+class DeviceExec;
+
+// A plan built into device kernels (`MetalProgram`).
+class DeviceProgram {
+ public:
+  DeviceProgram(Backend* b, const Plan& plan);  // throws std::runtime_error with the device's message
+  ~DeviceProgram();
+  DeviceProgram(const DeviceProgram&) = delete;
+  Backend* backend() const { return b_; }
+  void* handle() const { return p_; }
+  const Plan& plan() const { return *plan_; }
+  std::unique_ptr<DeviceExec> exec() const;  // throws std::runtime_error
+ private:
+  Backend* b_;
+  void* p_ = nullptr;
+  const Plan* plan_;
+};
+
+// One frame of slot buffers (`MetalExec`): the `Exec` trait over the C ABI.
+class DeviceExec {
+ public:
+  DeviceExec(Backend* b, void* e, const Plan* plan) : b_(b), e_(e), plan_(plan) {}
+  ~DeviceExec() { b_->exec_free(e_); }
+  void load(size_t k, const Tensor& t);
+  void step() { b_->exec_step(e_); }
+  void steps(size_t begin, size_t end) { b_->exec_steps(e_, (int64_t)begin, (int64_t)end); }
+  void swap(size_t a, size_t c) { b_->exec_swap(e_, (int64_t)a, (int64_t)c); }
+  Tensor prefix(size_t slot, size_t n, const Shape& shape) const;
+  void write_prefix(size_t slot, const Tensor& t);
+  double scalar(size_t slot) const { return b_->exec_scalar(e_, (int64_t)slot); }
+  std::optional<std::string> failure() const;
+  Backend* backend() const { return b_; }
+  void* handle() const { return e_; }
+ private:
+  Backend* b_;
+  void* e_;
+  const Plan* plan_;
+};
+
+// Runs a graph once with a fresh frame on `b` (plan.rs:997-1006 `eval`).
+std::vector<Tensor> eval_on(Backend* b, const Graph& g, const std::vector<uint32_t>& outputs,
+                            const std::vector<const Tensor*>& inputs);
+
+}  // namespace rg

@@ -1,0 +1,362 @@
+// Python bindings of the engine: the `_rg` module. Mirrors the reference's src/python.rs:1-303
+// (Tensor, Graph, Compiled, compile, available_devices, DiagnosticError), plus
+// `register_backend` to load device libraries.
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include "validate.h"
+
+namespace py = pybind11;
+using namespace rg;
+
+namespace {
+
+PyObject* g_diag_error = nullptr;
+
+[[noreturn]] void raise_diag(const Json& d) { throw DiagError{d}; }
+
+DType dtype_of(const std::string& s) {
+  DType d;
+  if (!parse_dtype(s, &d)) throw py::value_error("unsupported dtype " + s);
+  return d;
+}
+
+struct PyTensor {
+  Tensor t;
+};
+
+PyTensor make_tensor(py::bytes data, const std::vector<size_t>& shape, const std::string& dtype) {
+  PyTensor p;
+  p.t.dtype = dtype_of(dtype);
+  p.t.shape = shape;
+  std::string s = data;
+  if (s.size() != numel(shape) * dsize(p.t.dtype))
+    throw py::value_error(std::to_string(s.size()) + " bytes do not fit shape of " + dname(p.t.dtype));
+  p.t.data.assign(s.begin(), s.end());
+  return p;
+}
+
+template <class T>
+T attr(const py::object& attrs, const char* key) {
+  if (attrs.is_none() || !py::cast<py::dict>(attrs).contains(key)) throw py::value_error(std::string("missing attribute ") + key);
+  try {
+    return py::cast<T>(py::cast<py::dict>(attrs)[key]);
+  } catch (py::cast_error&) {
+    throw py::value_error(std::string("invalid attribute ") + key);
+  }
+}
+
+Op parse_op(const std::string& name, const py::object& a) {
+  static const std::map<std::string, rg_op> simple = {
+      {"neg", RG_OP_NEG},   {"exp", RG_OP_EXP},       {"log", RG_OP_LOG},          {"sqrt", RG_OP_SQRT},
+      {"sin", RG_OP_SIN},   {"cos", RG_OP_COS},       {"tanh", RG_OP_TANH},        {"abs", RG_OP_ABS},
+      {"sign", RG_OP_SIGN}, {"add", RG_OP_ADD},       {"sub", RG_OP_SUB},          {"mul", RG_OP_MUL},
+      {"div", RG_OP_DIV},   {"pow", RG_OP_POW},       {"maximum", RG_OP_MAX},      {"minimum", RG_OP_MIN},
+      {"gt", RG_OP_GT},     {"ge", RG_OP_GE},         {"where", RG_OP_WHERE},      {"matmul", RG_OP_MATMUL},
+      {"floor", RG_OP_FLOOR}, {"stop_gradient", RG_OP_STOP_GRADIENT}, {"take_along", RG_OP_TAKE_ALONG},
+      {"argmax", RG_OP_ARGMAX}};
+  auto it = simple.find(name);
+  if (it != simple.end()) return Op::make(it->second);
+  Op o;
+  if (name == "sum" || name == "max" || name == "min") {
+    o.kind = RG_OP_REDUCE;
+    o.rk = name == "sum" ? RK::Sum : name == "max" ? RK::Max : RK::Min;
+    o.v = attr<Shape>(a, "axes");
+    o.keepdims = attr<bool>(a, "keepdims");
+  } else if (name == "reshape") {
+    o.kind = RG_OP_RESHAPE;
+    o.v = attr<Shape>(a, "shape");
+  } else if (name == "transpose") {
+    o.kind = RG_OP_TRANSPOSE;
+    o.v = attr<Shape>(a, "perm");
+  } else if (name == "broadcast_to") {
+    o.kind = RG_OP_BROADCAST_TO;
+    o.v = attr<Shape>(a, "shape");
+  } else if (name == "slice") {
+    o.kind = RG_OP_SLICE;
+    o.v = attr<Shape>(a, "starts");
+    o.w = attr<Shape>(a, "stops");
+  } else if (name == "pad") {
+    o.kind = RG_OP_PAD;
+    o.v = attr<Shape>(a, "starts");
+    o.w = attr<Shape>(a, "shape");
+  } else if (name == "cast") {
+    o.kind = RG_OP_CAST;
+    o.dt = dtype_of(attr<std::string>(a, "dtype"));
+  } else if (name == "take") {
+    o.kind = RG_OP_TAKE;
+    o.a = attr<size_t>(a, "axis");
+  } else if (name == "concat") {
+    o.kind = RG_OP_CONCAT;
+    o.a = attr<size_t>(a, "axis");
+  } else if (name == "arg_top_k") {
+    o.kind = RG_OP_ARG_TOP_K;
+    o.a = attr<size_t>(a, "k");
+  } else if (name == "cumsum") {
+    o.kind = RG_OP_CUMSUM;
+    o.reverse = attr<bool>(a, "reverse");
+  } else if (name == "random_uniform" || name == "random_normal") {
+    o.kind = name == "random_uniform" ? RG_OP_RAND_UNIFORM : RG_OP_RAND_NORMAL;
+    o.v = attr<Shape>(a, "shape");
+    o.dt = dtype_of(attr<std::string>(a, "dtype"));
+  } else if (name == "key_split") {
+    o.kind = RG_OP_KEY_SPLIT;
+    o.a = attr<size_t>(a, "n");
+  } else if (name == "take_grad") {
+    o.kind = RG_OP_TAKE_GRAD;
+    o.a = attr<size_t>(a, "axis");
+    o.v = attr<Shape>(a, "shape");
+  } else if (name == "take_along_grad") {
+    o.kind = RG_OP_TAKE_ALONG_GRAD;
+    o.v = attr<Shape>(a, "shape");
+  } else {
+    throw py::value_error("unknown op " + name);
+  }
+  return o;
+}
+
+struct PyGraph {
+  Graph g;
+  void set_source(const std::optional<std::string>& s) {
+    g.cur_source = s ? std::make_shared<const std::string>(*s) : nullptr;
+  }
+};
+
+struct PyCompiled {
+  std::unique_ptr<Compiled> c;
+};
+
+std::vector<Tensor> tensors(const std::vector<PyTensor>& v) {
+  std::vector<Tensor> out;
+  for (auto& p : v) out.push_back(p.t);
+  return out;
+}
+
+std::vector<PyTensor> wrap(std::vector<Tensor> v) {
+  std::vector<PyTensor> out;
+  for (auto& t : v) out.push_back(PyTensor{std::move(t)});
+  return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_rg, m) {
+  g_diag_error = PyErr_NewException("rustautograd_amd._rg.DiagnosticError", PyExc_Exception, nullptr);
+  m.add_object("DiagnosticError", py::handle(g_diag_error));
+  py::register_exception_translator([](std::exception_ptr p) {
+    try {
+      if (p) std::rethrow_exception(p);
+    } catch (const DiagError& d) {
+      std::string text = d.d.dump();
+      py::gil_scoped_acquire gil;
+      py::object err = py::reinterpret_steal<py::object>(PyObject_CallFunction(g_diag_error, "s", text.c_str()));
+      try {
+        err.attr("diagnostic") = py::module_::import("json").attr("loads")(text);
+      } catch (...) {
+      }
+      PyErr_SetObject(g_diag_error, err.ptr());
+    }
+  });
+
+  py::class_<PyTensor>(m, "Tensor")
+      .def(py::init(&make_tensor), py::arg("data"), py::arg("shape"), py::arg("dtype"))
+      .def_property_readonly("shape", [](const PyTensor& t) { return t.t.shape; })
+      .def_property_readonly("dtype", [](const PyTensor& t) { return std::string(dname(t.t.dtype)); })
+      .def("is_finite", [](const PyTensor& t) { return t.t.is_finite(); })
+      .def("tobytes", [](const PyTensor& t) { return py::bytes((const char*)t.t.data.data(), t.t.data.size()); });
+
+  py::class_<PyGraph>(m, "Graph")
+      .def(py::init<>())
+      .def("input",
+           [](PyGraph& g, const std::vector<size_t>& shape, const std::string& dtype, std::optional<std::string> source) {
+             g.set_source(source);
+             return g.g.input(shape, dtype_of(dtype));
+           },
+           py::arg("shape"), py::arg("dtype"), py::arg("source") = py::none())
+      .def("constant",
+           [](PyGraph& g, const PyTensor& t, std::optional<std::string> source) {
+             g.set_source(source);
+             return g.g.constant(t.t);
+           },
+           py::arg("t"), py::arg("source") = py::none())
+      .def("op",
+           [](PyGraph& g, const std::string& name, const std::vector<uint32_t>& inputs, py::object attrs,
+              std::optional<std::string> source) {
+             Op op = parse_op(name, attrs);
+             g.set_source(source);
+             return g.g.add(op, inputs);
+           },
+           py::arg("name"), py::arg("inputs"), py::arg("attrs") = py::none(), py::arg("source") = py::none())
+      .def("grad",
+           [](PyGraph& g, uint32_t y, const std::vector<uint32_t>& wrts, std::optional<std::string> source) {
+             g.set_source(source);
+             return grad(g.g, y, wrts);
+           },
+           py::arg("y"), py::arg("wrts"), py::arg("source") = py::none())
+      .def("placeholder",
+           [](PyGraph& g, const std::vector<size_t>& shape, const std::string& dtype) {
+             return g.g.placeholder(shape, dtype_of(dtype));
+           })
+      .def("custom",
+           [](PyGraph& g, uint32_t y, uint32_t placeholder, const std::vector<std::pair<uint32_t, uint32_t>>& rules,
+              std::optional<std::string> source) {
+             g.set_source(source);
+             Op o = Op::make(RG_OP_CUSTOM);
+             o.placeholder = placeholder;
+             o.rules = rules;
+             return g.g.add(o, {y});
+           },
+           py::arg("y"), py::arg("placeholder"), py::arg("rules"), py::arg("source") = py::none())
+      .def("grad_records",
+           [](const PyGraph& g) {
+             std::vector<std::tuple<uint32_t, uint32_t, uint32_t>> out;
+             for (auto& r : g.g.grads) out.push_back({r.y, r.wrt, r.grad});
+             return out;
+           })
+      .def("shape", [](const PyGraph& g, uint32_t id) { return g.g.shape(id); })
+      .def("dtype", [](const PyGraph& g, uint32_t id) { return std::string(dname(g.g.dtype(id))); })
+      .def("__len__", [](const PyGraph& g) { return g.g.nodes.size(); })
+      .def("eval", [](const PyGraph& g, const std::vector<uint32_t>& ids) {
+        // One-off evaluation for eager operations; the graph must have no inputs.
+        Backend* b = eager_backend();
+        std::vector<Tensor> out;
+        {
+          py::gil_scoped_release nogil;
+          out = eval_on(b, g.g, ids, {});
+        }
+        return wrap(std::move(out));
+      });
+
+  py::class_<PyCompiled>(m, "Compiled")
+      .def_property_readonly("report_json", [](const PyCompiled& c) { return c.c->report.dump(); })
+      .def_property_readonly("output_shapes",
+                             [](const PyCompiled& c) {
+                               std::vector<Shape> s;
+                               for (auto& o : c.c->plan.outputs) s.push_back(o.shape);
+                               return s;
+                             })
+      .def_property_readonly("device", [](const PyCompiled& c) { return c.c->device->name; })
+      .def("plan_summary",
+           [](const PyCompiled& c) {
+             // Per-step description for measurement tools: kind, op, dtype, n, shapes.
+             py::list out;
+             for (auto& s : c.c->plan.steps) {
+               py::dict d;
+               if (s.fused) {
+                 d["kind"] = "fused";
+                 py::list ops;
+                 for (auto& m : s.group.ops) ops.append(m.op.name());
+                 d["ops"] = ops;
+                 d["n"] = s.group.n;
+                 d["dtype"] = dname(s.group.dtype);
+                 d["inputs"] = s.group.input_shapes;
+                 d["n_outputs"] = s.group.outputs.size();
+               } else {
+                 d["kind"] = "instr";
+                 d["op"] = s.instr.op.name();
+                 d["ta"] = s.instr.op.ta;
+                 d["tb"] = s.instr.op.tb;
+                 d["n"] = s.instr.n;
+                 d["dtype"] = dname(s.instr.dtype);
+                 d["shape"] = s.instr.shape;
+                 d["arg_shapes"] = s.instr.arg_shapes;
+               }
+               out.append(d);
+             }
+             return out;
+           })
+      .def("call",
+           [](const PyCompiled& c, const std::vector<PyTensor>& inputs) {
+             auto in = tensors(inputs);
+             c.c->check_inputs(in);
+             std::vector<Tensor> out;
+             {
+               py::gil_scoped_release nogil;
+               out = c.c->try_call(in);
+             }
+             return wrap(std::move(out));
+           })
+      .def("check",
+           [](PyCompiled& c, const std::vector<PyTensor>& inputs) {
+             auto in = tensors(inputs);
+             c.c->check_inputs(in);
+             py::gil_scoped_release nogil;
+             return c.c->check(in).dump();
+           })
+      .def("profile",
+           [](const PyCompiled& c, const std::vector<PyTensor>& inputs, size_t repeats) {
+             auto in = tensors(inputs);
+             c.c->check_inputs(in);
+             py::gil_scoped_release nogil;
+             return c.c->profile(in, repeats).dump();
+           })
+      .def("run",
+           [](const PyCompiled& c, const std::vector<std::pair<size_t, size_t>>& state_map, const std::vector<size_t>& data_inputs,
+              const std::vector<size_t>& history, const std::vector<PyTensor>& state,
+              const std::vector<std::vector<PyTensor>>& batches, size_t steps) {
+             RunSpec spec{state_map, data_inputs, history};
+             c.c->validate_spec(spec);
+             auto st = tensors(state);
+             std::vector<std::vector<Tensor>> bs;
+             for (auto& b : batches) bs.push_back(tensors(b));
+             RunOut out;
+             {
+               py::gil_scoped_release nogil;
+               out = c.c->run(spec, st, bs, steps);
+             }
+             if (out.device_error) {
+               Json d = device_failure(c.c->device->name, *out.device_error);
+               d["observation"]["completed_steps"] = out.steps;
+               raise_diag(d);
+             }
+             std::optional<size_t> bad;
+             if (out.nonfinite_step >= 0) bad = (size_t)out.nonfinite_step;
+             return py::make_tuple(wrap(out.state), wrap(out.outputs), out.history, out.steps, bad, out.seconds);
+           })
+      .def("replay",
+           [](const PyCompiled& c, const std::vector<std::pair<size_t, size_t>>& state_map, const std::vector<size_t>& data_inputs,
+              const std::vector<size_t>& history, const std::vector<PyTensor>& state,
+              const std::vector<std::vector<PyTensor>>& batches, size_t steps) -> py::object {
+             RunSpec spec{state_map, data_inputs, history};
+             auto st = tensors(state);
+             std::vector<std::vector<Tensor>> bs;
+             for (auto& b : batches) bs.push_back(tensors(b));
+             std::optional<std::tuple<size_t, size_t, std::vector<Tensor>>> found;
+             {
+               py::gil_scoped_release nogil;
+               found = c.c->replay(spec, st, bs, steps);
+             }
+             if (!found) return py::none();
+             return py::make_tuple(std::get<0>(*found), std::get<1>(*found), wrap(std::get<2>(*found)));
+           });
+
+  m.def("compile", [](const PyGraph& graph, const std::vector<uint32_t>& outputs, const std::vector<PyTensor>& examples,
+                      const std::string& level, const std::string& device, const std::string& optimize) {
+    OptMode mode;
+    if (!parse_opt_mode(optimize, &mode)) throw py::value_error("unknown optimize mode " + optimize);
+    Backend* b = find_backend(device);
+    if (!b) {
+      Json obs = Json::obj();
+      obs["device"] = device;
+      obs["available"] = Json(available_backends());
+      raise_diag(diag("DEVICE_UNAVAILABLE", "error", Json(), obs, "unknown_device", "verified"));
+    }
+    Level lv;
+    if (!parse_level(level, &lv)) throw py::value_error("unknown validation level " + level);
+    auto ex = tensors(examples);
+    PyCompiled pc;
+    {
+      py::gil_scoped_release nogil;
+      pc.c = compile_mode(graph.g, outputs, ex, lv, b, mode);
+    }
+    return pc;
+  });
+  m.def("available_devices", []() { return available_backends(); });
+  m.def("register_backend", [](const std::string& name, const std::string& path, const std::string& prefix) {
+    try {
+      register_backend(name, path, prefix);
+    } catch (std::runtime_error& e) {
+      throw py::import_error(e.what());
+    }
+  });
+}

@@ -1,0 +1,607 @@
+// Planning: fusion schedules, group compilation, the slot allocator and plan serialization.
+// Follows the reference's src/plan.rs:184-238 (Allocator), 240-309 (aliases, arg kinds,
+// fusability, hoisting), 311-414 (greedy and level schedules), 416-457 (compile_group) and
+// 466-634 (build_fused / build_with).
+#include "plan.h"
+
+#include <algorithm>
+#include <set>
+
+namespace rg {
+
+namespace {
+
+struct Allocator {
+  std::vector<std::pair<DType, size_t>> slots;
+  std::vector<bool> pinned;
+  std::vector<uint32_t> refs;
+  std::vector<size_t> free;
+  bool reuse = true;
+  std::vector<size_t> held;
+  size_t live = 0, peak = 0;
+
+  size_t new_slot(DType d, size_t n, bool pin) {
+    slots.push_back({d, n});
+    pinned.push_back(pin);
+    refs.push_back(1);
+    held.push_back(0);
+    return slots.size() - 1;
+  }
+  size_t alloc(DType d, size_t n) {
+    size_t s = pick(d, n);
+    held[s] = n * dsize(d);
+    live += held[s];
+    peak = std::max(peak, live);
+    return s;
+  }
+  size_t pick(DType d, size_t n) {
+    // A small value in a big buffer would pin the big buffer for its whole lifetime.
+    int64_t best = -1;
+    for (size_t k = 0; k < free.size(); k++) {
+      size_t s = free[k];
+      if (slots[s].first == d && slots[s].second >= n && slots[s].second <= std::max<size_t>(n, 1) * 4) {
+        if (best < 0 || slots[s].second < slots[free[(size_t)best]].second) best = (int64_t)k;
+      }
+    }
+    if (best >= 0) {
+      size_t s = free[(size_t)best];
+      free[(size_t)best] = free.back();  // swap_remove
+      free.pop_back();
+      refs[s] = 1;
+      return s;
+    }
+    return new_slot(d, n, false);
+  }
+  void release(size_t s) {
+    refs[s] -= 1;
+    if (refs[s] == 0 && !pinned[s]) {
+      live -= held[s];
+      if (reuse) free.push_back(s);
+    }
+  }
+};
+
+bool is_alias(const Graph& g, size_t id) {
+  const Node& n = g.nodes[id];
+  switch (n.op.kind) {
+    case RG_OP_RESHAPE: case RG_OP_STOP_GRADIENT: case RG_OP_CUSTOM: return true;
+    case RG_OP_CAST: return n.op.dt == g.nodes[n.inputs[0]].dtype;
+    default: return false;
+  }
+}
+
+bool arg_kind(const Shape& s, const Shape& shape, rg_arg_kind* k, size_t* row) {
+  size_t n = numel(s);
+  if (s == shape) {
+    *k = RG_ARG_FULL;
+  } else if (n == 1) {
+    *k = RG_ARG_SPLAT;
+  } else if (!s.empty() && !shape.empty() && s.back() == shape.back() && n == s.back()) {
+    *k = RG_ARG_ROW;
+    *row = n;
+  } else {
+    return false;
+  }
+  return true;
+}
+
+// Rough per-element cost in ns, used only to decide when CPU threads pay off (plan.rs:267-276).
+double op_cost_ns(const Op& op) {
+  switch (op.kind) {
+    case RG_OP_EXP: case RG_OP_LOG: case RG_OP_SIN: case RG_OP_COS: case RG_OP_TANH: return 0.6;
+    case RG_OP_POW: return 10.0;
+    case RG_OP_DIV: case RG_OP_SQRT: return 0.2;
+    default: return 0.06;
+  }
+}
+
+bool is_elementwise(const Op& op) {
+  return op.is_unary_elementwise() || op.is_binary_elementwise() || op.kind == RG_OP_WHERE;
+}
+
+bool fusable(const Graph& g, size_t id, bool device) {
+  const Node& n = g.nodes[id];
+  if (!is_elementwise(n.op) || n.dtype == DType::I32) return false;
+  if (device) return true;
+  rg_arg_kind k;
+  size_t row;
+  for (uint32_t x : n.inputs)
+    if (!arg_kind(g.shape(x), n.shape, &k, &row)) return false;
+  return true;
+}
+
+bool on_cpu_for_metal(const Op& op, DType dtype, size_t n, const std::vector<DType>& arg_dtypes) {
+  bool wide = dtype == DType::F64 || std::find(arg_dtypes.begin(), arg_dtypes.end(), DType::F64) != arg_dtypes.end();
+  bool small_int = dtype == DType::I32 && n <= 64 &&
+                   std::all_of(arg_dtypes.begin(), arg_dtypes.end(), [](DType d) { return d == DType::I32; });
+  return wide || small_int || op.kind == RG_OP_RAND_NORMAL || op.kind == RG_OP_KEY_SPLIT;
+}
+
+bool leaf(const Node& n) { return n.op.kind == RG_OP_INPUT || n.op.kind == RG_OP_CONST; }
+
+std::vector<bool> hoisted(const Graph& g, const std::vector<bool>& keep) {
+  std::vector<bool> up(g.nodes.size(), false);
+  for (size_t i = 0; i < g.nodes.size(); i++) {
+    const Node& n = g.nodes[i];
+    if (!keep[i] || leaf(n)) continue;
+    bool ready = true, all_up = true;
+    std::vector<DType> dts;
+    for (uint32_t x : n.inputs) {
+      ready &= up[x] || leaf(g.nodes[x]);
+      all_up &= up[x];
+      dts.push_back(g.dtype(x));
+    }
+    up[i] = ready && (on_cpu_for_metal(n.op, n.dtype, n.n(), dts) || (is_alias(g, i) && all_up));
+  }
+  return up;
+}
+
+struct Item {
+  bool group;
+  size_t node;
+  std::vector<size_t> members;
+};
+
+size_t distinct_external(const Graph& g, const std::vector<size_t>& members, const Node& extra) {
+  std::set<uint32_t> s;
+  auto in = [&](uint32_t x) { return std::find(members.begin(), members.end(), (size_t)x) != members.end(); };
+  for (size_t m : members)
+    for (uint32_t x : g.nodes[m].inputs)
+      if (!in(x)) s.insert(x);
+  for (uint32_t x : extra.inputs)
+    if (!in(x)) s.insert(x);
+  return s.size();
+}
+
+std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg) {
+  std::vector<bool> up = cfg.hoist ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
+  std::vector<Item> items;
+  for (size_t i = 0; i < g.nodes.size(); i++)
+    if (up[i]) items.push_back({false, i, {}});
+  auto dev_fusable = [&](size_t i) {
+    return fusable(g, i, true) && (cfg.fuse_f64 || g.nodes[i].dtype != DType::F64);
+  };
+  std::vector<size_t> level(g.nodes.size(), 0);
+  std::vector<std::vector<size_t>> by_level;
+  for (size_t i = 0; i < g.nodes.size(); i++) {
+    const Node& n = g.nodes[i];
+    if (!keep[i] || up[i] || leaf(n)) continue;
+    size_t deepest = 0;
+    for (uint32_t x : n.inputs) deepest = std::max(deepest, level[x]);
+    bool joins = dev_fusable(i) && deepest > 0;
+    if (joins) {
+      for (uint32_t x : n.inputs) {
+        if (!(level[x] < deepest ||
+              (dev_fusable(x) && g.nodes[x].shape == n.shape && g.nodes[x].dtype == n.dtype))) {
+          joins = false;
+          break;
+        }
+      }
+    }
+    level[i] = (is_alias(g, i) || joins) ? deepest : deepest + 1;
+    if (by_level.size() <= level[i]) by_level.resize(level[i] + 1);
+    by_level[level[i]].push_back(i);
+  }
+  for (auto& nodes : by_level) {
+    std::vector<std::vector<size_t>> groups;
+    std::vector<size_t> aliases;
+    for (size_t i : nodes) {
+      const Node& n = g.nodes[i];
+      if (is_alias(g, i)) {
+        aliases.push_back(i);  // reads a value of this level, so it follows the groups
+      } else if (dev_fusable(i)) {
+        // The last group of this shape, which earlier members may feed.
+        int64_t found = -1;
+        for (size_t k = groups.size(); k-- > 0;) {
+          const Node& f = g.nodes[groups[k][0]];
+          if (f.shape == n.shape && f.dtype == n.dtype) {
+            found = (int64_t)k;
+            break;
+          }
+        }
+        bool fits = found >= 0 &&
+                    distinct_external(g, groups[(size_t)found], n) + groups[(size_t)found].size() + 1 <= cfg.max_bindings;
+        if (found >= 0 && fits) groups[(size_t)found].push_back(i);
+        else groups.push_back({i});
+      } else {
+        items.push_back({false, i, {}});
+      }
+    }
+    for (auto& m : groups) {
+      if (m.size() >= 2) items.push_back({true, 0, m});
+      else
+        for (size_t x : m) items.push_back({false, x, {}});
+    }
+    for (size_t a : aliases) items.push_back({false, a, {}});
+  }
+  return items;
+}
+
+// Greedy fusion: one open group. Instructions independent of the group are emitted first; one
+// that reads a member closes the group, which keeps the group free of cycles (plan.rs:311-350).
+std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg) {
+  if (cfg.device && cfg.levels) return schedule_levels(g, keep, cfg);
+  std::vector<Item> items;
+  std::vector<size_t> open;
+  auto close = [&]() {
+    double cost = 0;
+    for (size_t m : open) cost += op_cost_ns(g.nodes[m].op) * (double)g.nodes[m].n();
+    if (open.size() >= (cfg.device ? 2u : 1u) && cost >= cfg.parallel_ns) {
+      items.push_back({true, 0, open});
+    } else {
+      for (size_t m : open) items.push_back({false, m, {}});
+    }
+    open.clear();
+  };
+  std::vector<bool> up = (cfg.device && cfg.hoist) ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
+  for (size_t i = 0; i < g.nodes.size(); i++)
+    if (up[i]) items.push_back({false, i, {}});
+  for (size_t i = 0; i < g.nodes.size(); i++) {
+    const Node& n = g.nodes[i];
+    if (!keep[i] || up[i] || leaf(n)) continue;
+    if (fusable(g, i, cfg.device) && !(cfg.device && !cfg.fuse_f64 && n.dtype == DType::F64)) {
+      bool same = open.empty() || (g.nodes[open[0]].shape == n.shape && g.nodes[open[0]].dtype == n.dtype);
+      size_t inputs = distinct_external(g, open, n);
+      if (!same || (cfg.device && inputs + open.size() + 1 > cfg.max_bindings)) close();
+      open.push_back(i);
+    } else {
+      bool reads = false;
+      for (uint32_t x : n.inputs) reads |= std::find(open.begin(), open.end(), (size_t)x) != open.end();
+      if (reads) close();
+      items.push_back({false, i, {}});
+    }
+  }
+  close();
+  return items;
+}
+
+Fused compile_group(const Graph& g, const std::vector<size_t>& members, const std::vector<size_t>& slot_of,
+                    const std::vector<std::pair<size_t, size_t>>& out_slots) {
+  const Node& first = g.nodes[members[0]];
+  Fused f;
+  std::vector<std::pair<uint32_t, std::pair<bool, size_t>>> ext;  // (node, operand)
+  size_t regs = 0;
+  auto member = [&](uint32_t x) { return std::find(members.begin(), members.end(), (size_t)x) != members.end(); };
+  for (size_t m : members) {
+    for (uint32_t x : g.nodes[m].inputs) {
+      bool seen = member(x);
+      for (auto& e : ext) seen |= e.first == x;
+      if (seen) continue;
+      rg_arg_kind kind;
+      size_t row = 0;
+      if (!arg_kind(g.shape(x), first.shape, &kind, &row)) kind = RG_ARG_BROADCAST;
+      f.input_shapes.push_back(g.shape(x));
+      std::pair<bool, size_t> operand;
+      size_t reg = SIZE_MAX;
+      if (kind == RG_ARG_FULL) {
+        operand = {false, f.inputs.size()};
+      } else {
+        reg = regs++;
+        operand = {true, reg};
+      }
+      f.inputs.push_back({slot_of[x], kind, row, reg});
+      ext.push_back({x, operand});
+    }
+  }
+  std::vector<size_t> reg_of(g.nodes.size(), SIZE_MAX);
+  for (size_t m : members) {
+    MicroOp mo;
+    mo.op = g.nodes[m].op;
+    for (uint32_t x : g.nodes[m].inputs) {
+      bool found = false;
+      for (auto& e : ext)
+        if (e.first == x) {
+          mo.args.push_back(e.second);
+          found = true;
+          break;
+        }
+      if (!found) mo.args.push_back({true, reg_of[x]});
+    }
+    reg_of[m] = regs;
+    mo.reg = regs;
+    f.ops.push_back(std::move(mo));
+    regs++;
+  }
+  for (auto& [m, s] : out_slots) f.outputs.push_back({reg_of[m], s});
+  f.dtype = first.dtype;
+  f.n = first.n();
+  f.regs = regs;
+  f.shape = first.shape;
+  return f;
+}
+
+rg_mode binary_mode(const Op& op, const Shape& shape, const std::vector<Shape>& args) {
+  if (!op.is_binary_elementwise()) return RG_MODE_SAME;
+  const Shape &a = args[0], &b = args[1];
+  auto one = [](const Shape& s) { return numel(s) == 1; };
+  if (a == shape && b == shape) return RG_MODE_SAME;
+  if (one(a) && b == shape) return RG_MODE_ASCALAR;
+  if (a == shape && one(b)) return RG_MODE_BSCALAR;
+  return RG_MODE_GENERAL;
+}
+
+Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse, const Fuse* fuse) {
+  std::vector<bool> keep = g.reachable(outputs);
+  size_t total = g.nodes.size();
+  std::vector<uint32_t> uses(total, 0);
+  for (size_t i = 0; i < total; i++)
+    if (keep[i])
+      for (uint32_t x : g.nodes[i].inputs) uses[x]++;
+  for (uint32_t o : outputs) uses[o]++;  // outputs stay live past the last instruction
+
+  Allocator a;
+  a.reuse = reuse;
+  std::vector<size_t> value_slot(total, SIZE_MAX);
+  Plan p;
+  p.input_slots.assign(g.n_inputs, 0);
+  p.input_ns.assign(g.n_inputs, 0);
+  for (size_t i = 0; i < total; i++) {
+    const Node& node = g.nodes[i];
+    if (node.op.kind == RG_OP_INPUT) {
+      size_t s = a.new_slot(node.dtype, node.n(), true);
+      p.input_slots[node.op.a] = s;
+      p.input_ns[node.op.a] = node.n();
+      value_slot[i] = s;
+    } else if (node.op.kind == RG_OP_CONST && keep[i]) {
+      size_t s = a.new_slot(node.dtype, node.n(), true);
+      p.consts.push_back({s, node.op.t});
+      value_slot[i] = s;
+    }
+  }
+
+  std::vector<Item> items;
+  if (fuse) {
+    items = schedule(g, keep, *fuse);
+  } else {
+    for (size_t i = 0; i < total; i++)
+      if (keep[i] && !leaf(g.nodes[i])) items.push_back({false, i, {}});
+  }
+
+  for (auto& item : items) {
+    if (item.group) {
+      const auto& members = item.members;
+      std::vector<uint32_t> external;
+      for (size_t m : members) {
+        p.naive_bytes += g.nodes[m].n() * dsize(g.nodes[m].dtype);
+        for (uint32_t x : g.nodes[m].inputs) {
+          uses[x]--;
+          if (std::find(members.begin(), members.end(), (size_t)x) == members.end() &&
+              std::find(external.begin(), external.end(), x) == external.end())
+            external.push_back(x);
+        }
+      }
+      // Destinations come first so they can never share a buffer with an input.
+      std::vector<std::pair<size_t, size_t>> out_slots;
+      for (size_t m : members) {
+        if (uses[m] > 0) {
+          size_t s = a.alloc(g.nodes[m].dtype, g.nodes[m].n());
+          value_slot[m] = s;
+          out_slots.push_back({m, s});
+        }
+      }
+      Step st;
+      st.fused = true;
+      st.group = compile_group(g, members, value_slot, out_slots);
+      p.steps.push_back(std::move(st));
+      for (uint32_t x : external)
+        if (uses[x] == 0) a.release(value_slot[x]);
+      continue;
+    }
+    size_t i = item.node;
+    const Node& node = g.nodes[i];
+    if (node.op.kind == RG_OP_OUTPUT) continue;
+    if (is_alias(g, i)) {
+      size_t x = node.inputs[0];
+      size_t s = value_slot[x];
+      a.refs[s]++;
+      value_slot[i] = s;
+      uses[x]--;
+      if (uses[x] == 0) a.release(s);
+      continue;
+    }
+    Instr in;
+    for (uint32_t x : node.inputs) {
+      in.arg_shapes.push_back(g.shape(x));
+      in.args.push_back(value_slot[x]);
+    }
+    in.mode = binary_mode(node.op, node.shape, in.arg_shapes);
+    for (uint32_t x : node.inputs) uses[x]--;
+    std::vector<uint32_t> dying;
+    for (uint32_t x : node.inputs)
+      if (uses[x] == 0) dying.push_back(x);
+    std::sort(dying.begin(), dying.end());
+    dying.erase(std::unique(dying.begin(), dying.end()), dying.end());
+    // A dying same-shape argument of an elementwise op can be overwritten in place.
+    bool elementwise = node.op.is_unary_elementwise() || node.op.is_binary_elementwise();
+    auto inplace = [&](uint32_t x) {
+      return elementwise && in.mode != RG_MODE_GENERAL && g.shape(x) == node.shape && g.dtype(x) == node.dtype;
+    };
+    for (uint32_t x : dying)
+      if (inplace(x)) a.release(value_slot[x]);
+    size_t dst = a.alloc(node.dtype, node.n());
+    for (uint32_t x : dying)
+      if (!inplace(x)) a.release(value_slot[x]);
+    value_slot[i] = dst;
+    p.naive_bytes += node.n() * dsize(node.dtype);
+    in.op = node.op;
+    in.node = (uint32_t)i;
+    in.dtype = node.dtype;
+    in.dst = dst;
+    in.shape = node.shape;
+    in.n = node.n();
+    Step st;
+    st.instr = std::move(in);
+    p.steps.push_back(std::move(st));
+  }
+  for (uint32_t o : outputs) p.outputs.push_back({value_slot[o], g.shape(o), g.nodes[o].n()});
+  p.reference = !reuse;
+  p.slots = std::move(a.slots);
+  p.pinned = std::move(a.pinned);
+  p.peak_live_bytes = a.peak;
+  return p;
+}
+
+}  // namespace
+
+size_t Plan::planned_bytes() const {
+  size_t b = 0;
+  for (size_t s = 0; s < slots.size(); s++)
+    if (!pinned[s]) b += dsize(slots[s].first) * slots[s].second;
+  return b;
+}
+
+double Plan::gpu_cost_estimate(const Fuse& f) const {
+  double c = 0;
+  for (auto& s : steps)
+    c += f.per_dispatch_ns + f.per_element_ns * (double)(s.fused ? s.group.n * s.group.outputs.size() : s.instr.n);
+  return c;
+}
+
+size_t Plan::n_fused() const {
+  size_t k = 0;
+  for (auto& s : steps) k += s.fused;
+  return k;
+}
+
+size_t Plan::n_fused_ops() const {
+  size_t k = 0;
+  for (auto& s : steps)
+    if (s.fused) k += s.group.ops.size();
+  return k;
+}
+
+Plan build_plan(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse) {
+  return build_with(g, outputs, reuse, nullptr);
+}
+
+Plan build_fused(const Graph& g, const std::vector<uint32_t>& outputs, const Fuse& cfg) {
+  Plan plan = build_with(g, outputs, true, &cfg);
+  if (!(cfg.device && cfg.levels)) return plan;
+  // Level order cuts dispatch dependencies but keeps values alive longer; keep the cheaper.
+  Fuse greedy_cfg = cfg;
+  greedy_cfg.levels = false;
+  Plan greedy = build_with(g, outputs, true, &greedy_cfg);
+  if (plan.peak_live_bytes > cfg.level_max_peak || greedy.gpu_cost_estimate(cfg) < plan.gpu_cost_estimate(cfg))
+    return greedy;
+  return plan;
+}
+
+static void put_op_attr(std::vector<int64_t>& a, const Op& op) {
+  auto vec = [&](const Shape& s) {
+    for (auto x : s) a.push_back((int64_t)x);
+  };
+  switch (op.kind) {
+    case RG_OP_MATMUL_T: a.push_back(op.ta); a.push_back(op.tb); break;
+    case RG_OP_REDUCE:
+      a.push_back((int64_t)op.rk);
+      a.push_back(op.keepdims);
+      a.push_back((int64_t)op.v.size());
+      vec(op.v);
+      break;
+    case RG_OP_TRANSPOSE: case RG_OP_BROADCAST_TO: case RG_OP_RESHAPE: case RG_OP_TAKE_ALONG_GRAD: vec(op.v); break;
+    case RG_OP_SLICE: case RG_OP_PAD:
+      a.push_back((int64_t)op.v.size());
+      vec(op.v);
+      vec(op.w);
+      break;
+    case RG_OP_CAST: a.push_back((int64_t)op.dt); break;
+    case RG_OP_TAKE: case RG_OP_CONCAT: case RG_OP_KEY_SPLIT: case RG_OP_ARG_TOP_K: a.push_back((int64_t)op.a); break;
+    case RG_OP_TAKE_GRAD: a.push_back((int64_t)op.a); vec(op.v); break;
+    case RG_OP_RAND_UNIFORM: case RG_OP_RAND_NORMAL: a.push_back((int64_t)op.dt); vec(op.v); break;
+    case RG_OP_CUMSUM: a.push_back(op.reverse); break;
+    default: break;
+  }
+}
+
+void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) const {
+  auto& w = *words;
+  w.clear();
+  blob->clear();
+  auto shape = [&](const Shape& s) {
+    w.push_back((int64_t)s.size());
+    for (auto d : s) w.push_back((int64_t)d);
+  };
+  w.push_back(RG_PLAN_MAGIC);
+  w.push_back(RG_PLAN_VERSION);
+  w.push_back((int64_t)slots.size());
+  for (size_t s = 0; s < slots.size(); s++) {
+    w.push_back((int64_t)slots[s].first);
+    w.push_back((int64_t)slots[s].second);
+    w.push_back(pinned[s] ? 1 : 0);
+  }
+  w.push_back((int64_t)consts.size());
+  for (auto& [slot, t] : consts) {
+    // 16-byte alignment keeps every constant readable as a vector.
+    while (blob->size() % 16) blob->push_back(0);
+    w.push_back((int64_t)slot);
+    w.push_back((int64_t)t->n());
+    w.push_back((int64_t)blob->size());
+    blob->insert(blob->end(), t->data.begin(), t->data.end());
+  }
+  w.push_back((int64_t)input_slots.size());
+  for (size_t k = 0; k < input_slots.size(); k++) {
+    w.push_back((int64_t)input_slots[k]);
+    w.push_back((int64_t)input_ns[k]);
+  }
+  w.push_back((int64_t)outputs.size());
+  for (auto& o : outputs) {
+    w.push_back((int64_t)o.slot);
+    w.push_back((int64_t)o.n);
+    shape(o.shape);
+  }
+  w.push_back((int64_t)steps.size());
+  for (auto& st : steps) {
+    if (!st.fused) {
+      const Instr& in = st.instr;
+      w.push_back(RG_STEP_INSTR);
+      w.push_back(in.op.kind);
+      w.push_back((int64_t)in.dtype);
+      w.push_back((int64_t)in.dst);
+      w.push_back((int64_t)in.n);
+      w.push_back(in.mode);
+      w.push_back(in.node);
+      shape(in.shape);
+      w.push_back((int64_t)in.args.size());
+      for (size_t k = 0; k < in.args.size(); k++) {
+        w.push_back((int64_t)in.args[k]);
+        shape(in.arg_shapes[k]);
+      }
+      std::vector<int64_t> attr;
+      put_op_attr(attr, in.op);
+      w.push_back((int64_t)attr.size());
+      w.insert(w.end(), attr.begin(), attr.end());
+    } else {
+      const Fused& f = st.group;
+      w.push_back(RG_STEP_FUSED);
+      w.push_back((int64_t)f.dtype);
+      w.push_back((int64_t)f.n);
+      w.push_back((int64_t)f.regs);
+      shape(f.shape);
+      w.push_back((int64_t)f.inputs.size());
+      for (size_t k = 0; k < f.inputs.size(); k++) {
+        w.push_back((int64_t)f.inputs[k].slot);
+        w.push_back(f.inputs[k].kind);
+        w.push_back((int64_t)f.inputs[k].row_len);
+        w.push_back(f.inputs[k].reg == SIZE_MAX ? -1 : (int64_t)f.inputs[k].reg);
+        shape(f.input_shapes[k]);
+      }
+      w.push_back((int64_t)f.ops.size());
+      for (auto& m : f.ops) {
+        w.push_back(m.op.kind);
+        w.push_back((int64_t)m.reg);
+        w.push_back((int64_t)m.args.size());
+        for (auto& [is_reg, idx] : m.args) {
+          w.push_back(is_reg ? 1 : 0);
+          w.push_back((int64_t)idx);
+        }
+      }
+      w.push_back((int64_t)f.outputs.size());
+      for (auto& [r, s] : f.outputs) {
+        w.push_back((int64_t)r);
+        w.push_back((int64_t)s);
+      }
+    }
+  }
+}
+
+}  // namespace rg

@@ -1,0 +1,112 @@
+// Plan IR: fused groups and instructions over numbered slots, with buffer reuse.
+// Restates the reference's src/plan.rs:12-27 (Fuse), 75-168 (types), 184-238 (allocator),
+// 249-457 (scheduling and group compilation) and 462-655 (building).
+#pragma once
+#include <functional>
+#include <memory>
+#include <vector>
+
+#include "graph.h"
+
+namespace rg {
+
+struct Fuse {
+  // Estimated group cost at which a CPU group pays for the thread pool (plan.rs:14-18).
+  double parallel_ns;
+  // Compile groups to device kernels: chains of any cost (plan.rs:19).
+  bool device;
+  // Order device work by dependency level (plan.rs:21).
+  bool levels;
+  // Most buffers one fused kernel may bind. Metal binds about 31 (plan.rs:249-250); a HIP
+  // kernel argument block holds far more, so the HIP flavour only caps code size.
+  size_t max_bindings;
+  // Schedule float64/small-integer bookkeeping first, as the Metal backend does for its CPU
+  // fallback (plan.rs:283-309). The HIP backend has no CPU fallback and keeps natural order.
+  bool hoist;
+  // Whether float64 elementwise chains may form device groups (Metal cannot, plan.rs:381).
+  bool fuse_f64;
+  // Level order is refused above this peak of live intermediates (plan.rs:251, 475).
+  size_t level_max_peak;
+  // Cost model of `gpu_cost_estimate` (plan.rs:481-492).
+  double per_dispatch_ns, per_element_ns;
+
+  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1}; }
+  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1}; }
+  // MI355X: ~4 us per dispatch inside a captured graph, ~0.001 ns per fp32 element written at
+  // HBM speed, and 288 GB of HBM so level order is capped far higher.
+  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001}; }
+};
+
+struct Instr {
+  Op op;
+  uint32_t node = 0;
+  DType dtype = DType::F32;
+  size_t dst = 0;
+  std::vector<size_t> args;
+  Shape shape;
+  std::vector<Shape> arg_shapes;
+  size_t n = 0;
+  rg_mode mode = RG_MODE_SAME;
+};
+
+struct FusedIn {
+  size_t slot;
+  rg_arg_kind kind;
+  size_t row_len;  // Row(L)
+  size_t reg;      // register of non-Full inputs, SIZE_MAX for Full
+};
+
+struct MicroOp {
+  Op op;
+  size_t reg;
+  std::vector<std::pair<bool, size_t>> args;  // (is register, index)
+};
+
+struct Fused {
+  DType dtype = DType::F32;
+  size_t n = 0;
+  std::vector<FusedIn> inputs;
+  std::vector<MicroOp> ops;
+  std::vector<std::pair<size_t, size_t>> outputs;  // (register, slot); never aliases an input
+  size_t regs = 0;
+  Shape shape;
+  std::vector<Shape> input_shapes;
+};
+
+struct Step {
+  bool fused = false;
+  Instr instr;
+  Fused group;
+};
+
+struct PlanOutput {
+  size_t slot;
+  Shape shape;
+  size_t n;
+};
+
+struct Plan {
+  std::vector<Step> steps;
+  std::vector<std::pair<DType, size_t>> slots;
+  std::vector<bool> pinned;
+  std::vector<std::pair<size_t, std::shared_ptr<const Tensor>>> consts;
+  std::vector<size_t> input_slots, input_ns;
+  std::vector<PlanOutput> outputs;
+  bool reference = false;
+  size_t naive_bytes = 0;
+  size_t peak_live_bytes = 0;
+
+  size_t planned_bytes() const;
+  double gpu_cost_estimate(const Fuse& f) const;
+  size_t n_fused() const;
+  size_t n_fused_ops() const;
+  // The flat descriptor of include/rg_plan.h and its constant blob.
+  void serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) const;
+};
+
+// Linear-scan liveness; reuse=false gives every value its own buffer (plan.rs:462-465).
+Plan build_plan(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse);
+// Buffer reuse plus fused groups (plan.rs:466-479).
+Plan build_fused(const Graph& g, const std::vector<uint32_t>& outputs, const Fuse& cfg);
+
+}  // namespace rg

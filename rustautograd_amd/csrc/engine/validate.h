@@ -1,0 +1,76 @@
+// Compile, validate and run (reference src/validate.rs).
+#pragma once
+#include <memory>
+#include <optional>
+
+#include "backend.h"
+#include "optimize.h"
+
+namespace rg {
+
+enum class Level { None = 0, Basic = 1, Standard = 2, Thorough = 3 };
+bool parse_level(const std::string& s, Level* out);
+
+struct RunSpec {
+  std::vector<std::pair<size_t, size_t>> state;  // (input index, output index) fed back
+  std::vector<size_t> data;                      // data input indices
+  std::vector<size_t> history;                   // scalar outputs recorded per step
+};
+
+struct RunOut {
+  std::vector<Tensor> state, outputs;
+  std::vector<std::vector<double>> history;
+  size_t steps = 0;
+  int64_t nonfinite_step = -1;
+  double seconds = 0;  // time in the step loop, excluding one-time setup
+  std::optional<std::string> device_error;
+};
+
+class Compiled {
+ public:
+  Graph raw;
+  std::vector<uint32_t> outputs;
+  Plan plan, raw_plan;
+  Json report;
+  Level level = Level::None;
+  OptMode mode = OptMode::Standard;
+  OptStats opt_stats;
+  Backend* device = nullptr;
+  std::unique_ptr<DeviceProgram> program;
+  std::unique_ptr<DeviceProgram> raw_program;  // built on first use by diagnostics
+
+  void check_inputs(const std::vector<Tensor>& inputs) const;
+  std::vector<Tensor> try_call(const std::vector<Tensor>& inputs) const;
+  Json check(const std::vector<Tensor>& inputs);
+  Json profile(const std::vector<Tensor>& inputs, size_t repeats) const;
+  void validate_spec(const RunSpec& spec) const;
+  RunOut run(const RunSpec& spec, const std::vector<Tensor>& state, const std::vector<std::vector<Tensor>>& batches,
+             size_t steps) const;
+  // First step at which the state or an output turns non-finite: (step, batch, state before).
+  std::optional<std::tuple<size_t, size_t, std::vector<Tensor>>> replay(const RunSpec& spec, const std::vector<Tensor>& state,
+                                                                       const std::vector<std::vector<Tensor>>& batches,
+                                                                       size_t steps) const;
+  Json validate(const std::vector<Tensor>& examples);
+  std::vector<uint32_t> raw_outputs() const;
+
+ private:
+  struct Observed {
+    std::vector<Json> roots, hard;
+    size_t propagated = 0;
+    std::vector<Tensor> vals;
+  };
+  Observed observed(const std::vector<Tensor>& inputs);
+  std::pair<Json, std::vector<Json>> gradient_stats(const std::vector<Tensor>& vals) const;
+  Json optimizer_check(const std::vector<Tensor>& examples) const;  // throws DiagError on mismatch
+  std::pair<Json, std::vector<Json>> device_check(const std::vector<Tensor>& examples) const;
+  std::pair<Json, std::vector<Json>> grad_check(const std::vector<Tensor>& examples) const;
+};
+
+// compile_mode (validate.rs:393-421): build, validate, and fall back to the standard plan when a
+// rewrite fails the equivalence check.
+std::unique_ptr<Compiled> compile_mode(const Graph& raw, const std::vector<uint32_t>& outputs,
+                                       const std::vector<Tensor>& examples, Level level, Backend* device, OptMode mode);
+
+Json device_failure(const std::string& device, const std::string& error);
+
+}  // namespace rg
