@@ -50,6 +50,13 @@ typedef struct rg_run_result {
 
 /* metal.rs:58-60 `available()`: 1 when a gfx950 device is present. */
 int rg_hip_available(void);
+/* Total HBM of device 0 in bytes, for the planner's memory warning (no reference counterpart;
+ * the reference asks the OS for physical memory, python/rg/_core.py:939-955). */
+uint64_t rg_hip_device_memory_bytes(void);
+/* Generates and compiles the JIT kernels of every fused group of a plan for gfx950 without a
+ * device; returns the kernel count or -1 with the compiler log. No reference counterpart: it
+ * checks the code generator in build environments without a GPU. */
+int rg_hip_compile_check(const int64_t* plan_words, size_t n_words, char* err, size_t err_len);
 
 /* metal.rs:380-503 `MetalProgram::new(&Plan)`: builds the kernels for every plan step (JIT
  * compiled fused groups plus precompiled instruction kernels). Refuses a slot larger than the

@@ -352,6 +352,18 @@ PYBIND11_MODULE(_rg, m) {
     return pc;
   });
   m.def("available_devices", []() { return available_backends(); });
+  m.def("plan_words", [](const PyGraph& graph, const std::vector<uint32_t>& outputs, const std::string& flavor, const std::string& optimize) {
+    // The serialized plan a device would receive (include/rg_plan.h), without needing the device.
+    OptMode mode;
+    if (!parse_opt_mode(optimize, &mode)) throw py::value_error("unknown optimize mode " + optimize);
+    bool dev = flavor != "cpu";
+    Optimized opt = optimize_mode(graph.g, outputs, dev, mode);
+    Plan plan = build_fused(opt.g, opt.outputs, dev ? Fuse::hip() : Fuse::cpu());
+    std::vector<int64_t> words;
+    std::vector<uint8_t> blob;
+    plan.serialize(&words, &blob);
+    return py::make_tuple(words, py::bytes((const char*)blob.data(), blob.size()));
+  });
   m.def("register_backend", [](const std::string& name, const std::string& path, const std::string& prefix) {
     try {
       register_backend(name, path, prefix);

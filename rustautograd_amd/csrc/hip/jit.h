@@ -1,0 +1,35 @@
+// Fused elementwise groups as JIT-compiled kernels: one kernel per group, specialised to its
+// micro-op chain, input kinds, shape and element count (all compile-time constants), compiled
+// for gfx950 with hiprtc. The reference compiles one MSL function per group body for the same
+// reason (src/metal.rs:122-152, 455-479).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../../../include/rg_plan.h"
+
+namespace rgjit {
+
+constexpr int TPB = 256;
+
+struct FusedKernel {
+  std::string name;
+  uint32_t grid = 0;     // blocks of TPB threads
+  int vec = 1;           // elements per thread
+  hipFunction_t fn = nullptr;
+};
+
+// Source of one kernel named `name` computing group `f`. `inplace` lists outputs whose slot is
+// also an input slot (the kernel then reads each element before writing it).
+std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k);
+
+// Compiles all sources into one code object for gfx950 and resolves each kernel. Modules are
+// cached by source text for the life of the process. Throws std::runtime_error with the log.
+void compile(const std::string& source, std::vector<FusedKernel*>& kernels);
+
+// The gfx950 code object for `source` (ops prelude added); throws with the compiler log.
+std::vector<char> compile_code(const std::string& source);
+
+}  // namespace rgjit

@@ -1,0 +1,100 @@
+// Host-side launchers of the precompiled CDNA4 kernels (kernels.hip, gemm.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "../../../include/rg_plan.h"
+
+namespace rgk {
+
+constexpr int MAX_DIMS = 8;
+
+// Division by a runtime constant through a multiply-high and a shift (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994), valid for n < 2^31.
+struct FastDiv {
+  uint32_t d = 1, mul = 0, shift = 0;
+  FastDiv() = default;
+  explicit FastDiv(uint32_t div) : d(div) {
+    uint32_t l = 0;
+    while ((1ull << l) < div) l++;
+    uint64_t p = 31 + l;
+    mul = (uint32_t)(((1ull << p) + div - 1) / div);
+    shift = (uint32_t)(p - 32);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return d == 1 ? n : (__umulhi(n, mul) >> shift); }
+};
+
+// An output index space of up to MAX_DIMS dims and, per operand, the flat stride of each dim.
+struct Strided {
+  int rank = 0;
+  FastDiv size[MAX_DIMS];   // dim sizes, innermost last
+  uint32_t st[3][MAX_DIMS];  // strides of up to three operands
+  uint32_t base[3] = {0, 0, 0};
+};
+
+// Builds `Strided` for an output shape and up to three operand stride lists, merging adjacent
+// dims that are contiguous for every operand and dropping size-1 dims.
+Strided make_strided(const std::vector<int64_t>& shape, const std::vector<std::vector<int64_t>>& strides);
+std::vector<int64_t> row_strides(const std::vector<int64_t>& shape);
+// Strides of `shape` right-aligned to `rank` dims with 0 on broadcast dims.
+std::vector<int64_t> bcast_strides(const std::vector<int64_t>& shape, size_t rank);
+
+void unary(hipStream_t s, int dtype, int op, const void* a, void* d, uint64_t n);
+void binary(hipStream_t s, int dtype, int op, const void* a, const void* b, void* d, uint64_t n, int mode, const Strided* g);
+void where(hipStream_t s, int esize, const void* c, const void* a, const void* b, void* d, uint64_t n, int dtype);
+void gather(hipStream_t s, int esize, const void* src, void* dst, uint64_t n, const Strided& g);
+void pad(hipStream_t s, int esize, const void* src, void* dst, uint64_t n, const std::vector<int64_t>& out_shape,
+         const std::vector<int64_t>& starts, const std::vector<int64_t>& in_shape);
+void concat_piece(hipStream_t s, int esize, const void* src, void* dst, uint64_t outer, uint64_t len, uint64_t total, uint64_t at);
+void take(hipStream_t s, int esize, const void* src, const int32_t* idx, void* dst, uint64_t n, uint64_t block,
+          uint64_t n_idx, uint64_t dim);
+void take_along(hipStream_t s, int esize, const void* src, const int32_t* idx, void* dst, uint64_t n, uint64_t k, uint64_t v);
+void take_grad(hipStream_t s, int dtype, const void* ct, const int32_t* idx, void* dst, uint64_t n, uint64_t block,
+               uint64_t n_idx, uint64_t dim);
+void take_along_grad(hipStream_t s, int dtype, const void* ct, const int32_t* idx, void* dst, uint64_t n, uint64_t k,
+                     uint64_t v);
+void rand_uniform(hipStream_t s, int dtype, const int32_t* key, void* dst, uint64_t n);
+void rand_normal(hipStream_t s, int dtype, const int32_t* key, void* dst, uint64_t n);
+void key_split(hipStream_t s, const int32_t* key, int32_t* dst, uint64_t pairs);
+void cast(hipStream_t s, int from, int to, const void* a, void* d, uint64_t n);
+void argmax(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, uint64_t v);
+void arg_top_k(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, uint64_t v, uint64_t k);
+void cumsum(hipStream_t s, int dtype, const void* a, void* d, uint64_t rows, uint64_t v, bool reverse);
+
+// Reductions over a canonical pattern; see runtime.cpp for how shapes map onto them.
+void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t rows, uint64_t len);
+void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k,
+                 void* partial, uint64_t chunks);
+uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k);
+void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer,
+                    const Strided& inner, uint64_t red_n);
+
+// Run-loop helpers.
+void copy_bytes(hipStream_t s, void* dst, const void* src, uint64_t bytes);
+void record_history(hipStream_t s, int dtype, const void* slot, double* hist, const uint64_t* counter, uint64_t stride);
+void load_batch(hipStream_t s, void* dst, const void* batches, uint64_t bytes, uint64_t n_batches, const uint64_t* counter);
+void counter_inc(hipStream_t s, uint64_t* counter);
+void fill_zero(hipStream_t s, void* dst, uint64_t bytes);
+
+// Dense products. A is [M,K] (or [K,M] when ta), B is [K,N] (or [N,K] when tb), C is [M,N],
+// all row-major, over `batch` matrices at the given element offsets (nullptr = contiguous).
+struct GemmArgs {
+  int dtype;
+  bool ta, tb;
+  uint64_t m, n, k, batch;
+  const void* a;
+  const void* b;
+  void* c;
+  const int64_t* a_off;  // device arrays of per-batch element offsets, or nullptr
+  const int64_t* b_off;
+  uint64_t a_stride, b_stride;  // per-batch element strides when the offset arrays are null
+  void* workspace;              // split-K partial sums
+  uint64_t workspace_bytes;
+};
+// Workspace bytes the product needs for its split-K partials.
+uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch);
+void gemm(hipStream_t s, const GemmArgs& g);
+
+}  // namespace rgk

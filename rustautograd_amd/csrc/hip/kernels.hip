@@ -1,0 +1,671 @@
+// Precompiled CDNA4 kernels for every plan instruction that is not a fused group or a product:
+// single elementwise operations, structural copies, int32 gather/scatter, RNG, casts, argmax,
+// sort and scan, reductions, and the helpers of the device-resident step loop.
+//
+// All of these are HBM-bound: wave64 blocks of 256 threads, coalesced row-major access, no LDS
+// except where a reduction combines partial results.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "kernels.h"
+#include "ops.h"
+
+namespace rgk {
+
+namespace {
+
+constexpr int TPB = 256;
+
+inline uint32_t blocks_for(uint64_t n, uint64_t per_block) { return (uint32_t)((n + per_block - 1) / per_block); }
+
+template <class T> struct Red;
+template <> struct Red<float> {
+  static __device__ __forceinline__ float init(int kind) { return kind == RG_REDUCE_SUM ? 0.0f : kind == RG_REDUCE_MAX ? -INFINITY : INFINITY; }
+};
+template <> struct Red<double> {
+  static __device__ __forceinline__ double init(int kind) { return kind == RG_REDUCE_SUM ? 0.0 : kind == RG_REDUCE_MAX ? -INFINITY : INFINITY; }
+};
+
+template <class T>
+__device__ __forceinline__ T combine(int kind, T acc, T x) {
+  return kind == RG_REDUCE_SUM ? acc + x : kind == RG_REDUCE_MAX ? rg_max(acc, x) : rg_min(acc, x);
+}
+
+__device__ __forceinline__ void decompose(const Strided& g, uint32_t i, uint32_t* off, int nops) {
+  for (int k = 0; k < nops; k++) off[k] = g.base[k];
+  for (int d = g.rank - 1; d >= 0; d--) {
+    uint32_t q = g.size[d].div(i);
+    uint32_t c = i - q * g.size[d].d;
+    for (int k = 0; k < nops; k++) off[k] += c * g.st[k][d];
+    i = q;
+  }
+}
+
+// ---- elementwise -------------------------------------------------------------------------
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_unary(int op, const T* __restrict__ a, T* d, uint32_t n) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i < n) d[i] = rg_unary<T>(op, a[i]);
+}
+
+// mode: 0 same shape, 1 a is a scalar, 2 b is a scalar (src/plan.rs:1008-1023).
+template <class T>
+__global__ void __launch_bounds__(TPB) k_binary(int op, const T* a, const T* b, T* d, uint32_t n, int mode) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  T x = mode == 1 ? a[0] : a[i];
+  T y = mode == 2 ? b[0] : b[i];
+  d[i] = rg_binary<T>(op, x, y);
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_binary_general(int op, const T* a, const T* b, T* d, uint32_t n, Strided g) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  uint32_t off[2];
+  decompose(g, i, off, 2);
+  d[i] = rg_binary<T>(op, a[off[0]], b[off[1]]);
+}
+
+__global__ void __launch_bounds__(TPB) k_binary_int(int op, const int* a, const int* b, int* d, uint32_t n, int mode) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  int x = mode == 1 ? a[0] : a[i];
+  int y = mode == 2 ? b[0] : b[i];
+  d[i] = rg_binary_int(op, x, y);
+}
+
+__global__ void __launch_bounds__(TPB) k_binary_int_general(int op, const int* a, const int* b, int* d, uint32_t n, Strided g) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  uint32_t off[2];
+  decompose(g, i, off, 2);
+  d[i] = rg_binary_int(op, a[off[0]], b[off[1]]);
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_where(const T* c, const T* a, const T* b, T* d, uint32_t n) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i < n) d[i] = c[i] != (T)0 ? a[i] : b[i];
+}
+
+// ---- structural copies (any dtype, moved as 32- or 64-bit words) ------------------------
+
+template <class E>
+__global__ void __launch_bounds__(TPB) k_gather(const E* __restrict__ src, E* __restrict__ dst, uint32_t n, Strided g) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  uint32_t off[1];
+  decompose(g, i, off, 1);
+  dst[i] = src[off[0]];
+}
+
+struct PadDims {
+  int rank;
+  FastDiv size[MAX_DIMS];
+  uint32_t start[MAX_DIMS], len[MAX_DIMS], src_st[MAX_DIMS];
+};
+
+template <class E>
+__global__ void __launch_bounds__(TPB) k_pad(const E* __restrict__ src, E* __restrict__ dst, uint32_t n, PadDims p) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  uint32_t off = 0, rem = i;
+  bool inside = true;
+  for (int d = p.rank - 1; d >= 0; d--) {
+    uint32_t q = p.size[d].div(rem);
+    uint32_t c = rem - q * p.size[d].d;
+    rem = q;
+    if (c < p.start[d] || c >= p.start[d] + p.len[d]) inside = false;
+    else off += (c - p.start[d]) * p.src_st[d];
+  }
+  dst[i] = inside ? src[off] : (E)0;
+}
+
+template <class E>
+__global__ void __launch_bounds__(TPB) k_concat_piece(const E* __restrict__ src, E* __restrict__ dst, uint32_t n, FastDiv len,
+                                                      uint32_t total, uint32_t at) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  uint32_t o = len.div(i);
+  uint32_t q = i - o * len.d;
+  dst[o * total + at + q] = src[i];
+}
+
+__device__ __forceinline__ uint32_t clamp_index(int ix, uint32_t dim) { return ix < 0 ? 0u : ((uint32_t)ix >= dim ? dim - 1 : (uint32_t)ix); }
+
+template <class E>
+__global__ void __launch_bounds__(TPB) k_take(const E* __restrict__ src, const int* __restrict__ idx, E* __restrict__ dst, uint32_t n,
+                                              FastDiv block, FastDiv n_idx, uint32_t dim) {
+  uint32_t t = blockIdx.x * TPB + threadIdx.x;
+  if (t >= n) return;
+  uint32_t r = block.div(t);
+  uint32_t q = t - r * block.d;
+  uint32_t o = n_idx.div(r);
+  uint32_t j = r - o * n_idx.d;
+  dst[t] = src[(o * dim + clamp_index(idx[j], dim)) * block.d + q];
+}
+
+template <class E>
+__global__ void __launch_bounds__(TPB) k_take_along(const E* __restrict__ src, const int* __restrict__ idx, E* __restrict__ dst,
+                                                    uint32_t n, FastDiv k, uint32_t v) {
+  uint32_t j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  dst[j] = src[k.div(j) * v + clamp_index(idx[j], v)];
+}
+
+// ---- deterministic scatter-add ------------------------------------------------------------
+// Each output element sums the cotangents whose index hits it, in increasing index position:
+// the CPU's sequential order (src/plan.rs:1502-1531), so results are bit-identical. Index chunks
+// are staged in LDS and shared by the block.
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_take_grad(const T* __restrict__ ct, const int* __restrict__ idx, T* __restrict__ dst,
+                                                   uint32_t n, FastDiv block, FastDiv dim, uint32_t n_idx) {
+  __shared__ int sidx[1024];
+  uint32_t t = blockIdx.x * TPB + threadIdx.x;
+  bool live = t < n;
+  uint32_t r = block.div(live ? t : 0);
+  uint32_t q = (live ? t : 0) - r * block.d;
+  uint32_t o = dim.div(r);
+  uint32_t dd = r - o * dim.d;
+  T acc = (T)0;
+  for (uint32_t j0 = 0; j0 < n_idx; j0 += 1024) {
+    uint32_t m = min(1024u, n_idx - j0);
+    __syncthreads();
+    for (uint32_t x = threadIdx.x; x < m; x += TPB) sidx[x] = idx[j0 + x];
+    __syncthreads();
+    if (live)
+      for (uint32_t x = 0; x < m; x++)
+        if (clamp_index(sidx[x], dim.d) == dd) acc = acc + ct[((uint64_t)o * n_idx + j0 + x) * block.d + q];
+  }
+  if (live) dst[t] = acc;
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_take_along_grad(const T* __restrict__ ct, const int* __restrict__ idx, T* __restrict__ dst,
+                                                         uint32_t n, FastDiv v, uint32_t k) {
+  uint32_t t = blockIdx.x * TPB + threadIdx.x;
+  if (t >= n) return;
+  uint32_t r = v.div(t);
+  uint32_t c = t - r * v.d;
+  T acc = (T)0;
+  for (uint32_t x = 0; x < k; x++)
+    if (clamp_index(idx[r * k + x], v.d) == c) acc = acc + ct[r * k + x];
+  dst[t] = acc;
+}
+
+// ---- random streams (SplitMix64 of key and index, src/plan.rs:1391-1435) ----------------
+
+constexpr uint64_t GAMMA = 0x9E3779B97F4A7C15ull;
+constexpr uint64_t GAMMA_SPLIT = 0xD1B54A32D192ED03ull;
+
+__device__ __forceinline__ uint64_t mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t read_key(const int* k) { return ((uint64_t)(uint32_t)k[0] << 32) | (uint64_t)(uint32_t)k[1]; }
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_rand_uniform(const int* __restrict__ key, T* __restrict__ dst, uint32_t n) {
+  uint32_t j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  uint64_t kk = read_key(key);
+  constexpr int mant = sizeof(T) == 4 ? 24 : 53;
+  uint64_t bits = mix(kk + ((uint64_t)j + 1) * GAMMA) >> (64 - mant);
+  dst[j] = (T)((double)bits * (1.0 / (double)(1ull << mant)));
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_rand_normal(const int* __restrict__ key, T* __restrict__ dst, uint32_t n) {
+  uint32_t j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  uint64_t kk = read_key(key);
+  const double scale = 1.0 / 9007199254740992.0;  // 2^-53
+  double u1 = 1.0 - (double)(mix(kk + (2 * (uint64_t)j + 1) * GAMMA) >> 11) * scale;
+  double u2 = (double)(mix(kk + (2 * (uint64_t)j + 2) * GAMMA) >> 11) * scale;
+  dst[j] = (T)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+}
+
+__global__ void __launch_bounds__(TPB) k_key_split(const int* __restrict__ key, int* __restrict__ dst, uint32_t pairs) {
+  uint32_t j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= pairs) return;
+  uint64_t bits = mix(read_key(key) + ((uint64_t)j + 1) * GAMMA_SPLIT);
+  dst[2 * j] = (int)(uint32_t)(bits >> 32);
+  dst[2 * j + 1] = (int)(uint32_t)bits;
+}
+
+// ---- casts (Rust `as`: float to int truncates, saturates, NaN is 0) ---------------------
+
+__device__ __forceinline__ int sat_i32(double x) {
+  if (x != x) return 0;
+  if (x >= 2147483647.0) return 2147483647;
+  if (x <= -2147483648.0) return (int)0x80000000u;
+  return (int)x;
+}
+
+template <class S, class D>
+__global__ void __launch_bounds__(TPB) k_cast(const S* __restrict__ a, D* __restrict__ d, uint32_t n) {
+  uint32_t i = blockIdx.x * TPB + threadIdx.x;
+  if (i >= n) return;
+  if constexpr (sizeof(D) == 4 && !std::is_floating_point<D>::value) d[i] = sat_i32((double)a[i]);
+  else d[i] = (D)a[i];
+}
+
+// ---- argmax, top-k, cumsum (one row per thread, in the CPU's order) --------------------
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_argmax(const T* __restrict__ a, int* __restrict__ d, uint32_t rows, uint32_t v) {
+  uint32_t r = blockIdx.x * TPB + threadIdx.x;
+  if (r >= rows) return;
+  const T* row = a + (uint64_t)r * v;
+  uint32_t best = 0;
+  for (uint32_t j = 0; j < v; j++)
+    if (row[j] > row[best]) best = j;
+  d[r] = (int)best;
+}
+
+// Rank order of src/plan.rs:838-848: larger first, ties by index, NaN last.
+template <class T>
+__device__ __forceinline__ bool before(const T* row, uint32_t x, uint32_t y) {
+  T p = row[x], q = row[y];
+  bool pn = p != p, qn = q != q;
+  if (pn || qn) return pn != qn ? qn : x < y;
+  if (p != q) return p > q;
+  return x < y;
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_arg_top_k(const T* __restrict__ a, int* __restrict__ d, uint32_t rows, uint32_t v, uint32_t k) {
+  uint32_t r = blockIdx.x * TPB + threadIdx.x;
+  if (r >= rows) return;
+  const T* row = a + (uint64_t)r * v;
+  // Each output is the successor of the previous one in the total order.
+  uint32_t prev = 0;
+  for (uint32_t p = 0; p < k; p++) {
+    uint32_t best = 0xffffffffu;
+    for (uint32_t j = 0; j < v; j++) {
+      if (p > 0 && !before(row, prev, j)) continue;
+      if (best == 0xffffffffu || before(row, j, best)) best = j;
+    }
+    d[(uint64_t)r * k + p] = (int)best;
+    prev = best;
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_cumsum(const T* __restrict__ a, T* __restrict__ d, uint32_t rows, uint32_t v, int reverse) {
+  uint32_t r = blockIdx.x * TPB + threadIdx.x;
+  if (r >= rows) return;
+  const T* x = a + (uint64_t)r * v;
+  T* y = d + (uint64_t)r * v;
+  T acc = (T)0;
+  if (reverse)
+    for (uint32_t j = v; j-- > 0;) y[j] = acc = acc + x[j];
+  else
+    for (uint32_t j = 0; j < v; j++) y[j] = acc = acc + x[j];
+}
+
+__global__ void __launch_bounds__(TPB) k_cumsum_int(const int* __restrict__ a, int* __restrict__ d, uint32_t rows, uint32_t v, int reverse) {
+  uint32_t r = blockIdx.x * TPB + threadIdx.x;
+  if (r >= rows) return;
+  const int* x = a + (uint64_t)r * v;
+  int* y = d + (uint64_t)r * v;
+  uint32_t acc = 0;
+  if (reverse)
+    for (uint32_t j = v; j-- > 0;) y[j] = (int)(acc += (uint32_t)x[j]);
+  else
+    for (uint32_t j = 0; j < v; j++) y[j] = (int)(acc += (uint32_t)x[j]);
+}
+
+// ---- reductions ---------------------------------------------------------------------------
+
+template <class T>
+__device__ __forceinline__ T wave_combine(int kind, T v) {
+  for (int m = 32; m >= 1; m >>= 1) v = combine(kind, v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// One wave per row: rows up to a few thousand elements (LayerNorm, softmax, cross-entropy).
+template <class T>
+__global__ void __launch_bounds__(TPB) k_reduce_rows_wave(int kind, const T* __restrict__ a, T* __restrict__ d, uint32_t rows, uint32_t len) {
+  uint32_t row = blockIdx.x * (TPB / 64) + threadIdx.x / 64;
+  uint32_t lane = threadIdx.x % 64;
+  if (row >= rows) return;
+  const T* x = a + (uint64_t)row * len;
+  T acc = Red<T>::init(kind);
+  for (uint32_t j = lane; j < len; j += 64) acc = combine(kind, acc, x[j]);
+  acc = wave_combine(kind, acc);
+  if (lane == 0) d[row] = acc;
+}
+
+// One block per row segment: long rows and full reductions. Segment g covers
+// [g*seg, min(len, (g+1)*seg)) of row `blockIdx.y`.
+template <class T>
+__global__ void __launch_bounds__(TPB) k_reduce_rows_block(int kind, const T* __restrict__ a, T* __restrict__ d, uint64_t len, uint64_t seg) {
+  __shared__ T part[TPB / 64];
+  uint64_t row = blockIdx.y;
+  uint64_t begin = (uint64_t)blockIdx.x * seg, end = min(len, begin + seg);
+  const T* x = a + row * len;
+  T acc = Red<T>::init(kind);
+  for (uint64_t j = begin + threadIdx.x; j < end; j += TPB) acc = combine(kind, acc, x[j]);
+  acc = wave_combine(kind, acc);
+  if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    T r = part[0];
+    for (int w = 1; w < TPB / 64; w++) r = combine(kind, r, part[w]);
+    d[row * gridDim.x + blockIdx.x] = r;
+  }
+}
+
+// Leading-axis reduction of [batch, r, k] over r: threads own columns (coalesced), row chunks
+// give parallelism, and partial results combine in a fixed order in a second pass.
+template <class T>
+__global__ void __launch_bounds__(TPB) k_reduce_cols(int kind, const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
+                                                      uint32_t chunk_rows, uint32_t chunks) {
+  uint32_t c = blockIdx.x * TPB + threadIdx.x;
+  uint32_t b = blockIdx.y, s = blockIdx.z;
+  if (c >= k) return;
+  uint32_t r0 = s * chunk_rows, r1 = min(r, r0 + chunk_rows);
+  const T* x = a + (uint64_t)b * r * k + c;
+  T acc = Red<T>::init(kind);
+  for (uint32_t row = r0; row < r1; row++) acc = combine(kind, acc, x[(uint64_t)row * k]);
+  out[((uint64_t)b * chunks + s) * k + c] = acc;
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_reduce_cols_finish(int kind, const T* __restrict__ part, T* __restrict__ d, uint32_t k, uint32_t chunks) {
+  uint32_t c = blockIdx.x * TPB + threadIdx.x;
+  uint32_t b = blockIdx.y;
+  if (c >= k) return;
+  T acc = Red<T>::init(kind);
+  for (uint32_t s = 0; s < chunks; s++) acc = combine(kind, acc, part[((uint64_t)b * chunks + s) * k + c]);
+  d[(uint64_t)b * k + c] = acc;
+}
+
+template <class T>
+__global__ void __launch_bounds__(TPB) k_reduce_general(int kind, const T* __restrict__ a, T* __restrict__ d, uint32_t out_n, Strided outer,
+                                                        Strided inner, uint32_t red_n) {
+  uint32_t o = blockIdx.x * TPB + threadIdx.x;
+  if (o >= out_n) return;
+  uint32_t base[1];
+  decompose(outer, o, base, 1);
+  T acc = Red<T>::init(kind);
+  for (uint32_t r = 0; r < red_n; r++) {
+    uint32_t off[1];
+    decompose(inner, r, off, 1);
+    acc = combine(kind, acc, a[base[0] + off[0]]);
+  }
+  d[o] = acc;
+}
+
+// ---- step-loop helpers ------------------------------------------------------------------
+
+__global__ void __launch_bounds__(TPB) k_copy_words(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, uint64_t words) {
+  uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x;
+  if (i < words) dst[i] = src[i];
+}
+
+__global__ void k_record_history(int dtype, const void* slot, double* hist, const uint64_t* counter, uint64_t stride) {
+  double v = dtype == RG_F32 ? (double)((const float*)slot)[0] : dtype == RG_F64 ? ((const double*)slot)[0] : (double)((const int*)slot)[0];
+  hist[*counter % stride] = v;
+}
+
+__global__ void __launch_bounds__(TPB) k_load_batch(uint32_t* __restrict__ dst, const uint32_t* __restrict__ batches, uint64_t words,
+                                                     uint64_t n_batches, const uint64_t* counter) {
+  uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x;
+  if (i >= words) return;
+  uint64_t b = *counter % n_batches;
+  dst[i] = batches[b * words + i];
+}
+
+__global__ void k_counter_inc(uint64_t* counter) { *counter += 1; }
+
+__global__ void __launch_bounds__(TPB) k_fill_zero(uint32_t* dst, uint64_t words) {
+  uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x;
+  if (i < words) dst[i] = 0;
+}
+
+}  // namespace
+
+// ---- host side --------------------------------------------------------------------------
+
+std::vector<int64_t> row_strides(const std::vector<int64_t>& shape) {
+  std::vector<int64_t> st(shape.size(), 1);
+  for (size_t i = shape.size(); i-- > 1;) st[i - 1] = st[i] * shape[i];
+  return st;
+}
+
+std::vector<int64_t> bcast_strides(const std::vector<int64_t>& shape, size_t rank) {
+  auto st = row_strides(shape);
+  size_t lead = rank - shape.size();
+  std::vector<int64_t> out(rank, 0);
+  for (size_t i = 0; i < rank; i++) out[i] = (i < lead || shape[i - lead] == 1) ? 0 : st[i - lead];
+  return out;
+}
+
+Strided make_strided(const std::vector<int64_t>& shape, const std::vector<std::vector<int64_t>>& strides) {
+  size_t nops = strides.size();
+  std::vector<int64_t> sz;
+  std::vector<std::vector<int64_t>> st(nops);
+  for (size_t d = 0; d < shape.size(); d++) {
+    if (shape[d] == 1) continue;
+    if (!sz.empty()) {
+      bool merge = true;
+      for (size_t k = 0; k < nops; k++)
+        if (st[k].back() != strides[k][d] * shape[d]) merge = false;
+      if (merge) {
+        sz.back() *= shape[d];
+        for (size_t k = 0; k < nops; k++) st[k].back() = strides[k][d];
+        continue;
+      }
+    }
+    sz.push_back(shape[d]);
+    for (size_t k = 0; k < nops; k++) st[k].push_back(strides[k][d]);
+  }
+  if (sz.size() > (size_t)MAX_DIMS) throw std::runtime_error("too many non-mergeable dimensions for a strided kernel");
+  Strided g;
+  g.rank = (int)sz.size();
+  for (size_t d = 0; d < sz.size(); d++) {
+    g.size[d] = FastDiv((uint32_t)sz[d]);
+    for (size_t k = 0; k < nops; k++) g.st[k][d] = (uint32_t)st[k][d];
+  }
+  return g;
+}
+
+#define RG_LAUNCH(kernel, n, ...)                                                   \
+  do {                                                                              \
+    if ((n) > 0) hipLaunchKernelGGL(kernel, dim3(blocks_for((n), TPB)), dim3(TPB), 0, s, __VA_ARGS__); \
+  } while (0)
+
+void unary(hipStream_t s, int dtype, int op, const void* a, void* d, uint64_t n) {
+  if (dtype == RG_F32) RG_LAUNCH(k_unary<float>, n, op, (const float*)a, (float*)d, (uint32_t)n);
+  else RG_LAUNCH(k_unary<double>, n, op, (const double*)a, (double*)d, (uint32_t)n);
+}
+
+void binary(hipStream_t s, int dtype, int op, const void* a, const void* b, void* d, uint64_t n, int mode, const Strided* g) {
+  if (dtype == RG_I32) {
+    if (g) RG_LAUNCH(k_binary_int_general, n, op, (const int*)a, (const int*)b, (int*)d, (uint32_t)n, *g);
+    else RG_LAUNCH(k_binary_int, n, op, (const int*)a, (const int*)b, (int*)d, (uint32_t)n, mode);
+  } else if (dtype == RG_F32) {
+    if (g) RG_LAUNCH(k_binary_general<float>, n, op, (const float*)a, (const float*)b, (float*)d, (uint32_t)n, *g);
+    else RG_LAUNCH(k_binary<float>, n, op, (const float*)a, (const float*)b, (float*)d, (uint32_t)n, mode);
+  } else {
+    if (g) RG_LAUNCH(k_binary_general<double>, n, op, (const double*)a, (const double*)b, (double*)d, (uint32_t)n, *g);
+    else RG_LAUNCH(k_binary<double>, n, op, (const double*)a, (const double*)b, (double*)d, (uint32_t)n, mode);
+  }
+}
+
+void where(hipStream_t s, int esize, const void* c, const void* a, const void* b, void* d, uint64_t n, int dtype) {
+  if (dtype == RG_F32) RG_LAUNCH(k_where<float>, n, (const float*)c, (const float*)a, (const float*)b, (float*)d, (uint32_t)n);
+  else if (dtype == RG_F64) RG_LAUNCH(k_where<double>, n, (const double*)c, (const double*)a, (const double*)b, (double*)d, (uint32_t)n);
+  else RG_LAUNCH(k_where<int>, n, (const int*)c, (const int*)a, (const int*)b, (int*)d, (uint32_t)n);
+  (void)esize;
+}
+
+void gather(hipStream_t s, int esize, const void* src, void* dst, uint64_t n, const Strided& g) {
+  if (esize == 4) RG_LAUNCH(k_gather<uint32_t>, n, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, g);
+  else RG_LAUNCH(k_gather<uint64_t>, n, (const uint64_t*)src, (uint64_t*)dst, (uint32_t)n, g);
+}
+
+void pad(hipStream_t s, int esize, const void* src, void* dst, uint64_t n, const std::vector<int64_t>& out_shape,
+         const std::vector<int64_t>& starts, const std::vector<int64_t>& in_shape) {
+  if (out_shape.size() > (size_t)MAX_DIMS) throw std::runtime_error("pad rank above 8");
+  PadDims p;
+  p.rank = (int)out_shape.size();
+  auto st = row_strides(in_shape);
+  for (size_t d = 0; d < out_shape.size(); d++) {
+    p.size[d] = FastDiv((uint32_t)out_shape[d]);
+    p.start[d] = (uint32_t)starts[d];
+    p.len[d] = (uint32_t)in_shape[d];
+    p.src_st[d] = (uint32_t)st[d];
+  }
+  if (esize == 4) RG_LAUNCH(k_pad<uint32_t>, n, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, p);
+  else RG_LAUNCH(k_pad<uint64_t>, n, (const uint64_t*)src, (uint64_t*)dst, (uint32_t)n, p);
+}
+
+void concat_piece(hipStream_t s, int esize, const void* src, void* dst, uint64_t outer, uint64_t len, uint64_t total, uint64_t at) {
+  uint64_t n = outer * len;
+  if (len == 0) return;
+  FastDiv l((uint32_t)len);
+  if (esize == 4) RG_LAUNCH(k_concat_piece<uint32_t>, n, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, l, (uint32_t)total, (uint32_t)at);
+  else RG_LAUNCH(k_concat_piece<uint64_t>, n, (const uint64_t*)src, (uint64_t*)dst, (uint32_t)n, l, (uint32_t)total, (uint32_t)at);
+}
+
+void take(hipStream_t s, int esize, const void* src, const int32_t* idx, void* dst, uint64_t n, uint64_t block, uint64_t n_idx,
+          uint64_t dim) {
+  if (n_idx == 0 || block == 0) return;
+  FastDiv fb((uint32_t)block), fi((uint32_t)n_idx);
+  if (esize == 4) RG_LAUNCH(k_take<uint32_t>, n, (const uint32_t*)src, idx, (uint32_t*)dst, (uint32_t)n, fb, fi, (uint32_t)dim);
+  else RG_LAUNCH(k_take<uint64_t>, n, (const uint64_t*)src, idx, (uint64_t*)dst, (uint32_t)n, fb, fi, (uint32_t)dim);
+}
+
+void take_along(hipStream_t s, int esize, const void* src, const int32_t* idx, void* dst, uint64_t n, uint64_t k, uint64_t v) {
+  if (k == 0) return;
+  FastDiv fk((uint32_t)k);
+  if (esize == 4) RG_LAUNCH(k_take_along<uint32_t>, n, (const uint32_t*)src, idx, (uint32_t*)dst, (uint32_t)n, fk, (uint32_t)v);
+  else RG_LAUNCH(k_take_along<uint64_t>, n, (const uint64_t*)src, idx, (uint64_t*)dst, (uint32_t)n, fk, (uint32_t)v);
+}
+
+void take_grad(hipStream_t s, int dtype, const void* ct, const int32_t* idx, void* dst, uint64_t n, uint64_t block, uint64_t n_idx,
+               uint64_t dim) {
+  if (block == 0) return;
+  FastDiv fb((uint32_t)block), fd((uint32_t)dim);
+  if (dtype == RG_F32) RG_LAUNCH(k_take_grad<float>, n, (const float*)ct, idx, (float*)dst, (uint32_t)n, fb, fd, (uint32_t)n_idx);
+  else RG_LAUNCH(k_take_grad<double>, n, (const double*)ct, idx, (double*)dst, (uint32_t)n, fb, fd, (uint32_t)n_idx);
+}
+
+void take_along_grad(hipStream_t s, int dtype, const void* ct, const int32_t* idx, void* dst, uint64_t n, uint64_t k, uint64_t v) {
+  FastDiv fv((uint32_t)v);
+  if (dtype == RG_F32) RG_LAUNCH(k_take_along_grad<float>, n, (const float*)ct, idx, (float*)dst, (uint32_t)n, fv, (uint32_t)k);
+  else RG_LAUNCH(k_take_along_grad<double>, n, (const double*)ct, idx, (double*)dst, (uint32_t)n, fv, (uint32_t)k);
+}
+
+void rand_uniform(hipStream_t s, int dtype, const int32_t* key, void* dst, uint64_t n) {
+  if (dtype == RG_F32) RG_LAUNCH(k_rand_uniform<float>, n, key, (float*)dst, (uint32_t)n);
+  else RG_LAUNCH(k_rand_uniform<double>, n, key, (double*)dst, (uint32_t)n);
+}
+
+void rand_normal(hipStream_t s, int dtype, const int32_t* key, void* dst, uint64_t n) {
+  if (dtype == RG_F32) RG_LAUNCH(k_rand_normal<float>, n, key, (float*)dst, (uint32_t)n);
+  else RG_LAUNCH(k_rand_normal<double>, n, key, (double*)dst, (uint32_t)n);
+}
+
+void key_split(hipStream_t s, const int32_t* key, int32_t* dst, uint64_t pairs) { RG_LAUNCH(k_key_split, pairs, key, dst, (uint32_t)pairs); }
+
+void cast(hipStream_t s, int from, int to, const void* a, void* d, uint64_t n) {
+#define RG_CAST(S, D) RG_LAUNCH((k_cast<S, D>), n, (const S*)a, (D*)d, (uint32_t)n)
+  if (from == RG_F32 && to == RG_F64) RG_CAST(float, double);
+  else if (from == RG_F32 && to == RG_I32) RG_CAST(float, int);
+  else if (from == RG_F64 && to == RG_F32) RG_CAST(double, float);
+  else if (from == RG_F64 && to == RG_I32) RG_CAST(double, int);
+  else if (from == RG_I32 && to == RG_F32) RG_CAST(int, float);
+  else if (from == RG_I32 && to == RG_F64) RG_CAST(int, double);
+  else hipMemcpyAsync(d, a, n * (from == RG_F64 ? 8 : 4), hipMemcpyDeviceToDevice, s);
+#undef RG_CAST
+}
+
+void argmax(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, uint64_t v) {
+  if (dtype == RG_F32) RG_LAUNCH(k_argmax<float>, rows, (const float*)a, d, (uint32_t)rows, (uint32_t)v);
+  else RG_LAUNCH(k_argmax<double>, rows, (const double*)a, d, (uint32_t)rows, (uint32_t)v);
+}
+
+void arg_top_k(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, uint64_t v, uint64_t k) {
+  if (dtype == RG_F32) RG_LAUNCH(k_arg_top_k<float>, rows, (const float*)a, d, (uint32_t)rows, (uint32_t)v, (uint32_t)k);
+  else RG_LAUNCH(k_arg_top_k<double>, rows, (const double*)a, d, (uint32_t)rows, (uint32_t)v, (uint32_t)k);
+}
+
+void cumsum(hipStream_t s, int dtype, const void* a, void* d, uint64_t rows, uint64_t v, bool reverse) {
+  if (dtype == RG_F32) RG_LAUNCH(k_cumsum<float>, rows, (const float*)a, (float*)d, (uint32_t)rows, (uint32_t)v, (int)reverse);
+  else if (dtype == RG_F64) RG_LAUNCH(k_cumsum<double>, rows, (const double*)a, (double*)d, (uint32_t)rows, (uint32_t)v, (int)reverse);
+  else RG_LAUNCH(k_cumsum_int, rows, (const int*)a, (int*)d, (uint32_t)rows, (uint32_t)v, (int)reverse);
+}
+
+void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t rows, uint64_t len) {
+  if (rows == 0) return;
+  if (len <= 4096) {
+    uint32_t grid = blocks_for(rows, TPB / 64);
+    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_rows_wave<float>, dim3(grid), dim3(TPB), 0, s, kind, (const float*)a, (float*)d, (uint32_t)rows, (uint32_t)len);
+    else hipLaunchKernelGGL(k_reduce_rows_wave<double>, dim3(grid), dim3(TPB), 0, s, kind, (const double*)a, (double*)d, (uint32_t)rows, (uint32_t)len);
+  } else {
+    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_rows_block<float>, dim3(1, (uint32_t)rows), dim3(TPB), 0, s, kind, (const float*)a, (float*)d, len, len);
+    else hipLaunchKernelGGL(k_reduce_rows_block<double>, dim3(1, (uint32_t)rows), dim3(TPB), 0, s, kind, (const double*)a, (double*)d, len, len);
+  }
+}
+
+uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k) {
+  // Aim for >= 1024 blocks (4 per CU) with at least 16 rows per chunk.
+  uint64_t col_blocks = (k + TPB - 1) / TPB * batch;
+  uint64_t want = (1024 + col_blocks - 1) / col_blocks;
+  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 16));
+  return std::min<uint64_t>(chunks, 65535);
+}
+
+void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k, void* partial,
+                 uint64_t chunks) {
+  uint32_t chunk_rows = (uint32_t)((r + chunks - 1) / chunks);
+  dim3 grid(blocks_for(k, TPB), (uint32_t)batch, (uint32_t)chunks);
+  void* out = chunks == 1 ? d : partial;
+  if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols<float>, grid, dim3(TPB), 0, s, kind, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
+  else hipLaunchKernelGGL(k_reduce_cols<double>, grid, dim3(TPB), 0, s, kind, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
+  if (chunks > 1) {
+    dim3 g2(blocks_for(k, TPB), (uint32_t)batch);
+    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols_finish<float>, g2, dim3(TPB), 0, s, kind, (const float*)partial, (float*)d, (uint32_t)k, (uint32_t)chunks);
+    else hipLaunchKernelGGL(k_reduce_cols_finish<double>, g2, dim3(TPB), 0, s, kind, (const double*)partial, (double*)d, (uint32_t)k, (uint32_t)chunks);
+  }
+}
+
+void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer, const Strided& inner,
+                    uint64_t red_n) {
+  if (dtype == RG_F32) RG_LAUNCH(k_reduce_general<float>, out_n, kind, (const float*)a, (float*)d, (uint32_t)out_n, outer, inner, (uint32_t)red_n);
+  else RG_LAUNCH(k_reduce_general<double>, out_n, kind, (const double*)a, (double*)d, (uint32_t)out_n, outer, inner, (uint32_t)red_n);
+}
+
+void copy_bytes(hipStream_t s, void* dst, const void* src, uint64_t bytes) {
+  uint64_t words = bytes / 4;
+  RG_LAUNCH(k_copy_words, words, (uint32_t*)dst, (const uint32_t*)src, words);
+}
+
+void record_history(hipStream_t s, int dtype, const void* slot, double* hist, const uint64_t* counter, uint64_t stride) {
+  hipLaunchKernelGGL(k_record_history, dim3(1), dim3(1), 0, s, dtype, slot, hist, counter, stride);
+}
+
+void load_batch(hipStream_t s, void* dst, const void* batches, uint64_t bytes, uint64_t n_batches, const uint64_t* counter) {
+  uint64_t words = bytes / 4;
+  RG_LAUNCH(k_load_batch, words, (uint32_t*)dst, (const uint32_t*)batches, words, n_batches, counter);
+}
+
+void counter_inc(hipStream_t s, uint64_t* counter) { hipLaunchKernelGGL(k_counter_inc, dim3(1), dim3(1), 0, s, counter); }
+
+void fill_zero(hipStream_t s, void* dst, uint64_t bytes) {
+  uint64_t words = bytes / 4;
+  RG_LAUNCH(k_fill_zero, words, (uint32_t*)dst, words);
+}
+
+}  // namespace rgk

@@ -1,0 +1,827 @@
+// The HIP executor behind include/rg_hip.h: lowers every plan step to a kernel launch, owns slot
+// frames in HBM, latches device failures, and runs the step loop on the device with HIP graphs.
+// Replaces the reference's MetalProgram / MetalExec (src/metal.rs:362-750).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../../include/rg_hip.h"
+#include "jit.h"
+#include "kernels.h"
+
+using namespace rgplan;
+
+namespace {
+
+constexpr size_t ALIGN = 256;
+
+std::string err_str(hipError_t e) { return std::string(hipGetErrorName(e)) + ": " + hipGetErrorString(e); }
+
+#define HIP_OK(expr)                                                              \
+  do {                                                                            \
+    hipError_t e_ = (expr);                                                       \
+    if (e_ != hipSuccess) throw std::runtime_error(std::string(#expr) + " -> " + err_str(e_)); \
+  } while (0)
+
+int esize(int dtype) { return dtype == RG_F64 ? 8 : 4; }
+
+uint64_t prod(const std::vector<int64_t>& s) {
+  uint64_t n = 1;
+  for (auto d : s) n *= (uint64_t)d;
+  return n;
+}
+
+// One launch of a plan step: (stream, slot pointer table, workspace).
+using StepFn = std::function<void(hipStream_t, void* const*, void*)>;
+
+struct Frame {
+  void* arena = nullptr;
+  uint64_t bytes = 0;
+  std::vector<void*> slot;
+  void* workspace = nullptr;
+  hipStream_t stream = nullptr;
+};
+
+struct Program {
+  Plan plan;
+  std::vector<uint8_t> blob;
+  std::vector<StepFn> steps;
+  std::vector<std::unique_ptr<rgjit::FusedKernel>> fused;
+  std::vector<void*> device_tables;  // per-batch GEMM offset tables
+  uint64_t workspace_bytes = 0;
+  std::vector<uint64_t> slot_bytes;
+  std::mutex mu;
+  std::vector<Frame*> pool;
+  std::atomic<bool> inject{false};
+  int device = 0;
+  ~Program() {
+    for (auto* f : pool) {
+      hipStreamDestroy(f->stream);
+      hipFree(f->arena);
+      delete f;
+    }
+    for (void* p : device_tables) hipFree(p);
+  }
+};
+
+struct Exec {
+  Program* prog;
+  Frame* frame;
+  std::string failure;
+};
+
+void put(char* buf, size_t len, const std::string& s) {
+  if (buf && len) snprintf(buf, len, "%s", s.c_str());
+}
+
+// ---- lowering of instructions --------------------------------------------------------------
+
+void* P(void* const* slots, int64_t s) { return slots[s]; }
+
+StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
+  const auto &sa = i.args[0].shape, &sb = i.args[1].shape;
+  size_t ar = sa.size(), br = sb.size();
+  uint64_t m, k;
+  if (ar >= 2 && !ta) { m = sa[ar - 2]; k = sa[ar - 1]; }
+  else if (ar >= 2) { m = sa[ar - 1]; k = sa[ar - 2]; }
+  else { m = 1; k = sa[0]; }
+  uint64_t n = br >= 2 ? (uint64_t)(tb ? sb[br - 2] : sb[br - 1]) : 1;
+  std::vector<int64_t> ba(sa.begin(), sa.begin() + (ar >= 2 ? ar - 2 : 0)), bb(sb.begin(), sb.begin() + (br >= 2 ? br - 2 : 0));
+  int dtype = i.dtype;
+  int64_t as = i.args[0].slot, bs = i.args[1].slot, dst = i.dst;
+  rgk::GemmArgs base{};
+  base.dtype = dtype;
+  base.ta = ta;
+  base.tb = tb;
+  base.n = n;
+  base.k = k;
+  if (bb.empty() && !ta) {
+    // Row-major batches of the left operand form one matrix: a single product (plan.rs:1471-1475).
+    base.m = prod(ba) * m;
+    base.batch = 1;
+  } else {
+    size_t r = std::max(ba.size(), bb.size());
+    std::vector<int64_t> batch(r);
+    for (size_t q = 0; q < r; q++) {
+      int64_t x = q < r - ba.size() ? 1 : ba[q - (r - ba.size())];
+      int64_t y = q < r - bb.size() ? 1 : bb[q - (r - bb.size())];
+      batch[q] = std::max(x, y);
+    }
+    auto sa_st = rgk::bcast_strides(ba, r), sb_st = rgk::bcast_strides(bb, r);
+    uint64_t count = prod(batch);
+    std::vector<int64_t> ao(count), bo(count);
+    std::vector<int64_t> idx(r, 0);
+    for (uint64_t c = 0; c < count; c++) {
+      int64_t x = 0, y = 0;
+      for (size_t d = 0; d < r; d++) {
+        x += idx[d] * sa_st[d];
+        y += idx[d] * sb_st[d];
+      }
+      ao[c] = x * (int64_t)(m * k);
+      bo[c] = y * (int64_t)(k * n);
+      for (size_t d = r; d-- > 0;) {
+        if (++idx[d] < batch[d]) break;
+        idx[d] = 0;
+      }
+    }
+    auto affine = [&](const std::vector<int64_t>& o, uint64_t* stride) {
+      int64_t st = count > 1 ? o[1] - o[0] : 0;
+      for (uint64_t c = 0; c < count; c++)
+        if (o[c] != (int64_t)c * st || st < 0) return false;
+      *stride = (uint64_t)st;
+      return true;
+    };
+    base.m = m;
+    base.batch = count;
+    auto upload = [&](const std::vector<int64_t>& o) {
+      void* d = nullptr;
+      HIP_OK(hipMalloc(&d, o.size() * 8));
+      HIP_OK(hipMemcpy(d, o.data(), o.size() * 8, hipMemcpyHostToDevice));
+      prog.device_tables.push_back(d);
+      return (const int64_t*)d;
+    };
+    if (!affine(ao, &base.a_stride)) base.a_off = upload(ao);
+    if (!affine(bo, &base.b_stride)) base.b_off = upload(bo);
+  }
+  uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch);
+  prog.workspace_bytes = std::max(prog.workspace_bytes, ws);
+  base.workspace_bytes = ws;
+  if (i.n == 0) return [](hipStream_t, void* const*, void*) {};
+  return [base, as, bs, dst](hipStream_t s, void* const* sl, void* wsp) {
+    rgk::GemmArgs g = base;
+    g.a = sl[as];
+    g.b = sl[bs];
+    g.c = sl[dst];
+    g.workspace = wsp;
+    rgk::gemm(s, g);
+  };
+}
+
+StepFn lower_reduce(Program& prog, const Instr& i) {
+  int kind = (int)i.attr[0];
+  size_t n_axes = (size_t)i.attr[2];
+  std::vector<bool> red(i.args[0].shape.size(), false);
+  for (size_t q = 0; q < n_axes; q++) red[(size_t)i.attr[3 + q]] = true;
+  const auto& in = i.args[0].shape;
+  // Canonical pattern: drop size-1 dims, merge neighbours with the same role.
+  std::vector<std::pair<int64_t, bool>> pat;
+  for (size_t d = 0; d < in.size(); d++) {
+    if (in[d] == 1) continue;
+    if (!pat.empty() && pat.back().second == red[d]) pat.back().first *= in[d];
+    else pat.push_back({in[d], red[d]});
+  }
+  int dtype = i.dtype;
+  int64_t a = i.args[0].slot, dst = i.dst;
+  uint64_t out_n = (uint64_t)i.n;
+  if (out_n == 0 || prod(in) == 0) return [](hipStream_t, void* const*, void*) {};
+  if (pat.size() == 1 && pat[0].second) {  // full reduction
+    uint64_t len = pat[0].first;
+    constexpr uint64_t SEG = 1u << 16;
+    if (len > (1u << 20) && len % SEG == 0) {
+      // Partials of 2^16-element rows, then one row of partials.
+      uint64_t parts = len / SEG;
+      prog.workspace_bytes = std::max<uint64_t>(prog.workspace_bytes, parts * esize(dtype));
+      return [=](hipStream_t s, void* const* sl, void* ws) {
+        rgk::reduce_rows(s, dtype, kind, sl[a], ws, parts, SEG);
+        rgk::reduce_rows(s, dtype, kind, ws, sl[dst], 1, parts);
+      };
+    }
+    return [=](hipStream_t s, void* const* sl, void*) { rgk::reduce_rows(s, dtype, kind, sl[a], sl[dst], 1, len); };
+  }
+  if (pat.size() == 2 && !pat[0].second && pat[1].second) {  // [K, R]: rows
+    uint64_t rows = pat[0].first, len = pat[1].first;
+    return [=](hipStream_t s, void* const* sl, void*) { rgk::reduce_rows(s, dtype, kind, sl[a], sl[dst], rows, len); };
+  }
+  if ((pat.size() == 2 && pat[0].second && !pat[1].second) || (pat.size() == 3 && !pat[0].second && pat[1].second && !pat[2].second)) {
+    uint64_t batch = pat.size() == 3 ? pat[0].first : 1;
+    uint64_t r = pat[pat.size() - 2].first, k = pat.back().first;
+    uint64_t chunks = rgk::reduce_cols_chunks(batch, r, k);
+    if (chunks > 1) prog.workspace_bytes = std::max<uint64_t>(prog.workspace_bytes, batch * chunks * k * esize(dtype));
+    return [=](hipStream_t s, void* const* sl, void* ws) { rgk::reduce_cols(s, dtype, kind, sl[a], sl[dst], batch, r, k, ws, chunks); };
+  }
+  // General: one thread per output over the reduced index space.
+  std::vector<int64_t> keep_shape, red_shape, keep_st, red_st;
+  auto st = rgk::row_strides(in);
+  for (size_t d = 0; d < in.size(); d++) {
+    if (red[d]) {
+      red_shape.push_back(in[d]);
+      red_st.push_back(st[d]);
+    } else {
+      keep_shape.push_back(in[d]);
+      keep_st.push_back(st[d]);
+    }
+  }
+  rgk::Strided outer = rgk::make_strided(keep_shape, {keep_st});
+  rgk::Strided inner = rgk::make_strided(red_shape, {red_st});
+  uint64_t red_n = prod(red_shape);
+  return [=](hipStream_t s, void* const* sl, void*) { rgk::reduce_general(s, dtype, kind, sl[a], sl[dst], out_n, outer, inner, red_n); };
+}
+
+StepFn lower_instr(Program& prog, const Instr& i) {
+  int dtype = i.dtype;
+  int64_t dst = i.dst;
+  uint64_t n = (uint64_t)i.n;
+  auto arg = [&](size_t k) { return i.args[k].slot; };
+  auto slot_dtype = [&](int64_t s) { return prog.plan.slots[(size_t)s].dtype; };
+  switch (i.op) {
+    case RG_OP_NEG: case RG_OP_EXP: case RG_OP_LOG: case RG_OP_SQRT: case RG_OP_SIN: case RG_OP_COS: case RG_OP_TANH:
+    case RG_OP_ABS: case RG_OP_SIGN: case RG_OP_FLOOR: {
+      int op = i.op;
+      int64_t a = arg(0);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::unary(s, dtype, op, sl[a], sl[dst], n); };
+    }
+    case RG_OP_ADD: case RG_OP_SUB: case RG_OP_MUL: case RG_OP_DIV: case RG_OP_POW: case RG_OP_MAX: case RG_OP_MIN:
+    case RG_OP_GT: case RG_OP_GE: {
+      int op = i.op;
+      int64_t a = arg(0), b = arg(1);
+      int mode = (int)i.mode;
+      if (mode == RG_MODE_GENERAL) {
+        size_t r = i.shape.size();
+        rgk::Strided g = rgk::make_strided(i.shape, {rgk::bcast_strides(i.args[0].shape, r), rgk::bcast_strides(i.args[1].shape, r)});
+        return [=](hipStream_t s, void* const* sl, void*) { rgk::binary(s, dtype, op, sl[a], sl[b], sl[dst], n, 3, &g); };
+      }
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::binary(s, dtype, op, sl[a], sl[b], sl[dst], n, mode, nullptr); };
+    }
+    case RG_OP_WHERE: {
+      int64_t c = arg(0), a = arg(1), b = arg(2);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::where(s, esize(dtype), sl[c], sl[a], sl[b], sl[dst], n, dtype); };
+    }
+    case RG_OP_MATMUL: return lower_gemm(prog, i, false, false);
+    case RG_OP_MATMUL_T: return lower_gemm(prog, i, i.attr[0] != 0, i.attr[1] != 0);
+    case RG_OP_REDUCE: return lower_reduce(prog, i);
+    case RG_OP_TRANSPOSE: case RG_OP_BROADCAST_TO: case RG_OP_SLICE: {
+      int64_t a = arg(0);
+      size_t r = i.shape.size();
+      std::vector<int64_t> src;
+      uint32_t base = 0;
+      if (i.op == RG_OP_TRANSPOSE) {
+        auto st = rgk::row_strides(i.args[0].shape);
+        for (auto p : i.attr) src.push_back(st[(size_t)p]);
+      } else if (i.op == RG_OP_BROADCAST_TO) {
+        src = rgk::bcast_strides(i.args[0].shape, r);
+      } else {
+        src = rgk::row_strides(i.args[0].shape);
+        for (size_t d = 0; d < r; d++) base += (uint32_t)(i.attr[1 + d] * src[d]);
+      }
+      rgk::Strided g = rgk::make_strided(i.shape, {src});
+      g.base[0] = base;
+      int es = esize(dtype);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::gather(s, es, sl[a], sl[dst], n, g); };
+    }
+    case RG_OP_PAD: {
+      int64_t a = arg(0);
+      size_t r = (size_t)i.attr[0];
+      std::vector<int64_t> starts(i.attr.begin() + 1, i.attr.begin() + 1 + (ptrdiff_t)r);
+      auto out_shape = i.shape, in_shape = i.args[0].shape;
+      int es = esize(dtype);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::pad(s, es, sl[a], sl[dst], n, out_shape, starts, in_shape); };
+    }
+    case RG_OP_CONCAT: {
+      size_t axis = (size_t)i.attr[0];
+      uint64_t tail = 1, outer = 1;
+      for (size_t d = axis + 1; d < i.shape.size(); d++) tail *= (uint64_t)i.shape[d];
+      for (size_t d = 0; d < axis; d++) outer *= (uint64_t)i.shape[d];
+      uint64_t total = (uint64_t)i.shape[axis] * tail, at = 0;
+      std::vector<std::pair<int64_t, std::pair<uint64_t, uint64_t>>> pieces;
+      for (auto& x : i.args) {
+        uint64_t len = (uint64_t)x.shape[axis] * tail;
+        pieces.push_back({x.slot, {len, at}});
+        at += len;
+      }
+      int es = esize(dtype);
+      return [=](hipStream_t s, void* const* sl, void*) {
+        for (auto& p : pieces) rgk::concat_piece(s, es, sl[p.first], sl[dst], outer, p.second.first, total, p.second.second);
+      };
+    }
+    case RG_OP_TAKE: {
+      size_t axis = (size_t)i.attr[0];
+      const auto& xs = i.args[0].shape;
+      uint64_t block = 1;
+      for (size_t d = axis + 1; d < xs.size(); d++) block *= (uint64_t)xs[d];
+      uint64_t dim = (uint64_t)xs[axis], n_idx = prod(i.args[1].shape);
+      int64_t a = arg(0), ix = arg(1);
+      int es = esize(dtype);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::take(s, es, sl[a], (const int32_t*)sl[ix], sl[dst], n, block, n_idx, dim); };
+    }
+    case RG_OP_TAKE_ALONG: {
+      uint64_t v = (uint64_t)i.args[0].shape.back(), kk = (uint64_t)i.args[1].shape.back();
+      int64_t a = arg(0), ix = arg(1);
+      int es = esize(dtype);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::take_along(s, es, sl[a], (const int32_t*)sl[ix], sl[dst], n, kk, v); };
+    }
+    case RG_OP_TAKE_GRAD: {
+      size_t axis = (size_t)i.attr[0];
+      std::vector<int64_t> shape(i.attr.begin() + 1, i.attr.end());
+      uint64_t block = 1;
+      for (size_t d = axis + 1; d < shape.size(); d++) block *= (uint64_t)shape[d];
+      uint64_t dim = (uint64_t)shape[axis], n_idx = prod(i.args[1].shape);
+      int64_t c = arg(0), ix = arg(1);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::take_grad(s, dtype, sl[c], (const int32_t*)sl[ix], sl[dst], n, block, n_idx, dim); };
+    }
+    case RG_OP_TAKE_ALONG_GRAD: {
+      uint64_t v = (uint64_t)i.attr.back(), kk = (uint64_t)i.args[1].shape.back();
+      int64_t c = arg(0), ix = arg(1);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::take_along_grad(s, dtype, sl[c], (const int32_t*)sl[ix], sl[dst], n, kk, v); };
+    }
+    case RG_OP_RAND_UNIFORM: {
+      int64_t key = arg(0);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::rand_uniform(s, dtype, (const int32_t*)sl[key], sl[dst], n); };
+    }
+    case RG_OP_RAND_NORMAL: {
+      int64_t key = arg(0);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::rand_normal(s, dtype, (const int32_t*)sl[key], sl[dst], n); };
+    }
+    case RG_OP_KEY_SPLIT: {
+      int64_t key = arg(0);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::key_split(s, (const int32_t*)sl[key], (int32_t*)sl[dst], n / 2); };
+    }
+    case RG_OP_CAST: {
+      int64_t a = arg(0);
+      int from = slot_dtype(a), to = (int)i.attr[0];
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::cast(s, from, to, sl[a], sl[dst], n); };
+    }
+    case RG_OP_ARGMAX: {
+      int64_t a = arg(0);
+      int from = slot_dtype(a);
+      uint64_t v = (uint64_t)i.args[0].shape.back();
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::argmax(s, from, sl[a], (int32_t*)sl[dst], n, v); };
+    }
+    case RG_OP_ARG_TOP_K: {
+      int64_t a = arg(0);
+      int from = slot_dtype(a);
+      uint64_t v = (uint64_t)i.args[0].shape.back(), kk = (uint64_t)i.attr[0];
+      uint64_t rows = prod(i.args[0].shape) / std::max<uint64_t>(v, 1);
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::arg_top_k(s, from, sl[a], (int32_t*)sl[dst], rows, v, kk); };
+    }
+    case RG_OP_CUMSUM: {
+      int64_t a = arg(0);
+      uint64_t v = (uint64_t)i.shape.back();
+      bool rev = i.attr[0] != 0;
+      uint64_t rows = v ? n / v : 0;
+      return [=](hipStream_t s, void* const* sl, void*) { rgk::cumsum(s, dtype, sl[a], sl[dst], rows, v, rev); };
+    }
+    default:
+      throw std::runtime_error(std::string("operation ") + std::to_string(i.op) + " has no HIP kernel in this build");
+  }
+}
+
+void build_program(Program& prog) {
+  std::ostringstream src;
+  std::vector<rgjit::FusedKernel*> kernels;
+  for (size_t k = 0; k < prog.plan.steps.size(); k++) {
+    const Step& st = prog.plan.steps[k];
+    if (st.kind == RG_STEP_FUSED) {
+      auto fk = std::make_unique<rgjit::FusedKernel>();
+      src << rgjit::generate(st.fused, "rgf" + std::to_string(k), fk.get());
+      kernels.push_back(fk.get());
+      prog.fused.push_back(std::move(fk));
+    }
+  }
+  rgjit::compile(src.str(), kernels);
+  size_t fi = 0;
+  for (size_t k = 0; k < prog.plan.steps.size(); k++) {
+    const Step& st = prog.plan.steps[k];
+    if (st.kind == RG_STEP_FUSED) {
+      rgjit::FusedKernel* fk = prog.fused[fi++].get();
+      std::vector<int64_t> ins, outs;
+      for (auto& in : st.fused.inputs) ins.push_back(in.slot);
+      for (auto& o : st.fused.outputs) outs.push_back(o.second);
+      if (fk->grid == 0) {
+        prog.steps.push_back([](hipStream_t, void* const*, void*) {});
+        continue;
+      }
+      prog.steps.push_back([fk, ins, outs](hipStream_t s, void* const* sl, void*) {
+        void* ptrs[160];
+        void* args[160];
+        size_t q = 0;
+        for (auto x : ins) ptrs[q++] = sl[x];
+        for (auto x : outs) ptrs[q++] = sl[x];
+        for (size_t j = 0; j < q; j++) args[j] = &ptrs[j];
+        hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, rgjit::TPB, 1, 1, 0, s, args, nullptr);
+      });
+    } else {
+      const Instr& in = st.instr;
+      prog.steps.push_back(lower_instr(prog, in));
+    }
+  }
+  for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));
+}
+
+Frame* new_frame(Program& p) {
+  auto* f = new Frame;
+  uint64_t total = 0;
+  std::vector<uint64_t> off;
+  for (auto b : p.slot_bytes) {
+    off.push_back(total);
+    total += (b + ALIGN - 1) / ALIGN * ALIGN;
+  }
+  uint64_t ws_off = total;
+  total += (p.workspace_bytes + ALIGN - 1) / ALIGN * ALIGN;
+  total = std::max<uint64_t>(total, ALIGN);
+  hipError_t e = hipMalloc(&f->arena, total);
+  if (e != hipSuccess) {
+    delete f;
+    throw std::runtime_error("could not allocate a device frame of " + std::to_string(total) + " bytes: " + err_str(e));
+  }
+  f->bytes = total;
+  HIP_OK(hipMemset(f->arena, 0, total));
+  for (auto o : off) f->slot.push_back((char*)f->arena + o);
+  f->workspace = (char*)f->arena + ws_off;
+  HIP_OK(hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking));
+  for (auto& c : p.plan.consts) {
+    uint64_t bytes = (uint64_t)c.n * esize(p.plan.slots[(size_t)c.slot].dtype);
+    if (bytes) HIP_OK(hipMemcpy(f->slot[(size_t)c.slot], p.blob.data() + c.offset, bytes, hipMemcpyHostToDevice));
+  }
+  return f;
+}
+
+bool latch(Exec* e, hipError_t err, const char* what) {
+  if (err == hipSuccess) return false;
+  if (e->failure.empty()) e->failure = std::string(what) + ": " + err_str(err);
+  return true;
+}
+
+void run_steps(Exec* e, size_t begin, size_t end) {
+  if (!e->failure.empty()) return;
+  if (e->prog->inject.exchange(false)) {
+    e->failure = "injected failure";
+    return;
+  }
+  Frame* f = e->frame;
+  try {
+    for (size_t k = begin; k < end; k++) e->prog->steps[k](f->stream, f->slot.data(), f->workspace);
+  } catch (std::exception& ex) {
+    e->failure = ex.what();
+    return;
+  }
+  if (latch(e, hipGetLastError(), "kernel launch")) return;
+  latch(e, hipStreamSynchronize(f->stream), "device execution");
+}
+
+double now() { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); }
+
+}  // namespace
+
+extern "C" {
+
+int rg_hip_available(void) {
+  static int avail = [] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return 0;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  }();
+  return avail;
+}
+
+uint64_t rg_hip_device_memory_bytes(void) {
+  size_t free_b = 0, total = 0;
+  if (hipMemGetInfo(&free_b, &total) != hipSuccess) return 0;
+  return total;
+}
+
+void* rg_hip_program_new(const int64_t* words, size_t n_words, const void* blob, size_t blob_bytes, char* err, size_t err_len) {
+  auto* p = new Program;
+  try {
+    if (!rg_hip_available()) throw std::runtime_error("no gfx950 device is visible to HIP");
+    p->plan = parse(words, n_words);
+    p->blob.assign((const uint8_t*)blob, (const uint8_t*)blob + blob_bytes);
+    size_t free_b = 0, total = 0;
+    HIP_OK(hipMemGetInfo(&free_b, &total));
+    for (auto& s : p->plan.slots) {
+      uint64_t bytes = (uint64_t)s.cap * esize(s.dtype);
+      if (bytes > total)
+        throw std::runtime_error("a " + std::string(s.dtype == RG_F64 ? "float64" : s.dtype == RG_F32 ? "float32" : "int32") + " buffer of " +
+                                 std::to_string(s.cap) + " elements exceeds this device's limit of " + std::to_string(total) + " bytes");
+      if (s.cap >= (1ll << 31)) throw std::runtime_error("a buffer of " + std::to_string(s.cap) + " elements exceeds the 2^31 element index range");
+    }
+    for (auto& st : p->plan.steps)
+      if (st.kind == RG_STEP_INSTR && (st.instr.op == RG_OP_SCAN || st.instr.op == RG_OP_WHILE || st.instr.op == RG_OP_COND))
+        throw std::runtime_error("control flow is not part of the HIP backend");
+    build_program(*p);
+    return p;
+  } catch (std::exception& e) {
+    put(err, err_len, e.what());
+    delete p;
+    return nullptr;
+  }
+}
+
+void rg_hip_program_free(void* program) { delete (Program*)program; }
+
+// Generates and compiles every fused group of a plan for gfx950 without touching a device:
+// the build-time check of the code generator. Returns the number of kernels, or -1.
+int rg_hip_compile_check(const int64_t* words, size_t n_words, char* err, size_t err_len) {
+  try {
+    Plan plan = parse(words, n_words);
+    std::ostringstream src;
+    int count = 0;
+    for (size_t k = 0; k < plan.steps.size(); k++) {
+      if (plan.steps[k].kind != RG_STEP_FUSED) continue;
+      rgjit::FusedKernel fk;
+      src << rgjit::generate(plan.steps[k].fused, "rgf" + std::to_string(k), &fk);
+      count++;
+    }
+    if (count) rgjit::compile_code(src.str());
+    return count;
+  } catch (std::exception& e) {
+    put(err, err_len, e.what());
+    return -1;
+  }
+}
+
+uint64_t rg_hip_program_allocated_bytes(void* program) {
+  (void)program;
+  size_t free_b = 0, total = 0;
+  if (hipMemGetInfo(&free_b, &total) != hipSuccess) return 0;
+  return total - free_b;
+}
+
+void rg_hip_program_inject_failure(void* program) { ((Program*)program)->inject = true; }
+
+void* rg_hip_exec_new(void* program, char* err, size_t err_len) {
+  auto* p = (Program*)program;
+  auto* e = new Exec{p, nullptr, {}};
+  {
+    std::lock_guard<std::mutex> lock(p->mu);
+    if (!p->pool.empty()) {
+      e->frame = p->pool.back();
+      p->pool.pop_back();
+      return e;
+    }
+  }
+  try {
+    e->frame = new_frame(*p);
+  } catch (std::exception& ex) {
+    put(err, err_len, ex.what());
+    delete e;
+    return nullptr;
+  }
+  return e;
+}
+
+void rg_hip_exec_free(void* exec) {
+  auto* e = (Exec*)exec;
+  hipStreamSynchronize(e->frame->stream);
+  {
+    std::lock_guard<std::mutex> lock(e->prog->mu);
+    e->prog->pool.push_back(e->frame);
+  }
+  delete e;
+}
+
+int rg_hip_exec_write(void* exec, int64_t slot, const void* src, uint64_t bytes) {
+  auto* e = (Exec*)exec;
+  if (slot < 0 || (size_t)slot >= e->frame->slot.size() || bytes > e->prog->slot_bytes[(size_t)slot]) return -1;
+  if (!bytes) return 0;
+  if (latch(e, hipMemcpyAsync(e->frame->slot[(size_t)slot], src, bytes, hipMemcpyHostToDevice, e->frame->stream), "write")) return -1;
+  return latch(e, hipStreamSynchronize(e->frame->stream), "write") ? -1 : 0;
+}
+
+int rg_hip_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes) {
+  auto* e = (Exec*)exec;
+  if (slot < 0 || (size_t)slot >= e->frame->slot.size() || bytes > e->prog->slot_bytes[(size_t)slot]) return -1;
+  if (!bytes) return 0;
+  if (latch(e, hipMemcpyAsync(dst, e->frame->slot[(size_t)slot], bytes, hipMemcpyDeviceToHost, e->frame->stream), "read")) return -1;
+  return latch(e, hipStreamSynchronize(e->frame->stream), "read") ? -1 : 0;
+}
+
+double rg_hip_exec_scalar(void* exec, int64_t slot) {
+  auto* e = (Exec*)exec;
+  int d = e->prog->plan.slots[(size_t)slot].dtype;
+  uint8_t buf[8] = {0};
+  if (rg_hip_exec_read(exec, slot, buf, esize(d)) != 0) return NAN;
+  if (d == RG_F32) { float v; memcpy(&v, buf, 4); return v; }
+  if (d == RG_F64) { double v; memcpy(&v, buf, 8); return v; }
+  int32_t v;
+  memcpy(&v, buf, 4);
+  return v;
+}
+
+void rg_hip_exec_swap(void* exec, int64_t a, int64_t b) {
+  auto* e = (Exec*)exec;
+  std::swap(e->frame->slot[(size_t)a], e->frame->slot[(size_t)b]);
+}
+
+void rg_hip_exec_steps(void* exec, int64_t begin, int64_t end) { run_steps((Exec*)exec, (size_t)begin, (size_t)end); }
+
+void rg_hip_exec_step(void* exec) { run_steps((Exec*)exec, 0, ((Exec*)exec)->prog->steps.size()); }
+
+int rg_hip_exec_failure(void* exec, char* buf, size_t len) {
+  auto* e = (Exec*)exec;
+  if (e->failure.empty()) return 0;
+  put(buf, len, e->failure);
+  return 1;
+}
+
+int rg_hip_exec_step_timed(void* exec, double* seconds) {
+  auto* e = (Exec*)exec;
+  Frame* f = e->frame;
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  for (size_t k = 0; k < e->prog->steps.size() && e->failure.empty(); k++) {
+    hipEventRecord(a, f->stream);
+    e->prog->steps[k](f->stream, f->slot.data(), f->workspace);
+    hipEventRecord(b, f->stream);
+    if (latch(e, hipEventSynchronize(b), "timed step")) break;
+    float ms = 0;
+    hipEventElapsedTime(&ms, a, b);
+    seconds[k] += ms * 1e-3;
+  }
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return e->failure.empty() ? 0 : -1;
+}
+
+int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len) {
+  auto* e = (Exec*)exec;
+  Frame* f = e->frame;
+  repeats = std::max<int64_t>(repeats, 1);
+  hipEvent_t a, b;
+  hipEventCreate(&a);
+  hipEventCreate(&b);
+  double t0 = now();
+  hipEventRecord(a, f->stream);
+  for (int64_t r = 0; r < repeats && e->failure.empty(); r++)
+    for (auto& st : e->prog->steps) st(f->stream, f->slot.data(), f->workspace);
+  hipEventRecord(b, f->stream);
+  latch(e, hipEventSynchronize(b), "breakdown");
+  double wall = now() - t0;
+  float ms = 0;
+  hipEventElapsedTime(&ms, a, b);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  size_t fused = 0;
+  for (auto& st : e->prog->plan.steps) fused += st.kind == RG_STEP_FUSED;
+  std::ostringstream s;
+  s << "{\"wall_ms\":" << wall / repeats * 1e3 << ",\"gpu_ms\":" << ms / repeats << ",\"per_step\":{\"dispatches\":"
+    << e->prog->steps.size() << ",\"fused_kernels\":" << fused << ",\"cpu_steps\":0}}";
+  put(json, len, s.str());
+  return e->failure.empty() ? 0 : -1;
+}
+
+// The step loop on the device (validate.rs:289-363 semantics). Each step is a replay of one of
+// two captured graphs: the swaps of the state handoff are disjoint pairs, so the slot table
+// alternates between two permutations and each has its graph. Batches, history and the step
+// counter live in device memory; history is read back once per chunk, and a non-finite value
+// re-runs that chunk from a snapshot to stop exactly after the bad step's handoff.
+int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
+  auto* e = (Exec*)exec;
+  Program* p = e->prog;
+  Frame* f = e->frame;
+  out->done = 0;
+  out->nonfinite_step = -1;
+  out->seconds = 0;
+  if (!e->failure.empty()) return -1;
+  if (p->inject.exchange(false)) {
+    e->failure = "injected failure";
+    return -1;
+  }
+  std::vector<void*> owned;
+  auto dalloc = [&](uint64_t bytes) {
+    void* ptr = nullptr;
+    HIP_OK(hipMalloc(&ptr, std::max<uint64_t>(bytes, 16)));
+    owned.push_back(ptr);
+    return ptr;
+  };
+  std::vector<hipGraphExec_t> execs;
+  std::vector<hipGraph_t> graphs;
+  int rc = 0;
+  try {
+    const int64_t steps = d->steps;
+    const uint64_t chunk = d->n_history > 0 ? 64 : (uint64_t)std::max<int64_t>(steps, 1);
+    // Device-side run state.
+    auto* counter = (uint64_t*)dalloc(8);
+    double* hist = (double*)dalloc((uint64_t)std::max<int64_t>(d->n_history, 1) * std::max<uint64_t>(chunk, 1) * 8);
+    std::vector<void*> batch_bufs;
+    for (int64_t j = 0; j < d->n_data && d->n_batches > 1; j++) {
+      void* b = dalloc(d->data_bytes[j] * d->n_batches);
+      for (int64_t k = 0; k < d->n_batches; k++)
+        HIP_OK(hipMemcpy((char*)b + d->data_bytes[j] * k, d->batches[k * d->n_data + j], d->data_bytes[j], hipMemcpyHostToDevice));
+      batch_bufs.push_back(b);
+    }
+    std::vector<void*> temps;
+    for (int64_t c = 0; c < d->n_copies; c++) {
+      int64_t os = d->copies[3 * c + 1];
+      temps.push_back(dalloc(p->slot_bytes[(size_t)os]));
+    }
+    // State slots that change across steps, for the snapshot of a chunk.
+    std::vector<int64_t> state_slots;
+    for (int64_t k = 0; k < d->n_swaps; k++) state_slots.push_back(d->swaps[2 * k]);
+    for (int64_t k = 0; k < d->n_copies; k++) state_slots.push_back(d->copies[3 * k]);
+    std::vector<void*> snap;
+    if (d->n_history > 0)
+      for (auto s : state_slots) snap.push_back(dalloc(p->slot_bytes[(size_t)s]));
+
+    // The two slot tables and their graphs.
+    std::vector<void*> table[2];
+    table[0] = f->slot;
+    table[1] = f->slot;
+    for (int64_t k = 0; k < d->n_swaps; k++) std::swap(table[1][(size_t)d->swaps[2 * k]], table[1][(size_t)d->swaps[2 * k + 1]]);
+    int n_graphs = d->n_swaps > 0 ? 2 : 1;
+    for (int g = 0; g < n_graphs; g++) {
+      const std::vector<void*>& t = table[g];
+      HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));
+      for (int64_t j = 0; j < (int64_t)batch_bufs.size(); j++)
+        rgk::load_batch(f->stream, t[(size_t)d->data_slots[j]], batch_bufs[j], d->data_bytes[j], d->n_batches, counter);
+      for (auto& st : p->steps) st(f->stream, t.data(), f->workspace);
+      for (int64_t h = 0; h < d->n_history; h++) {
+        int64_t s = d->history_slots[h];
+        rgk::record_history(f->stream, p->plan.slots[(size_t)s].dtype, t[(size_t)s], hist + h * chunk, counter, chunk);
+      }
+      // Copies read every source before writing any destination (validate.rs:349-355).
+      for (int64_t c = 0; c < d->n_copies; c++) {
+        int64_t os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
+        rgk::copy_bytes(f->stream, temps[c], t[(size_t)os], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
+      }
+      const std::vector<void*>& next = table[(g + 1) % n_graphs];
+      for (int64_t c = 0; c < d->n_copies; c++) {
+        int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
+        rgk::copy_bytes(f->stream, next[(size_t)is], temps[c], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
+      }
+      rgk::counter_inc(f->stream, counter);
+      hipGraph_t graph;
+      hipError_t ce = hipStreamEndCapture(f->stream, &graph);
+      if (ce != hipSuccess) throw std::runtime_error("graph capture failed: " + err_str(ce));
+      graphs.push_back(graph);
+      hipGraphExec_t ge;
+      HIP_OK(hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0));
+      execs.push_back(ge);
+    }
+    HIP_OK(hipGetLastError());
+    auto set_counter = [&](uint64_t v) {
+      HIP_OK(hipStreamSynchronize(f->stream));
+      HIP_OK(hipMemcpy(counter, &v, 8, hipMemcpyHostToDevice));
+    };
+    set_counter(0);
+    double t0 = now();
+    int64_t done = 0;
+    std::vector<double> hbuf((size_t)std::max<int64_t>(d->n_history, 1) * chunk);
+    while (done < steps) {
+      int64_t c0 = done, c1 = std::min<int64_t>(steps, done + (int64_t)chunk);
+      int parity0 = (int)(c0 % n_graphs);
+      if (d->n_history > 0) {
+        for (size_t q = 0; q < state_slots.size(); q++)
+          rgk::copy_bytes(f->stream, snap[q], table[parity0][(size_t)state_slots[q]], p->slot_bytes[(size_t)state_slots[q]]);
+      }
+      for (int64_t k = c0; k < c1; k++)
+        if (latch(e, hipGraphLaunch(execs[(size_t)(k % n_graphs)], f->stream), "graph launch")) break;
+      if (!e->failure.empty() || latch(e, hipStreamSynchronize(f->stream), "device execution")) {
+        rc = -1;
+        break;
+      }
+      int64_t bad = -1;
+      if (d->n_history > 0) {
+        HIP_OK(hipMemcpy(hbuf.data(), hist, (size_t)d->n_history * chunk * 8, hipMemcpyDeviceToHost));
+        for (int64_t k = c0; k < c1 && bad < 0; k++)
+          for (int64_t h = 0; h < d->n_history; h++)
+            if (!std::isfinite(hbuf[(size_t)(h * chunk + (k - c0))])) bad = k;
+        for (int64_t h = 0; h < d->n_history; h++)
+          for (int64_t k = c0; k < (bad >= 0 ? bad + 1 : c1); k++) d->history[h * steps + k] = hbuf[(size_t)(h * chunk + (k - c0))];
+      }
+      if (bad >= 0) {
+        // Back to the chunk start, then exactly through the bad step.
+        for (size_t q = 0; q < state_slots.size(); q++)
+          rgk::copy_bytes(f->stream, table[parity0][(size_t)state_slots[q]], snap[q], p->slot_bytes[(size_t)state_slots[q]]);
+        set_counter((uint64_t)c0);
+        for (int64_t k = c0; k <= bad; k++) latch(e, hipGraphLaunch(execs[(size_t)(k % n_graphs)], f->stream), "graph launch");
+        if (latch(e, hipStreamSynchronize(f->stream), "device execution")) {
+          rc = -1;
+          break;
+        }
+        done = bad + 1;
+        out->nonfinite_step = bad;
+        break;
+      }
+      done = c1;
+    }
+    out->seconds = now() - t0;
+    out->done = done;
+    // The frame's table reflects every handoff made.
+    f->slot = table[(size_t)(done % n_graphs)];
+  } catch (std::exception& ex) {
+    if (e->failure.empty()) e->failure = ex.what();
+    rc = -1;
+  }
+  hipStreamSynchronize(f->stream);
+  for (auto g : execs) hipGraphExecDestroy(g);
+  for (auto g : graphs) hipGraphDestroy(g);
+  for (void* ptr : owned) hipFree(ptr);
+  return rc;
+}
+
+}  // extern "C"

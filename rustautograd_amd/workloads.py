@@ -1,0 +1,173 @@
+"""The five benchmark programs, written against the public API.
+
+C1 linear regression, C2 MLP regression, C3/C4 char-level GPT training steps, C5 matrix chain.
+The GPT follows the reference's examples/gpt.py:20-68 (tok/pos embeddings, pre-norm transformer
+blocks, final LayerNorm, head, cross-entropy, AdamW) with the batch of token ids drawn inside the
+step from a key carried in the state, so a run never returns to the host.
+"""
+
+import math
+from typing import NamedTuple
+
+import numpy as np
+
+import rustautograd_amd as rg
+from rustautograd_amd import nn, optim, random
+
+
+# ---- C1: linear regression (README example of the reference) ---------------------------------
+
+def linreg(n=256, d=8, lr=0.05, seed=0):
+    """Returns (step, w0, batch): `w -= lr * grad(mean((X@w - y)^2))`, loss as aux."""
+    x = np.random.default_rng(seed).normal(size=(n, d)).astype(np.float32)
+    y = x @ np.arange(d, dtype=np.float32)
+
+    def loss(w, x, y):
+        r = x @ w - y
+        return (r * r).mean()
+
+    def step(w, batch):
+        xb, yb = batch
+        l, g = rg.value_and_grad(loss)(w, xb, yb)
+        return w - lr * g, l
+
+    return step, rg.zeros(d), (rg.tensor(x), rg.tensor(y))
+
+
+# ---- C2: MLP regression ---------------------------------------------------------------------
+
+class MLPConfig(NamedTuple):
+    batch: int = 4096
+    d_in: int = 512
+    hidden: int = 2048
+    lr: float = 1e-3
+    weight_decay: float = 0.01
+
+
+def mlp_train_step(cfg=MLPConfig()):
+    """Linear(512->2048)-gelu-Linear(2048->2048)-gelu-Linear(2048->1), AdamW; x ~ N(0,1) drawn in
+    the step from the state key, target = sum(sin(x[:, :16]), axis=1, keepdims)."""
+    model = nn.Sequential(nn.Linear(cfg.d_in, cfg.hidden), nn.gelu, nn.Linear(cfg.hidden, cfg.hidden), nn.gelu, nn.Linear(cfg.hidden, 1))
+    params = model.init(random.key(0))
+    opt = optim.adamw(cfg.lr, weight_decay=cfg.weight_decay)
+
+    def loss_fn(p, x, t):
+        return nn.mse_loss(model(p, x), t)
+
+    def step(state):
+        k_next, k_x = random.split(state["key"])
+        x = random.normal(k_x, (cfg.batch, cfg.d_in))
+        target = rg.sin(x[:, :16]).sum(axis=1, keepdims=True)
+        value, grads = rg.value_and_grad(loss_fn)(state["params"], x, target)
+        p, o = opt.update(grads, state["opt"], state["params"])
+        return {"params": p, "opt": o, "key": k_next}, value
+
+    state = {"params": params, "opt": opt.init(params), "key": random.key(1)}
+    return step, state
+
+
+# ---- C3 / C4: character-level GPT -------------------------------------------------------------
+
+class GPTConfig(NamedTuple):
+    vocab: int
+    block: int
+    d: int
+    heads: int
+    layers: int
+    batch: int
+    tied: bool = False
+    lr: float = 3e-4
+
+
+GPT_CONFIGS = {
+    "C3": GPTConfig(vocab=96, block=128, d=128, heads=4, layers=4, batch=32, tied=True),
+    "C4": GPTConfig(vocab=96, block=256, d=256, heads=8, layers=6, batch=32, tied=False),
+}
+
+
+class GPT:
+    """examples/gpt.py:20-47 of the reference; `tied` reads the head from the token table."""
+
+    def __init__(self, vocab, block, d=128, heads=4, layers=4, tied=False):
+        self.block = block
+        self.tied = tied
+        self.tok = nn.Embedding(vocab, d)
+        self.pos = nn.Embedding(block, d)
+        self.blocks = [nn.TransformerBlock(d, heads) for _ in range(layers)]
+        self.norm = nn.LayerNorm(d)
+        self.head = nn.Linear(d, vocab, bias=False)
+        self.mask = rg.tril(block)
+
+    def init(self, key):
+        keys = random.split(key, len(self.blocks) + 3)
+        p = {
+            "tok": self.tok.init(keys[0]),
+            "pos": self.pos.init(keys[1]),
+            "norm": self.norm.init(),
+            "blocks": [b.init(keys[3 + i]) for i, b in enumerate(self.blocks)],
+        }
+        if not self.tied:
+            p["head"] = self.head.init(keys[2])
+        return p
+
+    def __call__(self, p, idx):
+        t = idx.shape[1]
+        x = self.tok(p["tok"], idx) + self.pos(p["pos"], rg.arange(t))
+        mask = self.mask[:t, :t]
+        for i, b in enumerate(self.blocks):
+            x = b(p["blocks"][i], x, mask)
+        h = self.norm(p["norm"], x)
+        return h @ p["tok"]["table"].T if self.tied else self.head(p["head"], h)
+
+
+def gpt_train_step(cfg):
+    """Returns (step, state). Each step draws `batch` sequences of `block + 1` ids uniform in
+    [0, vocab) from the state key (random.randint: f64 uniform, floor, int32), trains on
+    x = ids[:, :-1], y = ids[:, 1:] with cross-entropy and AdamW, and returns the loss as aux."""
+    model = GPT(cfg.vocab, cfg.block, cfg.d, cfg.heads, cfg.layers, cfg.tied)
+    params = model.init(random.key(0))
+    opt = optim.adamw(cfg.lr, weight_decay=0.01)
+
+    def loss_fn(p, x, y):
+        return nn.cross_entropy(model(p, x), y)
+
+    def step(state):
+        k_next, k_ids = random.split(state["key"])
+        ids = random.randint(k_ids, (cfg.batch, cfg.block + 1), 0, cfg.vocab)
+        x, y = ids[:, :-1], ids[:, 1:]
+        value, grads = rg.value_and_grad(loss_fn)(state["params"], x, y)
+        p, o = opt.update(grads, state["opt"], state["params"])
+        return {"params": p, "opt": o, "key": k_next}, value
+
+    state = {"params": params, "opt": opt.init(params), "key": random.key(1)}
+    return step, state
+
+
+def gpt_gemm_flops(cfg):
+    """2*M*N*K summed over every product of one training step (forward, both backward products
+    of each forward product); the algorithmic flop count of the step."""
+    b, t, d, h, f, v = cfg.batch, cfg.block, cfg.d, cfg.heads, 4 * cfg.d, cfg.vocab
+    hd = d // h
+    tokens = b * t
+    per_layer = tokens * d * 3 * d + b * h * t * hd * t + b * h * t * t * hd + tokens * d * d + tokens * d * f + tokens * f * d
+    fwd = cfg.layers * per_layer + tokens * d * v
+    return 2 * 3 * fwd
+
+
+# ---- C5: matrix chain -------------------------------------------------------------------------
+
+def matrix_chain(n=4096, k=8, seed=0):
+    """sum((A@B)@C@D) with A (k,n), B and C (n,n), D (n,k), all ~ N(0, 1/sqrt(n)); gradients with
+    respect to B and C. Written in the expensive left-to-right order."""
+    rng = np.random.default_rng(seed)
+    sigma = 1.0 / math.sqrt(n)
+    a, b, c, d = (rng.normal(0.0, sigma, size=s).astype(np.float32) for s in ((k, n), (n, n), (n, n), (n, k)))
+
+    def f(a, b, c, d):
+        return (((a @ b) @ c) @ d).sum()
+
+    def program(a, b, c, d):
+        value, (gb, gc) = rg.value_and_grad(f, argnums=(1, 2))(a, b, c, d)
+        return value, gb, gc
+
+    return program, tuple(rg.tensor(x) for x in (a, b, c, d))

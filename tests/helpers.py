@@ -1,0 +1,77 @@
+"""Shared helpers: build a graph through the engine API, run it on a device, compare results."""
+
+import numpy as np
+
+import rustautograd_amd as rg
+from rustautograd_amd import _rg
+
+
+def t(a, dtype="float32"):
+    return rg.tensor(np.asarray(a, dtype=dtype))
+
+
+def seq(shape, dtype="float32"):
+    """0.25 + |sin(0.73 i)|: positive, irregular values (the reference's tests/metal.rs:50-53)."""
+    n = int(np.prod(shape)) if shape else 1
+    return rg.tensor((0.25 + np.abs(np.sin(np.arange(n) * 0.73))).reshape(shape).astype(dtype))
+
+
+def run_graph(device, build, inputs, optimize="none", n_out=None):
+    """Traces `build(g, ids)` over fresh inputs, compiles it for `device` and calls it once."""
+    g = _rg.Graph()
+    ids = [g.input(list(x.shape), x.dtype) for x in inputs]
+    out = build(g, ids)
+    outs = out if isinstance(out, (list, tuple)) else [out]
+    c = _rg.compile(g, list(outs), [x._t for x in inputs], "none", device, optimize)
+    res = c.call([x._t for x in inputs])
+    return [rg.Tensor(r).numpy() for r in res]
+
+
+def op(g, name, ins, **attrs):
+    return g.op(name, list(ins), attrs or None)
+
+
+def ulp_distance(a, b):
+    """Distance in units in the last place between float arrays of the same dtype (NaN == NaN)."""
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.dtype == np.float32:
+        ia, ib = a.view(np.int32).astype(np.int64), b.view(np.int32).astype(np.int64)
+        ia = np.where(ia < 0, np.int64(-(2 ** 31)) - ia, ia)
+        ib = np.where(ib < 0, np.int64(-(2 ** 31)) - ib, ib)
+    else:
+        ia, ib = a.view(np.int64).astype(object), b.view(np.int64).astype(object)
+        ia = np.array([(-(2 ** 63)) - x if x < 0 else x for x in ia.ravel()], dtype=object).reshape(a.shape)
+        ib = np.array([(-(2 ** 63)) - x if x < 0 else x for x in ib.ravel()], dtype=object).reshape(b.shape)
+    d = np.abs(ia - ib)
+    both_nan = np.isnan(a) & np.isnan(b)
+    return np.where(both_nan, 0, d)
+
+
+def close(got, want, tol, what=""):
+    """|got - want| <= tol * max(1, max|want|) elementwise, NaN matching NaN (tests/metal.rs:33-40)."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
+    finite = want[np.isfinite(want)]
+    scale = max(1.0, float(np.abs(finite).max())) if finite.size else 1.0
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    ok = same | (np.abs(got - want) <= tol * scale)
+    if not ok.all():
+        j = int(np.argmax(~ok.ravel()))
+        raise AssertionError(f"{what}[{j}]: hip {got.ravel()[j]!r} cpu {want.ravel()[j]!r} (tol {tol} x {scale})")
+
+
+def agree(build, inputs, tol=2e-6, what="", ulps=None):
+    """Runs `build` on the HIP device and on the CPU oracle and compares every output."""
+    hip = run_graph("hip", build, inputs)
+    cpu = run_graph("cpu", build, inputs)
+    for k, (a, b) in enumerate(zip(hip, cpu)):
+        if ulps is not None and a.dtype in (np.float32, np.float64):
+            d = ulp_distance(a, b)
+            assert d.max() <= ulps, f"{what} output {k}: {int(d.max())} ulp apart; hip {a.ravel()[np.argmax(d)]} cpu {b.ravel()[np.argmax(d)]}"
+        elif a.dtype == np.int32:
+            assert np.array_equal(a, b), f"{what} output {k}: int32 results differ"
+        else:
+            close(a, b, tol, f"{what} output {k}")
+    return hip, cpu

@@ -1,0 +1,202 @@
+"""HIP kernels against the CPU oracle, op by op (the pattern of the reference's tests/metal.rs:55-178).
+
+Bars: int32, index and byte work bit-exact; fp32 elementwise within 2 ulp of the oracle (glibc
+libm vs the device math library); reductions and products within 1e-4 relative to the largest
+magnitude.
+"""
+
+import numpy as np
+import pytest
+
+from helpers import agree, close, op, run_graph, seq, t
+
+pytestmark = pytest.mark.gpu
+
+UNARY = ["neg", "exp", "log", "sqrt", "sin", "cos", "tanh", "abs", "sign", "floor"]
+BINARY = ["add", "sub", "mul", "div", "pow", "maximum", "minimum", "gt", "ge"]
+PATTERNS = [((4, 3), (4, 3)), ((4, 3), ()), ((), (4, 3)), ((4, 3), (3,)), ((4, 1), (1, 3)), ((2, 1, 3), (4, 1))]
+
+
+@pytest.mark.parametrize("name", UNARY)
+def test_unary_ops_within_two_ulp(name):
+    agree(lambda g, i: op(g, name, [i[0]]), [seq((5, 7))], what=name, ulps=2)
+
+
+@pytest.mark.parametrize("name", BINARY)
+@pytest.mark.parametrize("shapes", PATTERNS)
+def test_binary_ops_every_broadcast_pattern(name, shapes):
+    a, b = shapes
+    agree(lambda g, i: op(g, name, [i[0], i[1]]), [seq(a), seq(b)], what=f"{name} {a} {b}", ulps=2)
+
+
+def test_where_and_fused_chains():
+    agree(lambda g, i: op(g, "where", [op(g, "gt", [i[0], i[1]]), i[0], i[1]]), [seq((3, 3)), t(np.full((3, 3), 0.5))], ulps=0)
+
+    # A chain of every fusable op in one group, over Full, Splat, Row and Broadcast inputs.
+    def chain(g, i):
+        x = i[0]
+        y = op(g, "add", [x, i[1]])           # Row
+        y = op(g, "mul", [y, i[2]])           # Splat
+        y = op(g, "sub", [y, i[3]])           # Broadcast (column)
+        y = op(g, "tanh", [y])
+        y = op(g, "exp", [y])
+        y = op(g, "log", [op(g, "add", [y, i[2]])])
+        y = op(g, "div", [y, op(g, "sqrt", [op(g, "abs", [x])])])
+        y = op(g, "maximum", [y, op(g, "neg", [x])])
+        y = op(g, "minimum", [y, op(g, "sin", [x])])
+        z = op(g, "pow", [op(g, "abs", [y]), op(g, "cos", [x])])
+        w = op(g, "where", [op(g, "ge", [z, y]), z, op(g, "floor", [y])])
+        return [w, op(g, "sign", [op(g, "sub", [w, x])])]
+    agree(chain, [seq((64, 33)), seq((33,)), t(1.5), seq((64, 1))], what="chain", ulps=4)
+
+
+def test_vectorized_and_tail_paths_of_fused_kernels():
+    for n in (1, 3, 4, 1023, 1025, 4096 * 3 + 5):
+        agree(lambda g, i: op(g, "mul", [op(g, "add", [i[0], i[1]]), i[0]]), [seq((n,)), seq((n,))], what=f"n={n}", ulps=0)
+    agree(lambda g, i: op(g, "exp", [op(g, "mul", [i[0], i[1]])]), [seq((37, 64)), seq((64,))], what="row L%4==0", ulps=2)
+    agree(lambda g, i: op(g, "exp", [op(g, "mul", [i[0], i[1]])]), [seq((37, 63)), seq((63,))], what="row L%4!=0", ulps=2)
+
+
+def test_ieee_special_values():
+    specials = [0.0, -0.0, 1.0, -1.0, 2.5, -2.5, np.inf, -np.inf, np.nan, 1e30, -1e30, 1e-30]
+    x = t(specials)
+    for name in ["exp", "log", "sqrt", "tanh", "abs", "sign", "floor", "neg"]:
+        agree(lambda g, i: op(g, name, [i[0]]), [x], what=f"special {name}", ulps=2)
+    trig = t([0.0, 1.0, -2.5, np.inf, -np.inf, np.nan])
+    for name in ["sin", "cos"]:
+        agree(lambda g, i: op(g, name, [i[0]]), [trig], what=f"special {name}", ulps=2)
+    pairs = [(a, b) for a in specials for b in specials]
+    a, b = t([p[0] for p in pairs]), t([p[1] for p in pairs])
+    for name in ["add", "sub", "mul", "div", "maximum", "minimum", "gt", "ge"]:
+        agree(lambda g, i: op(g, name, [i[0], i[1]]), [a, b], what=f"special {name}", ulps=0)
+    agree(lambda g, i: op(g, "pow", [i[0], i[1]]), [t([-2.0, -2.0, -3.0, 2.0, 0.0, -2.0]), t([2.0, 3.0, -1.0, 0.5, 2.0, 0.5])],
+          what="pow negative base", ulps=2)
+
+
+def test_structural_ops_are_bit_exact():
+    x = seq((3, 4, 5))
+    agree(lambda g, i: op(g, "transpose", [i[0]], perm=[2, 0, 1]), [x], ulps=0)
+    agree(lambda g, i: op(g, "broadcast_to", [i[0]], shape=[2, 3, 4, 5]), [x], ulps=0)
+    agree(lambda g, i: op(g, "slice", [i[0]], starts=[1, 0, 2], stops=[3, 4, 4]), [x], ulps=0)
+    agree(lambda g, i: op(g, "pad", [i[0]], starts=[1, 2, 0], shape=[5, 6, 7]), [x], ulps=0)
+    for axis in range(3):
+        agree(lambda g, i: op(g, "concat", [i[0], i[0], i[0]], axis=axis), [x], ulps=0)
+        agree(lambda g, i: op(g, "take", [i[0], i[1]], axis=axis), [x, t([[1, 0], [2, 2]], "int32")], ulps=0)
+    ix = t(np.arange(24).reshape(3, 4, 2) % 5, "int32")
+    agree(lambda g, i: op(g, "take_along", [i[0], i[1]]), [x, ix], ulps=0)
+    agree(lambda g, i: op(g, "take_along_grad", [i[0], i[1]], shape=[3, 4, 5]), [seq((3, 4, 2)), ix], ulps=0)
+    agree(lambda g, i: op(g, "take_grad", [i[0], i[1]], axis=0, shape=[2, 5]), [seq((3, 5)), t([1, 1, 0], "int32")], ulps=0)
+    agree(lambda g, i: op(g, "argmax", [i[0]]), [x])
+    agree(lambda g, i: op(g, "cast", [op(g, "cast", [i[0]], dtype="int32")], dtype="float32"), [t([1.5, -1.5, 3.9])], ulps=0)
+    agree(lambda g, i: op(g, "add", [i[0], i[0]]), [t([1, -2, 3], "int32")])
+    agree(lambda g, i: op(g, "take", [i[0], i[1]], axis=0), [seq((3,)), t([9, -4, 1], "int32")], ulps=0)
+    # Repeated and clamped indices in several rows (tests/metal.rs:317-320).
+    idx = t([1, 1, 0, 4, 9, -3, 2, 2, 3, 3, 4, 0], "int32")
+    agree(lambda g, i: op(g, "take_along_grad", [i[0], op(g, "reshape", [i[1]], shape=[2, 3, 2])], shape=[2, 3, 5]),
+          [seq((2, 3, 2)), idx], ulps=0)
+
+
+def test_casts_saturate_and_map_nan_to_zero():
+    x = t([np.nan, 3e9, -3e9, 2.9, -2.9, 0.5, -0.0], "float64")
+    agree(lambda g, i: op(g, "cast", [i[0]], dtype="int32"), [x])
+    agree(lambda g, i: op(g, "cast", [i[0]], dtype="float32"), [t([1e300, 1.0000001, -2.5e-45], "float64")], ulps=0)
+
+
+@pytest.mark.parametrize("kind", ["sum", "max", "min"])
+def test_reductions_over_every_axis_set(kind):
+    x = seq((3, 4, 5))
+    for axes in [[0], [1], [2], [0, 2], [1, 2], [0, 1, 2], [], [0, 1]]:
+        for keepdims in (True, False):
+            agree(lambda g, i: op(g, kind, [i[0]], axes=axes, keepdims=keepdims), [x], tol=1e-6, what=f"{kind} {axes} {keepdims}")
+
+
+@pytest.mark.parametrize("shape,axes", [((8192, 256), [1]), ((65536, 96), [1]), ((8192, 768), [0]), ((32, 256, 1024), [0, 1]),
+                                        ((4, 50000), [1]), ((3 << 20,), [0]), ((2, 3000, 7), [1]), ((5, 7, 9, 11), [0, 2])])
+def test_reductions_at_model_shapes(shape, axes):
+    rng = np.random.default_rng(3)
+    x = t(rng.normal(size=shape).astype(np.float32))
+    for kind in ("sum", "max"):
+        hip, cpu = run_graph("hip", lambda g, i: op(g, kind, [i[0]], axes=axes, keepdims=False), [x]), \
+            run_graph("cpu", lambda g, i: op(g, kind, [i[0]], axes=axes, keepdims=False), [x])
+        close(hip[0], cpu[0], 1e-4, f"{kind} {shape} {axes}")
+
+
+MATMUL_CASES = [((3,), (3,)), ((2, 3), (3,)), ((3,), (3, 2)), ((2, 3), (3, 4)), ((5, 2, 3), (3, 4)), ((5, 2, 3), (5, 3, 4)),
+                ((2, 3), (7, 3, 4)), ((1, 2, 3), (6, 3, 4)), ((5, 1, 2, 3), (1, 4, 3, 2))]
+
+
+@pytest.mark.parametrize("a,b", MATMUL_CASES)
+def test_matmul_ranks_and_batches(a, b):
+    agree(lambda g, i: op(g, "matmul", [i[0], i[1]]), [seq(a), seq(b)], tol=2e-6, what=f"matmul {a} {b}")
+
+
+def _swap(g, x, rank):
+    p = list(range(rank))
+    p[-2], p[-1] = p[-1], p[-2]
+    return op(g, "transpose", [x], perm=p)
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 256, 768), (300, 70, 130), (8192, 256, 96), (256, 8192, 768), (64, 64, 64), (33, 17, 65)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_mfma_products_with_transpose_flags(m, k, n, ta, tb):
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    a = rng.normal(size=(k, m) if ta else (m, k)).astype(np.float32)
+    b = rng.normal(size=(n, k) if tb else (k, n)).astype(np.float32)
+
+    def build(g, i):
+        x = _swap(g, i[0], 2) if ta else i[0]
+        y = _swap(g, i[1], 2) if tb else i[1]
+        return op(g, "matmul", [x, y])
+    hip = run_graph("hip", build, [t(a), t(b)], optimize="standard")[0]
+    want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    close(hip, want, 1e-4, f"gemm {m}x{k}x{n} ta={ta} tb={tb}")
+
+
+def test_batched_attention_products():
+    rng = np.random.default_rng(5)
+    q = rng.normal(size=(4, 8, 256, 32)).astype(np.float32)
+    kk = rng.normal(size=(4, 8, 256, 32)).astype(np.float32)
+
+    def build(g, i):
+        s = op(g, "matmul", [i[0], _swap(g, i[1], 4)])
+        return [s, op(g, "matmul", [s, i[1]])]
+    hip = run_graph("hip", build, [t(q), t(kk)], optimize="standard")
+    s = q.astype(np.float64) @ np.swapaxes(kk, -1, -2).astype(np.float64)
+    close(hip[0], s, 1e-5, "qk")
+    close(hip[1], s @ kk.astype(np.float64), 1e-5, "sv")
+
+
+def test_random_bits_are_identical_to_cpu():
+    key = t([7, -11], "int32")
+
+    def build(g, i):
+        return [op(g, "random_uniform", [i[0]], shape=[1000], dtype="float32"), op(g, "key_split", [i[0]], n=5),
+                op(g, "random_uniform", [i[0]], shape=[10], dtype="float64"), op(g, "random_uniform", [i[0]], shape=[1 << 16], dtype="float32")]
+    hip = run_graph("hip", build, [key])
+    cpu = run_graph("cpu", build, [key])
+    for a, b in zip(hip, cpu):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def test_normal_sampling_matches_cpu():
+    key = t([3, 4], "int32")
+    agree(lambda g, i: op(g, "random_normal", [i[0]], shape=[4096], dtype="float32"), [key], ulps=1)
+    agree(lambda g, i: op(g, "random_normal", [i[0]], shape=[512], dtype="float64"), [key], ulps=4)
+
+
+def test_sort_and_scan_kernels():
+    x = t([[3.0, 1.0, 3.0, np.nan, 2.0, -1.0, 3.0, 0.5]] * 3)
+    agree(lambda g, i: op(g, "arg_top_k", [i[0]], k=3), [x])
+    agree(lambda g, i: op(g, "arg_top_k", [i[0]], k=8), [x])
+    agree(lambda g, i: op(g, "cumsum", [i[0]], reverse=True), [seq((3, 8))], ulps=0)
+    agree(lambda g, i: op(g, "cumsum", [i[0]], reverse=False), [t(np.arange(12).reshape(3, 4), "int32")])
+
+
+def test_float64_programs_run_on_the_device():
+    def build(g, i):
+        e = op(g, "exp", [i[0]])
+        w = op(g, "cast", [e], dtype="float64")
+        l = op(g, "log", [w])
+        back = op(g, "cast", [l], dtype="float32")
+        return [op(g, "mul", [back, i[0]]), l]
+    agree(build, [seq((4,))], tol=2e-6)
