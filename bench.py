@@ -1,0 +1,174 @@
+"""Headline benchmark: train steps/s of the d=256, 6-layer char-GPT on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+One step is one full AdamW training step of the C4 program (B=32, T=256, d=256, 8 heads, 6 layers,
+vocab 96, fp32): ids drawn in the step from the state key, forward, backward, update. The timed
+region is `rg.run(compiled, state, steps=K)`: the device-resident step loop, synchronized on
+both sides. Prints one JSON line with the throughput, the roofline of the dominant kernel class
+(per-step device times from HIP events on the execution stream), and the CPU oracle's time for
+one step of the same program on this host as the baseline.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def _numel(s):
+    n = 1
+    for d in s:
+        n *= d
+    return n
+
+
+def classify(plan, seconds):
+    """Groups plan steps into kernel classes with their algorithmic work and device time."""
+    classes = {}
+
+    def add(name, t, flops=0.0, nbytes=0.0):
+        c = classes.setdefault(name, {"seconds": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0})
+        c["seconds"] += t
+        c["flops"] += flops
+        c["bytes"] += nbytes
+        c["launches"] += 1
+
+    for st, t in zip(plan, seconds):
+        ds = 8 if st["dtype"] == "float64" else 4
+        if st["kind"] == "fused":
+            n = st["n"]
+            add("fused_elementwise", t, nbytes=sum(_numel(s) for s in st["inputs"]) * ds + n * st["n_outputs"] * ds)
+            continue
+        op, shape, args = st["op"], st["shape"], st["arg_shapes"]
+        if op in ("matmul", "matmul_t"):
+            a = args[0]
+            k = a[-1] if len(a) >= 1 and not st["ta"] else (a[-2] if len(a) >= 2 else a[0])
+            flops = 2.0 * _numel(shape) * k
+            m_rows = _numel(shape) // (shape[-1] if shape else 1)
+            mfma = st["dtype"] == "float32" and len(shape) >= 2 and shape[-1] >= 32 and m_rows >= 32
+            add("gemm_mfma" if mfma else "gemm_plain", t, flops=flops, nbytes=(sum(_numel(s) for s in args) + _numel(shape)) * ds)
+        elif op in ("sum", "max", "min"):
+            add("reduce", t, nbytes=(_numel(args[0]) + st["n"]) * ds)
+        elif op in ("take", "take_along"):
+            add("gather_scatter", t, nbytes=_numel(args[1]) * 4 + 2 * st["n"] * ds)
+        elif op in ("take_grad", "take_along_grad"):
+            add("gather_scatter", t, nbytes=(_numel(args[0]) + st["n"]) * ds + _numel(args[1]) * 4)
+        else:
+            add("structural_other", t, nbytes=(sum(_numel(s) for s in args) + st["n"]) * ds)
+    for c in classes.values():
+        if c["flops"]:
+            c["achieved"] = c["flops"] / c["seconds"] / 1e12 if c["seconds"] else 0.0
+            c["unit"] = "TFLOP/s"
+        else:
+            c["achieved"] = c["bytes"] / c["seconds"] / 1e9 if c["seconds"] else 0.0
+            c["unit"] = "GB/s"
+    return classes
+
+
+def cpu_baseline(cfg, steps=1):
+    """The CPU oracle (a restatement of rg's CPU interpreter) running the same program."""
+    from rustautograd_amd import _native, workloads
+    import rustautograd_amd as rg
+    import ctypes
+    path = os.path.join(ROOT, "oracle", "_build", "librg_cpu.so")
+    _native.register_backend("cpu", path, "rg_cpu_")
+    threads = ctypes.CDLL(path).rg_cpu_threads()
+    step, state = workloads.gpt_train_step(cfg)
+    c = rg.compile(step, (state,), validate="none", device="cpu")
+    r = rg.run(c, state, steps=steps)
+    return {"value": r.steps / r.elapsed, "unit": "steps/s", "cores": int(threads), "kind": "port",
+            "sample": f"{r.steps} full training step(s) of the same C4 program on the oracle (oracle/cpu_exec.cpp), "
+                      f"{r.elapsed:.1f} s, OpenMP threads where the reference uses rayon"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="C4", choices=["C3", "C4"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import rustautograd_amd as rg
+    from rustautograd_amd import _native, workloads
+    if "hip" not in rg.devices():
+        raise SystemExit(f"HIP backend unavailable: {_native.hip_error()}")
+    cfg = workloads.GPT_CONFIGS[args.workload]
+    step, state = workloads.gpt_train_step(cfg)
+    t0 = time.perf_counter()
+    compiled = rg.compile(step, (state,), validate="basic", device="hip")
+    compile_s = time.perf_counter() - t0
+    print(f"# compiled {args.workload} in {compile_s:.1f}s: {compiled.report['graph']['steps']} plan steps, "
+          f"{compiled.report['graph']['fused_groups']} fused groups", file=sys.stderr, flush=True)
+
+    warm = rg.run(compiled, state, steps=args.warmup) if args.warmup else None
+    cur = warm.state if warm else state
+    t0 = time.perf_counter()
+    res = rg.run(compiled, cur, steps=args.steps)
+    wall = time.perf_counter() - t0
+    assert res.steps == args.steps, res
+    value = args.steps / wall
+    print(f"# {args.steps} steps in {wall:.3f}s (device loop {res.elapsed:.3f}s), loss {res.history['aux'][0]:.4f} -> "
+          f"{res.history['aux'][-1]:.4f}", file=sys.stderr, flush=True)
+
+    # Per-step device times (HIP events around each plan step on the execution stream).
+    from rustautograd_amd._core import _flatten
+    inputs = [rg.tensor(x)._t for x in _flatten((res.state,))[0]]
+    reps = 3
+    seconds = [s / reps for s in compiled._n.step_times(inputs, reps)]
+    classes = classify(compiled.plan_summary(), seconds)
+    dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])
+    if dom["unit"] == "TFLOP/s":
+        roof = {"bound": "mfma", "achieved": round(dom["achieved"], 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(dom["achieved"] / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+    else:
+        roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": None}
+    roof["kernel"] = dom_name
+    kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
+                   "unit": v["unit"],
+                   "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4)}
+               for k, v in sorted(classes.items(), key=lambda kv: -kv[1]["seconds"])}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
+    out = {
+        "metric": "train steps/s, char-GPT d=256 6L on 1 MI355X; % of HBM / fp32-MFMA roofline",
+        "value": round(value, 3),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 / value, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: token ids uniform in [0,96) drawn inside the step from a seeded key; random-init weights",
+        "config": {"workload": f"{args.workload} char-GPT training step", "batch": cfg.batch, "seq_len": cfg.block, "d_model": cfg.d,
+                   "heads": cfg.heads, "layers": cfg.layers, "vocab": cfg.vocab, "optimizer": "adamw", "lr": cfg.lr,
+                   "gemm_gflop_per_step": round(workloads.gpt_gemm_flops(cfg) / 1e9, 2)},
+        "roofline": roof,
+        "kernels": kernels,
+        "device_ms_per_step": round(sum(seconds) * 1e3, 3),
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

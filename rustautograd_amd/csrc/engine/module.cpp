@@ -4,6 +4,8 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <chrono>
+
 #include "validate.h"
 
 namespace py = pybind11;
@@ -264,6 +266,30 @@ PYBIND11_MODULE(_rg, m) {
                out.append(d);
              }
              return out;
+           })
+      .def("step_times",
+           [](const PyCompiled& c, const std::vector<PyTensor>& inputs, size_t repeats) {
+             // Device seconds of each plan step, summed over `repeats` runs (metal.rs:690-698).
+             auto in = tensors(inputs);
+             c.c->check_inputs(in);
+             std::vector<double> seconds(c.c->plan.steps.size(), 0.0);
+             py::gil_scoped_release nogil;
+             auto e = c.c->program->exec();
+             for (size_t k = 0; k < in.size(); k++) e->load(k, in[k]);
+             Backend* b = c.c->device;
+             for (size_t r = 0; r < repeats; r++) {
+               if (b->exec_step_timed) {
+                 b->exec_step_timed(e->handle(), seconds.data());
+               } else {
+                 for (size_t s = 0; s < seconds.size(); s++) {
+                   auto t0 = std::chrono::steady_clock::now();
+                   e->steps(s, s + 1);
+                   seconds[s] += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+                 }
+               }
+             }
+             if (auto f = e->failure()) raise_diag(device_failure(b->name, *f));
+             return seconds;
            })
       .def("call",
            [](const PyCompiled& c, const std::vector<PyTensor>& inputs) {

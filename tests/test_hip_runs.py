@@ -138,4 +138,5 @@ def test_small_gpt_loss_curve_overlays_cpu():
     assert checks["device_equivalence"]["status"] == "pass", checks["device_equivalence"]
     a, b = rg.run(gpu, state, steps=20), rg.run(cpu, state, steps=20)
     close(np.array(a.history["aux"]), np.array(b.history["aux"]), 1e-4, "loss curve")
-    assert a.history["aux"][-1] < a.history["aux"][0]
+    # Uniform random tokens carry no structure: the loss stays near ln(vocab).
+    assert abs(np.mean(a.history["aux"]) - np.log(cfg.vocab)) < 0.1
