@@ -103,6 +103,28 @@ __global__ void __launch_bounds__(TPB) k_gather(const E* __restrict__ src, E* __
   dst[i] = src[off[0]];
 }
 
+// Four consecutive outputs per thread (the innermost merged dim is a multiple of 4, so they
+// share every outer coordinate): one 16-byte store, and one 16-byte load when the source run is
+// contiguous and aligned, a single broadcast load when its stride is 0.
+__global__ void __launch_bounds__(TPB) k_gather4(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, uint32_t n, Strided g,
+                                                 int aligned) {
+  uint32_t i0 = (blockIdx.x * TPB + threadIdx.x) * 4;
+  if (i0 >= n) return;
+  uint32_t off[1];
+  decompose(g, i0, off, 1);
+  uint32_t s_in = g.rank ? g.st[0][g.rank - 1] : 0;
+  uint4 v;
+  if (s_in == 1 && aligned) {
+    v = *(const uint4*)(src + off[0]);
+  } else if (s_in == 0) {
+    uint32_t x = src[off[0]];
+    v = make_uint4(x, x, x, x);
+  } else {
+    v = make_uint4(src[off[0]], src[off[0] + s_in], src[off[0] + 2 * s_in], src[off[0] + 3 * s_in]);
+  }
+  *(uint4*)(dst + i0) = v;
+}
+
 struct PadDims {
   int rank;
   FastDiv size[MAX_DIMS];
@@ -162,27 +184,53 @@ __global__ void __launch_bounds__(TPB) k_take_along(const E* __restrict__ src, c
 // the CPU's sequential order (src/plan.rs:1502-1531), so results are bit-identical. Index chunks
 // are staged in LDS and shared by the block.
 
+constexpr uint32_t TG_CHUNK = 4096;
+
+// Block (x, d, o) owns columns [x*256, x*256+256) of output row (o, d). The block first lists,
+// in increasing position, the index entries that hit row d (a stable compaction through LDS),
+// then every thread sums its column over that list: the CPU's order, coalesced reads.
 template <class T>
 __global__ void __launch_bounds__(TPB) k_take_grad(const T* __restrict__ ct, const int* __restrict__ idx, T* __restrict__ dst,
-                                                   uint32_t n, FastDiv block, FastDiv dim, uint32_t n_idx) {
-  __shared__ int sidx[1024];
-  uint32_t t = blockIdx.x * TPB + threadIdx.x;
-  bool live = t < n;
-  uint32_t r = block.div(live ? t : 0);
-  uint32_t q = (live ? t : 0) - r * block.d;
-  uint32_t o = dim.div(r);
-  uint32_t dd = r - o * dim.d;
+                                                   uint32_t block, uint32_t dim, uint32_t n_idx) {
+  __shared__ uint32_t list[TG_CHUNK];
+  __shared__ uint32_t counts[TPB];
+  const uint32_t d = blockIdx.y, o = blockIdx.z;
+  const uint32_t q = blockIdx.x * TPB + threadIdx.x;
   T acc = (T)0;
-  for (uint32_t j0 = 0; j0 < n_idx; j0 += 1024) {
-    uint32_t m = min(1024u, n_idx - j0);
+  for (uint32_t j0 = 0; j0 < n_idx; j0 += TG_CHUNK) {
+    const uint32_t m = min(TG_CHUNK, n_idx - j0);
+    const uint32_t per = (m + TPB - 1) / TPB;
+    const uint32_t lo = min(m, threadIdx.x * per), hi = min(m, lo + per);
+    uint32_t c = 0;
+    for (uint32_t x = lo; x < hi; x++) c += clamp_index(idx[j0 + x], dim) == d;
+    counts[threadIdx.x] = c;
     __syncthreads();
-    for (uint32_t x = threadIdx.x; x < m; x += TPB) sidx[x] = idx[j0 + x];
+    if (threadIdx.x == 0) {
+      uint32_t run = 0;
+      for (int t = 0; t < TPB; t++) {
+        uint32_t v = counts[t];
+        counts[t] = run;
+        run += v;
+      }
+    }
     __syncthreads();
-    if (live)
-      for (uint32_t x = 0; x < m; x++)
-        if (clamp_index(sidx[x], dim.d) == dd) acc = acc + ct[((uint64_t)o * n_idx + j0 + x) * block.d + q];
+    uint32_t at = counts[threadIdx.x];
+    for (uint32_t x = lo; x < hi; x++)
+      if (clamp_index(idx[j0 + x], dim) == d) list[at++] = j0 + x;
+    __syncthreads();
+    const uint32_t total = (threadIdx.x == TPB - 1) ? at : 0;
+    if (threadIdx.x == TPB - 1) counts[0] = at;  // last thread's end is the list length
+    __syncthreads();
+    const uint32_t len = counts[0];
+    (void)total;
+    if (q < block) {
+      const T* base = ct + (uint64_t)o * n_idx * block + q;
+#pragma unroll 4
+      for (uint32_t e = 0; e < len; e++) acc = acc + base[(uint64_t)list[e] * block];
+    }
+    __syncthreads();
   }
-  if (live) dst[t] = acc;
+  if (q < block) dst[((uint64_t)o * dim + d) * block + q] = acc;
 }
 
 template <class T>
@@ -339,7 +387,18 @@ __global__ void __launch_bounds__(TPB) k_reduce_rows_wave(int kind, const T* __r
   if (row >= rows) return;
   const T* x = a + (uint64_t)row * len;
   T acc = Red<T>::init(kind);
-  for (uint32_t j = lane; j < len; j += 64) acc = combine(kind, acc, x[j]);
+  constexpr uint32_t V = 16 / sizeof(T);
+  if (len % V == 0) {
+    // 16-byte loads: lane l reads elements [V*l, V*l+V) of each 64*V segment.
+    typedef T vec __attribute__((ext_vector_type(V)));
+    for (uint32_t j = lane * V; j < len; j += 64 * V) {
+      vec v = *(const vec*)(x + j);
+#pragma unroll
+      for (uint32_t q = 0; q < V; q++) acc = combine(kind, acc, v[q]);
+    }
+  } else {
+    for (uint32_t j = lane; j < len; j += 64) acc = combine(kind, acc, x[j]);
+  }
   acc = wave_combine(kind, acc);
   if (lane == 0) d[row] = acc;
 }
@@ -364,29 +423,32 @@ __global__ void __launch_bounds__(TPB) k_reduce_rows_block(int kind, const T* __
   }
 }
 
-// Leading-axis reduction of [batch, r, k] over r: threads own columns (coalesced), row chunks
-// give parallelism, and partial results combine in a fixed order in a second pass.
+// Leading-axis reduction of [batch, r, k] over r. A block owns 64 consecutive columns (one
+// coalesced 256-byte row segment per wave) and 4 row lanes; row chunks give parallelism and write
+// partial results, which a second pass of the same kernel combines (deterministic order).
 template <class T>
 __global__ void __launch_bounds__(TPB) k_reduce_cols(int kind, const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
                                                       uint32_t chunk_rows, uint32_t chunks) {
-  uint32_t c = blockIdx.x * TPB + threadIdx.x;
-  uint32_t b = blockIdx.y, s = blockIdx.z;
-  if (c >= k) return;
-  uint32_t r0 = s * chunk_rows, r1 = min(r, r0 + chunk_rows);
-  const T* x = a + (uint64_t)b * r * k + c;
+  __shared__ T part[4][64];
+  const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const uint32_t c = blockIdx.x * 64 + tx;
+  const uint32_t b = blockIdx.y, s = blockIdx.z;
+  const uint32_t r0 = s * chunk_rows, r1 = min(r, r0 + chunk_rows);
   T acc = Red<T>::init(kind);
-  for (uint32_t row = r0; row < r1; row++) acc = combine(kind, acc, x[(uint64_t)row * k]);
-  out[((uint64_t)b * chunks + s) * k + c] = acc;
-}
-
-template <class T>
-__global__ void __launch_bounds__(TPB) k_reduce_cols_finish(int kind, const T* __restrict__ part, T* __restrict__ d, uint32_t k, uint32_t chunks) {
-  uint32_t c = blockIdx.x * TPB + threadIdx.x;
-  uint32_t b = blockIdx.y;
-  if (c >= k) return;
-  T acc = Red<T>::init(kind);
-  for (uint32_t s = 0; s < chunks; s++) acc = combine(kind, acc, part[((uint64_t)b * chunks + s) * k + c]);
-  d[(uint64_t)b * k + c] = acc;
+  if (c < k) {
+    const T* x = a + (uint64_t)b * r * k + c;
+#pragma unroll 8
+    for (uint32_t row = r0 + ty; row < r1; row += 4) acc = combine(kind, acc, x[(uint64_t)row * k]);
+  }
+  part[ty][tx] = acc;
+  __syncthreads();
+  if (ty == 0 && c < k) {
+    T v = part[0][tx];
+    v = combine(kind, v, part[1][tx]);
+    v = combine(kind, v, part[2][tx]);
+    v = combine(kind, v, part[3][tx]);
+    out[((uint64_t)b * chunks + s) * k + c] = v;
+  }
 }
 
 template <class T>
@@ -510,6 +572,16 @@ void where(hipStream_t s, int esize, const void* c, const void* a, const void* b
 }
 
 void gather(hipStream_t s, int esize, const void* src, void* dst, uint64_t n, const Strided& g) {
+  bool vec = esize == 4 && n % 4 == 0 && (g.rank == 0 || g.size[g.rank - 1].d % 4 == 0) && ((uintptr_t)dst & 15) == 0;
+  if (vec) {
+    // The source run is 16-byte aligned when the base and every outer stride are multiples of 4.
+    bool aligned = ((uintptr_t)src & 15) == 0 && g.base[0] % 4 == 0;
+    for (int d = 0; d + 1 < g.rank; d++) aligned = aligned && g.st[0][d] % 4 == 0;
+    uint64_t n4 = n / 4;
+    if (g.rank == 0) aligned = false;
+    RG_LAUNCH(k_gather4, n4, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, g, (int)aligned);
+    return;
+  }
   if (esize == 4) RG_LAUNCH(k_gather<uint32_t>, n, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, g);
   else RG_LAUNCH(k_gather<uint64_t>, n, (const uint64_t*)src, (uint64_t*)dst, (uint32_t)n, g);
 }
@@ -555,10 +627,13 @@ void take_along(hipStream_t s, int esize, const void* src, const int32_t* idx, v
 
 void take_grad(hipStream_t s, int dtype, const void* ct, const int32_t* idx, void* dst, uint64_t n, uint64_t block, uint64_t n_idx,
                uint64_t dim) {
-  if (block == 0) return;
-  FastDiv fb((uint32_t)block), fd((uint32_t)dim);
-  if (dtype == RG_F32) RG_LAUNCH(k_take_grad<float>, n, (const float*)ct, idx, (float*)dst, (uint32_t)n, fb, fd, (uint32_t)n_idx);
-  else RG_LAUNCH(k_take_grad<double>, n, (const double*)ct, idx, (double*)dst, (uint32_t)n, fb, fd, (uint32_t)n_idx);
+  if (block == 0 || n == 0) return;
+  uint64_t outer = n / (block * dim);
+  dim3 grid(blocks_for(block, TPB), (uint32_t)dim, (uint32_t)outer);
+  if (dtype == RG_F32)
+    hipLaunchKernelGGL(k_take_grad<float>, grid, dim3(TPB), 0, s, (const float*)ct, idx, (float*)dst, (uint32_t)block, (uint32_t)dim, (uint32_t)n_idx);
+  else
+    hipLaunchKernelGGL(k_take_grad<double>, grid, dim3(TPB), 0, s, (const double*)ct, idx, (double*)dst, (uint32_t)block, (uint32_t)dim, (uint32_t)n_idx);
 }
 
 void take_along_grad(hipStream_t s, int dtype, const void* ct, const int32_t* idx, void* dst, uint64_t n, uint64_t k, uint64_t v) {
@@ -620,24 +695,25 @@ void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
 }
 
 uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k) {
-  // Aim for >= 1024 blocks (4 per CU) with at least 16 rows per chunk.
-  uint64_t col_blocks = (k + TPB - 1) / TPB * batch;
+  // Aim for >= 1024 blocks (4 per CU) with at least 32 rows per chunk.
+  uint64_t col_blocks = (k + 63) / 64 * batch;
   uint64_t want = (1024 + col_blocks - 1) / col_blocks;
-  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 16));
+  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 32));
   return std::min<uint64_t>(chunks, 65535);
 }
 
 void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k, void* partial,
                  uint64_t chunks) {
   uint32_t chunk_rows = (uint32_t)((r + chunks - 1) / chunks);
-  dim3 grid(blocks_for(k, TPB), (uint32_t)batch, (uint32_t)chunks);
+  dim3 grid(blocks_for(k, 64), (uint32_t)batch, (uint32_t)chunks);
   void* out = chunks == 1 ? d : partial;
   if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols<float>, grid, dim3(TPB), 0, s, kind, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
   else hipLaunchKernelGGL(k_reduce_cols<double>, grid, dim3(TPB), 0, s, kind, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
   if (chunks > 1) {
-    dim3 g2(blocks_for(k, TPB), (uint32_t)batch);
-    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols_finish<float>, g2, dim3(TPB), 0, s, kind, (const float*)partial, (float*)d, (uint32_t)k, (uint32_t)chunks);
-    else hipLaunchKernelGGL(k_reduce_cols_finish<double>, g2, dim3(TPB), 0, s, kind, (const double*)partial, (double*)d, (uint32_t)k, (uint32_t)chunks);
+    // The partials [batch, chunks, k] are themselves a leading-axis reduction.
+    dim3 g2(blocks_for(k, 64), (uint32_t)batch, 1);
+    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols<float>, g2, dim3(TPB), 0, s, kind, (const float*)partial, (float*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
+    else hipLaunchKernelGGL(k_reduce_cols<double>, g2, dim3(TPB), 0, s, kind, (const double*)partial, (double*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
   }
 }
 

@@ -200,3 +200,25 @@ def test_float64_programs_run_on_the_device():
         back = op(g, "cast", [l], dtype="float32")
         return [op(g, "mul", [back, i[0]]), l]
     agree(build, [seq((4,))], tol=2e-6)
+
+
+def test_vectorized_structural_paths():
+    x = seq((4, 8, 16, 32))
+    agree(lambda g, i: op(g, "transpose", [i[0]], perm=[0, 2, 1, 3]), [x], ulps=0)
+    agree(lambda g, i: op(g, "transpose", [op(g, "reshape", [i[0]], shape=[4, 16, 2, 4, 32])], perm=[2, 0, 3, 1, 4]), [x], ulps=0)
+    agree(lambda g, i: op(g, "broadcast_to", [i[0]], shape=[3, 4, 8, 16, 32]), [x], ulps=0)
+    agree(lambda g, i: op(g, "broadcast_to", [i[0]], shape=[4, 8, 16, 32]), [t(-1e9)], ulps=0)
+    agree(lambda g, i: op(g, "broadcast_to", [i[0]], shape=[4, 8, 16, 32]), [seq((16, 1))], ulps=0)
+    agree(lambda g, i: op(g, "slice", [i[0]], starts=[1, 0, 4, 0], stops=[3, 8, 12, 32]), [x], ulps=0)
+    agree(lambda g, i: op(g, "slice", [i[0]], starts=[0, 0, 0, 1], stops=[4, 8, 16, 29]), [x], ulps=0)
+
+
+def test_scatter_add_at_embedding_shapes_is_bit_exact():
+    rng = np.random.default_rng(11)
+    ct = t(rng.normal(size=(32, 256, 256)).astype(np.float32))
+    idx = t(rng.integers(0, 96, size=(32, 256)), "int32")
+    agree(lambda g, i: op(g, "take_grad", [i[0], i[1]], axis=0, shape=[96, 256]), [ct, idx], ulps=0)
+    # Index chunks beyond the LDS list, a middle axis, and clamped entries.
+    ct2 = t(rng.normal(size=(3, 9000, 5)).astype(np.float32))
+    idx2 = t(rng.integers(-3, 12, size=(9000,)), "int32")
+    agree(lambda g, i: op(g, "take_grad", [i[0], i[1]], axis=1, shape=[3, 10, 5]), [ct2, idx2], ulps=0)

@@ -134,8 +134,20 @@ def test_small_gpt_loss_curve_overlays_cpu():
     step, state = workloads.gpt_train_step(cfg)
     gpu = rg.compile(step, (state,), validate="standard", device="hip")
     cpu = rg.compile(step, (state,), validate="basic", device="cpu")
+    assert gpu.report.ok, gpu.report["diagnostics"]
     checks = {c["name"]: c for c in gpu.report["checks"]}
-    assert checks["device_equivalence"]["status"] == "pass", checks["device_equivalence"]
+    assert checks["finite"]["status"] == "pass" and checks["optimizer_equivalence"]["status"] == "pass"
+    # The device check compares the state after one AdamW update. The attention key bias has a
+    # mathematically zero gradient (softmax ignores a per-row shift of the scores), so its value is
+    # rounding noise that Adam scales to +-lr; a DEVICE_MISMATCH may only point there.
+    dev = checks["device_equivalence"]
+    assert dev["detail"]["max_relative_error"] < 0.05, dev
+    from rustautograd_amd._core import _paths
+    names = _paths(gpu._out_def, "out")
+    for d in gpu.report["diagnostics"]:
+        assert d["code"] == "DEVICE_MISMATCH", d
+        name, element = names[d["observation"]["output_index"]], d["observation"]["element"]
+        assert name.endswith("attn.qkv.b") and cfg.d <= element < 2 * cfg.d, d
     a, b = rg.run(gpu, state, steps=20), rg.run(cpu, state, steps=20)
     close(np.array(a.history["aux"]), np.array(b.history["aux"]), 1e-4, "loss curve")
     # Uniform random tokens carry no structure: the loss stays near ln(vocab).
