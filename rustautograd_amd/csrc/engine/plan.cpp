@@ -142,6 +142,35 @@ struct Item {
   std::vector<size_t> members;
 };
 
+// BroadcastTo nodes whose every kept consumer is a device-fusable node, and which are not plan
+// outputs: fused kernels read their source through a broadcast index instead.
+std::vector<bool> absorbed_broadcasts(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs,
+                                      const Fuse& cfg) {
+  std::vector<bool> abs(g.nodes.size(), false);
+  if (!cfg.device || !cfg.absorb_broadcasts) return abs;
+  std::vector<bool> any_use(g.nodes.size(), false), bad(g.nodes.size(), false);
+  for (size_t i = 0; i < g.nodes.size(); i++) {
+    if (!keep[i]) continue;
+    const Node& n = g.nodes[i];
+    bool dev_fusable = fusable(g, i, true) && (cfg.fuse_f64 || n.dtype != DType::F64);
+    for (uint32_t x : n.inputs) {
+      any_use[x] = true;
+      if (!dev_fusable) bad[x] = true;
+    }
+  }
+  for (uint32_t o : outputs) bad[o] = true;
+  for (size_t i = 0; i < g.nodes.size(); i++)
+    abs[i] = keep[i] && g.nodes[i].op.kind == RG_OP_BROADCAST_TO && any_use[i] && !bad[i];
+  return abs;
+}
+
+bool reads_absorbed(const Graph& g, const std::vector<size_t>& members, const std::vector<bool>& abs) {
+  for (size_t m : members)
+    for (uint32_t x : g.nodes[m].inputs)
+      if (abs[x]) return true;
+  return false;
+}
+
 size_t distinct_external(const Graph& g, const std::vector<size_t>& members, const Node& extra) {
   std::set<uint32_t> s;
   auto in = [&](uint32_t x) { return std::find(members.begin(), members.end(), (size_t)x) != members.end(); };
@@ -153,7 +182,7 @@ size_t distinct_external(const Graph& g, const std::vector<size_t>& members, con
   return s.size();
 }
 
-std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg) {
+std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg, const std::vector<bool>& abs) {
   std::vector<bool> up = cfg.hoist ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
   std::vector<Item> items;
   for (size_t i = 0; i < g.nodes.size(); i++)
@@ -168,6 +197,10 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     if (!keep[i] || up[i] || leaf(n)) continue;
     size_t deepest = 0;
     for (uint32_t x : n.inputs) deepest = std::max(deepest, level[x]);
+    if (abs[i]) {
+      level[i] = deepest;  // a view of its source: no kernel, no level of its own
+      continue;
+    }
     bool joins = dev_fusable(i) && deepest > 0;
     if (joins) {
       for (uint32_t x : n.inputs) {
@@ -208,7 +241,8 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
       }
     }
     for (auto& m : groups) {
-      if (m.size() >= 2) items.push_back({true, 0, m});
+      // A node reading an absorbed broadcast needs the fused kernel's broadcast indexing.
+      if (m.size() >= 2 || reads_absorbed(g, m, abs)) items.push_back({true, 0, m});
       else
         for (size_t x : m) items.push_back({false, x, {}});
     }
@@ -219,14 +253,14 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
 
 // Greedy fusion: one open group. Instructions independent of the group are emitted first; one
 // that reads a member closes the group, which keeps the group free of cycles (plan.rs:311-350).
-std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg) {
-  if (cfg.device && cfg.levels) return schedule_levels(g, keep, cfg);
+std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg, const std::vector<bool>& abs) {
+  if (cfg.device && cfg.levels) return schedule_levels(g, keep, cfg, abs);
   std::vector<Item> items;
   std::vector<size_t> open;
   auto close = [&]() {
     double cost = 0;
     for (size_t m : open) cost += op_cost_ns(g.nodes[m].op) * (double)g.nodes[m].n();
-    if (open.size() >= (cfg.device ? 2u : 1u) && cost >= cfg.parallel_ns) {
+    if ((open.size() >= (cfg.device ? 2u : 1u) || (!open.empty() && reads_absorbed(g, open, abs))) && cost >= cfg.parallel_ns) {
       items.push_back({true, 0, open});
     } else {
       for (size_t m : open) items.push_back({false, m, {}});
@@ -238,7 +272,7 @@ std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const 
     if (up[i]) items.push_back({false, i, {}});
   for (size_t i = 0; i < g.nodes.size(); i++) {
     const Node& n = g.nodes[i];
-    if (!keep[i] || up[i] || leaf(n)) continue;
+    if (!keep[i] || up[i] || leaf(n) || abs[i]) continue;
     if (fusable(g, i, cfg.device) && !(cfg.device && !cfg.fuse_f64 && n.dtype == DType::F64)) {
       bool same = open.empty() || (g.nodes[open[0]].shape == n.shape && g.nodes[open[0]].dtype == n.dtype);
       size_t inputs = distinct_external(g, open, n);
@@ -256,7 +290,7 @@ std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const 
 }
 
 Fused compile_group(const Graph& g, const std::vector<size_t>& members, const std::vector<size_t>& slot_of,
-                    const std::vector<std::pair<size_t, size_t>>& out_slots) {
+                    const std::vector<std::pair<size_t, size_t>>& out_slots, const std::vector<bool>& abs) {
   const Node& first = g.nodes[members[0]];
   Fused f;
   std::vector<std::pair<uint32_t, std::pair<bool, size_t>>> ext;  // (node, operand)
@@ -269,8 +303,10 @@ Fused compile_group(const Graph& g, const std::vector<size_t>& members, const st
       if (seen) continue;
       rg_arg_kind kind;
       size_t row = 0;
-      if (!arg_kind(g.shape(x), first.shape, &kind, &row)) kind = RG_ARG_BROADCAST;
-      f.input_shapes.push_back(g.shape(x));
+      // An absorbed broadcast is read from its source, whose slot it shares.
+      const Shape& xs = abs[x] ? g.shape(g.nodes[x].inputs[0]) : g.shape(x);
+      if (!arg_kind(xs, first.shape, &kind, &row)) kind = RG_ARG_BROADCAST;
+      f.input_shapes.push_back(xs);
       std::pair<bool, size_t> operand;
       size_t reg = SIZE_MAX;
       if (kind == RG_ARG_FULL) {
@@ -350,8 +386,9 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   }
 
   std::vector<Item> items;
+  std::vector<bool> abs = fuse ? absorbed_broadcasts(g, keep, outputs, *fuse) : std::vector<bool>(total, false);
   if (fuse) {
-    items = schedule(g, keep, *fuse);
+    items = schedule(g, keep, *fuse, abs);
   } else {
     for (size_t i = 0; i < total; i++)
       if (keep[i] && !leaf(g.nodes[i])) items.push_back({false, i, {}});
@@ -360,6 +397,17 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   for (auto& item : items) {
     if (item.group) {
       const auto& members = item.members;
+      // Absorbed broadcasts become aliases of their source on first use (as plan.rs:565-575).
+      for (size_t m : members)
+        for (uint32_t x : g.nodes[m].inputs)
+          if (abs[x] && value_slot[x] == SIZE_MAX) {
+            size_t src = g.nodes[x].inputs[0];
+            size_t s = value_slot[src];
+            a.refs[s]++;
+            value_slot[x] = s;
+            uses[src]--;
+            if (uses[src] == 0) a.release(s);
+          }
       std::vector<uint32_t> external;
       for (size_t m : members) {
         p.naive_bytes += g.nodes[m].n() * dsize(g.nodes[m].dtype);
@@ -381,7 +429,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       }
       Step st;
       st.fused = true;
-      st.group = compile_group(g, members, value_slot, out_slots);
+      st.group = compile_group(g, members, value_slot, out_slots, abs);
       p.steps.push_back(std::move(st));
       for (uint32_t x : external)
         if (uses[x] == 0) a.release(value_slot[x]);

@@ -29,12 +29,15 @@ struct Fuse {
   size_t level_max_peak;
   // Cost model of `gpu_cost_estimate` (plan.rs:481-492).
   double per_dispatch_ns, per_element_ns;
+  // A BroadcastTo read only by fusable nodes is not materialized: the consuming fused kernels
+  // index its source directly (the reference materializes it, graph.rs:368-379, for Where).
+  bool absorb_broadcasts;
 
-  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1}; }
-  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1}; }
+  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false}; }
+  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false}; }
   // MI355X: ~4 us per dispatch inside a captured graph, ~0.001 ns per fp32 element written at
   // HBM speed, and 288 GB of HBM so level order is capped far higher.
-  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001}; }
+  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true}; }
 };
 
 struct Instr {

@@ -1,11 +1,12 @@
 // Dense products for MatMul / MatMulT (reference src/plan.rs:1453-1493, flags from
 // src/optimize.rs:338-350).
 //
-// fp32: a 128x128 block tile staged through LDS in K steps of 16, four wave64s each owning a
-// 64x64 sub-tile computed with v_mfma_f32_32x32x2f32 (2x2 MFMA tiles, 64 accumulator registers
-// per lane). Transposed operands are read through their flags: the loader transposes while
-// staging, so no copy is made. Products whose output has too few tiles to fill 256 CUs split K
-// and combine the partial sums in a fixed order (deterministic).
+// fp32: block tiles of 128x128, 128x64, 64x128, 64x64, 128x32 or 32x128 staged through LDS in
+// K steps of 16, four wave64s per block each owning 32x32 MFMA tiles (v_mfma_f32_32x32x2f32).
+// Transposed operands are read through their flags: the loader transposes while staging, so no
+// copy is made. The tile is chosen per product so that the launch fills 256 CUs with little
+// padding (32-wide tiles for 32-wide attention heads); products whose output still has too few
+// tiles split K and combine the partial sums in a fixed order (deterministic).
 // fp64 and tiny or skinny fp32 products use a plain kernel, one thread per output element.
 #include <hip/hip_runtime.h>
 
@@ -19,88 +20,109 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16, PAD = 4;
-constexpr int LDA_S = BM + PAD, LDB_S = BN + PAD;
+constexpr int BK = 16, PAD = 4;
 
 __device__ __forceinline__ int64_t batch_offset(const int64_t* offs, uint64_t stride, uint32_t b) {
   return offs ? offs[b] : (int64_t)(stride * b);
 }
 
-// Loads 8 consecutive elements of a row-major matrix row starting at column c, zero-filling
-// past `cols` (and entirely when the row is out of range).
-__device__ __forceinline__ void load8(const float* row, int64_t c, int64_t cols, bool row_ok, bool vec, float v[8]) {
-  if (vec && row_ok && c + 8 <= cols) {
-    float4 x = *(const float4*)(row + c);
-    float4 y = *(const float4*)(row + c + 4);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-    v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+// Loads N (2, 4 or 8) consecutive elements of a row-major row starting at column c, zero-filling
+// past `cols` and when the row is out of range. `vec`: the row and c allow 16/8-byte loads.
+template <int N>
+__device__ __forceinline__ void loadn(const float* row, int64_t c, int64_t cols, bool row_ok, bool vec, float v[N]) {
+  if (vec && row_ok && c + N <= cols) {
+    if constexpr (N == 2) {
+      float2 x = *(const float2*)(row + c);
+      v[0] = x.x; v[1] = x.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < N; q += 4) {
+        float4 x = *(const float4*)(row + c + q);
+        v[q] = x.x; v[q + 1] = x.y; v[q + 2] = x.z; v[q + 3] = x.w;
+      }
+    }
   } else {
 #pragma unroll
-    for (int q = 0; q < 8; q++) v[q] = (row_ok && c + q < cols) ? row[c + q] : 0.0f;
+    for (int q = 0; q < N; q++) v[q] = (row_ok && c + q < cols) ? row[c + q] : 0.0f;
   }
 }
 
-template <bool TA, bool TB>
+// C = op(A) op(B) for one BM x BN block tile. Four wave64s in a WM x WN grid; each wave owns a
+// (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles (v_mfma_f32_32x32x2f32). Operands are staged
+// through double-buffered LDS in K steps of 16, K-major, so each MFMA operand is one
+// conflict-free 32-lane LDS row read; transposed operands are transposed while staging.
+template <int BM, int BN, int WM, int WN, bool TA, bool TB>
 __global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                                                    int M, int N, int K, const int64_t* a_off, const int64_t* b_off, uint64_t a_stride,
                                                    uint64_t b_stride, int splits, int k_per_split, float* __restrict__ partial,
                                                    bool vec_a, bool vec_b) {
-  __shared__ float As[2][BK][LDA_S];
-  __shared__ float Bs[2][BK][LDB_S];
+  static_assert(WM * WN == 4, "four waves");
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile of at least 32x32");
+  // Loader geometry: 256 threads cover a BM x 16 (A) and a 16 x BN (B) tile.
+  constexpr int EA = BM * BK / 256, EB = BN * BK / 256;
+  __shared__ float As[2][BK][BM + PAD];
+  __shared__ float Bs[2][BK][BN + PAD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const uint32_t z = blockIdx.z;
-  const uint32_t b = z / splits, sp = z % splits;
+  const int wm = wave / WN, wn = wave % WN;
+  const uint32_t b = blockIdx.z / splits, sp = blockIdx.z % splits;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const float* Ab = A + batch_offset(a_off, a_stride, b);
   const float* Bb = B + batch_offset(b_off, b_stride, b);
   const int kbeg = sp * k_per_split, kend = min(K, kbeg + k_per_split);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
-  float ra[8], rb[8];
-  // Thread roles in the loaders (256 threads x 8 elements = one 128x16 operand tile).
+  float ra[EA], rb[EB];
   auto load_tiles = [&](int k0) {
-    if (!TA) {  // A is [M,K]: thread reads 8 consecutive k of row m
-      int m = tid >> 1, kc = (tid & 1) * 8;
-      load8(Ab + (int64_t)(m0 + m) * K, k0 + kc, kend, m0 + m < M, vec_a, ra);
-    } else {    // A is [K,M]: thread reads 8 consecutive m of row k
-      int k = tid >> 4, mc = (tid & 15) * 8;
-      load8(Ab + (int64_t)(k0 + k) * M, m0 + mc, M, k0 + k < kend, vec_a, ra);
+    if (!TA) {  // A is [M,K]: rows of 16 k, BM/... threads per row
+      constexpr int TPR = BK / EA;
+      int m = tid / TPR, kc = (tid % TPR) * EA;
+      loadn<EA>(Ab + (int64_t)(m0 + m) * K, k0 + kc, kend, m0 + m < M, vec_a, ra);
+    } else {    // A is [K,M]: 16 rows of BM m
+      constexpr int TPR = BM / EA;
+      int k = tid / TPR, mc = (tid % TPR) * EA;
+      loadn<EA>(Ab + (int64_t)(k0 + k) * M, m0 + mc, M, k0 + k < kend, vec_a, ra);
     }
-    if (!TB) {  // B is [K,N]: 8 consecutive n of row k
-      int k = tid >> 4, nc = (tid & 15) * 8;
-      load8(Bb + (int64_t)(k0 + k) * N, n0 + nc, N, k0 + k < kend, vec_b, rb);
-    } else {    // B is [N,K]: 8 consecutive k of row n
-      int n = tid >> 1, kc = (tid & 1) * 8;
-      load8(Bb + (int64_t)(n0 + n) * K, k0 + kc, kend, n0 + n < N, vec_b, rb);
+    if (!TB) {  // B is [K,N]: 16 rows of BN n
+      constexpr int TPR = BN / EB;
+      int k = tid / TPR, nc = (tid % TPR) * EB;
+      loadn<EB>(Bb + (int64_t)(k0 + k) * N, n0 + nc, N, k0 + k < kend, vec_b, rb);
+    } else {    // B is [N,K]: rows of 16 k
+      constexpr int TPR = BK / EB;
+      int n = tid / TPR, kc = (tid % TPR) * EB;
+      loadn<EB>(Bb + (int64_t)(n0 + n) * K, k0 + kc, kend, n0 + n < N, vec_b, rb);
     }
   };
   auto store_tiles = [&](int buf) {
     if (!TA) {
-      int m = tid >> 1, kc = (tid & 1) * 8;
+      constexpr int TPR = BK / EA;
+      int m = tid / TPR, kc = (tid % TPR) * EA;
 #pragma unroll
-      for (int q = 0; q < 8; q++) As[buf][kc + q][m] = ra[q];
+      for (int q = 0; q < EA; q++) As[buf][kc + q][m] = ra[q];
     } else {
-      int k = tid >> 4, mc = (tid & 15) * 8;
-      *(float4*)&As[buf][k][mc] = make_float4(ra[0], ra[1], ra[2], ra[3]);
-      *(float4*)&As[buf][k][mc + 4] = make_float4(ra[4], ra[5], ra[6], ra[7]);
+      constexpr int TPR = BM / EA;
+      int k = tid / TPR, mc = (tid % TPR) * EA;
+#pragma unroll
+      for (int q = 0; q < EA; q++) As[buf][k][mc + q] = ra[q];
     }
     if (!TB) {
-      int k = tid >> 4, nc = (tid & 15) * 8;
-      *(float4*)&Bs[buf][k][nc] = make_float4(rb[0], rb[1], rb[2], rb[3]);
-      *(float4*)&Bs[buf][k][nc + 4] = make_float4(rb[4], rb[5], rb[6], rb[7]);
-    } else {
-      int n = tid >> 1, kc = (tid & 1) * 8;
+      constexpr int TPR = BN / EB;
+      int k = tid / TPR, nc = (tid % TPR) * EB;
 #pragma unroll
-      for (int q = 0; q < 8; q++) Bs[buf][kc + q][n] = rb[q];
+      for (int q = 0; q < EB; q++) Bs[buf][k][nc + q] = rb[q];
+    } else {
+      constexpr int TPR = BK / EB;
+      int n = tid / TPR, kc = (tid % TPR) * EB;
+#pragma unroll
+      for (int q = 0; q < EB; q++) Bs[buf][kc + q][n] = rb[q];
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TN; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
@@ -115,14 +137,15 @@ __global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, 
     if (t + 1 < nk) load_tiles(kbeg + (t + 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 2) {
-      float a0 = As[buf][kk + lk][wm * 64 + lrow];
-      float a1 = As[buf][kk + lk][wm * 64 + 32 + lrow];
-      float b0 = Bs[buf][kk + lk][wn * 64 + lrow];
-      float b1 = Bs[buf][kk + lk][wn * 64 + 32 + lrow];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+      float av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) av[i] = As[buf][kk + lk][wm * WTM + i * 32 + lrow];
+#pragma unroll
+      for (int j = 0; j < TN; j++) bv[j] = Bs[buf][kk + lk][wn * WTN + j * 32 + lrow];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
     if (t + 1 < nk) store_tiles(buf ^ 1);
     __syncthreads();
@@ -130,13 +153,13 @@ __global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, 
   // Accumulator register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
   float* out = splits > 1 ? partial + ((uint64_t)b * splits + sp) * (uint64_t)M * N : C + (uint64_t)b * M * N;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TN; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        int col = n0 + wn * 64 + j * 32 + lrow;
+        int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        int col = n0 + wn * WTN + j * 32 + lrow;
         if (row < M && col < N) out[(uint64_t)row * N + col] = acc[i][j][r];
       }
 }
@@ -174,26 +197,52 @@ bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
   return dtype == RG_F32 && m >= 32 && n >= 32 && k >= 8 && m * n * k >= (1u << 18);
 }
 
-int split_count(uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
-  uint64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN) * batch;
+struct TileCfg {
+  int bm, bn;
+};
+
+// Block tile: the largest tile that still gives two blocks per CU (512) with little padding
+// waste; 32-wide tiles for 32-wide outputs (attention heads).
+TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t batch) {
+  static const TileCfg cands[] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}, {128, 32}, {32, 128}};
+  TileCfg best = {64, 64};
+  double best_score = -1;
+  for (auto c : cands) {
+    uint64_t tm = (m + c.bm - 1) / c.bm, tn = (n + c.bn - 1) / c.bn;
+    double waste = (double)(tm * c.bm * tn * c.bn) / (double)(m * n);
+    uint64_t blocks = tm * tn * batch;
+    // Prefer enough blocks, then low waste, then bigger tiles (more reuse per load).
+    double fill = std::min(1.0, (double)blocks / 512.0);
+    double score = fill / waste * (1.0 + 0.15 * (c.bm * c.bn) / (128.0 * 128.0));
+    if (score > best_score) {
+      best_score = score;
+      best = c;
+    }
+  }
+  return best;
+}
+
+int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
+  uint64_t tiles = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn) * batch;
   if (tiles >= 256 || k < 1024) return 1;
   uint64_t want = (512 + tiles - 1) / tiles;
-  uint64_t most = k / 256;
-  return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 32));
+  uint64_t most = k / 512;
+  return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 16));
 }
 
 }  // namespace
 
 uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
   if (!use_mfma(dtype, m, n, k)) return 0;
-  int s = split_count(m, n, k, batch);
+  int s = split_count(pick_tile(m, n, batch), m, n, k, batch);
   return s > 1 ? (uint64_t)s * batch * m * n * sizeof(float) : 0;
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m == 0 || g.n == 0 || g.batch == 0) return;
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
-    int splits = split_count(g.m, g.n, g.k, g.batch);
+    TileCfg t = pick_tile(g.m, g.n, g.batch);
+    int splits = split_count(t, g.m, g.n, g.k, g.batch);
     int kps = (int)(((g.k + splits - 1) / splits + BK - 1) / BK * BK);
     splits = (int)((g.k + kps - 1) / kps);
     auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -202,19 +251,29 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     // Vector loads run along K for A (untransposed) or M (transposed); likewise for B.
     bool vec_a = aligned(g.a) && offs_ok_a && ((g.ta ? g.m : g.k) % 4 == 0);
     bool vec_b = aligned(g.b) && offs_ok_b && ((g.tb ? g.k : g.n) % 4 == 0);
-    dim3 grid((uint32_t)((g.n + BN - 1) / BN), (uint32_t)((g.m + BM - 1) / BM), (uint32_t)(g.batch * splits));
+    dim3 grid((uint32_t)((g.n + t.bn - 1) / t.bn), (uint32_t)((g.m + t.bm - 1) / t.bm), (uint32_t)(g.batch * splits));
     float* part = splits > 1 ? (float*)g.workspace : nullptr;
     auto A = (const float*)g.a;
     auto B = (const float*)g.b;
     auto Cm = (float*)g.c;
     int M = (int)g.m, N = (int)g.n, K = (int)g.k;
-#define RG_GEMM(TA, TB)                                                                                                     \
-  hipLaunchKernelGGL((k_gemm_mfma<TA, TB>), grid, dim3(256), 0, s, A, B, Cm, M, N, K, g.a_off, g.b_off, g.a_stride, g.b_stride, \
-                     splits, kps, part, vec_a, vec_b)
-    if (!g.ta && !g.tb) RG_GEMM(false, false);
-    else if (g.ta && !g.tb) RG_GEMM(true, false);
-    else if (!g.ta && g.tb) RG_GEMM(false, true);
-    else RG_GEMM(true, true);
+#define RG_GEMM(BM_, BN_, WM_, WN_, TA_, TB_)                                                                                   \
+  hipLaunchKernelGGL((k_gemm_mfma<BM_, BN_, WM_, WN_, TA_, TB_>), grid, dim3(256), 0, s, A, B, Cm, M, N, K, g.a_off, g.b_off,  \
+                     g.a_stride, g.b_stride, splits, kps, part, vec_a, vec_b)
+#define RG_GEMM_FLAGS(BM_, BN_, WM_, WN_)                  \
+  do {                                                     \
+    if (!g.ta && !g.tb) RG_GEMM(BM_, BN_, WM_, WN_, false, false); \
+    else if (g.ta && !g.tb) RG_GEMM(BM_, BN_, WM_, WN_, true, false); \
+    else if (!g.ta && g.tb) RG_GEMM(BM_, BN_, WM_, WN_, false, true); \
+    else RG_GEMM(BM_, BN_, WM_, WN_, true, true);           \
+  } while (0)
+    if (t.bm == 128 && t.bn == 128) RG_GEMM_FLAGS(128, 128, 2, 2);
+    else if (t.bm == 128 && t.bn == 64) RG_GEMM_FLAGS(128, 64, 2, 2);
+    else if (t.bm == 64 && t.bn == 128) RG_GEMM_FLAGS(64, 128, 2, 2);
+    else if (t.bm == 64 && t.bn == 64) RG_GEMM_FLAGS(64, 64, 2, 2);
+    else if (t.bm == 128 && t.bn == 32) RG_GEMM_FLAGS(128, 32, 4, 1);
+    else RG_GEMM_FLAGS(32, 128, 1, 4);
+#undef RG_GEMM_FLAGS
 #undef RG_GEMM
     if (splits > 1) {
       uint64_t mn = g.m * g.n;

@@ -147,6 +147,21 @@ __global__ void __launch_bounds__(TPB) k_pad(const E* __restrict__ src, E* __res
   dst[i] = inside ? src[off] : (E)0;
 }
 
+__global__ void __launch_bounds__(TPB) k_pad4(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, uint32_t n, PadDims p) {
+  uint32_t i0 = (blockIdx.x * TPB + threadIdx.x) * 4;
+  if (i0 >= n) return;
+  uint32_t off = 0, rem = i0;
+  bool inside = true;
+  for (int d = p.rank - 1; d >= 0; d--) {
+    uint32_t q = p.size[d].div(rem);
+    uint32_t c = rem - q * p.size[d].d;
+    rem = q;
+    if (c < p.start[d] || c >= p.start[d] + p.len[d]) inside = false;
+    else off += (c - p.start[d]) * p.src_st[d];
+  }
+  *(uint4*)(dst + i0) = inside ? *(const uint4*)(src + off) : make_uint4(0, 0, 0, 0);
+}
+
 template <class E>
 __global__ void __launch_bounds__(TPB) k_concat_piece(const E* __restrict__ src, E* __restrict__ dst, uint32_t n, FastDiv len,
                                                       uint32_t total, uint32_t at) {
@@ -426,10 +441,10 @@ __global__ void __launch_bounds__(TPB) k_reduce_rows_block(int kind, const T* __
 // Leading-axis reduction of [batch, r, k] over r. A block owns 64 consecutive columns (one
 // coalesced 256-byte row segment per wave) and 4 row lanes; row chunks give parallelism and write
 // partial results, which a second pass of the same kernel combines (deterministic order).
-template <class T>
-__global__ void __launch_bounds__(TPB) k_reduce_cols(int kind, const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
-                                                      uint32_t chunk_rows, uint32_t chunks) {
-  __shared__ T part[4][64];
+template <class T, int LANES>
+__global__ void __launch_bounds__(64 * LANES) k_reduce_cols(int kind, const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
+                                                             uint32_t chunk_rows, uint32_t chunks) {
+  __shared__ T part[LANES][64];
   const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const uint32_t c = blockIdx.x * 64 + tx;
   const uint32_t b = blockIdx.y, s = blockIdx.z;
@@ -438,15 +453,14 @@ __global__ void __launch_bounds__(TPB) k_reduce_cols(int kind, const T* __restri
   if (c < k) {
     const T* x = a + (uint64_t)b * r * k + c;
 #pragma unroll 8
-    for (uint32_t row = r0 + ty; row < r1; row += 4) acc = combine(kind, acc, x[(uint64_t)row * k]);
+    for (uint32_t row = r0 + ty; row < r1; row += LANES) acc = combine(kind, acc, x[(uint64_t)row * k]);
   }
   part[ty][tx] = acc;
   __syncthreads();
   if (ty == 0 && c < k) {
     T v = part[0][tx];
-    v = combine(kind, v, part[1][tx]);
-    v = combine(kind, v, part[2][tx]);
-    v = combine(kind, v, part[3][tx]);
+#pragma unroll
+    for (int l = 1; l < LANES; l++) v = combine(kind, v, part[l][tx]);
     out[((uint64_t)b * chunks + s) * k + c] = v;
   }
 }
@@ -598,6 +612,13 @@ void pad(hipStream_t s, int esize, const void* src, void* dst, uint64_t n, const
     p.len[d] = (uint32_t)in_shape[d];
     p.src_st[d] = (uint32_t)st[d];
   }
+  size_t last = out_shape.size() - 1;
+  bool vec = esize == 4 && !out_shape.empty() && starts[last] == 0 && in_shape[last] == out_shape[last] && out_shape[last] % 4 == 0 &&
+             ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0;
+  if (vec) {
+    RG_LAUNCH(k_pad4, n / 4, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, p);
+    return;
+  }
   if (esize == 4) RG_LAUNCH(k_pad<uint32_t>, n, (const uint32_t*)src, (uint32_t*)dst, (uint32_t)n, p);
   else RG_LAUNCH(k_pad<uint64_t>, n, (const uint64_t*)src, (uint64_t*)dst, (uint32_t)n, p);
 }
@@ -695,11 +716,12 @@ void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
 }
 
 uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k) {
-  // Aim for >= 1024 blocks (4 per CU) with at least 32 rows per chunk.
+  // About 512 blocks in the first pass (2 per CU), at least 64 rows per chunk, and at most 256
+  // chunks so the combining pass stays one round of loads per thread.
   uint64_t col_blocks = (k + 63) / 64 * batch;
-  uint64_t want = (1024 + col_blocks - 1) / col_blocks;
-  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 32));
-  return std::min<uint64_t>(chunks, 65535);
+  uint64_t want = (512 + col_blocks - 1) / col_blocks;
+  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 64));
+  return std::min<uint64_t>(chunks, 256);
 }
 
 void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k, void* partial,
@@ -707,13 +729,13 @@ void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
   uint32_t chunk_rows = (uint32_t)((r + chunks - 1) / chunks);
   dim3 grid(blocks_for(k, 64), (uint32_t)batch, (uint32_t)chunks);
   void* out = chunks == 1 ? d : partial;
-  if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols<float>, grid, dim3(TPB), 0, s, kind, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
-  else hipLaunchKernelGGL(k_reduce_cols<double>, grid, dim3(TPB), 0, s, kind, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
+  if (dtype == RG_F32) hipLaunchKernelGGL((k_reduce_cols<float, 4>), grid, dim3(256), 0, s, kind, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
+  else hipLaunchKernelGGL((k_reduce_cols<double, 4>), grid, dim3(256), 0, s, kind, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
   if (chunks > 1) {
-    // The partials [batch, chunks, k] are themselves a leading-axis reduction.
+    // The partials [batch, chunks, k] are themselves a leading-axis reduction: 16 row lanes.
     dim3 g2(blocks_for(k, 64), (uint32_t)batch, 1);
-    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_cols<float>, g2, dim3(TPB), 0, s, kind, (const float*)partial, (float*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
-    else hipLaunchKernelGGL(k_reduce_cols<double>, g2, dim3(TPB), 0, s, kind, (const double*)partial, (double*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
+    if (dtype == RG_F32) hipLaunchKernelGGL((k_reduce_cols<float, 16>), g2, dim3(1024), 0, s, kind, (const float*)partial, (float*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
+    else hipLaunchKernelGGL((k_reduce_cols<double, 16>), g2, dim3(1024), 0, s, kind, (const double*)partial, (double*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
   }
 }
 

@@ -733,9 +733,11 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     table[1] = f->slot;
     for (int64_t k = 0; k < d->n_swaps; k++) std::swap(table[1][(size_t)d->swaps[2 * k]], table[1][(size_t)d->swaps[2 * k + 1]]);
     int n_graphs = d->n_swaps > 0 ? 2 : 1;
-    for (int g = 0; g < n_graphs; g++) {
+    // Everything one step enqueues under slot table g: batch loads, the plan, history records,
+    // the state copies (all sources read before any destination is written, validate.rs:349-355)
+    // and the step counter.
+    auto enqueue_step = [&](int g) {
       const std::vector<void*>& t = table[g];
-      HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));
       for (int64_t j = 0; j < (int64_t)batch_bufs.size(); j++)
         rgk::load_batch(f->stream, t[(size_t)d->data_slots[j]], batch_bufs[j], d->data_bytes[j], d->n_batches, counter);
       for (auto& st : p->steps) st(f->stream, t.data(), f->workspace);
@@ -743,7 +745,6 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
         int64_t s = d->history_slots[h];
         rgk::record_history(f->stream, p->plan.slots[(size_t)s].dtype, t[(size_t)s], hist + h * chunk, counter, chunk);
       }
-      // Copies read every source before writing any destination (validate.rs:349-355).
       for (int64_t c = 0; c < d->n_copies; c++) {
         int64_t os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
         rgk::copy_bytes(f->stream, temps[c], t[(size_t)os], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
@@ -754,6 +755,14 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
         rgk::copy_bytes(f->stream, next[(size_t)is], temps[c], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
       }
       rgk::counter_inc(f->stream, counter);
+    };
+    // Each slot table is captured once as a HIP graph and replayed; RG_HIP_GRAPHS=0 launches the
+    // same kernels directly instead (for tools that do not follow graph launches).
+    const char* env = getenv("RG_HIP_GRAPHS");
+    const bool use_graphs = !(env && env[0] == '0');
+    for (int g = 0; g < n_graphs && use_graphs; g++) {
+      HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));
+      enqueue_step(g);
       hipGraph_t graph;
       hipError_t ce = hipStreamEndCapture(f->stream, &graph);
       if (ce != hipSuccess) throw std::runtime_error("graph capture failed: " + err_str(ce));
@@ -762,6 +771,11 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       HIP_OK(hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0));
       execs.push_back(ge);
     }
+    auto launch = [&](int64_t k) -> hipError_t {
+      if (use_graphs) return hipGraphLaunch(execs[(size_t)(k % n_graphs)], f->stream);
+      enqueue_step((int)(k % n_graphs));
+      return hipGetLastError();
+    };
     HIP_OK(hipGetLastError());
     auto set_counter = [&](uint64_t v) {
       HIP_OK(hipStreamSynchronize(f->stream));
@@ -779,7 +793,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
           rgk::copy_bytes(f->stream, snap[q], table[parity0][(size_t)state_slots[q]], p->slot_bytes[(size_t)state_slots[q]]);
       }
       for (int64_t k = c0; k < c1; k++)
-        if (latch(e, hipGraphLaunch(execs[(size_t)(k % n_graphs)], f->stream), "graph launch")) break;
+        if (latch(e, launch(k), "step launch")) break;
       if (!e->failure.empty() || latch(e, hipStreamSynchronize(f->stream), "device execution")) {
         rc = -1;
         break;
@@ -798,7 +812,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
         for (size_t q = 0; q < state_slots.size(); q++)
           rgk::copy_bytes(f->stream, table[parity0][(size_t)state_slots[q]], snap[q], p->slot_bytes[(size_t)state_slots[q]]);
         set_counter((uint64_t)c0);
-        for (int64_t k = c0; k <= bad; k++) latch(e, hipGraphLaunch(execs[(size_t)(k % n_graphs)], f->stream), "graph launch");
+        for (int64_t k = c0; k <= bad; k++) latch(e, launch(k), "step launch");
         if (latch(e, hipStreamSynchronize(f->stream), "device execution")) {
           rc = -1;
           break;
