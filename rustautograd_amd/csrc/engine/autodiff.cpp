@@ -19,7 +19,7 @@ uint32_t reshape(Graph& g, uint32_t x, const Shape& s) {
 }
 
 // Sums `ct` back down to `target` after a broadcast (autodiff.rs:6-16).
-uint32_t unbroadcast(Graph& g, uint32_t ct, const Shape& target) {
+uint32_t unbroadcast(Graph& g, uint32_t ct, Shape target) {  // by value: adding nodes moves g.nodes
   Shape shape = g.shape(ct);
   if (shape == target) return ct;
   size_t lead = shape.size() - target.size();

@@ -253,6 +253,16 @@ PYBIND11_MODULE(_rg, m) {
                  d["dtype"] = dname(s.group.dtype);
                  d["inputs"] = s.group.input_shapes;
                  d["n_outputs"] = s.group.outputs.size();
+                 static const char* kinds[] = {"full", "splat", "row", "broadcast"};
+                 py::list in_kinds, in_slots, out_slots;
+                 for (auto& in : s.group.inputs) {
+                   in_kinds.append(kinds[in.kind]);
+                   in_slots.append(in.slot);
+                 }
+                 for (auto& o : s.group.outputs) out_slots.append(o.second);
+                 d["input_kinds"] = in_kinds;
+                 d["input_slots"] = in_slots;
+                 d["output_slots"] = out_slots;
                } else {
                  d["kind"] = "instr";
                  d["op"] = s.instr.op.name();
@@ -262,6 +272,8 @@ PYBIND11_MODULE(_rg, m) {
                  d["dtype"] = dname(s.instr.dtype);
                  d["shape"] = s.instr.shape;
                  d["arg_shapes"] = s.instr.arg_shapes;
+                 d["dst"] = s.instr.dst;
+                 d["args"] = s.instr.args;
                }
                out.append(d);
              }
@@ -390,6 +402,25 @@ PYBIND11_MODULE(_rg, m) {
     plan.serialize(&words, &blob);
     return py::make_tuple(words, py::bytes((const char*)blob.data(), blob.size()));
   });
+  m.def("matrix_search_products",
+        [](const PyGraph& graph, const std::vector<uint32_t>& outputs, bool device) -> py::object {
+          // The products (M, K, N) of the form the matrix search extracts, or None when it keeps
+          // the traced form (egraph.rs:405-426). Test hook: compile applies its own acceptance.
+          SearchStats st;
+          auto found = matrix_search(graph.g, outputs, device ? CostModel::Device : CostModel::Cpu, OptMode::SearchLinear, &st);
+          if (!found) return py::none();
+          const Graph& h = found->first;
+          std::vector<bool> keep = h.reachable(found->second);
+          py::list out;
+          for (size_t i = 0; i < h.nodes.size(); i++) {
+            const Node& n = h.nodes[i];
+            if (!keep[i] || n.op.kind != RG_OP_MATMUL) continue;
+            const Shape& a = h.shape(n.inputs[0]);
+            const Shape& b = h.shape(n.inputs[1]);
+            out.append(py::make_tuple(a[0], a[1], b[1]));
+          }
+          return std::move(out);
+        });
   m.def("register_backend", [](const std::string& name, const std::string& path, const std::string& prefix) {
     try {
       register_backend(name, path, prefix);

@@ -75,3 +75,52 @@ def agree(build, inputs, tol=2e-6, what="", ulps=None):
         else:
             close(a, b, tol, f"{what} output {k}")
     return hip, cpu
+
+
+class G:
+    """A graph under construction, in the vocabulary of the reference's tests/engine.rs:34-46."""
+
+    def __init__(self):
+        self.g = _rg.Graph()
+
+    def input(self, shape, dtype="float64"):
+        return self.g.input(list(shape), dtype)
+
+    def const(self, values, shape=None, dtype="float64"):
+        a = np.asarray(values, dtype=dtype)
+        if shape is not None:
+            a = a.reshape(shape)
+        return self.g.constant(rg.tensor(a)._t)
+
+    def scalar(self, v, dtype="float64"):
+        return self.const(v, (), dtype)
+
+    def op(self, name, ins, **attrs):
+        return self.g.op(name, list(ins), attrs or None)
+
+    def un(self, name, a, **attrs):
+        return self.op(name, [a], **attrs)
+
+    def bin(self, name, a, b):
+        return self.op(name, [a, b])
+
+    def sum_all(self, x):
+        return self.op("sum", [x], axes=list(range(len(self.shape(x)))), keepdims=False)
+
+    def grad(self, y, wrts):
+        return list(self.g.grad(y, list(wrts)))
+
+    def shape(self, x):
+        return tuple(self.g.shape(x))
+
+    def compile(self, outs, inputs, device="cpu", optimize="none", level="none"):
+        return _rg.compile(self.g, list(outs), [rg.tensor(np.asarray(x))._t for x in inputs], level, device, optimize)
+
+    def eval(self, outs, inputs=(), device="cpu", optimize="none"):
+        """Compiles `outs` for `device` (the CPU oracle by default) and returns them as numpy arrays."""
+        c = self.compile(outs, inputs, device, optimize)
+        return [rg.Tensor(r).numpy() for r in c.call([rg.tensor(np.asarray(x))._t for x in inputs])]
+
+
+def diag_code(excinfo):
+    return excinfo.value.diagnostic["code"]

@@ -1,0 +1,131 @@
+"""The drop-in boundary: the C ABI of include/rg_hip.h, checked without a GPU.
+
+librg_hip.so must load on a host without a device, export every entry point the header declares,
+report itself unavailable rather than crash, and compile a plan's fused kernels for gfx950
+through hiprtc (which needs no device). The CPU oracle implements the same ABI under the
+`rg_cpu_` prefix, which is what lets the engine drive either library.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import rustautograd_amd as rg
+from rustautograd_amd import _native, _rg, workloads
+from helpers import G
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rg_hip.h")
+PLAN_HEADER = os.path.join(ROOT, "include", "rg_plan.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(rg_hip_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_full_surface():
+    names = _declared()
+    for required in ("rg_hip_available", "rg_hip_program_new", "rg_hip_program_free", "rg_hip_exec_new", "rg_hip_exec_free",
+                     "rg_hip_exec_write", "rg_hip_exec_read", "rg_hip_exec_scalar", "rg_hip_exec_swap", "rg_hip_exec_step",
+                     "rg_hip_exec_failure", "rg_hip_exec_step_timed", "rg_hip_exec_breakdown", "rg_hip_exec_run",
+                     "rg_hip_program_allocated_bytes", "rg_hip_program_inject_failure"):
+        assert required in names
+
+
+def test_hip_library_loads_and_exports_every_declared_symbol():
+    assert os.path.exists(_native.HIP_LIBRARY), "librg_hip.so is not built"
+    lib = ctypes.CDLL(_native.HIP_LIBRARY)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"librg_hip.so lacks {missing}"
+
+
+# Entry points the engine binds as optional (backend.cpp), with a host-side fallback each: the
+# per-step timer, the JSON breakdown and the device-resident run loop (the oracle uses the
+# engine's host run loop, validate.rs:289-363), plus the HIP-only build check and memory query.
+OPTIONAL = {"rg_hip_exec_step_timed", "rg_hip_exec_breakdown", "rg_hip_exec_run", "rg_hip_compile_check", "rg_hip_device_memory_bytes"}
+
+
+def test_oracle_implements_the_same_abi():
+    from conftest import ORACLE
+    lib = ctypes.CDLL(ORACLE)
+    missing = [n for n in _declared() if n not in OPTIONAL and not hasattr(lib, n.replace("rg_hip_", "rg_cpu_"))]
+    assert not missing, f"oracle lacks {missing}"
+
+
+def test_plan_header_enums_are_dense():
+    """Op codes are a dense enum ending in RG_OP_COUNT, which the descriptor parser relies on."""
+    text = open(PLAN_HEADER).read()
+    body = re.search(r"enum rg_op\s*\{(.*?)\}", text, re.S).group(1)
+    names = [re.match(r"\s*(RG_OP_[A-Z0-9_]+)", part).group(1) for part in body.split(",") if part.strip()]
+    values = [int(v) for v in re.findall(r"=\s*(\d+)", body)]
+    assert names[0] == "RG_OP_INPUT" and values[0] == 0
+    assert names[-1] == "RG_OP_COUNT" and len(set(names)) == len(names)
+
+
+@pytest.mark.skipif(rg.devices().count("hip") > 0, reason="a device is present: the gpu tests cover it")
+def test_without_a_device_the_product_fails_loudly():
+    lib = ctypes.CDLL(_native.HIP_LIBRARY)
+    assert lib.rg_hip_available() == 0
+    assert _native.hip_error()
+    with pytest.raises(rg.DiagnosticError) as e:
+        rg.compile(lambda x: x * 2.0, (rg.tensor(np.ones(3, np.float32)),), device="hip")
+    d = e.value.diagnostic
+    assert d["code"] == "DEVICE_UNAVAILABLE" and d["observation"]["device"] == "hip"
+    assert "hip" not in rg.devices()
+
+
+def test_product_package_never_touches_the_oracle():
+    """Only tests/, smoke() and the bench's CPU baseline may use oracle/."""
+    pkg = os.path.join(ROOT, "rustautograd_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".h", ".hip")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text and "rg_cpu_" not in text, f"{f} references the oracle"
+
+
+def _compile_check(words):
+    lib = ctypes.CDLL(_native.HIP_LIBRARY)
+    f = lib.rg_hip_compile_check
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t]
+    arr = (ctypes.c_int64 * len(words))(*words)
+    err = ctypes.create_string_buffer(8192)
+    n = f(arr, len(words), err, len(err))
+    return n, err.value.decode()
+
+
+def test_fused_kernels_of_a_small_program_compile_for_gfx950():
+    """The generated HIP source of every fused group builds with hiprtc for gfx950."""
+    g = G()
+    x = g.input((64, 300), "float32")
+    b = g.input((300,), "float32")
+    h = g.un("tanh", g.bin("add", x, b))
+    y = g.sum_all(g.bin("mul", g.un("exp", h), h))
+    gx = g.grad(y, [x])[0]
+    words, _ = _rg.plan_words(g.g, [y, gx], "hip", "standard")
+    n, err = _compile_check(words)
+    assert n >= 1, err
+
+
+def test_c3_program_compiles_for_gfx950():
+    """Every fused kernel of a whole GPT training step (C3 at reduced depth) compiles."""
+    cfg = workloads.GPT_CONFIGS["C3"]._replace(batch=2, block=16, layers=1)
+    step, state = workloads.gpt_train_step(cfg)
+    from rustautograd_amd import _core
+    leaves, in_def = _core._as_tensors((state,))
+    g = _rg.Graph()
+    tracers = [_core.Tracer(g, g.input(list(t.shape), t.dtype, None)) for t in leaves]
+    _core._traces.append(g)
+    try:
+        out = step(*_core._unflatten(in_def, tracers))
+        ids = [_core._node(g, leaf, "float32") for leaf in _core._flatten(out)[0]]
+    finally:
+        _core._traces.pop()
+    words, _ = _rg.plan_words(g, ids, "hip", "search-linear")
+    n, err = _compile_check(words)
+    assert n >= 10, err

@@ -1,0 +1,213 @@
+"""Random graphs: every plan flavour agrees with torch float64 on values and gradients.
+
+Restates the reference's fuzz tests (tests/engine.rs:225-316 random_graphs_agree_across_plans,
+:364-437 fused_plans_agree_with_reference_on_random_graphs). Each case builds the same random
+program twice: in the engine and in torch (float64, autograd), which is the independent oracle.
+The engine's program is then planned four ways and executed on the CPU oracle:
+
+  cpu / none       : the CPU plan, no rewrites (the reference interpreter's order)
+  cpu / standard   : simplification, CSE, transposed-product flags, buffer reuse
+  devplan / standard: the HIP planner's plan (device rewrites, level order, device fusion,
+                      absorbed broadcasts) run on the CPU oracle
+  devplan / search : the same after matrix-product reassociation
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import rustautograd_amd as rg
+from helpers import G
+
+from conftest import DEVPLAN
+
+
+class XorShift:
+    """The reference tests' generator (tests/engine.rs:18-32)."""
+
+    def __init__(self, seed):
+        self.s = seed & 0xFFFFFFFFFFFFFFFF
+
+    def next(self):
+        s = self.s
+        s ^= (s << 13) & 0xFFFFFFFFFFFFFFFF
+        s ^= s >> 7
+        s ^= (s << 17) & 0xFFFFFFFFFFFFFFFF
+        self.s = s
+        return s
+
+    def below(self, n):
+        return self.next() % n
+
+    def unit(self):
+        return (self.next() % 1_000_000) / 1_000_000.0
+
+
+def _max(a, b):
+    # rg's maximum: a if a > b, else b if b >= a, else NaN; ties send the gradient to a.
+    return torch.where(a >= b, a, b)
+
+
+class Twin:
+    """Builds one random program in the engine and in torch side by side."""
+
+    def __init__(self):
+        self.g = G()
+        self.ids, self.ts = [], []
+
+    def add_input(self, shape, values):
+        self.ids.append(self.g.input(shape))
+        t = torch.tensor(np.asarray(values, dtype=np.float64).reshape(shape), requires_grad=True)
+        self.ts.append(t)
+        return len(self.ids) - 1
+
+    def push(self, make_id, make_t):
+        try:
+            i = make_id()
+        except rg.DiagnosticError:
+            return None
+        self.ids.append(i)
+        self.ts.append(make_t())
+        return len(self.ids) - 1
+
+
+def _apply(tw, r, k, a, b, op_id):
+    g, ids, ts = tw.g, tw.ids, tw.ts
+    ia, ib, ta, tb = ids[a], ids[b], ts[a], ts[b]
+    sa = g.shape(ia)
+    if op_id == 0:
+        return tw.push(lambda: g.bin("add", ia, ib), lambda: ta + tb)
+    if op_id == 1:
+        return tw.push(lambda: g.bin("sub", ia, ib), lambda: ta - tb)
+    if op_id == 2:
+        return tw.push(lambda: g.bin("mul", ia, ib), lambda: ta * tb)
+    if op_id == 3:
+        return tw.push(lambda: g.bin("div", ia, ib), lambda: ta / tb)
+    if op_id == 4:
+        return tw.push(lambda: g.bin("maximum", ia, ib), lambda: _max(ta, tb))
+    if op_id == 5:
+        return tw.push(lambda: g.un("neg", ia), lambda: -ta)
+    if op_id == 6:
+        return tw.push(lambda: g.un("tanh", ia), lambda: torch.tanh(ta))
+    if op_id == 7:
+        return tw.push(lambda: g.un("abs", ia), lambda: torch.abs(ta))
+    if op_id == 8:
+        return tw.push(lambda: g.un("sin", ia), lambda: torch.sin(ta))
+    if op_id == 9:
+        n = int(np.prod(sa)) if sa else 1
+        return tw.push(lambda: g.un("reshape", ia, shape=[n]), lambda: ta.reshape(n))
+    if op_id == 10:
+        return tw.push(lambda: g.un("stop_gradient", ia), lambda: ta.detach())
+    if op_id == 11:
+        perm = list(range(len(sa)))[::-1]
+        return tw.push(lambda: g.un("transpose", ia, perm=perm), lambda: ta.permute(*perm) if perm else ta)
+    if op_id == 12:
+        axes = [d for d in range(len(sa)) if r.next() % 2 == 0]
+        keep = r.next() % 2 == 0
+        return tw.push(lambda: g.op("sum", [ia], axes=axes, keepdims=keep),
+                       lambda: ta.sum(dim=axes, keepdim=keep) if axes else ta)
+    if op_id == 13:
+        return tw.push(lambda: g.bin("matmul", ia, ib), lambda: torch.matmul(ta, tb))
+    if op_id == 14:
+        try:
+            c = g.bin("gt", ia, ib)
+        except rg.DiagnosticError:
+            return None
+        return tw.push(lambda: g.op("where", [c, ia, ib]), lambda: torch.where(ta > tb, ta, tb))
+    if op_id == 15:
+        v = [0.0, 1.0, 2.0, 0.5][r.below(4)]
+        return tw.push(lambda: g.bin("add", ia, g.scalar(v)), lambda: ta + v)
+    if op_id == 16:
+        v = [1.0, 2.0, 0.5][r.below(3)]
+        return tw.push(lambda: g.bin("mul", ia, g.scalar(v)), lambda: ta * v)
+    if op_id == 17:
+        return tw.push(lambda: g.op("slice", [ia], starts=[0] * len(sa), stops=list(sa)), lambda: ta[tuple(slice(0, d) for d in sa)])
+    if op_id == 18:
+        return tw.push(lambda: g.un("exp", ia), lambda: torch.exp(ta))
+    if op_id == 19:
+        return tw.push(lambda: g.un("sqrt", ia), lambda: torch.sqrt(ta))
+    raise AssertionError(op_id)
+
+
+FLAVOURS = [("cpu", "none"), ("cpu", "standard"), (DEVPLAN, "standard"), (DEVPLAN, "search-linear")]
+
+
+def _check_case(tw, outs, inputs, what):
+    g = tw.g
+    out_ids = [tw.ids[k] for k in outs]
+    # The torch side: values, and the gradient of sum(last value) with respect to the first input.
+    want = [tw.ts[k].detach().numpy() for k in outs]
+    y = tw.ts[-1].sum()
+    x0 = tw.ts[0]
+    if y.requires_grad:
+        (gw,) = torch.autograd.grad(y, [x0], allow_unused=True)
+    else:
+        gw = None
+    gw = np.zeros(x0.shape) if gw is None else gw.numpy()
+    y_id = g.sum_all(tw.ids[-1])
+    grad_id = g.grad(y_id, [tw.ids[0]])[0]
+    want.append(gw)
+    for device, mode in FLAVOURS:
+        got = g.eval(out_ids + [grad_id], inputs, device=device, optimize=mode)
+        for k, (w, v) in enumerate(zip(want, got)):
+            assert w.shape == v.shape, f"{what} {device}/{mode} output {k}: shape {v.shape} vs torch {w.shape}"
+            with np.errstate(invalid="ignore"):
+                ok = (w == v) | (np.abs(w - v) <= 1e-9 * np.maximum(np.abs(w), 1.0)) | (np.isnan(w) & np.isnan(v))
+            assert ok.all(), f"{what} {device}/{mode} output {k}: {v.ravel()[np.argmin(ok.ravel())]} vs torch {w.ravel()[np.argmin(ok.ravel())]}"
+
+
+@pytest.mark.parametrize("chunk", range(4))
+def test_random_graphs_agree_across_plans(chunk):
+    """Small shapes, 18 operations (engine.rs:225-316); 100 cases per chunk."""
+    r = XorShift(0x123456789ABCDEF1 + chunk)
+    for case in range(100):
+        tw = Twin()
+        da, db = 1 + r.below(4), 1 + r.below(4)
+        pool = [(), (1,), (da,), (db,), (da, db), (1, db), (da, 1)]
+        inputs = []
+        for _ in range(1 + r.below(3)):
+            s = pool[r.below(len(pool))]
+            v = 0.2 + np.array([r.unit() for _ in range(int(np.prod(s)) if s else 1)])
+            tw.add_input(s, v)
+            inputs.append(v.reshape(s))
+        for _ in range(1 + r.below(30)):
+            a, b = r.below(len(tw.ids)), r.below(len(tw.ids))
+            _apply(tw, r, case, a, b, r.below(18))
+        outs = [r.below(len(tw.ids)) for _ in range(1 + r.below(3))]
+        _check_case(tw, outs, inputs, f"chunk {chunk} case {case}")
+
+
+@pytest.mark.parametrize("chunk", range(3))
+def test_fused_plans_agree_on_random_graphs(chunk):
+    """Shapes crossing block, task and vector-width boundaries, long fusable chains (engine.rs:364-437)."""
+    r = XorShift(0xDEADBEEF0BADF00D + chunk)
+    groups = rows = 0
+    ops = [0, 1, 2, 3, 4, 6, 18, 7, 19, 8, 10, 9, 12, 14]
+    for case in range(40):
+        tw = Twin()
+        da, db = [1, 3, 40, 300][r.below(4)], [1, 7, 257, 600][r.below(4)]
+        pool = [(), (db,), (da, db), (1, db), (da, 1)]
+        inputs = []
+        for s in [(da, db), pool[r.below(5)], pool[r.below(5)]]:
+            v = 0.2 + np.array([r.unit() for _ in range(int(np.prod(s)) if s else 1)])
+            tw.add_input(s, v)
+            inputs.append(v.reshape(s))
+        for _ in range(2 + r.below(25)):
+            n = len(tw.ids)
+            a = n - 1 - r.below(min(n, 4))
+            b = r.below(n)
+            op_id = ops[r.below(len(ops))]
+            if op_id == 12:
+                sa = tw.g.shape(tw.ids[a])
+                axes = [d for d in range(len(sa)) if r.next() % 2 == 0]
+                ia, ta = tw.ids[a], tw.ts[a]
+                tw.push(lambda: tw.g.op("sum", [ia], axes=axes, keepdims=True), lambda: ta.sum(dim=axes, keepdim=True) if axes else ta)
+            else:
+                _apply(tw, r, case, a, b, op_id)
+        outs = [r.below(len(tw.ids)) for _ in range(2)]
+        _check_case(tw, outs, inputs, f"chunk {chunk} case {case}")
+        plan = tw.g.compile([tw.ids[k] for k in outs], inputs, device=DEVPLAN, optimize="standard").plan_summary()
+        fused = [s for s in plan if s["kind"] == "fused"]
+        groups += len(fused)
+        rows += sum(k == "row" for s in fused for k in s["input_kinds"])
+    assert groups > 20, f"the fuzz must exercise fusion: {groups} groups, {rows} row inputs"
