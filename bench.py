@@ -6,8 +6,8 @@ One step is one full AdamW training step of the C4 program (B=32, T=256, d=256, 
 vocab 96, fp32): ids drawn in the step from the state key, forward, backward, update. The timed
 region is `rg.run(compiled, state, steps=K)`: the device-resident step loop, synchronized on
 both sides. Prints one JSON line with the throughput, the roofline of the dominant kernel class
-(per-step device times from HIP events on the execution stream), and the CPU oracle's time for
-one step of the same program on this host as the baseline.
+(device time of each class's plan steps replayed back to back between HIP events on the execution
+stream), and the CPU oracle's time for one step of the same program on this host as the baseline.
 """
 
 import argparse
@@ -31,47 +31,83 @@ def _numel(s):
     return n
 
 
-def classify(plan, seconds):
-    """Groups plan steps into kernel classes with their algorithmic work and device time."""
+def classify(plan):
+    """Groups plan steps into kernel classes with their algorithmic work (flops for products,
+    bytes for everything else, as defined for the roofline) and the step indices of each."""
     classes = {}
 
-    def add(name, t, flops=0.0, nbytes=0.0):
-        c = classes.setdefault(name, {"seconds": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0})
-        c["seconds"] += t
+    def add(name, k, flops=0.0, nbytes=0.0):
+        c = classes.setdefault(name, {"steps": [], "flops": 0.0, "bytes": 0.0, "launches": 0})
+        c["steps"].append(k)
         c["flops"] += flops
         c["bytes"] += nbytes
         c["launches"] += 1
 
-    for st, t in zip(plan, seconds):
+    for k, st in enumerate(plan):
         ds = 8 if st["dtype"] == "float64" else 4
         if st["kind"] == "fused":
             n = st["n"]
-            add("fused_elementwise", t, nbytes=sum(_numel(s) for s in st["inputs"]) * ds + n * st["n_outputs"] * ds)
+            add("fused_elementwise", k, nbytes=sum(_numel(s) for s in st["inputs"]) * ds + n * st["n_outputs"] * ds)
             continue
         op, shape, args = st["op"], st["shape"], st["arg_shapes"]
         if op in ("matmul", "matmul_t"):
             a = args[0]
-            k = a[-1] if len(a) >= 1 and not st["ta"] else (a[-2] if len(a) >= 2 else a[0])
-            flops = 2.0 * _numel(shape) * k
+            kd = a[-1] if len(a) >= 1 and not st["ta"] else (a[-2] if len(a) >= 2 else a[0])
+            flops = 2.0 * _numel(shape) * kd
             m_rows = _numel(shape) // (shape[-1] if shape else 1)
             mfma = st["dtype"] == "float32" and len(shape) >= 2 and shape[-1] >= 32 and m_rows >= 32
-            add("gemm_mfma" if mfma else "gemm_plain", t, flops=flops, nbytes=(sum(_numel(s) for s in args) + _numel(shape)) * ds)
+            add("gemm_mfma" if mfma else "gemm_plain", k, flops=flops, nbytes=(sum(_numel(s) for s in args) + _numel(shape)) * ds)
         elif op in ("sum", "max", "min"):
-            add("reduce", t, nbytes=(_numel(args[0]) + st["n"]) * ds)
+            add("reduce", k, nbytes=(_numel(args[0]) + st["n"]) * ds)
         elif op in ("take", "take_along"):
-            add("gather_scatter", t, nbytes=_numel(args[1]) * 4 + 2 * st["n"] * ds)
+            add("gather_scatter", k, nbytes=_numel(args[1]) * 4 + 2 * st["n"] * ds)
         elif op in ("take_grad", "take_along_grad"):
-            add("gather_scatter", t, nbytes=(_numel(args[0]) + st["n"]) * ds + _numel(args[1]) * 4)
+            add("gather_scatter", k, nbytes=(_numel(args[0]) + st["n"]) * ds + _numel(args[1]) * 4)
         else:
-            add("structural_other", t, nbytes=(sum(_numel(s) for s in args) + st["n"]) * ds)
-    for c in classes.values():
-        if c["flops"]:
-            c["achieved"] = c["flops"] / c["seconds"] / 1e12 if c["seconds"] else 0.0
-            c["unit"] = "TFLOP/s"
-        else:
-            c["achieved"] = c["bytes"] / c["seconds"] / 1e9 if c["seconds"] else 0.0
-            c["unit"] = "GB/s"
+            add("structural_other", k, nbytes=(sum(_numel(s) for s in args) + st["n"]) * ds)
     return classes
+
+
+def time_classes(compiled, inputs, classes, repeats):
+    """Device seconds per step of each class: its steps run back to back `repeats` times between
+    two HIP events on the execution stream (rg_hip_exec_time_steps)."""
+    for c in classes.values():
+        c["seconds"] = compiled._n.time_steps(inputs, c["steps"], repeats) / repeats
+        if c["flops"]:
+            c["achieved"], c["unit"] = c["flops"] / c["seconds"] / 1e12, "TFLOP/s"
+        else:
+            c["achieved"], c["unit"] = c["bytes"] / c["seconds"] / 1e9, "GB/s"
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_hbm_traffic.txt")
+
+
+def measured_traffic(kernel_class):
+    """HBM bytes per launch of `kernel_class`, from the counter summary committed under profiles/
+    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script, scaled by the copy-kernel
+    calibration recorded in the same file), or None when no measurement exists."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel_class:
+                    return int(float(parts[2]))
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe(rg):
+    """A plain copy kernel of known size, for calibrating the FETCH_SIZE/WRITE_SIZE counters:
+    y = -x over 64 Mi fp32 elements (256 MiB read, 256 MiB written per launch), 10 launches."""
+    import numpy as np
+    n = 64 << 20
+    x = rg.tensor(np.ones(n, np.float32))
+    c = rg.compile(lambda x: -x, (x,), validate="none", device="hip")
+    for _ in range(10):
+        c(x)
+    print(json.dumps({"probe": "copy", "elements": n, "bytes_read_per_launch": 4 * n, "bytes_written_per_launch": 4 * n,
+                      "launches": 10}), flush=True)
 
 
 def cpu_baseline(cfg, steps=1):
@@ -97,6 +133,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="C4", choices=["C3", "C4"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--timing-reps", type=int, default=5, help="per-step HIP-event timing passes after the timed run (0: skip)")
+    ap.add_argument("--probe", choices=["copy"], help="run only a plain copy kernel of known size (for counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
@@ -106,6 +144,9 @@ def main():
     from rustautograd_amd import _native, workloads
     if "hip" not in rg.devices():
         raise SystemExit(f"HIP backend unavailable: {_native.hip_error()}")
+    if args.probe == "copy":
+        copy_probe(rg)
+        return
     cfg = workloads.GPT_CONFIGS[args.workload]
     step, state = workloads.gpt_train_step(cfg)
     t0 = time.perf_counter()
@@ -124,24 +165,32 @@ def main():
     print(f"# {args.steps} steps in {wall:.3f}s (device loop {res.elapsed:.3f}s), loss {res.history['aux'][0]:.4f} -> "
           f"{res.history['aux'][-1]:.4f}", file=sys.stderr, flush=True)
 
-    # Per-step device times (HIP events around each plan step on the execution stream).
-    from rustautograd_amd._core import _flatten
-    inputs = [rg.tensor(x)._t for x in _flatten((res.state,))[0]]
-    reps = 3
-    seconds = [s / reps for s in compiled._n.step_times(inputs, reps)]
-    classes = classify(compiled.plan_summary(), seconds)
-    dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])
-    if dom["unit"] == "TFLOP/s":
-        roof = {"bound": "mfma", "achieved": round(dom["achieved"], 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(dom["achieved"] / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}
-    else:
-        roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": None}
-    roof["kernel"] = dom_name
-    kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
-                   "unit": v["unit"],
-                   "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4)}
-               for k, v in sorted(classes.items(), key=lambda kv: -kv[1]["seconds"])}
+    # Per-class device times: each class's plan steps replayed back to back between two HIP
+    # events on the execution stream, after one full step has filled every slot.
+    roof, kernels, total_s = None, None, None
+    if args.timing_reps > 0:
+        from rustautograd_amd._core import _flatten
+        inputs = [rg.tensor(x)._t for x in _flatten((res.state,))[0]]
+        classes = classify(compiled.plan_summary())
+        time_classes(compiled, inputs, classes, 1)
+        time_classes(compiled, inputs, classes, args.timing_reps)
+        total_s = sum(c["seconds"] for c in classes.values())
+        dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])
+        per_launch = (dom["flops"] or dom["bytes"]) / dom["launches"]
+        avg_s = dom["seconds"] / dom["launches"]
+        if dom["unit"] == "TFLOP/s":
+            roof = {"bound": "mfma", "achieved": round(dom["achieved"], 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(dom["achieved"] / FP32_MFMA_PEAK_TFLOPS, 4)}
+        else:
+            roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4)}
+        roof["traffic"] = measured_traffic(dom_name)
+        roof.update({"kernel": dom_name, "launches_per_step": dom["launches"], "algorithmic_per_launch": round(per_launch),
+                     "avg_launch_us": round(avg_s * 1e6, 2)})
+        kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
+                       "unit": v["unit"],
+                       "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4)}
+                   for k, v in sorted(classes.items(), key=lambda kv: -kv[1]["seconds"])}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
     out = {
@@ -162,7 +211,7 @@ def main():
                    "gemm_gflop_per_step": round(workloads.gpt_gemm_flops(cfg) / 1e9, 2)},
         "roofline": roof,
         "kernels": kernels,
-        "device_ms_per_step": round(sum(seconds) * 1e3, 3),
+        "device_ms_per_step": round(total_s * 1e3, 3) if total_s else None,
         "cpu_baseline": cpu,
     }
     if cpu:

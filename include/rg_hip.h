@@ -93,6 +93,11 @@ int rg_hip_exec_failure(void* exec, char* buf, size_t len);
 int rg_hip_exec_step_timed(void* exec, double* seconds);
 /* metal.rs:700-713 `breakdown`: whole steps, and where the time went, as JSON. */
 int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len);
+/* Measurement helper next to `step_timed` (metal.rs:690-698), with no reference counterpart:
+ * runs the listed plan steps back to back, `repeats` times, between two HIP events on the
+ * execution stream, and stores the elapsed seconds. Gives a kernel class's average launch
+ * duration without per-step event overhead. Slot contents afterwards are unspecified. */
+int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, int64_t repeats, double* seconds);
 /* The device-resident `run_loop` (validate.rs:289-363): steps captured in HIP graphs and
  * replayed, batches and history kept on the device, state handed off by buffer swaps and
  * copies. Semantics equal the host loop: a non-finite history value stops the run after that

@@ -48,6 +48,7 @@ void register_backend(const std::string& name, const std::string& path, const st
   bind(*b, b->exec_failure, "exec_failure", true);
   bind(*b, b->exec_step_timed, "exec_step_timed", false);
   bind(*b, b->exec_breakdown, "exec_breakdown", false);
+  bind(*b, b->exec_time_steps, "exec_time_steps", false);
   bind(*b, b->exec_run, "exec_run", false);
   g_backends.push_back(std::move(b));
 }

@@ -34,6 +34,7 @@ struct Backend {
   int (*exec_failure)(void*, char*, size_t) = nullptr;
   int (*exec_step_timed)(void*, double*) = nullptr;  // optional
   int (*exec_breakdown)(void*, int64_t, char*, size_t) = nullptr;  // optional
+  int (*exec_time_steps)(void*, const int64_t*, int64_t, int64_t, double*) = nullptr;  // optional
   int (*exec_run)(void*, const rg_run_desc*, rg_run_result*) = nullptr;  // optional
 };
 

@@ -303,6 +303,25 @@ PYBIND11_MODULE(_rg, m) {
              if (auto f = e->failure()) raise_diag(device_failure(b->name, *f));
              return seconds;
            })
+      .def("time_steps",
+           [](const PyCompiled& c, const std::vector<PyTensor>& inputs, const std::vector<int64_t>& steps, size_t repeats) {
+             // Device seconds of `repeats` back-to-back passes over the listed plan steps, after
+             // one full step has filled every slot (rg_hip_exec_time_steps).
+             Backend* b = c.c->device;
+             if (!b->exec_time_steps) throw py::value_error("device " + b->name + " has no exec_time_steps");
+             auto in = tensors(inputs);
+             c.c->check_inputs(in);
+             double seconds = 0.0;
+             {
+               py::gil_scoped_release nogil;
+               auto e = c.c->program->exec();
+               for (size_t k = 0; k < in.size(); k++) e->load(k, in[k]);
+               e->steps(0, c.c->plan.steps.size());
+               b->exec_time_steps(e->handle(), steps.data(), (int64_t)steps.size(), (int64_t)repeats, &seconds);
+               if (auto f = e->failure()) raise_diag(device_failure(b->name, *f));
+             }
+             return seconds;
+           })
       .def("call",
            [](const PyCompiled& c, const std::vector<PyTensor>& inputs) {
              auto in = tensors(inputs);

@@ -503,6 +503,13 @@ __global__ void __launch_bounds__(TPB) k_load_batch(uint32_t* __restrict__ dst, 
 
 __global__ void k_counter_inc(uint64_t* counter) { *counter += 1; }
 
+// One thread waits until `ticks` of the constant-rate wall clock have passed: a bounded wait
+// that every launch leaves, used to hold a stream while the host enqueues timed work.
+__global__ void k_hold(uint64_t ticks) {
+  uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
 __global__ void __launch_bounds__(TPB) k_fill_zero(uint32_t* dst, uint64_t words) {
   uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x;
   if (i < words) dst[i] = 0;
@@ -760,6 +767,17 @@ void load_batch(hipStream_t s, void* dst, const void* batches, uint64_t bytes, u
 }
 
 void counter_inc(hipStream_t s, uint64_t* counter) { hipLaunchKernelGGL(k_counter_inc, dim3(1), dim3(1), 0, s, counter); }
+
+void hold_stream(hipStream_t s, double microseconds) {
+  static uint64_t khz = [] {
+    int dev = 0, rate = 0;
+    hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, dev) != hipSuccess || rate <= 0) rate = 100000;
+    return (uint64_t)rate;
+  }();
+  uint64_t ticks = (uint64_t)(microseconds * (double)khz / 1000.0);
+  hipLaunchKernelGGL(k_hold, dim3(1), dim3(1), 0, s, ticks);
+}
 
 void fill_zero(hipStream_t s, void* dst, uint64_t bytes) {
   uint64_t words = bytes / 4;

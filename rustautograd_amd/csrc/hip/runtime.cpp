@@ -630,17 +630,54 @@ int rg_hip_exec_failure(void* exec, char* buf, size_t len) {
 int rg_hip_exec_step_timed(void* exec, double* seconds) {
   auto* e = (Exec*)exec;
   Frame* f = e->frame;
+  size_t n = e->prog->steps.size();
+  std::vector<hipEvent_t> ev(n + 1);
+  for (auto& x : ev) hipEventCreate(&x);
+  // The stream is held while every step and an event after each are enqueued, so the device
+  // runs the steps back to back: the interval between consecutive events is then the step's
+  // device time rather than host launch latency (metal.rs:690-698 times one command buffer per
+  // step instead).
+  rgk::hold_stream(f->stream, 3000.0 + 15.0 * (double)n);
+  hipEventRecord(ev[0], f->stream);
+  for (size_t k = 0; k < n; k++) {
+    e->prog->steps[k](f->stream, f->slot.data(), f->workspace);
+    hipEventRecord(ev[k + 1], f->stream);
+  }
+  if (!latch(e, hipEventSynchronize(ev[n]), "timed step")) {
+    for (size_t k = 0; k < n; k++) {
+      float ms = 0;
+      hipEventElapsedTime(&ms, ev[k], ev[k + 1]);
+      seconds[k] += ms * 1e-3;
+    }
+  }
+  for (auto& x : ev) hipEventDestroy(x);
+  return e->failure.empty() ? 0 : -1;
+}
+
+int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, int64_t repeats, double* seconds) {
+  auto* e = (Exec*)exec;
+  Frame* f = e->frame;
+  *seconds = 0.0;
+  int64_t total = (int64_t)e->prog->steps.size();
+  for (int64_t k = 0; k < n_steps; k++)
+    if (steps[k] < 0 || steps[k] >= total) {
+      latch(e, hipErrorInvalidValue, "time_steps: step index out of range");
+      return -1;
+    }
+  if (n_steps == 0 || repeats <= 0) return 0;
   hipEvent_t a, b;
   hipEventCreate(&a);
   hipEventCreate(&b);
-  for (size_t k = 0; k < e->prog->steps.size() && e->failure.empty(); k++) {
-    hipEventRecord(a, f->stream);
-    e->prog->steps[k](f->stream, f->slot.data(), f->workspace);
-    hipEventRecord(b, f->stream);
-    if (latch(e, hipEventSynchronize(b), "timed step")) break;
+  // Hold the stream while the launches are enqueued, so the device never waits on the host.
+  rgk::hold_stream(f->stream, 2000.0 + 4.0 * (double)(n_steps * repeats));
+  hipEventRecord(a, f->stream);
+  for (int64_t r = 0; r < repeats; r++)
+    for (int64_t k = 0; k < n_steps; k++) e->prog->steps[steps[k]](f->stream, f->slot.data(), f->workspace);
+  hipEventRecord(b, f->stream);
+  if (!latch(e, hipEventSynchronize(b), "time_steps")) {
     float ms = 0;
     hipEventElapsedTime(&ms, a, b);
-    seconds[k] += ms * 1e-3;
+    *seconds = ms * 1e-3;
   }
   hipEventDestroy(a);
   hipEventDestroy(b);
