@@ -38,6 +38,8 @@ constexpr size_t PARALLEL_SUM = 1 << 20;
 constexpr size_t PARALLEL_MINMAX = 1 << 16;
 constexpr size_t REDUCE_ROWS = 64;
 constexpr size_t PARALLEL_FLOPS = 2000000;
+// Row-parallel 2-D products (rg_cpu_set_row_parallel_gemm); the reference runs them serially.
+bool g_row_parallel_gemm = false;
 constexpr uint64_t GAMMA = 0x9E3779B97F4A7C15ull;
 constexpr uint64_t GAMMA_SPLIT = 0xD1B54A32D192ED03ull;
 
@@ -361,7 +363,20 @@ void matmul(const Instr& i, std::vector<Buf>& s, bool ta, bool tb) {
   if (i.n == 0) return;
   if (bb.empty() && !ta) {
     // Row-major batches of the left operand are one big matrix: a single gemm call.
-    gemm<T>(prod(ba) * m, k, n, a, false, b, tb, dst);
+    size_t rows = prod(ba) * m;
+    if (g_row_parallel_gemm && rows * k * n >= PARALLEL_FLOPS && rows >= 128) {
+      // Checker-only speed-up (off by default, so the CPU baseline stays the reference's serial
+      // loop): blocks of rows on separate threads. Every element keeps its p-ascending sum, so
+      // results are bit-identical to the serial call.
+      size_t blocks = (rows + 63) / 64;
+#pragma omp parallel for schedule(static)
+      for (size_t q = 0; q < blocks; q++) {
+        size_t r0 = q * 64, r1 = std::min(rows, r0 + 64);
+        gemm<T>(r1 - r0, k, n, a + r0 * k, false, b, tb, dst + r0 * n);
+      }
+      return;
+    }
+    gemm<T>(rows, k, n, a, false, b, tb, dst);
     return;
   }
   size_t r = std::max(ba.size(), bb.size());
@@ -917,5 +932,6 @@ int rg_cpu_exec_step_timed(void* exec, double* seconds) {
 
 int rg_cpu_threads(void) { return omp_get_max_threads(); }
 void rg_cpu_set_threads(int n) { omp_set_num_threads(n); }
+void rg_cpu_set_row_parallel_gemm(int on) { g_row_parallel_gemm = on != 0; }
 
 }  // extern "C"

@@ -10,6 +10,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 import rustautograd_amd as rg
 from helpers import G, diag_code
@@ -528,3 +529,45 @@ def test_exact_rules_never_change_a_bit_on_special_values():
         got = g.eval(outs, [a, b], optimize=mode)
         for u, v in zip(want, got):
             assert np.array_equal(u.view(np.int64), v.view(np.int64)) or np.array_equal(u, v, equal_nan=True)
+
+
+def test_row_parallel_checker_gemm_is_bit_identical_to_the_serial_loop():
+    """The oracle's optional row split of 2-D products keeps every element's summation order."""
+    import ctypes
+    from conftest import ORACLE
+    lib = ctypes.CDLL(ORACLE)
+    r = np.random.default_rng(1)
+    a = r.normal(size=(3, 300, 256)).astype(np.float32)
+    b = r.normal(size=(256, 200)).astype(np.float32)
+    g = G()
+    x, w = g.input(a.shape, "float32"), g.input(b.shape, "float32")
+    c = g.compile([g.bin("matmul", x, w)], [a, b])
+    args = [rg.tensor(a)._t, rg.tensor(b)._t]
+    try:
+        lib.rg_cpu_set_row_parallel_gemm(0)
+        serial = rg.Tensor(c.call(args)[0]).numpy()
+        lib.rg_cpu_set_row_parallel_gemm(1)
+        parallel = rg.Tensor(c.call(args)[0]).numpy()
+    finally:
+        lib.rg_cpu_set_row_parallel_gemm(1)
+    assert np.array_equal(serial.view(np.int32), parallel.view(np.int32))
+    np.testing.assert_allclose(serial, a.astype(np.float64) @ b, rtol=1e-4, atol=1e-4)
+
+
+def test_where_with_broadcast_operand_differentiates_in_a_growing_graph():
+    """Regression: the gradient of where() through a broadcast operand, built while the node table
+    reallocates (unbroadcast once read its target shape through a reference into that table)."""
+    g = G()
+    x = g.input((300, 7))
+    t = g.un("tanh", x)
+    for _ in range(40):  # unrelated nodes, so the table grows during grad
+        t = g.un("sin", t)
+    a = g.op("sum", [x], axes=[1], keepdims=True)
+    w = g.op("where", [g.bin("gt", a, x), a, x])
+    gx = g.grad(g.sum_all(w), [x])[0]
+    x0 = 0.2 + np.abs(np.sin(np.arange(2100) * 0.37)).reshape(300, 7)
+    got = g.eval([gx], [x0])[0]
+    xt = torch.tensor(x0, requires_grad=True)
+    at = xt.sum(1, keepdim=True)
+    torch.where(at > xt, at, xt).sum().backward()
+    np.testing.assert_allclose(got, xt.grad.numpy(), rtol=1e-12)
