@@ -182,14 +182,40 @@ size_t distinct_external(const Graph& g, const std::vector<size_t>& members, con
   return s.size();
 }
 
-std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg, const std::vector<bool>& abs) {
+// Tails: fusable values whose every user is a tail of the same shape and dtype, ending in plan
+// outputs (e.g. an optimizer's per-parameter update chain). Computed users-first.
+std::vector<bool> tails(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const std::vector<bool>& abs,
+                        const std::function<bool(size_t)>& dev_fusable) {
+  size_t total = g.nodes.size();
+  std::vector<bool> is_out(total, false), tail(total, false), used(total, false);
+  for (uint32_t o : outputs) is_out[o] = true;
+  std::vector<std::vector<uint32_t>> users(total);
+  for (size_t i = 0; i < total; i++)
+    if (keep[i])
+      for (uint32_t x : g.nodes[i].inputs) users[x].push_back((uint32_t)i);
+  for (size_t i = total; i-- > 0;) {
+    const Node& n = g.nodes[i];
+    if (!keep[i] || abs[i] || is_alias(g, i) || !dev_fusable(i)) continue;
+    if (!is_out[i] && users[i].empty()) continue;
+    bool ok = true;
+    for (uint32_t u : users[i])
+      ok &= tail[u] && g.nodes[u].shape == n.shape && g.nodes[u].dtype == n.dtype;
+    tail[i] = ok;
+  }
+  return tail;
+}
+
+std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
+                                  const std::vector<bool>& abs) {
   std::vector<bool> up = cfg.hoist ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
   std::vector<Item> items;
   for (size_t i = 0; i < g.nodes.size(); i++)
     if (up[i]) items.push_back({false, i, {}});
-  auto dev_fusable = [&](size_t i) {
+  std::function<bool(size_t)> dev_fusable = [&](size_t i) {
     return fusable(g, i, true) && (cfg.fuse_f64 || g.nodes[i].dtype != DType::F64);
   };
+  std::vector<bool> tail = cfg.sink_tails ? tails(g, keep, outputs, abs, dev_fusable) : std::vector<bool>(g.nodes.size(), false);
+  std::vector<size_t> sunk;
   std::vector<size_t> level(g.nodes.size(), 0);
   std::vector<std::vector<size_t>> by_level;
   for (size_t i = 0; i < g.nodes.size(); i++) {
@@ -199,6 +225,10 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     for (uint32_t x : n.inputs) deepest = std::max(deepest, level[x]);
     if (abs[i]) {
       level[i] = deepest;  // a view of its source: no kernel, no level of its own
+      continue;
+    }
+    if (tail[i]) {
+      sunk.push_back(i);  // placed in the final level below
       continue;
     }
     bool joins = dev_fusable(i) && deepest > 0;
@@ -215,6 +245,9 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     if (by_level.size() <= level[i]) by_level.resize(level[i] + 1);
     by_level[level[i]].push_back(i);
   }
+  // Tails read earlier levels or same-shape tails only, so one last level can hold them all;
+  // node order keeps each producer ahead of its users within a group.
+  if (!sunk.empty()) by_level.push_back(sunk);
   for (auto& nodes : by_level) {
     std::vector<std::vector<size_t>> groups;
     std::vector<size_t> aliases;
@@ -253,8 +286,9 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
 
 // Greedy fusion: one open group. Instructions independent of the group are emitted first; one
 // that reads a member closes the group, which keeps the group free of cycles (plan.rs:311-350).
-std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const Fuse& cfg, const std::vector<bool>& abs) {
-  if (cfg.device && cfg.levels) return schedule_levels(g, keep, cfg, abs);
+std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
+                           const std::vector<bool>& abs) {
+  if (cfg.device && cfg.levels) return schedule_levels(g, keep, outputs, cfg, abs);
   std::vector<Item> items;
   std::vector<size_t> open;
   auto close = [&]() {
@@ -388,7 +422,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   std::vector<Item> items;
   std::vector<bool> abs = fuse ? absorbed_broadcasts(g, keep, outputs, *fuse) : std::vector<bool>(total, false);
   if (fuse) {
-    items = schedule(g, keep, *fuse, abs);
+    items = schedule(g, keep, outputs, *fuse, abs);
   } else {
     for (size_t i = 0; i < total; i++)
       if (keep[i] && !leaf(g.nodes[i])) items.push_back({false, i, {}});

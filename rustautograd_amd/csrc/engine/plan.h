@@ -32,12 +32,15 @@ struct Fuse {
   // A BroadcastTo read only by fusable nodes is not materialized: the consuming fused kernels
   // index its source directly (the reference materializes it, graph.rs:368-379, for Where).
   bool absorb_broadcasts;
+  // Level order only: fusable chains that feed nothing but plan outputs (optimizer updates) run
+  // in one final level, where chains of one shape share a kernel instead of one launch each.
+  bool sink_tails;
 
-  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false}; }
-  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false}; }
+  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false}; }
+  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false}; }
   // MI355X: ~4 us per dispatch inside a captured graph, ~0.001 ns per fp32 element written at
   // HBM speed, and 288 GB of HBM so level order is capped far higher.
-  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true}; }
+  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true}; }
 };
 
 struct Instr {

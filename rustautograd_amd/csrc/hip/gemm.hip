@@ -20,7 +20,7 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BK = 16, PAD = 4;
+constexpr int PAD = 4;
 
 __device__ __forceinline__ int64_t batch_offset(const int64_t* offs, uint64_t stride, uint32_t b) {
   return offs ? offs[b] : (int64_t)(stride * b);
@@ -47,26 +47,50 @@ __device__ __forceinline__ void loadn(const float* row, int64_t c, int64_t cols,
   }
 }
 
+// Which output tile a block computes. The dispatcher deals consecutive blocks round-robin over
+// the 8 XCDs, each with its own L2; with `swizzle`, XCD x instead receives the contiguous run
+// x*nb/8 ... (x+1)*nb/8 - 1 of tiles, and within a batch the tiles run in groups of 8 M-panels
+// per N sweep, so blocks resident on one XCD share their A and B panels in its L2.
+struct TileIndex {
+  uint32_t tm, tn, z;
+};
+
+__device__ __forceinline__ TileIndex tile_of(uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
+  uint32_t nb = gridDim.x, bid = blockIdx.x;
+  uint32_t per_batch = tiles_m * tiles_n;
+  if (!swizzle) return {(bid % per_batch) / tiles_n, bid % tiles_n, bid / per_batch};
+  uint32_t lid = (nb % 8 == 0) ? (bid % 8) * (nb / 8) + bid / 8 : bid;
+  uint32_t z = lid / per_batch, t = lid % per_batch;
+  constexpr uint32_t GROUP = 8;
+  uint32_t span = GROUP * tiles_n;
+  uint32_t first = (t / span) * GROUP;
+  uint32_t rows = min(tiles_m - first, GROUP);
+  uint32_t in = t % span;
+  return {first + in % rows, in / rows, z};
+}
+
 // C = op(A) op(B) for one BM x BN block tile. Four wave64s in a WM x WN grid; each wave owns a
 // (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles (v_mfma_f32_32x32x2f32). Operands are staged
-// through double-buffered LDS in K steps of 16, K-major, so each MFMA operand is one
+// through double-buffered LDS in K steps of BK, K-major, so each MFMA operand is one
 // conflict-free 32-lane LDS row read; transposed operands are transposed while staging.
-template <int BM, int BN, int WM, int WN, bool TA, bool TB>
+// The grid is one-dimensional: tiles_m * tiles_n * batch * splits blocks (tile_of).
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
 __global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                                                    int M, int N, int K, const int64_t* a_off, const int64_t* b_off, uint64_t a_stride,
                                                    uint64_t b_stride, int splits, int k_per_split, float* __restrict__ partial,
-                                                   bool vec_a, bool vec_b) {
+                                                   bool vec_a, bool vec_b, uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
   static_assert(WM * WN == 4, "four waves");
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1, "wave tile of at least 32x32");
-  // Loader geometry: 256 threads cover a BM x 16 (A) and a 16 x BN (B) tile.
+  // Loader geometry: 256 threads cover a BM x BK (A) and a BK x BN (B) tile.
   constexpr int EA = BM * BK / 256, EB = BN * BK / 256;
   __shared__ float As[2][BK][BM + PAD];
   __shared__ float Bs[2][BK][BN + PAD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const uint32_t b = blockIdx.z / splits, sp = blockIdx.z % splits;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const TileIndex ti = tile_of(tiles_m, tiles_n, swizzle);
+  const uint32_t b = ti.z / splits, sp = ti.z % splits;
+  const int m0 = ti.tm * BM, n0 = ti.tn * BN;
   const float* Ab = A + batch_offset(a_off, a_stride, b);
   const float* Bb = B + batch_offset(b_off, b_stride, b);
   const int kbeg = sp * k_per_split, kend = min(K, kbeg + k_per_split);
@@ -74,20 +98,20 @@ __global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, 
 
   float ra[EA], rb[EB];
   auto load_tiles = [&](int k0) {
-    if (!TA) {  // A is [M,K]: rows of 16 k, BM/... threads per row
+    if (!TA) {  // A is [M,K]: BM rows of BK k
       constexpr int TPR = BK / EA;
       int m = tid / TPR, kc = (tid % TPR) * EA;
       loadn<EA>(Ab + (int64_t)(m0 + m) * K, k0 + kc, kend, m0 + m < M, vec_a, ra);
-    } else {    // A is [K,M]: 16 rows of BM m
+    } else {    // A is [K,M]: BK rows of BM m
       constexpr int TPR = BM / EA;
       int k = tid / TPR, mc = (tid % TPR) * EA;
       loadn<EA>(Ab + (int64_t)(k0 + k) * M, m0 + mc, M, k0 + k < kend, vec_a, ra);
     }
-    if (!TB) {  // B is [K,N]: 16 rows of BN n
+    if (!TB) {  // B is [K,N]: BK rows of BN n
       constexpr int TPR = BN / EB;
       int k = tid / TPR, nc = (tid % TPR) * EB;
       loadn<EB>(Bb + (int64_t)(k0 + k) * N, n0 + nc, N, k0 + k < kend, vec_b, rb);
-    } else {    // B is [N,K]: rows of 16 k
+    } else {    // B is [N,K]: BN rows of BK k
       constexpr int TPR = BK / EB;
       int n = tid / TPR, kc = (tid % TPR) * EB;
       loadn<EB>(Bb + (int64_t)(n0 + n) * K, k0 + kc, kend, n0 + n < N, vec_b, rb);
@@ -198,28 +222,20 @@ bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
 }
 
 struct TileCfg {
-  int bm, bn;
+  int bm, bn, bk;
 };
 
-// Block tile: the largest tile that still gives two blocks per CU (512) with little padding
-// waste; 32-wide tiles for 32-wide outputs (attention heads).
+// Block tile, from measurements of C4's products on MI355X (K steps of 32 hide more load latency
+// for the smaller tiles): 32-wide tiles for outputs 32..96 wide or 32 tall (attention heads,
+// the vocabulary), the largest square-ish tile that still yields two blocks per CU (512), else
+// 64x64 (split over K later when even that leaves the CUs idle).
 TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t batch) {
-  static const TileCfg cands[] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}, {128, 32}, {32, 128}};
-  TileCfg best = {64, 64};
-  double best_score = -1;
-  for (auto c : cands) {
-    uint64_t tm = (m + c.bm - 1) / c.bm, tn = (n + c.bn - 1) / c.bn;
-    double waste = (double)(tm * c.bm * tn * c.bn) / (double)(m * n);
-    uint64_t blocks = tm * tn * batch;
-    // Prefer enough blocks, then low waste, then bigger tiles (more reuse per load).
-    double fill = std::min(1.0, (double)blocks / 512.0);
-    double score = fill / waste * (1.0 + 0.15 * (c.bm * c.bn) / (128.0 * 128.0));
-    if (score > best_score) {
-      best_score = score;
-      best = c;
-    }
-  }
-  return best;
+  auto blocks = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
+  if (n <= 96 && n % 32 == 0) return {128, 32, 32};
+  if (m <= 32) return {32, 128, 32};
+  if (blocks(128, 128) >= 512) return {128, 128, 16};
+  if (blocks(128, 64) >= 512) return {128, 64, 32};
+  return {64, 64, 32};
 }
 
 int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
@@ -228,6 +244,43 @@ int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t b
   uint64_t want = (512 + tiles - 1) / tiles;
   uint64_t most = k / 512;
   return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 16));
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+void launch_flags(hipStream_t s, bool ta, bool tb, dim3 grid, const float* A, const float* B, float* C, int M, int N, int K,
+                  const int64_t* a_off, const int64_t* b_off, uint64_t as, uint64_t bs, int splits, int kps, float* part, bool va,
+                  bool vb, uint32_t tm, uint32_t tn, int swizzle) {
+#define RG_GEMM(TA_, TB_)                                                                                                     \
+  hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, TA_, TB_>), grid, dim3(256), 0, s, A, B, C, M, N, K, a_off, b_off, as, bs, \
+                     splits, kps, part, va, vb, tm, tn, swizzle)
+  if (!ta && !tb) RG_GEMM(false, false);
+  else if (ta && !tb) RG_GEMM(true, false);
+  else if (!ta && tb) RG_GEMM(false, true);
+  else RG_GEMM(true, true);
+#undef RG_GEMM
+}
+
+// Instantiates the tile shapes pick_tile can return.
+void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, dim3 grid, const float* A, const float* B, float* C, int M, int N,
+                 int K, const int64_t* a_off, const int64_t* b_off, uint64_t as, uint64_t bs, int splits, int kps, float* part, bool va,
+                 bool vb, uint32_t tm, uint32_t tn, int swizzle) {
+#define RG_TILE(BM_, BN_, BK_, WM_, WN_)                                                                                      \
+  if (t.bm == BM_ && t.bn == BN_ && t.bk == BK_)                                                                               \
+    return launch_flags<BM_, BN_, BK_, WM_, WN_>(s, ta, tb, grid, A, B, C, M, N, K, a_off, b_off, as, bs, splits, kps, part, va, vb, \
+                                                 tm, tn, swizzle)
+  RG_TILE(128, 128, 16, 2, 2);
+  RG_TILE(128, 64, 16, 2, 2);
+  RG_TILE(64, 128, 16, 2, 2);
+  RG_TILE(64, 64, 16, 2, 2);
+  RG_TILE(128, 32, 16, 4, 1);
+  RG_TILE(32, 128, 16, 1, 4);
+  RG_TILE(128, 128, 32, 2, 2);
+  RG_TILE(128, 64, 32, 2, 2);
+  RG_TILE(64, 128, 32, 2, 2);
+  RG_TILE(64, 64, 32, 2, 2);
+  RG_TILE(128, 32, 32, 4, 1);
+  RG_TILE(32, 128, 32, 1, 4);
+#undef RG_TILE
 }
 
 }  // namespace
@@ -243,7 +296,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
     TileCfg t = pick_tile(g.m, g.n, g.batch);
     int splits = split_count(t, g.m, g.n, g.k, g.batch);
-    int kps = (int)(((g.k + splits - 1) / splits + BK - 1) / BK * BK);
+    int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
     splits = (int)((g.k + kps - 1) / kps);
     auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
     bool offs_ok_a = g.a_off == nullptr && g.a_stride % 4 == 0;
@@ -251,33 +304,15 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     // Vector loads run along K for A (untransposed) or M (transposed); likewise for B.
     bool vec_a = aligned(g.a) && offs_ok_a && ((g.ta ? g.m : g.k) % 4 == 0);
     bool vec_b = aligned(g.b) && offs_ok_b && ((g.tb ? g.k : g.n) % 4 == 0);
-    dim3 grid((uint32_t)((g.n + t.bn - 1) / t.bn), (uint32_t)((g.m + t.bm - 1) / t.bm), (uint32_t)(g.batch * splits));
+    uint32_t tiles_m = (uint32_t)((g.m + t.bm - 1) / t.bm), tiles_n = (uint32_t)((g.n + t.bn - 1) / t.bn);
+    dim3 grid((uint32_t)(tiles_m * tiles_n * g.batch * splits));
     float* part = splits > 1 ? (float*)g.workspace : nullptr;
-    auto A = (const float*)g.a;
-    auto B = (const float*)g.b;
-    auto Cm = (float*)g.c;
-    int M = (int)g.m, N = (int)g.n, K = (int)g.k;
-#define RG_GEMM(BM_, BN_, WM_, WN_, TA_, TB_)                                                                                   \
-  hipLaunchKernelGGL((k_gemm_mfma<BM_, BN_, WM_, WN_, TA_, TB_>), grid, dim3(256), 0, s, A, B, Cm, M, N, K, g.a_off, g.b_off,  \
-                     g.a_stride, g.b_stride, splits, kps, part, vec_a, vec_b)
-#define RG_GEMM_FLAGS(BM_, BN_, WM_, WN_)                  \
-  do {                                                     \
-    if (!g.ta && !g.tb) RG_GEMM(BM_, BN_, WM_, WN_, false, false); \
-    else if (g.ta && !g.tb) RG_GEMM(BM_, BN_, WM_, WN_, true, false); \
-    else if (!g.ta && g.tb) RG_GEMM(BM_, BN_, WM_, WN_, false, true); \
-    else RG_GEMM(BM_, BN_, WM_, WN_, true, true);           \
-  } while (0)
-    if (t.bm == 128 && t.bn == 128) RG_GEMM_FLAGS(128, 128, 2, 2);
-    else if (t.bm == 128 && t.bn == 64) RG_GEMM_FLAGS(128, 64, 2, 2);
-    else if (t.bm == 64 && t.bn == 128) RG_GEMM_FLAGS(64, 128, 2, 2);
-    else if (t.bm == 64 && t.bn == 64) RG_GEMM_FLAGS(64, 64, 2, 2);
-    else if (t.bm == 128 && t.bn == 32) RG_GEMM_FLAGS(128, 32, 4, 1);
-    else RG_GEMM_FLAGS(32, 128, 1, 4);
-#undef RG_GEMM_FLAGS
-#undef RG_GEMM
+    launch_mfma(s, t, g.ta, g.tb, grid, (const float*)g.a, (const float*)g.b, (float*)g.c, (int)g.m, (int)g.n, (int)g.k, g.a_off,
+                g.b_off, g.a_stride, g.b_stride, splits, kps, part, vec_a, vec_b, tiles_m, tiles_n, 1);
     if (splits > 1) {
       uint64_t mn = g.m * g.n;
-      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 255) / 256), (uint32_t)g.batch), dim3(256), 0, s, (const float*)part, Cm, mn, splits);
+      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 255) / 256), (uint32_t)g.batch), dim3(256), 0, s, (const float*)part,
+                         (float*)g.c, mn, splits);
     }
     return;
   }

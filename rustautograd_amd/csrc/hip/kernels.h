@@ -65,6 +65,7 @@ void cumsum(hipStream_t s, int dtype, const void* a, void* d, uint64_t rows, uin
 
 // Reductions over a canonical pattern; see runtime.cpp for how shapes map onto them.
 void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t rows, uint64_t len);
+// With chunks > 1, `partial` holds batch*chunks*k elements.
 void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k,
                  void* partial, uint64_t chunks);
 uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k);

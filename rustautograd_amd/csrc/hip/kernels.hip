@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "kernels.h"
 #include "ops.h"
@@ -388,20 +389,21 @@ __global__ void __launch_bounds__(TPB) k_cumsum_int(const int* __restrict__ a, i
 
 // ---- reductions ---------------------------------------------------------------------------
 
-template <class T>
-__device__ __forceinline__ T wave_combine(int kind, T v) {
-  for (int m = 32; m >= 1; m >>= 1) v = combine(kind, v, __shfl_xor(v, m, 64));
+template <int KIND, class T>
+__device__ __forceinline__ T wave_combine(T v) {
+  for (int m = 32; m >= 1; m >>= 1) v = combine(KIND, v, __shfl_xor(v, m, 64));
   return v;
 }
 
 // One wave per row: rows up to a few thousand elements (LayerNorm, softmax, cross-entropy).
-template <class T>
-__global__ void __launch_bounds__(TPB) k_reduce_rows_wave(int kind, const T* __restrict__ a, T* __restrict__ d, uint32_t rows, uint32_t len) {
+// KIND is a template argument so the combine step has no branch between the loads.
+template <class T, int KIND>
+__global__ void __launch_bounds__(TPB) k_reduce_rows_wave(const T* __restrict__ a, T* __restrict__ d, uint32_t rows, uint32_t len) {
   uint32_t row = blockIdx.x * (TPB / 64) + threadIdx.x / 64;
   uint32_t lane = threadIdx.x % 64;
   if (row >= rows) return;
   const T* x = a + (uint64_t)row * len;
-  T acc = Red<T>::init(kind);
+  T acc = Red<T>::init(KIND);
   constexpr uint32_t V = 16 / sizeof(T);
   if (len % V == 0) {
     // 16-byte loads: lane l reads elements [V*l, V*l+V) of each 64*V segment.
@@ -409,74 +411,92 @@ __global__ void __launch_bounds__(TPB) k_reduce_rows_wave(int kind, const T* __r
     for (uint32_t j = lane * V; j < len; j += 64 * V) {
       vec v = *(const vec*)(x + j);
 #pragma unroll
-      for (uint32_t q = 0; q < V; q++) acc = combine(kind, acc, v[q]);
+      for (uint32_t q = 0; q < V; q++) acc = combine(KIND, acc, v[q]);
     }
   } else {
-    for (uint32_t j = lane; j < len; j += 64) acc = combine(kind, acc, x[j]);
+    for (uint32_t j = lane; j < len; j += 64) acc = combine(KIND, acc, x[j]);
   }
-  acc = wave_combine(kind, acc);
+  acc = wave_combine<KIND>(acc);
   if (lane == 0) d[row] = acc;
 }
 
-// One block per row segment: long rows and full reductions. Segment g covers
-// [g*seg, min(len, (g+1)*seg)) of row `blockIdx.y`.
-template <class T>
-__global__ void __launch_bounds__(TPB) k_reduce_rows_block(int kind, const T* __restrict__ a, T* __restrict__ d, uint64_t len, uint64_t seg) {
+template <class T, int KIND>
+__global__ void __launch_bounds__(TPB) k_reduce_rows_block(const T* __restrict__ a, T* __restrict__ d, uint64_t len, uint64_t seg) {
   __shared__ T part[TPB / 64];
   uint64_t row = blockIdx.y;
   uint64_t begin = (uint64_t)blockIdx.x * seg, end = min(len, begin + seg);
   const T* x = a + row * len;
-  T acc = Red<T>::init(kind);
-  for (uint64_t j = begin + threadIdx.x; j < end; j += TPB) acc = combine(kind, acc, x[j]);
-  acc = wave_combine(kind, acc);
+  T acc = Red<T>::init(KIND);
+  for (uint64_t j = begin + threadIdx.x; j < end; j += TPB) acc = combine(KIND, acc, x[j]);
+  acc = wave_combine<KIND>(acc);
   if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
     T r = part[0];
-    for (int w = 1; w < TPB / 64; w++) r = combine(kind, r, part[w]);
+    for (int w = 1; w < TPB / 64; w++) r = combine(KIND, r, part[w]);
     d[row * gridDim.x + blockIdx.x] = r;
   }
 }
 
 // Leading-axis reduction of [batch, r, k] over r. A block owns 64 consecutive columns (one
-// coalesced 256-byte row segment per wave) and 4 row lanes; row chunks give parallelism and write
-// partial results, which a second pass of the same kernel combines (deterministic order).
-template <class T, int LANES>
-__global__ void __launch_bounds__(64 * LANES) k_reduce_cols(int kind, const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
+// coalesced 256-byte row segment per wave) and LANES row lanes; row chunks give parallelism and
+// write partial results, which a second pass of the same kernel combines (deterministic order).
+template <class T, int LANES, int KIND>
+__global__ void __launch_bounds__(64 * LANES) k_reduce_cols(const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
                                                              uint32_t chunk_rows, uint32_t chunks) {
   __shared__ T part[LANES][64];
   const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const uint32_t c = blockIdx.x * 64 + tx;
   const uint32_t b = blockIdx.y, s = blockIdx.z;
   const uint32_t r0 = s * chunk_rows, r1 = min(r, r0 + chunk_rows);
-  T acc = Red<T>::init(kind);
+  T acc = Red<T>::init(KIND);
   if (c < k) {
+    // Eight loads in flight per lane, then combined in row order.
     const T* x = a + (uint64_t)b * r * k + c;
-#pragma unroll 8
-    for (uint32_t row = r0 + ty; row < r1; row += LANES) acc = combine(kind, acc, x[(uint64_t)row * k]);
+    uint32_t row = r0 + ty;
+    for (; row + 7 * LANES < r1; row += 8 * LANES) {
+      T v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) v[q] = x[(uint64_t)(row + q * LANES) * k];
+#pragma unroll
+      for (int q = 0; q < 8; q++) acc = combine(KIND, acc, v[q]);
+    }
+    for (; row < r1; row += LANES) acc = combine(KIND, acc, x[(uint64_t)row * k]);
   }
   part[ty][tx] = acc;
   __syncthreads();
   if (ty == 0 && c < k) {
     T v = part[0][tx];
 #pragma unroll
-    for (int l = 1; l < LANES; l++) v = combine(kind, v, part[l][tx]);
+    for (int l = 1; l < LANES; l++) v = combine(KIND, v, part[l][tx]);
     out[((uint64_t)b * chunks + s) * k + c] = v;
   }
 }
 
-template <class T>
-__global__ void __launch_bounds__(TPB) k_reduce_general(int kind, const T* __restrict__ a, T* __restrict__ d, uint32_t out_n, Strided outer,
+template <class T, int KIND>
+__global__ void __launch_bounds__(TPB) k_reduce_general(const T* __restrict__ a, T* __restrict__ d, uint32_t out_n, Strided outer,
                                                         Strided inner, uint32_t red_n) {
   uint32_t o = blockIdx.x * TPB + threadIdx.x;
   if (o >= out_n) return;
   uint32_t base[1];
   decompose(outer, o, base, 1);
-  T acc = Red<T>::init(kind);
-  for (uint32_t r = 0; r < red_n; r++) {
+  T acc = Red<T>::init(KIND);
+  uint32_t r = 0;
+  for (; r + 4 <= red_n; r += 4) {  // four loads in flight, combined in order
+    T v[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t off[1];
+      decompose(inner, r + q, off, 1);
+      v[q] = a[base[0] + off[0]];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc = combine(KIND, acc, v[q]);
+  }
+  for (; r < red_n; r++) {
     uint32_t off[1];
     decompose(inner, r, off, 1);
-    acc = combine(kind, acc, a[base[0] + off[0]]);
+    acc = combine(KIND, acc, a[base[0] + off[0]]);
   }
   d[o] = acc;
 }
@@ -710,16 +730,27 @@ void cumsum(hipStream_t s, int dtype, const void* a, void* d, uint64_t rows, uin
   else RG_LAUNCH(k_cumsum_int, rows, (const int*)a, (int*)d, (uint32_t)rows, (uint32_t)v, (int)reverse);
 }
 
+// Calls F with the reduction kind as a compile-time constant.
+template <class F>
+void with_kind(int kind, F f) {
+  if (kind == RG_REDUCE_SUM) f(std::integral_constant<int, RG_REDUCE_SUM>());
+  else if (kind == RG_REDUCE_MAX) f(std::integral_constant<int, RG_REDUCE_MAX>());
+  else f(std::integral_constant<int, RG_REDUCE_MIN>());
+}
+
 void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t rows, uint64_t len) {
   if (rows == 0) return;
-  if (len <= 4096) {
-    uint32_t grid = blocks_for(rows, TPB / 64);
-    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_rows_wave<float>, dim3(grid), dim3(TPB), 0, s, kind, (const float*)a, (float*)d, (uint32_t)rows, (uint32_t)len);
-    else hipLaunchKernelGGL(k_reduce_rows_wave<double>, dim3(grid), dim3(TPB), 0, s, kind, (const double*)a, (double*)d, (uint32_t)rows, (uint32_t)len);
-  } else {
-    if (dtype == RG_F32) hipLaunchKernelGGL(k_reduce_rows_block<float>, dim3(1, (uint32_t)rows), dim3(TPB), 0, s, kind, (const float*)a, (float*)d, len, len);
-    else hipLaunchKernelGGL(k_reduce_rows_block<double>, dim3(1, (uint32_t)rows), dim3(TPB), 0, s, kind, (const double*)a, (double*)d, len, len);
-  }
+  with_kind(kind, [&](auto K) {
+    constexpr int KIND = decltype(K)::value;
+    if (len <= 4096) {
+      uint32_t grid = blocks_for(rows, TPB / 64);
+      if (dtype == RG_F32) hipLaunchKernelGGL((k_reduce_rows_wave<float, KIND>), dim3(grid), dim3(TPB), 0, s, (const float*)a, (float*)d, (uint32_t)rows, (uint32_t)len);
+      else hipLaunchKernelGGL((k_reduce_rows_wave<double, KIND>), dim3(grid), dim3(TPB), 0, s, (const double*)a, (double*)d, (uint32_t)rows, (uint32_t)len);
+    } else {
+      if (dtype == RG_F32) hipLaunchKernelGGL((k_reduce_rows_block<float, KIND>), dim3(1, (uint32_t)rows), dim3(TPB), 0, s, (const float*)a, (float*)d, len, len);
+      else hipLaunchKernelGGL((k_reduce_rows_block<double, KIND>), dim3(1, (uint32_t)rows), dim3(TPB), 0, s, (const double*)a, (double*)d, len, len);
+    }
+  });
 }
 
 uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k) {
@@ -736,20 +767,34 @@ void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
   uint32_t chunk_rows = (uint32_t)((r + chunks - 1) / chunks);
   dim3 grid(blocks_for(k, 64), (uint32_t)batch, (uint32_t)chunks);
   void* out = chunks == 1 ? d : partial;
-  if (dtype == RG_F32) hipLaunchKernelGGL((k_reduce_cols<float, 4>), grid, dim3(256), 0, s, kind, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
-  else hipLaunchKernelGGL((k_reduce_cols<double, 4>), grid, dim3(256), 0, s, kind, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k, chunk_rows, (uint32_t)chunks);
-  if (chunks > 1) {
-    // The partials [batch, chunks, k] are themselves a leading-axis reduction: 16 row lanes.
-    dim3 g2(blocks_for(k, 64), (uint32_t)batch, 1);
-    if (dtype == RG_F32) hipLaunchKernelGGL((k_reduce_cols<float, 16>), g2, dim3(1024), 0, s, kind, (const float*)partial, (float*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
-    else hipLaunchKernelGGL((k_reduce_cols<double, 16>), g2, dim3(1024), 0, s, kind, (const double*)partial, (double*)d, (uint32_t)chunks, (uint32_t)k, (uint32_t)chunks, 1u);
-  }
+  with_kind(kind, [&](auto K) {
+    constexpr int KIND = decltype(K)::value;
+    if (dtype == RG_F32)
+      hipLaunchKernelGGL((k_reduce_cols<float, 4, KIND>), grid, dim3(256), 0, s, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k,
+                         chunk_rows, (uint32_t)chunks);
+    else
+      hipLaunchKernelGGL((k_reduce_cols<double, 4, KIND>), grid, dim3(256), 0, s, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k,
+                         chunk_rows, (uint32_t)chunks);
+    if (chunks > 1) {
+      // The partials [batch, chunks, k] are themselves a leading-axis reduction: 16 row lanes.
+      dim3 g2(blocks_for(k, 64), (uint32_t)batch, 1);
+      if (dtype == RG_F32)
+        hipLaunchKernelGGL((k_reduce_cols<float, 16, KIND>), g2, dim3(1024), 0, s, (const float*)partial, (float*)d, (uint32_t)chunks,
+                           (uint32_t)k, (uint32_t)chunks, 1u);
+      else
+        hipLaunchKernelGGL((k_reduce_cols<double, 16, KIND>), g2, dim3(1024), 0, s, (const double*)partial, (double*)d, (uint32_t)chunks,
+                           (uint32_t)k, (uint32_t)chunks, 1u);
+    }
+  });
 }
 
 void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer, const Strided& inner,
                     uint64_t red_n) {
-  if (dtype == RG_F32) RG_LAUNCH(k_reduce_general<float>, out_n, kind, (const float*)a, (float*)d, (uint32_t)out_n, outer, inner, (uint32_t)red_n);
-  else RG_LAUNCH(k_reduce_general<double>, out_n, kind, (const double*)a, (double*)d, (uint32_t)out_n, outer, inner, (uint32_t)red_n);
+  with_kind(kind, [&](auto K) {
+    constexpr int KIND = decltype(K)::value;
+    if (dtype == RG_F32) RG_LAUNCH((k_reduce_general<float, KIND>), out_n, (const float*)a, (float*)d, (uint32_t)out_n, outer, inner, (uint32_t)red_n);
+    else RG_LAUNCH((k_reduce_general<double, KIND>), out_n, (const double*)a, (double*)d, (uint32_t)out_n, outer, inner, (uint32_t)red_n);
+  });
 }
 
 void copy_bytes(hipStream_t s, void* dst, const void* src, uint64_t bytes) {
