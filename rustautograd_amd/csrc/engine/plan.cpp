@@ -27,19 +27,20 @@ struct Allocator {
     held.push_back(0);
     return slots.size() - 1;
   }
-  size_t alloc(DType d, size_t n) {
-    size_t s = pick(d, n);
+  size_t alloc(DType d, size_t n, bool exact = false) {
+    size_t s = pick(d, n, exact);
     held[s] = n * dsize(d);
     live += held[s];
     peak = std::max(peak, live);
     return s;
   }
-  size_t pick(DType d, size_t n) {
+  size_t pick(DType d, size_t n, bool exact) {
     // A small value in a big buffer would pin the big buffer for its whole lifetime.
     int64_t best = -1;
     for (size_t k = 0; k < free.size(); k++) {
       size_t s = free[k];
-      if (slots[s].first == d && slots[s].second >= n && slots[s].second <= std::max<size_t>(n, 1) * 4) {
+      bool fits = exact ? slots[s].second == n : slots[s].second >= n && slots[s].second <= std::max<size_t>(n, 1) * 4;
+      if (slots[s].first == d && fits) {
         if (best < 0 || slots[s].second < slots[free[(size_t)best]].second) best = (int64_t)k;
       }
     }
@@ -421,6 +422,9 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
 
   std::vector<Item> items;
   std::vector<bool> abs = fuse ? absorbed_broadcasts(g, keep, outputs, *fuse) : std::vector<bool>(total, false);
+  std::vector<bool> exact(total, false);
+  if (fuse && fuse->exact_outputs)
+    for (uint32_t o : outputs) exact[o] = true;
   if (fuse) {
     items = schedule(g, keep, outputs, *fuse, abs);
   } else {
@@ -456,7 +460,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       std::vector<std::pair<size_t, size_t>> out_slots;
       for (size_t m : members) {
         if (uses[m] > 0) {
-          size_t s = a.alloc(g.nodes[m].dtype, g.nodes[m].n());
+          size_t s = a.alloc(g.nodes[m].dtype, g.nodes[m].n(), exact[m]);
           value_slot[m] = s;
           out_slots.push_back({m, s});
         }
@@ -500,7 +504,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
     };
     for (uint32_t x : dying)
       if (inplace(x)) a.release(value_slot[x]);
-    size_t dst = a.alloc(node.dtype, node.n());
+    size_t dst = a.alloc(node.dtype, node.n(), exact[i]);
     for (uint32_t x : dying)
       if (!inplace(x)) a.release(value_slot[x]);
     value_slot[i] = dst;
