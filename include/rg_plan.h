@@ -19,6 +19,18 @@
  *                    n_in, per input: slot, kind, row_len, reg, rank, dims,
  *                    n_ops, per micro-op: op, reg, n_args, per arg: is_reg, index,
  *                    n_out, per output: reg, slot                (plan.rs:85-111 `Fused`)
+ *     RG_STEP_ROWS   dtype, n, row_len, regs, rank, dims,
+ *                    n_in, per input: slot, kind, row_len, reg, rank, dims,
+ *                    n_ops, per micro-op: op, reg, aux, n_args, per arg: is_reg, index,
+ *                    n_out, per output: reg, slot
+ *                    A row group (no reference counterpart; device plans only): `dims` is
+ *                    [rows..., row_len], and each row is computed independently. A register
+ *                    holds either a whole row (element level) or one value per row (row level:
+ *                    per-row inputs, reductions, and ops on row-level values only). RG_OP_REDUCE
+ *                    micro-ops reduce an element-level register over the row, `aux` being the
+ *                    rg_reduce_kind. Inputs are read per element like a fused group's; a
+ *                    Broadcast input whose last dimension is 1 is row level. Outputs of
+ *                    row-level registers hold one value per row.
  *
  * Attribute words per op:
  *   MATMUL_T       ta, tb
@@ -64,7 +76,7 @@ enum rg_reduce_kind { RG_REDUCE_SUM = 0, RG_REDUCE_MAX = 1, RG_REDUCE_MIN = 2 };
 enum rg_arg_kind { RG_ARG_FULL = 0, RG_ARG_SPLAT = 1, RG_ARG_ROW = 2, RG_ARG_BROADCAST = 3 };
 /* Binary broadcast modes of a single elementwise instruction (plan.rs:119-125). */
 enum rg_mode { RG_MODE_SAME = 0, RG_MODE_ASCALAR = 1, RG_MODE_BSCALAR = 2, RG_MODE_GENERAL = 3 };
-enum rg_step_kind { RG_STEP_INSTR = 0, RG_STEP_FUSED = 1 };
+enum rg_step_kind { RG_STEP_INSTR = 0, RG_STEP_FUSED = 1, RG_STEP_ROWS = 2 };
 
 #ifdef __cplusplus
 #include <stdexcept>
@@ -93,12 +105,15 @@ struct FusedInput {
 struct MicroOp {
   int32_t op;
   int64_t reg;
+  int64_t aux = 0; /* RG_STEP_ROWS: the reduce kind of an RG_OP_REDUCE */
   std::vector<std::pair<int64_t, int64_t>> args; /* (is_reg, index) */
 };
 
+/* RG_STEP_FUSED, or RG_STEP_ROWS when row_len > 0. */
 struct Fused {
   int32_t dtype;
   int64_t n, regs;
+  int64_t row_len = 0;
   std::vector<int64_t> shape;
   std::vector<FusedInput> inputs;
   std::vector<MicroOp> ops;
@@ -203,10 +218,15 @@ inline Plan parse(const int64_t* w, size_t nw) {
         in.args.push_back(arg);
       }
       in.attr = vec(next());
-    } else if (st.kind == RG_STEP_FUSED) {
+    } else if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
+      const bool rows = st.kind == RG_STEP_ROWS;
       Fused& f = st.fused;
       f.dtype = (int32_t)next();
       f.n = next();
+      if (rows) {
+        f.row_len = next();
+        if (f.row_len <= 0) throw std::runtime_error("row group with an empty row");
+      }
       f.regs = next();
       f.shape = vec(next());
       int64_t nin = next();
@@ -224,6 +244,7 @@ inline Plan parse(const int64_t* w, size_t nw) {
         MicroOp m;
         m.op = (int32_t)next();
         m.reg = next();
+        if (rows) m.aux = next();
         int64_t nargs = next();
         for (int64_t b = 0; b < nargs; b++) {
           int64_t is_reg = next();

@@ -304,6 +304,76 @@ void run_fused(const Fused& f, std::vector<Buf>& s) {
   }
 }
 
+// A row group of a device plan (include/rg_plan.h RG_STEP_ROWS; no reference counterpart): each
+// row computed on its own. Every register is held as a full row; a row-level register (per-row
+// inputs, reductions, ops on row-level values) has the same value at every position and is
+// stored as one value per row. Reductions fold the row in element order.
+template <class T>
+void run_rows(const Fused& f, std::vector<Buf>& s) {
+  const size_t L = (size_t)f.row_len, n = (size_t)f.n, rows = n / L, rank = f.shape.size();
+  std::vector<bool> row_level((size_t)f.regs, false);
+  std::vector<std::vector<size_t>> bst(f.inputs.size());
+  auto ds = strides(f.shape);
+  for (size_t k = 0; k < f.inputs.size(); k++) {
+    auto& in = f.inputs[k];
+    if (in.kind == RG_ARG_BROADCAST) bst[k] = bstrides(in.shape, rank);
+    bool per_row = in.kind == RG_ARG_SPLAT || (in.kind == RG_ARG_BROADCAST && (in.shape.empty() || in.shape.back() == 1));
+    if (in.reg >= 0) row_level[(size_t)in.reg] = per_row;
+  }
+  for (auto& m : f.ops) {
+    bool r = true;
+    for (auto& a : m.args) r = r && a.first && row_level[(size_t)a.second];
+    row_level[(size_t)m.reg] = m.op == RG_OP_REDUCE || r;
+  }
+  std::vector<T*> outs;
+  for (auto& o : f.outputs) outs.push_back(s[(size_t)o.second].as<T>());
+  std::vector<const T*> ins;
+  for (auto& in : f.inputs) ins.push_back(s[(size_t)in.slot].as<T>());
+#pragma omp parallel
+  {
+    std::vector<T> reg((size_t)f.regs * L);
+#pragma omp for schedule(static)
+    for (size_t r = 0; r < rows; r++) {
+      for (size_t k = 0; k < f.inputs.size(); k++) {
+        auto& in = f.inputs[k];
+        if (in.reg < 0) continue;
+        T* d = reg.data() + (size_t)in.reg * L;
+        for (size_t j = 0; j < L; j++) {
+          size_t idx = r * L + j, src = 0;
+          if (in.kind == RG_ARG_SPLAT) src = 0;
+          else if (in.kind == RG_ARG_ROW) src = idx % (size_t)in.row_len;
+          else
+            for (size_t q = 0; q < rank; q++) src += (idx / ds[q]) % (size_t)f.shape[q] * bst[k][q];
+          d[j] = ins[k][src];
+        }
+      }
+      for (auto& m : f.ops) {
+        T* d = reg.data() + (size_t)m.reg * L;
+        const T* a[3];
+        for (size_t q = 0; q < m.args.size(); q++)
+          a[q] = m.args[q].first ? reg.data() + (size_t)m.args[q].second * L : ins[(size_t)m.args[q].second] + r * L;
+        if (m.op == RG_OP_REDUCE) {
+          T acc = a[0][0];
+          for (size_t j = 1; j < L; j++)
+            acc = m.aux == RG_REDUCE_SUM ? acc + a[0][j] : binary_op<T>(m.aux == RG_REDUCE_MAX ? RG_OP_MAX : RG_OP_MIN, acc, a[0][j]);
+          for (size_t j = 0; j < L; j++) d[j] = acc;
+        } else if (m.op == RG_OP_WHERE) {
+          for (size_t j = 0; j < L; j++) d[j] = a[0][j] != (T)0 ? a[1][j] : a[2][j];
+        } else if (is_unary(m.op)) {
+          for (size_t j = 0; j < L; j++) d[j] = unary_op<T>(m.op, a[0][j]);
+        } else {
+          for (size_t j = 0; j < L; j++) d[j] = binary_op<T>(m.op, a[0][j], a[1][j]);
+        }
+      }
+      for (size_t k = 0; k < f.outputs.size(); k++) {
+        const T* v = reg.data() + (size_t)f.outputs[k].first * L;
+        if (row_level[(size_t)f.outputs[k].first]) outs[k][r] = v[0];
+        else memcpy(outs[k] + r * L, v, L * sizeof(T));
+      }
+    }
+  }
+}
+
 template <class T, class F>
 void binary(const Instr& i, std::vector<Buf>& s, F f) {
   size_t n = (size_t)i.n;
@@ -785,7 +855,10 @@ void exec_instr(const Plan& p, const Instr& i, std::vector<Buf>& s) {
 
 void exec_step(Program* p, Frame& f, size_t k) {
   const Step& st = p->plan.steps[k];
-  if (st.kind == RG_STEP_FUSED) {
+  if (st.kind == RG_STEP_ROWS) {
+    if (st.fused.dtype == RG_F32) run_rows<float>(st.fused, f.slots);
+    else run_rows<double>(st.fused, f.slots);
+  } else if (st.kind == RG_STEP_FUSED) {
     if (st.fused.dtype == RG_F32) run_fused<float>(st.fused, f.slots);
     else run_fused<double>(st.fused, f.slots);
   } else {

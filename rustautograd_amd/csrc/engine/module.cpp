@@ -253,6 +253,7 @@ PYBIND11_MODULE(_rg, m) {
                  d["dtype"] = dname(s.group.dtype);
                  d["inputs"] = s.group.input_shapes;
                  d["n_outputs"] = s.group.outputs.size();
+                 d["row_len"] = s.group.row_len;  // > 0: a row group
                  static const char* kinds[] = {"full", "splat", "row", "broadcast"};
                  py::list in_kinds, in_slots, out_slots;
                  for (auto& in : s.group.inputs) {

@@ -4,6 +4,9 @@
 // 466-634 (build_fused / build_with).
 #include "plan.h"
 
+#include <queue>
+#include <set>
+
 #include <algorithm>
 #include <set>
 
@@ -141,6 +144,7 @@ struct Item {
   bool group;
   size_t node;
   std::vector<size_t> members;
+  bool rows = false;  // a row group (members in node order)
 };
 
 // BroadcastTo nodes whose every kept consumer is a device-fusable node, and which are not plan
@@ -206,6 +210,97 @@ std::vector<bool> tails(const Graph& g, const std::vector<bool>& keep, const std
   return tail;
 }
 
+// Longest rows a row-group kernel keeps in one wavefront's registers.
+constexpr size_t ROW_MAX = 1024;
+
+// A last-axis reduction with kept dimensions, the seed of a row group: [rows..., L] -> [rows..., 1].
+bool row_reduce(const Graph& g, size_t i) {
+  const Node& n = g.nodes[i];
+  if (n.op.kind != RG_OP_REDUCE || !n.op.keepdims || n.dtype == DType::I32) return false;
+  const Shape& s = g.shape(n.inputs[0]);
+  return s.size() >= 2 && s.back() >= 2 && s.back() <= ROW_MAX && n.op.v.size() == 1 && n.op.v[0] == s.size() - 1;
+}
+
+// Row groups, grown greedily in node order. A node joins the most recent group it reads from
+// when its shape fits the group (the full rows [P..., L] or the row values [P..., 1]; reductions
+// by their input) and none of its inputs depends on the group through a non-member, which keeps
+// every group a single schedulable unit. Groups without a reduction are dropped: plain fused
+// groups serve them. Hoisted, tail and absorbed nodes never join.
+std::vector<std::vector<size_t>> row_groups(const Graph& g, const std::vector<bool>& keep, const std::vector<bool>& abs,
+                                            const std::vector<bool>& excluded, const std::function<bool(size_t)>& dev_fusable,
+                                            size_t max_bindings) {
+  size_t total = g.nodes.size();
+  struct RG {
+    Shape full, row;
+    DType dtype;
+    std::vector<size_t> members;
+    std::set<uint32_t> external;
+    bool reduces = false;
+  };
+  std::vector<RG> groups;
+  std::vector<int64_t> gid(total, -1);
+  std::vector<std::vector<int64_t>> taint(total);  // sorted ids of groups a non-member depends on
+  auto tainted = [&](uint32_t x, int64_t k) { return std::binary_search(taint[x].begin(), taint[x].end(), k); };
+  for (size_t i = 0; i < total; i++) {
+    if (!keep[i] || leaf(g.nodes[i])) continue;
+    const Node& n = g.nodes[i];
+    bool member_ok = !excluded[i] && !abs[i] && !is_alias(g, i);
+    bool red = member_ok && row_reduce(g, i);
+    bool elem = member_ok && dev_fusable(i);
+    int64_t chosen = -1;
+    if (red || elem) {
+      for (uint32_t x : n.inputs) {
+        int64_t k = gid[x];
+        if (k < 0 || k <= chosen) continue;
+        const RG& G = groups[(size_t)k];
+        bool fits = n.dtype == G.dtype && (red ? g.shape(n.inputs[0]) == G.full : (n.shape == G.full || n.shape == G.row));
+        if (!fits) continue;
+        bool clean = true;
+        for (uint32_t y : n.inputs) clean &= !tainted(y, k);
+        if (!clean) continue;
+        std::set<uint32_t> ext = G.external;
+        for (uint32_t y : n.inputs)
+          if (gid[y] != k) ext.insert(y);
+        if (ext.size() + G.members.size() + 1 > max_bindings) continue;
+        chosen = k;
+      }
+      if (chosen < 0) {
+        const Shape& full = red ? g.shape(n.inputs[0]) : n.shape;
+        if (full.size() >= 2 && full.back() >= 2 && full.back() <= ROW_MAX && (red || n.shape == full)) {
+          RG G;
+          G.full = full;
+          G.row = full;
+          G.row.back() = 1;
+          G.dtype = n.dtype;
+          groups.push_back(std::move(G));
+          chosen = (int64_t)groups.size() - 1;
+        }
+      }
+    }
+    if (chosen >= 0) {
+      RG& G = groups[(size_t)chosen];
+      G.members.push_back(i);
+      G.reduces |= red;
+      for (uint32_t y : n.inputs)
+        if (gid[y] != chosen) G.external.insert(y);
+      gid[i] = chosen;
+    }
+    std::vector<int64_t> t;
+    for (uint32_t x : n.inputs) {
+      t.insert(t.end(), taint[x].begin(), taint[x].end());
+      if (gid[x] >= 0) t.push_back(gid[x]);
+    }
+    std::sort(t.begin(), t.end());
+    t.erase(std::unique(t.begin(), t.end()), t.end());
+    if (gid[i] >= 0) t.erase(std::remove(t.begin(), t.end(), gid[i]), t.end());
+    taint[i] = std::move(t);
+  }
+  std::vector<std::vector<size_t>> out;
+  for (auto& G : groups)
+    if (G.reduces && G.members.size() >= 2) out.push_back(G.members);
+  return out;
+}
+
 std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
                                   const std::vector<bool>& abs) {
   std::vector<bool> up = cfg.hoist ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
@@ -216,12 +311,62 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     return fusable(g, i, true) && (cfg.fuse_f64 || g.nodes[i].dtype != DType::F64);
   };
   std::vector<bool> tail = cfg.sink_tails ? tails(g, keep, outputs, abs, dev_fusable) : std::vector<bool>(g.nodes.size(), false);
+  const size_t total = g.nodes.size();
+  std::vector<std::vector<size_t>> rgs;
+  std::vector<int64_t> rg_of(total, -1);
+  if (cfg.row_groups) {
+    std::vector<bool> excluded(total, false);
+    for (size_t i = 0; i < total; i++) excluded[i] = up[i] || tail[i];
+    rgs = row_groups(g, keep, abs, excluded, dev_fusable, cfg.max_bindings);
+    for (size_t k = 0; k < rgs.size(); k++)
+      for (size_t m : rgs[k]) rg_of[m] = (int64_t)k;
+  }
+  // Scheduling units in a topological order of the graph with each row group contracted to one
+  // unit (unit total + k), ties broken by node order.
+  auto active = [&](size_t i) { return keep[i] && !up[i] && !leaf(g.nodes[i]); };
+  auto unit_of = [&](size_t i) -> size_t { return rg_of[i] >= 0 ? total + (size_t)rg_of[i] : i; };
+  std::vector<std::vector<size_t>> unit_users(total + rgs.size());
+  std::vector<size_t> indeg(total + rgs.size(), 0), first(total + rgs.size(), SIZE_MAX);
+  for (size_t i = 0; i < total; i++) {
+    if (!active(i)) continue;
+    size_t u = unit_of(i);
+    first[u] = std::min(first[u], i);
+    std::set<size_t> deps;
+    for (uint32_t x : g.nodes[i].inputs)
+      if (active(x) && unit_of(x) != u) deps.insert(unit_of(x));
+    for (size_t d : deps) {
+      unit_users[d].push_back(u);
+      indeg[u]++;
+    }
+  }
+  std::priority_queue<std::pair<size_t, size_t>, std::vector<std::pair<size_t, size_t>>, std::greater<>> ready;
+  for (size_t u = 0; u < total + rgs.size(); u++)
+    if (first[u] != SIZE_MAX && indeg[u] == 0) ready.push({first[u], u});
+  std::vector<size_t> order;
+  while (!ready.empty()) {
+    size_t u = ready.top().second;
+    ready.pop();
+    order.push_back(u);
+    for (size_t v : unit_users[u])
+      if (--indeg[v] == 0) ready.push({first[v], v});
+  }
   std::vector<size_t> sunk;
-  std::vector<size_t> level(g.nodes.size(), 0);
-  std::vector<std::vector<size_t>> by_level;
-  for (size_t i = 0; i < g.nodes.size(); i++) {
+  std::vector<size_t> level(total, 0);
+  std::vector<std::vector<size_t>> by_level;  // node ids, and total + k for row group k
+  for (size_t u : order) {
+    if (u >= total) {
+      const auto& members = rgs[u - total];
+      size_t deepest = 0;
+      for (size_t m : members)
+        for (uint32_t x : g.nodes[m].inputs)
+          if (rg_of[x] != (int64_t)(u - total)) deepest = std::max(deepest, level[x]);
+      for (size_t m : members) level[m] = deepest + 1;
+      if (by_level.size() <= deepest + 1) by_level.resize(deepest + 2);
+      by_level[deepest + 1].push_back(u);
+      continue;
+    }
+    size_t i = u;
     const Node& n = g.nodes[i];
-    if (!keep[i] || up[i] || leaf(n)) continue;
     size_t deepest = 0;
     for (uint32_t x : n.inputs) deepest = std::max(deepest, level[x]);
     if (abs[i]) {
@@ -236,7 +381,7 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     if (joins) {
       for (uint32_t x : n.inputs) {
         if (!(level[x] < deepest ||
-              (dev_fusable(x) && g.nodes[x].shape == n.shape && g.nodes[x].dtype == n.dtype))) {
+              (dev_fusable(x) && rg_of[x] < 0 && g.nodes[x].shape == n.shape && g.nodes[x].dtype == n.dtype))) {
           joins = false;
           break;
         }
@@ -251,8 +396,12 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   if (!sunk.empty()) by_level.push_back(sunk);
   for (auto& nodes : by_level) {
     std::vector<std::vector<size_t>> groups;
-    std::vector<size_t> aliases;
+    std::vector<size_t> aliases, rows;
     for (size_t i : nodes) {
+      if (i >= total) {
+        rows.push_back(i - total);  // row groups read lower levels only: they follow the groups
+        continue;
+      }
       const Node& n = g.nodes[i];
       if (is_alias(g, i)) {
         aliases.push_back(i);  // reads a value of this level, so it follows the groups
@@ -280,6 +429,7 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
       else
         for (size_t x : m) items.push_back({false, x, {}});
     }
+    for (size_t k : rows) items.push_back({true, 0, rgs[k], true});
     for (size_t a : aliases) items.push_back({false, a, {}});
   }
   return items;
@@ -325,8 +475,13 @@ std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const 
 }
 
 Fused compile_group(const Graph& g, const std::vector<size_t>& members, const std::vector<size_t>& slot_of,
-                    const std::vector<std::pair<size_t, size_t>>& out_slots, const std::vector<bool>& abs) {
+                    const std::vector<std::pair<size_t, size_t>>& out_slots, const std::vector<bool>& abs, bool rows) {
   const Node& first = g.nodes[members[0]];
+  // A row group's shape is the full rows its reductions read; a fused group's is its members'.
+  Shape shape = first.shape;
+  if (rows)
+    for (size_t m : members)
+      if (g.nodes[m].op.kind == RG_OP_REDUCE) shape = g.shape(g.nodes[m].inputs[0]);
   Fused f;
   std::vector<std::pair<uint32_t, std::pair<bool, size_t>>> ext;  // (node, operand)
   size_t regs = 0;
@@ -340,7 +495,7 @@ Fused compile_group(const Graph& g, const std::vector<size_t>& members, const st
       size_t row = 0;
       // An absorbed broadcast is read from its source, whose slot it shares.
       const Shape& xs = abs[x] ? g.shape(g.nodes[x].inputs[0]) : g.shape(x);
-      if (!arg_kind(xs, first.shape, &kind, &row)) kind = RG_ARG_BROADCAST;
+      if (!arg_kind(xs, shape, &kind, &row)) kind = RG_ARG_BROADCAST;
       f.input_shapes.push_back(xs);
       std::pair<bool, size_t> operand;
       size_t reg = SIZE_MAX;
@@ -375,9 +530,10 @@ Fused compile_group(const Graph& g, const std::vector<size_t>& members, const st
   }
   for (auto& [m, s] : out_slots) f.outputs.push_back({reg_of[m], s});
   f.dtype = first.dtype;
-  f.n = first.n();
+  f.n = numel(shape);
   f.regs = regs;
-  f.shape = first.shape;
+  f.shape = shape;
+  f.row_len = rows ? shape.back() : 0;
   return f;
 }
 
@@ -467,7 +623,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       }
       Step st;
       st.fused = true;
-      st.group = compile_group(g, members, value_slot, out_slots, abs);
+      st.group = compile_group(g, members, value_slot, out_slots, abs, item.rows);
       p.steps.push_back(std::move(st));
       for (uint32_t x : external)
         if (uses[x] == 0) a.release(value_slot[x]);
@@ -658,9 +814,11 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
       w.insert(w.end(), attr.begin(), attr.end());
     } else {
       const Fused& f = st.group;
-      w.push_back(RG_STEP_FUSED);
+      const bool rows = f.row_len > 0;
+      w.push_back(rows ? RG_STEP_ROWS : RG_STEP_FUSED);
       w.push_back((int64_t)f.dtype);
       w.push_back((int64_t)f.n);
+      if (rows) w.push_back((int64_t)f.row_len);
       w.push_back((int64_t)f.regs);
       shape(f.shape);
       w.push_back((int64_t)f.inputs.size());
@@ -675,6 +833,7 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
       for (auto& m : f.ops) {
         w.push_back(m.op.kind);
         w.push_back((int64_t)m.reg);
+        if (rows) w.push_back(m.op.kind == RG_OP_REDUCE ? (int64_t)m.op.rk : 0);
         w.push_back((int64_t)m.args.size());
         for (auto& [is_reg, idx] : m.args) {
           w.push_back(is_reg ? 1 : 0);

@@ -35,15 +35,18 @@ struct Fuse {
   // Level order only: fusable chains that feed nothing but plan outputs (optimizer updates) run
   // in one final level, where chains of one shape share a kernel instead of one launch each.
   bool sink_tails;
+  // Level order only: last-axis reductions and the fusable work around them on the same rows
+  // (normalisation, softmax, their backward forms) form row groups, one kernel each.
+  bool row_groups;
   // Plan outputs get buffers of exactly their size, so that a run loop can hand state over by
   // swapping buffers (validate.rs:303-318 swaps only equal-capacity slots) instead of copying.
   bool exact_outputs;
 
-  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false, false}; }
-  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false, false}; }
+  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false, false, false}; }
+  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false, false, false}; }
   // MI355X: ~4 us per dispatch inside a captured graph, ~0.001 ns per fp32 element written at
   // HBM speed, and 288 GB of HBM so level order is capped far higher.
-  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true, true}; }
+  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true, true, true}; }
 };
 
 struct Instr {
@@ -71,9 +74,13 @@ struct MicroOp {
   std::vector<std::pair<bool, size_t>> args;  // (is register, index)
 };
 
+// A fused group (row_len 0), or a row group: every member has the group's shape [rows..., L] or
+// the row shape [rows..., 1], and last-axis reductions may be members (include/rg_plan.h,
+// RG_STEP_ROWS). Row groups exist in device plans only.
 struct Fused {
   DType dtype = DType::F32;
   size_t n = 0;
+  size_t row_len = 0;
   std::vector<FusedIn> inputs;
   std::vector<MicroOp> ops;
   std::vector<std::pair<size_t, size_t>> outputs;  // (register, slot); never aliases an input

@@ -149,6 +149,199 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
   return s.str();
 }
 
+// A row group (RG_STEP_ROWS): one wavefront per row, each lane holding E elements of the row in
+// registers (E = L/64 rounded up to the vector width), with V-wide coalesced loads and stores.
+// Row-level values (per-row inputs, reductions) are one register per lane, equal across the
+// wave; a reduction folds each lane's elements in order, then the 64 lanes by a butterfly of
+// wave shuffles, so every lane ends with the same result.
+std::string generate_rows(const rgplan::Fused& f, const std::string& name, FusedKernel* k) {
+  const bool dbl = f.dtype == RG_F64;
+  const char* T = dbl ? "double" : "float";
+  const int64_t L = f.row_len, rows = f.n / f.row_len;
+  const int maxv = dbl ? 2 : 4;
+  int V = 1;
+  for (int v = maxv; v > 1; v /= 2)
+    if (L % (64 * v) == 0) {
+      V = v;
+      break;
+    }
+  const int64_t E = (L + 64 * V - 1) / (64 * V) * V;
+  const bool exact = L % (64 * V) == 0;
+  const char* VT = dbl ? (V == 2 ? "double2" : "double") : (V == 4 ? "float4" : V == 2 ? "float2" : "float");
+  const char* lanes[4] = {"x", "y", "z", "w"};
+  k->name = name;
+  k->vec = 1;
+  k->grid = (uint32_t)((rows + 3) / 4);
+
+  // Levels: true for row-level registers.
+  std::vector<int> level((size_t)f.regs, 0);
+  auto ds = f.shape;
+  const size_t rank = f.shape.size();
+  auto per_row = [&](const rgplan::FusedInput& in) {
+    return in.kind == RG_ARG_SPLAT || (in.kind == RG_ARG_BROADCAST && (in.shape.empty() || in.shape.back() == 1));
+  };
+  for (auto& in : f.inputs)
+    if (in.reg >= 0) level[(size_t)in.reg] = per_row(in);
+  for (auto& m : f.ops) {
+    bool r = true;
+    for (auto& a : m.args) r = r && a.first && level[(size_t)a.second];
+    level[(size_t)m.reg] = m.op == RG_OP_REDUCE || r;
+  }
+
+  std::ostringstream s;
+  bool alias = false;
+  for (auto& o : f.outputs)
+    for (auto& in : f.inputs) alias |= in.slot == o.second;
+  const char* R = alias ? "" : "__restrict__ ";
+  s << "extern \"C\" __global__ void __launch_bounds__(" << TPB << ") " << name << "(";
+  for (size_t j = 0; j < f.inputs.size(); j++) s << (j ? ", " : "") << "const " << T << "* " << R << "in" << j;
+  for (size_t j = 0; j < f.outputs.size(); j++) s << ", " << T << "* " << R << "out" << j;
+  s << ") {\n";
+  s << "  const unsigned lane = threadIdx.x & 63u;\n";
+  s << "  const unsigned long long row = (unsigned long long)blockIdx.x * 4ull + (threadIdx.x >> 6);\n";
+  s << "  if (row >= " << rows << "ull) return;\n";
+  // Element e of this lane sits at column J(e) of the row.
+  auto col = [&](int64_t e) {
+    return std::to_string((e / V) * 64 * V + e % V) + "u + lane * " + std::to_string(V) + "u";
+  };
+  auto valid = [&](int64_t e) { return exact ? std::string("true") : "(" + col(e) + " < " + std::to_string(L) + "u)"; };
+  // Offset of a broadcast input's row: coordinates of `row` over the leading dimensions.
+  auto row_offset = [&](const std::vector<int64_t>& is) {
+    size_t lead = rank - is.size();
+    std::vector<int64_t> st(is.size(), 1);
+    for (size_t i = is.size(); i-- > 1;) st[i - 1] = st[i] * is[i];
+    std::string idx;
+    int64_t inner = 1;  // product of the leading dimensions after d
+    std::vector<int64_t> inner_of(rank, 1);
+    for (size_t d = rank - 1; d-- > 0;) {
+      inner_of[d] = inner;
+      inner *= f.shape[d];
+    }
+    for (size_t d = 0; d + 1 < rank; d++) {
+      int64_t bs = (d < lead || is[d - lead] == 1) ? 0 : st[d - lead];
+      if (bs == 0 || f.shape[d] == 1) continue;
+      std::string c = "(row / " + std::to_string(inner_of[d]) + "ull)";
+      if (d > 0) c = "(" + c + " % " + std::to_string(f.shape[d]) + "ull)";
+      if (!idx.empty()) idx += " + ";
+      idx += c + " * " + std::to_string(bs) + "ull";
+    }
+    return idx.empty() ? std::string("0ull") : idx;
+  };
+  // Loads E elements of a row starting at pointer expression `base` into array `x`.
+  auto load_row = [&](const std::string& x, const std::string& base) {
+    s << "  " << T << " " << x << "[" << E << "];\n";
+    if (V > 1) {
+      for (int64_t c = 0; c < E / V; c++) {
+        s << "  { const " << VT << " t = *(const " << VT << "*)(" << base << " + " << col(c * V) << ");";
+        for (int v = 0; v < V; v++) s << " " << x << "[" << c * V + v << "] = t." << lanes[v] << ";";
+        s << " }\n";
+      }
+    } else {
+      for (int64_t e = 0; e < E; e++)
+        s << "  " << x << "[" << e << "] = " << valid(e) << " ? " << base << "[" << col(e) << "] : (" << T << ")0;\n";
+    }
+  };
+  std::vector<std::string> reg_name((size_t)f.regs);
+  for (size_t j = 0; j < f.inputs.size(); j++) {
+    const auto& in = f.inputs[j];
+    std::string x = "x" + std::to_string(j), p = "in" + std::to_string(j);
+    if (in.kind == RG_ARG_SPLAT) {
+      s << "  const " << T << " " << x << " = " << p << "[0];\n";
+    } else if (in.kind == RG_ARG_FULL) {
+      load_row(x, "(" + p + " + row * " + std::to_string(L) + "ull)");
+    } else if (in.kind == RG_ARG_ROW && in.row_len % L == 0) {
+      int64_t reps = in.row_len / L;
+      std::string base = reps == 1 ? p : "(" + p + " + (row % " + std::to_string(reps) + "ull) * " + std::to_string(L) + "ull)";
+      load_row(x, base);
+    } else if (in.kind == RG_ARG_ROW) {
+      s << "  " << T << " " << x << "[" << E << "];\n";
+      for (int64_t e = 0; e < E; e++)
+        s << "  " << x << "[" << e << "] = " << valid(e) << " ? " << p << "[(row * " << L << "ull + " << col(e) << ") % " << in.row_len
+          << "ull] : (" << T << ")0;\n";
+    } else if (per_row(in)) {
+      s << "  const " << T << " " << x << " = " << p << "[" << row_offset(in.shape) << "];\n";
+    } else {  // a broadcast whose last dimension runs along the row: rows start at multiples of L
+      std::string b = "b" + std::to_string(j);
+      s << "  const unsigned long long " << b << " = " << row_offset(in.shape) << ";\n";
+      load_row(x, "(" + p + " + " + b + ")");
+    }
+    if (in.reg >= 0) reg_name[(size_t)in.reg] = x;
+  }
+  auto operand = [&](const std::pair<int64_t, int64_t>& a, bool row_level, std::string* out_is_row) {
+    std::string n = a.first ? (reg_name[(size_t)a.second].empty() ? "r" + std::to_string(a.second) : reg_name[(size_t)a.second])
+                            : "x" + std::to_string(a.second);
+    bool r = a.first && level[(size_t)a.second];
+    (void)row_level;
+    *out_is_row = r ? "1" : "0";
+    return n;
+  };
+  for (auto& m : f.ops) {
+    std::string rn = "r" + std::to_string(m.reg);
+    if (m.op == RG_OP_REDUCE) {
+      std::string is_row;
+      std::string a = operand(m.args[0], false, &is_row);
+      const char* init = m.aux == RG_REDUCE_SUM ? "0" : m.aux == RG_REDUCE_MAX ? "-__builtin_huge_val()" : "__builtin_huge_val()";
+      auto comb = [&](const std::string& x, const std::string& y) {
+        return m.aux == RG_REDUCE_SUM ? x + " + " + y : std::string(m.aux == RG_REDUCE_MAX ? "rg_max(" : "rg_min(") + x + ", " + y + ")";
+      };
+      s << "  " << T << " " << rn << " = (" << T << ")" << init << ";\n";
+      for (int64_t e = 0; e < E; e++) {
+        std::string v = a + "[" + std::to_string(e) + "]";
+        if (exact) s << "  " << rn << " = " << comb(rn, v) << ";\n";
+        else s << "  if (" << valid(e) << ") " << rn << " = " << comb(rn, v) << ";\n";
+      }
+      s << "  for (int m = 32; m >= 1; m >>= 1) { const " << T << " o = __shfl_xor(" << rn << ", m, 64); " << rn << " = "
+        << comb(rn, "o") << "; }\n";
+      continue;
+    }
+    if (level[(size_t)m.reg]) {
+      std::vector<std::string> args;
+      for (auto& a : m.args) {
+        std::string r;
+        args.push_back(operand(a, true, &r));
+      }
+      s << "  const " << T << " " << rn << " = " << expr(m.op, args) << ";\n";
+      continue;
+    }
+    s << "  " << T << " " << rn << "[" << E << "];\n";
+    s << "#pragma unroll\n  for (int e = 0; e < " << E << "; e++) " << rn << "[e] = ";
+    std::vector<std::string> args;
+    for (auto& a : m.args) {
+      std::string r;
+      std::string n = operand(a, false, &r);
+      args.push_back(r == "1" || (!a.first && false) ? n : n + "[e]");
+    }
+    // Splat inputs are row level (a scalar); full inputs are element level.
+    for (size_t q = 0; q < m.args.size(); q++) {
+      const auto& a = m.args[q];
+      if (!a.first) continue;
+      if (level[(size_t)a.second]) args[q] = reg_name[(size_t)a.second].empty() ? "r" + std::to_string(a.second) : reg_name[(size_t)a.second];
+    }
+    s << expr(m.op, args) << ";\n";
+  }
+  for (size_t j = 0; j < f.outputs.size(); j++) {
+    int64_t r = f.outputs[j].first;
+    std::string rn = reg_name[(size_t)r].empty() ? "r" + std::to_string(r) : reg_name[(size_t)r];
+    std::string o = "out" + std::to_string(j);
+    if (level[(size_t)r]) {
+      s << "  if (lane == 0) " << o << "[row] = " << rn << ";\n";
+      continue;
+    }
+    std::string base = "(" + o + " + row * " + std::to_string(L) + "ull)";
+    if (V > 1) {
+      for (int64_t c = 0; c < E / V; c++) {
+        s << "  { " << VT << " t;";
+        for (int v = 0; v < V; v++) s << " t." << lanes[v] << " = " << rn << "[" << c * V + v << "];";
+        s << " *(" << VT << "*)(" << base << " + " << col(c * V) << ") = t; }\n";
+      }
+    } else {
+      for (int64_t e = 0; e < E; e++) s << "  if (" << valid(e) << ") " << base << "[" << col(e) << "] = " << rn << "[" << e << "];\n";
+    }
+  }
+  s << "}\n";
+  return s.str();
+}
+
 namespace {
 std::mutex g_mu;
 std::map<std::string, hipModule_t> g_modules;

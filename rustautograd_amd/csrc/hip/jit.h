@@ -25,6 +25,9 @@ struct FusedKernel {
 // also an input slot (the kernel then reads each element before writing it).
 std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k);
 
+// Source of one row-group kernel (RG_STEP_ROWS): `k->grid` blocks of four rows each.
+std::string generate_rows(const rgplan::Fused& f, const std::string& name, FusedKernel* k);
+
 // Compiles all sources into one code object for gfx950 and resolves each kernel. Modules are
 // cached by source text for the life of the process. Throws std::runtime_error with the log.
 void compile(const std::string& source, std::vector<FusedKernel*>& kernels);

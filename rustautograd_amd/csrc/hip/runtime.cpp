@@ -382,9 +382,10 @@ void build_program(Program& prog) {
   std::vector<rgjit::FusedKernel*> kernels;
   for (size_t k = 0; k < prog.plan.steps.size(); k++) {
     const Step& st = prog.plan.steps[k];
-    if (st.kind == RG_STEP_FUSED) {
+    if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
       auto fk = std::make_unique<rgjit::FusedKernel>();
-      src << rgjit::generate(st.fused, "rgf" + std::to_string(k), fk.get());
+      if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), fk.get());
+      else src << rgjit::generate(st.fused, "rgf" + std::to_string(k), fk.get());
       kernels.push_back(fk.get());
       prog.fused.push_back(std::move(fk));
     }
@@ -393,7 +394,7 @@ void build_program(Program& prog) {
   size_t fi = 0;
   for (size_t k = 0; k < prog.plan.steps.size(); k++) {
     const Step& st = prog.plan.steps[k];
-    if (st.kind == RG_STEP_FUSED) {
+    if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
       rgjit::FusedKernel* fk = prog.fused[fi++].get();
       std::vector<int64_t> ins, outs;
       for (auto& in : st.fused.inputs) ins.push_back(in.slot);
@@ -530,9 +531,11 @@ int rg_hip_compile_check(const int64_t* words, size_t n_words, char* err, size_t
     std::ostringstream src;
     int count = 0;
     for (size_t k = 0; k < plan.steps.size(); k++) {
-      if (plan.steps[k].kind != RG_STEP_FUSED) continue;
+      const auto& st = plan.steps[k];
+      if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
       rgjit::FusedKernel fk;
-      src << rgjit::generate(plan.steps[k].fused, "rgf" + std::to_string(k), &fk);
+      if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), &fk);
+      else src << rgjit::generate(st.fused, "rgf" + std::to_string(k), &fk);
       count++;
     }
     if (count) rgjit::compile_code(src.str());
@@ -703,7 +706,7 @@ int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len) {
   hipEventDestroy(a);
   hipEventDestroy(b);
   size_t fused = 0;
-  for (auto& st : e->prog->plan.steps) fused += st.kind == RG_STEP_FUSED;
+  for (auto& st : e->prog->plan.steps) fused += st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS;
   std::ostringstream s;
   s << "{\"wall_ms\":" << wall / repeats * 1e3 << ",\"gpu_ms\":" << ms / repeats << ",\"per_step\":{\"dispatches\":"
     << e->prog->steps.size() << ",\"fused_kernels\":" << fused << ",\"cpu_steps\":0}}";

@@ -202,8 +202,11 @@ def test_c2_mlp_step_devplan_matches_cpu_plan():
     a = rg.run(rg.compile(step, (state,), device=DEVPLAN), state, steps=5)
     b = rg.run(rg.compile(step, (state,), device="cpu"), state, steps=5)
     np.testing.assert_allclose(a.history["aux"], b.history["aux"], rtol=1e-4)
+    # Adam moves a parameter by about lr per step whatever the gradient's size, so an element
+    # whose gradient is rounding noise may differ by a fraction of lr; a wrong gradient would
+    # differ by ~lr * steps. Rows are reduced in a different order in the two plans.
     for (name, u), (_, v) in zip(rtree.paths(a.state["params"]), rtree.paths(b.state["params"])):
-        np.testing.assert_allclose(u.numpy(), v.numpy(), rtol=1e-4, atol=1e-6, err_msg=name)
+        np.testing.assert_allclose(u.numpy(), v.numpy(), rtol=1e-4, atol=0.01 * cfg.lr * 5, err_msg=name)
 
 
 def test_c5_matrix_chain_stays_skinny_and_exact_enough():

@@ -181,7 +181,7 @@ def test_random_graphs_agree_across_plans(chunk):
 def test_fused_plans_agree_on_random_graphs(chunk):
     """Shapes crossing block, task and vector-width boundaries, long fusable chains (engine.rs:364-437)."""
     r = XorShift(0xDEADBEEF0BADF00D + chunk)
-    groups = rows = 0
+    groups = rows = row_groups = 0
     ops = [0, 1, 2, 3, 4, 6, 18, 7, 19, 8, 10, 9, 12, 14]
     for case in range(40):
         tw = Twin()
@@ -210,4 +210,79 @@ def test_fused_plans_agree_on_random_graphs(chunk):
         fused = [s for s in plan if s["kind"] == "fused"]
         groups += len(fused)
         rows += sum(k == "row" for s in fused for k in s["input_kinds"])
+        row_groups += sum(s["row_len"] > 0 for s in fused)
     assert groups > 20, f"the fuzz must exercise fusion: {groups} groups, {rows} row inputs"
+
+
+def _row_program(r, tw, rows_shape, L):
+    """Random row-wise work (normalisation/softmax-like): elementwise ops on [..., L], last-axis
+    reductions to [..., 1], arithmetic on the per-row values and broadcasts back."""
+    g = tw.g
+    full, per_row = [], []
+    for k, t in enumerate(tw.ts):
+        (full if tuple(t.shape) == rows_shape + (L,) else per_row).append(k)
+    reduce = {"sum": lambda t: t.sum(-1, keepdim=True), "max": lambda t: t.amax(-1, keepdim=True),
+              "min": lambda t: t.amin(-1, keepdim=True)}
+    for _ in range(4 + r.below(14)):
+        choice = r.below(10)
+        a = full[-1 - r.below(min(len(full), 3))]
+        if choice < 3:
+            kind = ["sum", "max", "min"][r.below(3)]
+            k = tw.push(lambda: g.op(kind, [tw.ids[a]], axes=[len(rows_shape)], keepdims=True), lambda: reduce[kind](tw.ts[a]))
+            if k is not None:
+                per_row.append(k)
+        elif choice < 6 and per_row:
+            b = per_row[r.below(len(per_row))]
+            op = ["sub", "mul", "div", "add"][r.below(4)]
+            fn = {"sub": lambda x, y: x - y, "mul": lambda x, y: x * y, "div": lambda x, y: x / (y.abs() + 0.5),
+                  "add": lambda x, y: x + y}[op]
+            if op == "div":
+                ia, ib = tw.ids[a], tw.ids[b]
+                den = tw.push(lambda: g.bin("add", g.un("abs", ib), g.scalar(0.5)), lambda: tw.ts[b].abs() + 0.5)
+                k = tw.push(lambda: g.bin("div", ia, tw.ids[den]), lambda: tw.ts[a] / tw.ts[den])
+                per_row.append(den)
+            else:
+                k = tw.push(lambda: g.bin(op, tw.ids[a], tw.ids[b]), lambda: fn(tw.ts[a], tw.ts[b]))
+            if k is not None:
+                full.append(k)
+        elif choice < 7 and per_row:
+            b = per_row[r.below(len(per_row))]
+            k = tw.push(lambda: g.un("sqrt", g.bin("add", g.un("abs", tw.ids[b]), g.scalar(1.0))),
+                        lambda: torch.sqrt(tw.ts[b].abs() + 1.0))
+            if k is not None:
+                per_row.append(k)
+        else:
+            op = ["tanh", "sin", "exp_tanh", "mul_self"][r.below(4)]
+            if op == "exp_tanh":
+                k = tw.push(lambda: g.un("exp", g.un("tanh", tw.ids[a])), lambda: torch.exp(torch.tanh(tw.ts[a])))
+            elif op == "mul_self":
+                k = tw.push(lambda: g.bin("mul", tw.ids[a], tw.ids[a]), lambda: tw.ts[a] * tw.ts[a])
+            else:
+                k = tw.push(lambda: g.un(op, tw.ids[a]), lambda: getattr(torch, op)(tw.ts[a]))
+            if k is not None:
+                full.append(k)
+    return full, per_row
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_row_groups_agree_on_random_row_programs(chunk):
+    """Row-wise programs (what normalisation and softmax look like, forward and backward): the
+    HIP planner makes row groups of them; every flavour agrees with torch float64."""
+    r = XorShift(0x5EED0F0123456789 + chunk)
+    row_groups = 0
+    for case in range(25):
+        tw = Twin()
+        rows_shape = [(1,), (3,), (40,), (2, 5)][r.below(4)]
+        L = [7, 64, 96, 256, 300, 1000][r.below(6)]
+        inputs = []
+        for s in [rows_shape + (L,), rows_shape + (L,), rows_shape + (1,), (L,)]:
+            v = 0.2 + np.array([r.unit() for _ in range(int(np.prod(s)))])
+            tw.add_input(s, v)
+            inputs.append(v.reshape(s))
+        full, per_row = _row_program(r, tw, rows_shape, L)
+        outs = [full[-1], per_row[-1] if per_row else full[0]]
+        outs = [tw.ids.index(tw.ids[k]) for k in outs]
+        _check_case(tw, outs, inputs, f"chunk {chunk} case {case}")
+        plan = tw.g.compile([tw.ids[k] for k in outs], inputs, device=DEVPLAN, optimize="standard").plan_summary()
+        row_groups += sum(s["kind"] == "fused" and s["row_len"] > 0 for s in plan)
+    assert row_groups >= 15, f"row groups formed: {row_groups}"
