@@ -280,6 +280,16 @@ PYBIND11_MODULE(_rg, m) {
              }
              return out;
            })
+      .def("plan_io",
+           [](const PyCompiled& c) {
+             // Slots of the plan's inputs and outputs, and every slot's (dtype, capacity, pinned).
+             const Plan& p = c.c->plan;
+             std::vector<size_t> outs;
+             for (auto& o : p.outputs) outs.push_back(o.slot);
+             std::vector<std::tuple<std::string, size_t, bool>> slots;
+             for (size_t k = 0; k < p.slots.size(); k++) slots.push_back({dname(p.slots[k].first), p.slots[k].second, (bool)p.pinned[k]});
+             return py::make_tuple(p.input_slots, outs, slots);
+           })
       .def("step_times",
            [](const PyCompiled& c, const std::vector<PyTensor>& inputs, size_t repeats) {
              // Device seconds of each plan step, summed over `repeats` runs (metal.rs:690-698).

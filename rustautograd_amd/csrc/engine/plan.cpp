@@ -169,6 +169,16 @@ std::vector<bool> absorbed_broadcasts(const Graph& g, const std::vector<bool>& k
   return abs;
 }
 
+// Whether a node reads an input that is neither its own shape nor a scalar.
+bool indexed_inputs(const Graph& g, size_t i) {
+  for (uint32_t x : g.nodes[i].inputs) {
+    rg_arg_kind k;
+    size_t row;
+    if (!arg_kind(g.shape(x), g.nodes[i].shape, &k, &row) || (k != RG_ARG_FULL && k != RG_ARG_SPLAT)) return true;
+  }
+  return false;
+}
+
 bool reads_absorbed(const Graph& g, const std::vector<size_t>& members, const std::vector<bool>& abs) {
   for (size_t m : members)
     for (uint32_t x : g.nodes[m].inputs)
@@ -294,6 +304,35 @@ std::vector<std::vector<size_t>> row_groups(const Graph& g, const std::vector<bo
     t.erase(std::unique(t.begin(), t.end()), t.end());
     if (gid[i] >= 0) t.erase(std::remove(t.begin(), t.end(), gid[i]), t.end());
     taint[i] = std::move(t);
+  }
+  // Producers: an ungrouped row-compatible node whose every user is in one kept group, and whose
+  // inputs do not depend on that group, joins it (e.g. a gradient scaled before its row group).
+  // Users first, so chains of producers join too.
+  std::vector<std::vector<uint32_t>> users(total);
+  for (size_t i = 0; i < total; i++)
+    if (keep[i])
+      for (uint32_t x : g.nodes[i].inputs) users[x].push_back((uint32_t)i);
+  auto kept = [&](int64_t k) { return k >= 0 && groups[(size_t)k].reduces && groups[(size_t)k].members.size() >= 2; };
+  for (size_t i = total; i-- > 0;) {
+    if (!keep[i] || leaf(g.nodes[i]) || kept(gid[i]) || users[i].empty()) continue;
+    const Node& n = g.nodes[i];
+    if (excluded[i] || abs[i] || is_alias(g, i) || !dev_fusable(i)) continue;
+    int64_t k = gid[users[i][0]];
+    if (!kept(k)) continue;
+    bool ok = true;
+    for (uint32_t u : users[i]) ok &= gid[u] == k;
+    RG& G = groups[(size_t)k];
+    ok = ok && n.dtype == G.dtype && (n.shape == G.full || n.shape == G.row);
+    for (uint32_t y : n.inputs) ok = ok && !tainted(y, k);
+    if (!ok || G.external.size() + G.members.size() + n.inputs.size() + 1 > max_bindings) continue;
+    if (gid[i] >= 0) {  // leave its dropped group
+      auto& old = groups[(size_t)gid[i]].members;
+      old.erase(std::remove(old.begin(), old.end(), i), old.end());
+    }
+    G.members.insert(std::lower_bound(G.members.begin(), G.members.end(), i), i);
+    G.external.erase((uint32_t)i);
+    for (uint32_t y : n.inputs) G.external.insert(y);
+    gid[i] = k;
   }
   std::vector<std::vector<size_t>> out;
   for (auto& G : groups)
@@ -424,8 +463,10 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
       }
     }
     for (auto& m : groups) {
-      // A node reading an absorbed broadcast needs the fused kernel's broadcast indexing.
-      if (m.size() >= 2 || reads_absorbed(g, m, abs)) items.push_back({true, 0, m});
+      // A node reading an absorbed broadcast needs the fused kernel's broadcast indexing; one
+      // reading a row vector or a broadcast runs faster as a generated kernel than through the
+      // general strided instruction.
+      if (m.size() >= 2 || reads_absorbed(g, m, abs) || (cfg.device && indexed_inputs(g, m[0]))) items.push_back({true, 0, m});
       else
         for (size_t x : m) items.push_back({false, x, {}});
     }
