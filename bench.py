@@ -45,6 +45,13 @@ def classify(plan):
 
     for k, st in enumerate(plan):
         ds = 8 if st["dtype"] == "float64" else 4
+        if st["kind"] == "attention":
+            # The products of the nodes the step replaces: q k^T and P v forward; dO v^T, P^T dO,
+            # dS k and dS^T q backward (tiles the mask hides entirely are skipped, not subtracted).
+            per = 2.0 * st["bh"] * st["tq"] * st["tk"] * st["hd"]
+            add("attention", k, flops=(4 if st["backward"] else 2) * per,
+                nbytes=(len(st["input_slots"]) + len(st["output_slots"])) * st["n"] * ds)
+            continue
         if st["kind"] == "fused":
             n = st["n"]
             add("fused_elementwise", k, nbytes=sum(_numel(s) for s in st["inputs"]) * ds + n * st["n_outputs"] * ds)

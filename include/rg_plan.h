@@ -31,6 +31,20 @@
  *                    rg_reduce_kind. Inputs are read per element like a fused group's; a
  *                    Broadcast input whose last dimension is 1 is row level. Outputs of
  *                    row-level registers hold one value per row.
+ *     RG_STEP_ATTN   dtype, backward (0/1), bh, heads, tq, tk, hd, div (f64 bits), fill (f64 bits),
+ *                    mask_slot (-1: none), mask strides (4 words), stats_slot,
+ *                    n_in, in slots, n_out, out slots, node
+ *                    Fused attention (no reference counterpart; device plans only) over bh
+ *                    independent problems with row-major [bh][t][hd] operands:
+ *                      forward   in q, k, v        out O = softmax(where(mask, q k^T / div, fill)) v
+ *                      backward  in q, k, v, O, dO out dq, dk, dv (the gradients of O's graph)
+ *                    The softmax is over keys; the mask (f32, nonzero = visible) is read at
+ *                    b * s0 + h * s1 + q * s2 + k * s3 for problem b * heads + h. The stats
+ *                    slot holds 3 * bh * tq words of per-query statistics (written by the
+ *                    forward, read by the backward) followed, with a mask, by
+ *                    slices * (2 * tq * tk / 32 + tq) words of packed mask bits, slices being
+ *                    (s0 ? bh / heads : 1) * (s1 ? heads : 1). Planned only for hd in
+ *                    {16, 32, 64} and tq, tk multiples of 32 up to RG_ATTN_MAX_T.
  *
  * Attribute words per op:
  *   MATMUL_T       ta, tb
@@ -76,9 +90,12 @@ enum rg_reduce_kind { RG_REDUCE_SUM = 0, RG_REDUCE_MAX = 1, RG_REDUCE_MIN = 2 };
 enum rg_arg_kind { RG_ARG_FULL = 0, RG_ARG_SPLAT = 1, RG_ARG_ROW = 2, RG_ARG_BROADCAST = 3 };
 /* Binary broadcast modes of a single elementwise instruction (plan.rs:119-125). */
 enum rg_mode { RG_MODE_SAME = 0, RG_MODE_ASCALAR = 1, RG_MODE_BSCALAR = 2, RG_MODE_GENERAL = 3 };
-enum rg_step_kind { RG_STEP_INSTR = 0, RG_STEP_FUSED = 1, RG_STEP_ROWS = 2 };
+enum rg_step_kind { RG_STEP_INSTR = 0, RG_STEP_FUSED = 1, RG_STEP_ROWS = 2, RG_STEP_ATTN = 3 };
+/* Longest query or key sequence of a fused attention step. */
+#define RG_ATTN_MAX_T 256
 
 #ifdef __cplusplus
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
@@ -120,10 +137,24 @@ struct Fused {
   std::vector<std::pair<int64_t, int64_t>> outputs; /* (reg, slot) */
 };
 
+/* RG_STEP_ATTN */
+struct Attn {
+  int32_t dtype;
+  bool backward;
+  int64_t bh, heads, tq, tk, hd;
+  double div, fill;
+  int64_t mask_slot;
+  int64_t mask_strides[4];
+  int64_t stats_slot;
+  std::vector<int64_t> in, out;
+  int64_t node;
+};
+
 struct Step {
   int32_t kind;
   Instr instr;
   Fused fused;
+  Attn attn;
 };
 
 struct Slot {
@@ -259,6 +290,28 @@ inline Plan parse(const int64_t* w, size_t nw) {
         int64_t s = next();
         f.outputs.push_back({r, s});
       }
+    } else if (st.kind == RG_STEP_ATTN) {
+      Attn& a = st.attn;
+      a.dtype = (int32_t)next();
+      a.backward = next() != 0;
+      a.bh = next();
+      a.heads = next();
+      a.tq = next();
+      a.tk = next();
+      a.hd = next();
+      int64_t bits = next();
+      memcpy(&a.div, &bits, 8);
+      bits = next();
+      memcpy(&a.fill, &bits, 8);
+      a.mask_slot = next();
+      for (int k = 0; k < 4; k++) a.mask_strides[k] = next();
+      a.stats_slot = next();
+      a.in = vec(next());
+      a.out = vec(next());
+      a.node = next();
+      if (a.in.size() != (a.backward ? 5u : 3u) || a.out.size() != (a.backward ? 3u : 1u) || a.bh <= 0 || a.heads <= 0 ||
+          a.bh % a.heads != 0)
+        throw std::runtime_error("malformed attention step");
     } else {
       throw std::runtime_error("unknown plan step kind");
     }

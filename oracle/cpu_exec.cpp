@@ -853,9 +853,66 @@ void exec_instr(const Plan& p, const Instr& i, std::vector<Buf>& s) {
   }
 }
 
+// A fused attention step of a device plan (include/rg_plan.h RG_STEP_ATTN; no reference
+// counterpart). Evaluated per (batch, head) problem with the same operations, in the same order,
+// as the nodes the step replaces, so the result equals the unfused plan's bit for bit:
+//   S = q k^T (matmul_t tb), Y = where(mask, S / div, fill), m = max_row(Y), E = exp(Y - m),
+//   Z = sum_row(E) (plan.rs lane-wise row sum), P = E / Z, O = P v;
+// backward: dP = dO v^T, dv = P^T dO, dY = (dP / Z + sum_row(-dP * E / (Z * Z))) * E,
+//   dS = where(mask, dY, 0) / div, dq = dS k, dk = dS^T q
+// (the autodiff's form of those nodes, rustautograd_amd/csrc/engine/attention.cpp).
+void run_attention(const Attn& a, std::vector<Buf>& s) {
+  const size_t tq = (size_t)a.tq, tk = (size_t)a.tk, hd = (size_t)a.hd, bh = (size_t)a.bh, heads = (size_t)a.heads;
+  const float div = (float)a.div, fill = (float)a.fill;
+  auto ptr = [&](int64_t slot) { return s[(size_t)slot].as<float>(); };
+  const float* mask = a.mask_slot >= 0 ? ptr(a.mask_slot) : nullptr;
+#pragma omp parallel for schedule(static)
+  for (size_t b = 0; b < bh; b++) {
+    const float* q = ptr(a.in[0]) + b * tq * hd;
+    const float* k = ptr(a.in[1]) + b * tk * hd;
+    const float* v = ptr(a.in[2]) + b * tk * hd;
+    const float* mb = mask ? mask + (b / heads) * a.mask_strides[0] + (b % heads) * a.mask_strides[1] : nullptr;
+    auto visible = [&](size_t i, size_t j) { return !mb || mb[(int64_t)i * a.mask_strides[2] + (int64_t)j * a.mask_strides[3]] != 0.0f; };
+    std::vector<float> S(tq * tk), E(tq * tk), Z(tq), P(tq * tk);
+    gemm<float>(tq, hd, tk, q, false, k, true, S.data());
+    for (size_t i = 0; i < tq; i++) {
+      float* y = &S[i * tk];
+      float m = -INFINITY;
+      for (size_t j = 0; j < tk; j++) {
+        y[j] = visible(i, j) ? y[j] / div : fill;
+        m = nan_max(m, y[j]);
+      }
+      for (size_t j = 0; j < tk; j++) E[i * tk + j] = t_exp(y[j] - m);
+      Z[i] = fast_sum(&E[i * tk], tk);
+      for (size_t j = 0; j < tk; j++) P[i * tk + j] = E[i * tk + j] / Z[i];
+    }
+    if (!a.backward) {
+      gemm<float>(tq, tk, hd, P.data(), false, v, false, ptr(a.out[0]) + b * tq * hd);
+      continue;
+    }
+    const float* d_o = ptr(a.in[4]) + b * tq * hd;
+    std::vector<float> dP(tq * tk), dS(tq * tk), t(tk);
+    gemm<float>(tq, hd, tk, d_o, false, v, true, dP.data());
+    gemm<float>(tk, tq, hd, P.data(), true, d_o, false, ptr(a.out[2]) + b * tk * hd);
+    for (size_t i = 0; i < tq; i++) {
+      const float z = Z[i], zz = z * z;
+      for (size_t j = 0; j < tk; j++) t[j] = -dP[i * tk + j] * E[i * tk + j] / zz;
+      const float e = fast_sum(t.data(), tk);
+      for (size_t j = 0; j < tk; j++) {
+        const float h = (dP[i * tk + j] / z + e) * E[i * tk + j];
+        dS[i * tk + j] = (visible(i, j) ? h : 0.0f) / div;
+      }
+    }
+    gemm<float>(tq, tk, hd, dS.data(), false, k, false, ptr(a.out[0]) + b * tq * hd);
+    gemm<float>(tk, tq, hd, dS.data(), true, q, false, ptr(a.out[1]) + b * tk * hd);
+  }
+}
+
 void exec_step(Program* p, Frame& f, size_t k) {
   const Step& st = p->plan.steps[k];
-  if (st.kind == RG_STEP_ROWS) {
+  if (st.kind == RG_STEP_ATTN) {
+    run_attention(st.attn, f.slots);
+  } else if (st.kind == RG_STEP_ROWS) {
     if (st.fused.dtype == RG_F32) run_rows<float>(st.fused, f.slots);
     else run_rows<double>(st.fused, f.slots);
   } else if (st.kind == RG_STEP_FUSED) {

@@ -244,7 +244,21 @@ PYBIND11_MODULE(_rg, m) {
              py::list out;
              for (auto& s : c.c->plan.steps) {
                py::dict d;
-               if (s.fused) {
+               if (s.attn) {
+                 const Attn& a = s.att;
+                 d["kind"] = "attention";
+                 d["backward"] = a.backward;
+                 d["dtype"] = dname(a.dtype);
+                 d["bh"] = a.shape.bh;
+                 d["heads"] = a.shape.heads;
+                 d["tq"] = a.shape.tq;
+                 d["tk"] = a.shape.tk;
+                 d["hd"] = a.shape.hd;
+                 d["masked"] = a.mask_slot >= 0;
+                 d["n"] = a.shape.bh * a.shape.tq * a.shape.hd;
+                 d["input_slots"] = a.in;
+                 d["output_slots"] = a.out;
+               } else if (s.fused) {
                  d["kind"] = "fused";
                  py::list ops;
                  for (auto& m : s.group.ops) ops.append(m.op.name());

@@ -4,10 +4,9 @@
 // 466-634 (build_fused / build_with).
 #include "plan.h"
 
-#include <queue>
-#include <set>
-
 #include <algorithm>
+#include <cstring>
+#include <queue>
 #include <set>
 
 namespace rg {
@@ -144,7 +143,9 @@ struct Item {
   bool group;
   size_t node;
   std::vector<size_t> members;
-  bool rows = false;  // a row group (members in node order)
+  bool rows = false;     // a row group (members in node order)
+  int64_t attn = -1;     // an attention step: the region's index
+  bool attn_bwd = false;  // its backward step
 };
 
 // BroadcastTo nodes whose every kept consumer is a device-fusable node, and which are not plan
@@ -341,7 +342,7 @@ std::vector<std::vector<size_t>> row_groups(const Graph& g, const std::vector<bo
 }
 
 std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
-                                  const std::vector<bool>& abs) {
+                                  const std::vector<bool>& abs, const std::vector<int64_t>& claimed, size_t n_attn_units) {
   std::vector<bool> up = cfg.hoist ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
   std::vector<Item> items;
   for (size_t i = 0; i < g.nodes.size(); i++)
@@ -351,21 +352,27 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   };
   std::vector<bool> tail = cfg.sink_tails ? tails(g, keep, outputs, abs, dev_fusable) : std::vector<bool>(g.nodes.size(), false);
   const size_t total = g.nodes.size();
+  for (size_t i = 0; i < total; i++) tail[i] = tail[i] && claimed[i] < 0;
   std::vector<std::vector<size_t>> rgs;
   std::vector<int64_t> rg_of(total, -1);
   if (cfg.row_groups) {
     std::vector<bool> excluded(total, false);
-    for (size_t i = 0; i < total; i++) excluded[i] = up[i] || tail[i];
+    for (size_t i = 0; i < total; i++) excluded[i] = up[i] || tail[i] || claimed[i] >= 0;
     rgs = row_groups(g, keep, abs, excluded, dev_fusable, cfg.max_bindings);
     for (size_t k = 0; k < rgs.size(); k++)
       for (size_t m : rgs[k]) rg_of[m] = (int64_t)k;
   }
   // Scheduling units in a topological order of the graph with each row group contracted to one
-  // unit (unit total + k), ties broken by node order.
+  // unit (unit total + k) and each attention step to one (unit total + rgs.size() + its index),
+  // ties broken by node order.
+  const size_t n_units = total + rgs.size() + n_attn_units;
   auto active = [&](size_t i) { return keep[i] && !up[i] && !leaf(g.nodes[i]); };
-  auto unit_of = [&](size_t i) -> size_t { return rg_of[i] >= 0 ? total + (size_t)rg_of[i] : i; };
-  std::vector<std::vector<size_t>> unit_users(total + rgs.size());
-  std::vector<size_t> indeg(total + rgs.size(), 0), first(total + rgs.size(), SIZE_MAX);
+  auto unit_of = [&](size_t i) -> size_t {
+    if (claimed[i] >= 0) return total + rgs.size() + (size_t)claimed[i];
+    return rg_of[i] >= 0 ? total + (size_t)rg_of[i] : i;
+  };
+  std::vector<std::vector<size_t>> unit_users(n_units);
+  std::vector<size_t> indeg(n_units, 0), first(n_units, SIZE_MAX);
   for (size_t i = 0; i < total; i++) {
     if (!active(i)) continue;
     size_t u = unit_of(i);
@@ -379,7 +386,7 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     }
   }
   std::priority_queue<std::pair<size_t, size_t>, std::vector<std::pair<size_t, size_t>>, std::greater<>> ready;
-  for (size_t u = 0; u < total + rgs.size(); u++)
+  for (size_t u = 0; u < n_units; u++)
     if (first[u] != SIZE_MAX && indeg[u] == 0) ready.push({first[u], u});
   std::vector<size_t> order;
   while (!ready.empty()) {
@@ -391,14 +398,18 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   }
   std::vector<size_t> sunk;
   std::vector<size_t> level(total, 0);
-  std::vector<std::vector<size_t>> by_level;  // node ids, and total + k for row group k
+  // Members of each attention unit, in node order.
+  std::vector<std::vector<size_t>> attn_members(n_attn_units);
+  for (size_t i = 0; i < total; i++)
+    if (claimed[i] >= 0) attn_members[(size_t)claimed[i]].push_back(i);
+  std::vector<std::vector<size_t>> by_level;  // node ids, and total + k for unit k
   for (size_t u : order) {
     if (u >= total) {
-      const auto& members = rgs[u - total];
+      const auto& members = u < total + rgs.size() ? rgs[u - total] : attn_members[u - total - rgs.size()];
       size_t deepest = 0;
       for (size_t m : members)
         for (uint32_t x : g.nodes[m].inputs)
-          if (rg_of[x] != (int64_t)(u - total)) deepest = std::max(deepest, level[x]);
+          if (unit_of(x) != u) deepest = std::max(deepest, level[x]);
       for (size_t m : members) level[m] = deepest + 1;
       if (by_level.size() <= deepest + 1) by_level.resize(deepest + 2);
       by_level[deepest + 1].push_back(u);
@@ -435,8 +446,12 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   if (!sunk.empty()) by_level.push_back(sunk);
   for (auto& nodes : by_level) {
     std::vector<std::vector<size_t>> groups;
-    std::vector<size_t> aliases, rows;
+    std::vector<size_t> aliases, rows, attns;
     for (size_t i : nodes) {
+      if (i >= total + rgs.size()) {
+        attns.push_back(i - total - rgs.size());
+        continue;
+      }
       if (i >= total) {
         rows.push_back(i - total);  // row groups read lower levels only: they follow the groups
         continue;
@@ -471,6 +486,7 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
         for (size_t x : m) items.push_back({false, x, {}});
     }
     for (size_t k : rows) items.push_back({true, 0, rgs[k], true});
+    for (size_t k : attns) items.push_back({false, 0, {}, false, (int64_t)(k / 2), (k % 2) == 1});
     for (size_t a : aliases) items.push_back({false, a, {}});
   }
   return items;
@@ -479,8 +495,8 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
 // Greedy fusion: one open group. Instructions independent of the group are emitted first; one
 // that reads a member closes the group, which keeps the group free of cycles (plan.rs:311-350).
 std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
-                           const std::vector<bool>& abs) {
-  if (cfg.device && cfg.levels) return schedule_levels(g, keep, outputs, cfg, abs);
+                           const std::vector<bool>& abs, const std::vector<int64_t>& claimed, size_t n_attn_units) {
+  if (cfg.device && cfg.levels) return schedule_levels(g, keep, outputs, cfg, abs, claimed, n_attn_units);
   std::vector<Item> items;
   std::vector<size_t> open;
   auto close = [&]() {
@@ -617,19 +633,74 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
     }
   }
 
+  // Attention regions: members are computed by the fused steps, so their reads do not count;
+  // each step reads its region's operands instead (the backward also O and the mask).
+  std::vector<AttnRegion> regions;
+  std::vector<int64_t> claimed(total, -1);  // attention unit: 2 * region (+ 1 for the backward)
+  if (fuse && fuse->attention && fuse->device && fuse->levels) regions = match_attention(g, keep, outputs);
+  auto region_inputs = [&](const AttnRegion& r, bool bwd) {
+    std::vector<uint32_t> in = {r.q, r.k, r.v};
+    if (bwd) {
+      in.push_back(r.o);
+      in.push_back(r.d_o);
+    }
+    if (r.mask >= 0) in.push_back((uint32_t)r.mask);
+    return in;
+  };
+  for (size_t k = 0; k < regions.size(); k++) {
+    const AttnRegion& r = regions[k];
+    for (int b = 0; b < 2; b++) {
+      if (b && !r.has_bwd) continue;
+      for (uint32_t m : b ? r.bwd : r.fwd) {
+        claimed[m] = (int64_t)(2 * k + b);
+        for (uint32_t x : g.nodes[m].inputs) uses[x]--;
+      }
+      for (uint32_t x : region_inputs(r, b)) uses[x]++;
+    }
+  }
+  std::vector<size_t> stats_slot(regions.size(), SIZE_MAX);
+
   std::vector<Item> items;
   std::vector<bool> abs = fuse ? absorbed_broadcasts(g, keep, outputs, *fuse) : std::vector<bool>(total, false);
   std::vector<bool> exact(total, false);
   if (fuse && fuse->exact_outputs)
     for (uint32_t o : outputs) exact[o] = true;
   if (fuse) {
-    items = schedule(g, keep, outputs, *fuse, abs);
+    items = schedule(g, keep, outputs, *fuse, abs, claimed, 2 * regions.size());
   } else {
     for (size_t i = 0; i < total; i++)
       if (keep[i] && !leaf(g.nodes[i])) items.push_back({false, i, {}});
   }
 
   for (auto& item : items) {
+    if (item.attn >= 0) {
+      const AttnRegion& r = regions[(size_t)item.attn];
+      const bool bwd = item.attn_bwd;
+      Step st;
+      st.attn = true;
+      Attn& at = st.att;
+      at.backward = bwd;
+      at.shape = attn_shape(r, g);
+      at.div = r.div;
+      at.fill = r.fill;
+      std::vector<uint32_t> ins = region_inputs(r, bwd);
+      at.mask_slot = r.mask >= 0 ? (int64_t)value_slot[(size_t)r.mask] : -1;
+      for (size_t j = 0; j < (bwd ? 5u : 3u); j++) at.in.push_back(value_slot[ins[j]]);
+      if (!bwd) stats_slot[(size_t)item.attn] = a.new_slot(DType::F32, attn_stats_words(r, g), true);
+      at.stats_slot = stats_slot[(size_t)item.attn];
+      std::vector<uint32_t> outs = bwd ? std::vector<uint32_t>{r.dq, r.dk, r.dv} : std::vector<uint32_t>{r.o};
+      for (uint32_t o : outs) {
+        size_t sl = a.alloc(g.nodes[o].dtype, g.nodes[o].n(), exact[o]);
+        value_slot[o] = sl;
+        at.out.push_back(sl);
+        p.naive_bytes += g.nodes[o].n() * dsize(g.nodes[o].dtype);
+      }
+      at.node = bwd ? r.dq : r.o;
+      p.steps.push_back(std::move(st));
+      for (uint32_t x : ins)
+        if (--uses[x] == 0) a.release(value_slot[x]);
+      continue;
+    }
     if (item.group) {
       const auto& members = item.members;
       // Absorbed broadcasts become aliases of their source on first use (as plan.rs:565-575).
@@ -735,8 +806,11 @@ size_t Plan::planned_bytes() const {
 
 double Plan::gpu_cost_estimate(const Fuse& f) const {
   double c = 0;
-  for (auto& s : steps)
-    c += f.per_dispatch_ns + f.per_element_ns * (double)(s.fused ? s.group.n * s.group.outputs.size() : s.instr.n);
+  for (auto& s : steps) {
+    double n = s.attn ? (double)(s.att.shape.bh * s.att.shape.tq * s.att.shape.hd * s.att.out.size())
+                      : (double)(s.fused ? s.group.n * s.group.outputs.size() : s.instr.n);
+    c += f.per_dispatch_ns + f.per_element_ns * n;
+  }
   return c;
 }
 
@@ -834,6 +908,31 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
   }
   w.push_back((int64_t)steps.size());
   for (auto& st : steps) {
+    if (st.attn) {
+      const Attn& at = st.att;
+      w.push_back(RG_STEP_ATTN);
+      w.push_back((int64_t)at.dtype);
+      w.push_back(at.backward ? 1 : 0);
+      w.push_back((int64_t)at.shape.bh);
+      w.push_back((int64_t)at.shape.heads);
+      w.push_back((int64_t)at.shape.tq);
+      w.push_back((int64_t)at.shape.tk);
+      w.push_back((int64_t)at.shape.hd);
+      int64_t bits;
+      memcpy(&bits, &at.div, 8);
+      w.push_back(bits);
+      memcpy(&bits, &at.fill, 8);
+      w.push_back(bits);
+      w.push_back(at.mask_slot);
+      for (int k = 0; k < 4; k++) w.push_back(at.shape.mask_strides[k]);
+      w.push_back((int64_t)at.stats_slot);
+      w.push_back((int64_t)at.in.size());
+      for (size_t x : at.in) w.push_back((int64_t)x);
+      w.push_back((int64_t)at.out.size());
+      for (size_t x : at.out) w.push_back((int64_t)x);
+      w.push_back(at.node);
+      continue;
+    }
     if (!st.fused) {
       const Instr& in = st.instr;
       w.push_back(RG_STEP_INSTR);

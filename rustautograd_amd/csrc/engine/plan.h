@@ -41,13 +41,39 @@ struct Fuse {
   // Plan outputs get buffers of exactly their size, so that a run loop can hand state over by
   // swapping buffers (validate.rs:303-318 swaps only equal-capacity slots) instead of copying.
   bool exact_outputs;
+  // Level order only: scaled, masked softmax attention and its backward form become fused
+  // attention steps (attention.cpp).
+  bool attention;
 
-  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false, false, false}; }
-  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false, false, false}; }
+  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false, false, false, false}; }
+  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false, false, false, false}; }
   // MI355X: ~4 us per dispatch inside a captured graph, ~0.001 ns per fp32 element written at
   // HBM speed, and 288 GB of HBM so level order is capped far higher.
-  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true, true, true}; }
+  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true, true, true, true}; }
 };
+
+// An attention region of the graph (attention.cpp): the nodes a fused forward step computes
+// (`fwd`, with O = node `o` its one output) and, when the graph differentiates O, the nodes a
+// fused backward step computes (`bwd`, outputs dq, dk, dv for the cotangent node `d_o`).
+struct AttnRegion {
+  uint32_t q = 0, k = 0, v = 0, o = 0, s = 0, e = 0, z = 0, p = 0, y = 0;
+  int64_t mask = -1, mask_bcast = -1;  // the mask's source node and its broadcast
+  double div = 1.0, fill = 0.0;        // Y = where(mask, S / div, fill)
+  bool scaled = false;
+  std::vector<uint32_t> fwd, bwd, optional;
+  bool has_bwd = false;
+  uint32_t d_o = 0, dq = 0, dk = 0, dv = 0;
+};
+// Problem sizes of a region: bh = batch * heads independent (tq x hd, tk x hd) problems, the
+// mask's element strides over (batch, heads, query, key) and its number of distinct slices.
+struct AttnShape {
+  size_t bh = 1, heads = 1, tq = 0, tk = 0, hd = 0, mask_slices = 0;
+  int64_t mask_strides[4] = {0, 0, 0, 0};
+};
+std::vector<AttnRegion> match_attention(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs);
+AttnShape attn_shape(const AttnRegion& r, const Graph& g);
+// 32-bit words of the statistics slot a region's steps share (include/rg_plan.h RG_STEP_ATTN).
+size_t attn_stats_words(const AttnRegion& r, const Graph& g);
 
 struct Instr {
   Op op;
@@ -89,10 +115,24 @@ struct Fused {
   std::vector<Shape> input_shapes;
 };
 
+// A fused attention step (include/rg_plan.h RG_STEP_ATTN; device plans only).
+struct Attn {
+  bool backward = false;
+  DType dtype = DType::F32;
+  AttnShape shape;
+  double div = 1.0, fill = 0.0;
+  int64_t mask_slot = -1;
+  size_t stats_slot = 0;
+  std::vector<size_t> in, out;  // forward: q, k, v -> O; backward: q, k, v, O, dO -> dq, dk, dv
+  uint32_t node = 0;            // the O node (forward) or the dq node (backward)
+};
+
 struct Step {
   bool fused = false;
+  bool attn = false;
   Instr instr;
   Fused group;
+  Attn att;
 };
 
 struct PlanOutput {

@@ -708,7 +708,10 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
   for (size_t s = 0; s < plan.steps.size(); s++) {
     const Step& st = plan.steps[s];
     std::string key;
-    if (st.fused) {
+    if (st.attn) {
+      key = std::string(st.att.backward ? "attention backward" : "attention") + " bh=" + std::to_string(st.att.shape.bh) +
+            " t=" + std::to_string(st.att.shape.tq) + "x" + std::to_string(st.att.shape.tk) + " hd=" + std::to_string(st.att.shape.hd);
+    } else if (st.fused) {
       key = "fused[";
       for (size_t m = 0; m < st.group.ops.size(); m++) key += std::string(m ? "," : "") + st.group.ops[m].op.name();
       key += "] n=" + std::to_string(st.group.n);

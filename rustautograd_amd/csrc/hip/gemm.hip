@@ -1,12 +1,19 @@
 // Dense products for MatMul / MatMulT (reference src/plan.rs:1453-1493, flags from
 // src/optimize.rs:338-350).
 //
-// fp32: block tiles of 128x128, 128x64, 64x128, 64x64, 128x32 or 32x128 staged through LDS in
-// K steps of 16, four wave64s per block each owning 32x32 MFMA tiles (v_mfma_f32_32x32x2f32).
-// Transposed operands are read through their flags: the loader transposes while staging, so no
-// copy is made. The tile is chosen per product so that the launch fills 256 CUs with little
-// padding (32-wide tiles for 32-wide attention heads); products whose output still has too few
-// tiles split K and combine the partial sums in a fixed order (deterministic).
+// fp32: block tiles from 128x128 down to 128x32 / 32x128, four wave64s per block, each wave
+// owning a grid of 16x16 MFMA tiles (v_mfma_f32_16x16x4f32). Operands are staged through
+// double-buffered LDS in their own global layout, so no operand is transposed while staging:
+//  - a K-contiguous operand (A, or B when transposed) sits in LDS as [rows][BK + 4]; one 16-byte
+//    LDS read gives a lane four consecutive k of one tile row, feeding four MFMA k-steps;
+//  - an M- or N-contiguous operand sits as [BK][cols]; one read gives a lane T consecutive
+//    columns at one k, one for each of the wave's T tiles (tile t holds columns t, t + T, ...).
+// Global loads are 16-byte vectors without branches: a vector lies wholly inside or outside the
+// operand (leading dimensions are multiples of 4), and an outside vector reads a valid address
+// and is replaced by zeros; products whose tiles divide M, N and K skip even that check. The tile
+// is chosen per product to fill 256 CUs with little padding (32-wide tiles for 32-wide attention
+// heads); products whose output still has too few tiles split K and combine the partial sums in a
+// fixed order (deterministic). Unaligned operands take the same kernel with scalar loads.
 // fp64 and tiny or skinny fp32 products use a plain kernel, one thread per output element.
 #include <hip/hip_runtime.h>
 
@@ -18,33 +25,10 @@ namespace rgk {
 
 namespace {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-constexpr int PAD = 4;
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int64_t batch_offset(const int64_t* offs, uint64_t stride, uint32_t b) {
   return offs ? offs[b] : (int64_t)(stride * b);
-}
-
-// Loads N (2, 4 or 8) consecutive elements of a row-major row starting at column c, zero-filling
-// past `cols` and when the row is out of range. `vec`: the row and c allow 16/8-byte loads.
-template <int N>
-__device__ __forceinline__ void loadn(const float* row, int64_t c, int64_t cols, bool row_ok, bool vec, float v[N]) {
-  if (vec && row_ok && c + N <= cols) {
-    if constexpr (N == 2) {
-      float2 x = *(const float2*)(row + c);
-      v[0] = x.x; v[1] = x.y;
-    } else {
-#pragma unroll
-      for (int q = 0; q < N; q += 4) {
-        float4 x = *(const float4*)(row + c + q);
-        v[q] = x.x; v[q + 1] = x.y; v[q + 2] = x.z; v[q + 3] = x.w;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < N; q++) v[q] = (row_ok && c + q < cols) ? row[c + q] : 0.0f;
-  }
 }
 
 // Which output tile a block computes. The dispatcher deals consecutive blocks round-robin over
@@ -69,23 +53,80 @@ __device__ __forceinline__ TileIndex tile_of(uint32_t tiles_m, uint32_t tiles_n,
   return {first + in % rows, in / rows, z};
 }
 
-// C = op(A) op(B) for one BM x BN block tile. Four wave64s in a WM x WN grid; each wave owns a
-// (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA tiles (v_mfma_f32_32x32x2f32). Operands are staged
-// through double-buffered LDS in K steps of BK, K-major, so each MFMA operand is one
-// conflict-free 32-lane LDS row read; transposed operands are transposed while staging.
-// The grid is one-dimensional: tiles_m * tiles_n * batch * splits blocks (tile_of).
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
-__global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
-                                                   int M, int N, int K, const int64_t* a_off, const int64_t* b_off, uint64_t a_stride,
-                                                   uint64_t b_stride, int splits, int k_per_split, float* __restrict__ partial,
-                                                   bool vec_a, bool vec_b, uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
-  static_assert(WM * WN == 4, "four waves");
-  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
-  static_assert(TM >= 1 && TN >= 1, "wave tile of at least 32x32");
-  // Loader geometry: 256 threads cover a BM x BK (A) and a BK x BN (B) tile.
-  constexpr int EA = BM * BK / 256, EB = BN * BK / 256;
-  __shared__ float As[2][BK][BM + PAD];
-  __shared__ float Bs[2][BK][BN + PAD];
+// Load modes: every vector inside the operand (no checks), checked 16-byte vectors, or checked
+// scalar loads (operands whose rows are not 16-byte aligned).
+enum LoadMode { LOAD_EVEN = 0, LOAD_VEC = 1, LOAD_SCALAR = 2 };
+
+// Stages an R x W tile (W contiguous floats per row, W % 4 == 0) of a row-major operand with
+// leading dimension `ld`, rows r0.. (valid below `rows`) and columns c0.. (valid below `cols`),
+// through registers: NT threads, one 4-float vector per thread and pass.
+template <int R, int W, int NT, int MODE>
+struct Stager {
+  static constexpr int NVEC = R * W / 4;
+  static constexpr int PER = (NVEC + NT - 1) / NT;
+  float4 v[PER];
+  __device__ __forceinline__ void load(const float* base, int64_t ld, int r0, int c0, int rows, int cols, int tid) {
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+      const int idx = q * NT + tid;
+      const int r = idx / (W / 4), c = (idx % (W / 4)) * 4;
+      const bool live = NVEC % NT == 0 || idx < NVEC;
+      const int gr = r0 + r, gc = c0 + c;
+      if constexpr (MODE == LOAD_SCALAR) {
+        const float* p = base + (int64_t)gr * ld + gc;
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          bool ok = live && gr < rows && gc + e < cols;
+          t[e] = ok ? p[e] : 0.0f;
+        }
+        v[q] = make_float4(t[0], t[1], t[2], t[3]);
+      } else {
+        const bool ok = live && (MODE == LOAD_EVEN || (gr < rows && gc < cols));
+        const float4 x = *(const float4*)(ok ? base + (int64_t)gr * ld + gc : base);
+        v[q] = ok ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float* lds, int ldl, int tid) const {
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+      const int idx = q * NT + tid;
+      if (NVEC % NT == 0 || idx < NVEC) *(float4*)(lds + (idx / (W / 4)) * ldl + (idx % (W / 4)) * 4) = v[q];
+    }
+  }
+};
+
+template <int T>
+__device__ __forceinline__ void lds_read(const float* p, float* v) {
+  if constexpr (T == 1) {
+    v[0] = *p;
+  } else if constexpr (T == 2) {
+    float2 x = *(const float2*)p;
+    v[0] = x.x; v[1] = x.y;
+  } else {
+    float4 x = *(const float4*)p;
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  }
+}
+
+// C = op(A) op(B) for one BM x BN block tile; WM x WN wave64s, each owning (BM/WM) x (BN/WN) as
+// TM x TN MFMA tiles of 16x16. The grid is one-dimensional: tiles_m * tiles_n * batch * splits
+// blocks (tile_of); split `sp` covers K range [sp * k_per_split, (sp + 1) * k_per_split).
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE>
+__global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+                                                           int M, int N, int K, const int64_t* a_off, const int64_t* b_off,
+                                                           uint64_t a_stride, uint64_t b_stride, int splits, int k_per_split,
+                                                           float* __restrict__ partial, uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16;
+  static_assert(TM >= 1 && TN >= 1 && TM <= 4 && TN <= 4 && (TM & (TM - 1)) == 0 && (TN & (TN - 1)) == 0, "wave tiles");
+  static_assert(BK % 16 == 0, "K step");
+  constexpr bool AK = !TA, BKC = TB;  // K-contiguous operands
+  constexpr int LDA = AK ? BK + 4 : BM, LDB = BKC ? BK + 4 : BN;
+  constexpr int SA = AK ? BM * LDA : BK * LDA, SB = BKC ? BN * LDB : BK * LDB;
+  __shared__ float As[2][SA];
+  __shared__ float Bs[2][SB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const TileIndex ti = tile_of(tiles_m, tiles_n, swizzle);
@@ -96,96 +137,126 @@ __global__ void __launch_bounds__(256) k_gemm_mfma(const float* __restrict__ A, 
   const int kbeg = sp * k_per_split, kend = min(K, kbeg + k_per_split);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
-  float ra[EA], rb[EB];
+  Stager<AK ? BM : BK, AK ? BK : BM, NT, MODE> sa;
+  Stager<BKC ? BN : BK, BKC ? BK : BN, NT, MODE> sb;
   auto load_tiles = [&](int k0) {
-    if (!TA) {  // A is [M,K]: BM rows of BK k
-      constexpr int TPR = BK / EA;
-      int m = tid / TPR, kc = (tid % TPR) * EA;
-      loadn<EA>(Ab + (int64_t)(m0 + m) * K, k0 + kc, kend, m0 + m < M, vec_a, ra);
-    } else {    // A is [K,M]: BK rows of BM m
-      constexpr int TPR = BM / EA;
-      int k = tid / TPR, mc = (tid % TPR) * EA;
-      loadn<EA>(Ab + (int64_t)(k0 + k) * M, m0 + mc, M, k0 + k < kend, vec_a, ra);
-    }
-    if (!TB) {  // B is [K,N]: BK rows of BN n
-      constexpr int TPR = BN / EB;
-      int k = tid / TPR, nc = (tid % TPR) * EB;
-      loadn<EB>(Bb + (int64_t)(k0 + k) * N, n0 + nc, N, k0 + k < kend, vec_b, rb);
-    } else {    // B is [N,K]: BN rows of BK k
-      constexpr int TPR = BK / EB;
-      int n = tid / TPR, kc = (tid % TPR) * EB;
-      loadn<EB>(Bb + (int64_t)(n0 + n) * K, k0 + kc, kend, n0 + n < N, vec_b, rb);
-    }
-  };
-  auto store_tiles = [&](int buf) {
-    if (!TA) {
-      constexpr int TPR = BK / EA;
-      int m = tid / TPR, kc = (tid % TPR) * EA;
-#pragma unroll
-      for (int q = 0; q < EA; q++) As[buf][kc + q][m] = ra[q];
-    } else {
-      constexpr int TPR = BM / EA;
-      int k = tid / TPR, mc = (tid % TPR) * EA;
-#pragma unroll
-      for (int q = 0; q < EA; q++) As[buf][k][mc + q] = ra[q];
-    }
-    if (!TB) {
-      constexpr int TPR = BN / EB;
-      int k = tid / TPR, nc = (tid % TPR) * EB;
-#pragma unroll
-      for (int q = 0; q < EB; q++) Bs[buf][k][nc + q] = rb[q];
-    } else {
-      constexpr int TPR = BK / EB;
-      int n = tid / TPR, kc = (tid % TPR) * EB;
-#pragma unroll
-      for (int q = 0; q < EB; q++) Bs[buf][kc + q][n] = rb[q];
-    }
+    if (AK) sa.load(Ab, K, m0, k0, M, kend, tid);
+    else sa.load(Ab, M, k0, m0, kend, M, tid);
+    if (BKC) sb.load(Bb, K, n0, k0, N, kend, tid);
+    else sb.load(Bb, N, k0, n0, kend, N, tid);
   };
 
-  floatx16 acc[TM][TN];
+  floatx4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   if (nk > 0) {
     load_tiles(kbeg);
-    store_tiles(0);
+    sa.store(As[0], LDA, tid);
+    sb.store(Bs[0], LDB, tid);
   }
   __syncthreads();
-  const int lrow = lane & 31, lk = lane >> 5;
+  // MFMA 16x16x4 lane roles: lane l supplies row (A) / column (B) l % 16 at k = l / 16. Within a
+  // group of 16 k the four k-steps j give lane l the k index 4 * (l / 16) + j in both operands.
+  const int l16 = lane & 15, q4 = (lane >> 4) * 4;
   for (int t = 0; t < nk; t++) {
     const int buf = t & 1;
-    if (t + 1 < nk) load_tiles(kbeg + (t + 1) * BK);
+    const bool more = t + 1 < nk;
+    if (more) load_tiles(kbeg + (t + 1) * BK);
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      float av[TM], bv[TN];
+    for (int kg = 0; kg < BK; kg += 16) {
+      float a[4][TM], bv[4][TN];  // [k-step][tile]
+      if (AK) {
 #pragma unroll
-      for (int i = 0; i < TM; i++) av[i] = As[buf][kk + lk][wm * WTM + i * 32 + lrow];
+        for (int i = 0; i < TM; i++) {
+          float v[4];
+          lds_read<4>(as + (wm * WTM + i * 16 + l16) * LDA + kg + q4, v);
 #pragma unroll
-      for (int j = 0; j < TN; j++) bv[j] = Bs[buf][kk + lk][wn * WTN + j * 32 + lrow];
+          for (int j = 0; j < 4; j++) a[j][i] = v[j];
+        }
+      } else {
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+        for (int j = 0; j < 4; j++) lds_read<TM>(as + (kg + q4 + j) * LDA + wm * WTM + TM * l16, a[j]);
+      }
+      if (BKC) {
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TN; i++) {
+          float v[4];
+          lds_read<4>(bs + (wn * WTN + i * 16 + l16) * LDB + kg + q4, v);
+#pragma unroll
+          for (int j = 0; j < 4; j++) bv[j][i] = v[j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) lds_read<TN>(bs + (kg + q4 + j) * LDB + wn * WTN + TN * l16, bv[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int n = 0; n < TN; n++) {
+            // With a K-contiguous B the product is formed transposed (B supplies the MFMA rows), so
+            // that each lane ends up with four adjacent output columns.
+            if constexpr (BKC) acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j][n], a[j][i], acc[i][n], 0, 0, 0);
+            else acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][i], bv[j][n], acc[i][n], 0, 0, 0);
+          }
     }
-    if (t + 1 < nk) store_tiles(buf ^ 1);
+    if (more) {
+      sa.store(As[buf ^ 1], LDA, tid);
+      sb.store(Bs[buf ^ 1], LDB, tid);
+    }
     __syncthreads();
   }
-  // Accumulator register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  // Accumulator register r of lane l holds MFMA row 4 * (l / 16) + r, column l % 16 (for the
+  // transposed form: output row l % 16, column 4 * (l / 16) + r). MFMA tile i row rho is block row
+  // 16 i + rho (K-contiguous A) or TM rho + i (M-contiguous A); tile n column gamma is block column
+  // 16 n + gamma (K-contiguous B) or TN gamma + n (N-contiguous B). Either way a lane holds
+  // adjacent output columns: four in one tile (K-contiguous B) or one in each of its TN tiles.
   float* out = splits > 1 ? partial + ((uint64_t)b * splits + sp) * (uint64_t)M * N : C + (uint64_t)b * M * N;
+  const bool vec_out = MODE != LOAD_SCALAR && N % 4 == 0;
+  if constexpr (BKC) {
 #pragma unroll
-  for (int i = 0; i < TM; i++)
+    for (int i = 0; i < TM; i++) {
+      const int row = m0 + wm * WTM + (AK ? i * 16 + l16 : TM * l16 + i);
+      if (row >= M) continue;
+      float* crow = out + (uint64_t)row * N;
 #pragma unroll
-    for (int j = 0; j < TN; j++)
+      for (int n = 0; n < TN; n++) {
+        const int col = n0 + wn * WTN + n * 16 + q4;
+        if (vec_out && col + 4 <= N) {
+          *(float4*)(crow + col) = make_float4(acc[i][n][0], acc[i][n][1], acc[i][n][2], acc[i][n][3]);
+        } else {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        int col = n0 + wn * WTN + j * 32 + lrow;
-        if (row < M && col < N) out[(uint64_t)row * N + col] = acc[i][j][r];
+          for (int r = 0; r < 4; r++)
+            if (col + r < N) crow[col + r] = acc[i][n][r];
+        }
       }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int rho = q4 + r;
+        const int row = m0 + wm * WTM + (AK ? i * 16 + rho : TM * rho + i);
+        if (row >= M) continue;
+        float* crow = out + (uint64_t)row * N;
+        const int col = n0 + wn * WTN + TN * l16;
+        if (TN > 1 && vec_out && col + TN <= N) {
+          if constexpr (TN == 4) *(float4*)(crow + col) = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+          else if constexpr (TN == 2) *(float2*)(crow + col) = make_float2(acc[i][0][r], acc[i][1][r]);
+        } else {
+#pragma unroll
+          for (int n = 0; n < TN; n++)
+            if (col + n < N) crow[col + n] = acc[i][n][r];
+        }
+      }
+  }
 }
 
 __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ partial, float* __restrict__ C, uint64_t mn, int splits) {
@@ -222,20 +293,21 @@ bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
 }
 
 struct TileCfg {
-  int bm, bn, bk;
+  int bm, bn, bk, wm, wn;
 };
 
-// Block tile, from measurements of C4's products on MI355X (K steps of 32 hide more load latency
-// for the smaller tiles): 32-wide tiles for outputs 32..96 wide or 32 tall (attention heads,
-// the vocabulary), the largest square-ish tile that still yields two blocks per CU (512), else
-// 64x64 (split over K later when even that leaves the CUs idle).
+// Block tile, from measurements of C4's products on MI355X: 32-wide tiles for outputs 32..96 wide
+// or 32 tall (attention heads, the vocabulary); 128x128 when that still yields two blocks per CU
+// (512), then 128x64 at two blocks per CU, 64x128 at one, else 64x64 (split over K later when even
+// that leaves the CUs idle).
 TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t batch) {
   auto blocks = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
-  if (n <= 96 && n % 32 == 0) return {128, 32, 32};
-  if (m <= 32) return {32, 128, 32};
-  if (blocks(128, 128) >= 512) return {128, 128, 16};
-  if (blocks(128, 64) >= 512) return {128, 64, 32};
-  return {64, 64, 32};
+  if (n <= 96 && n % 32 == 0) return {128, 32, 32, 4, 1};
+  if (m <= 32) return {32, 128, 32, 1, 4};
+  if (blocks(128, 128) >= 512) return {128, 128, 16, 2, 2};
+  if (blocks(128, 64) >= 512) return {128, 64, 16, 2, 2};
+  if (blocks(64, 128) >= 256) return {64, 128, 32, 2, 2};
+  return {64, 64, 32, 2, 2};
 }
 
 int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
@@ -246,36 +318,43 @@ int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t b
   return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 16));
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
-void launch_flags(hipStream_t s, bool ta, bool tb, dim3 grid, const float* A, const float* B, float* C, int M, int N, int K,
-                  const int64_t* a_off, const int64_t* b_off, uint64_t as, uint64_t bs, int splits, int kps, float* part, bool va,
-                  bool vb, uint32_t tm, uint32_t tn, int swizzle) {
-#define RG_GEMM(TA_, TB_)                                                                                                     \
-  hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, TA_, TB_>), grid, dim3(256), 0, s, A, B, C, M, N, K, a_off, b_off, as, bs, \
-                     splits, kps, part, va, vb, tm, tn, swizzle)
-  if (!ta && !tb) RG_GEMM(false, false);
-  else if (ta && !tb) RG_GEMM(true, false);
-  else if (!ta && tb) RG_GEMM(false, true);
-  else RG_GEMM(true, true);
+struct Launch {
+  dim3 grid;
+  const float *a, *b;
+  float* c;
+  int m, n, k;
+  const int64_t *a_off, *b_off;
+  uint64_t as, bs;
+  int splits, kps;
+  float* part;
+  uint32_t tm, tn;
+};
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+void launch_mode(hipStream_t s, int mode, const Launch& l) {
+#define RG_GEMM(MODE_)                                                                                                             \
+  hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, TA, TB, MODE_>), l.grid, dim3(64 * WM * WN), 0, s, l.a, l.b, l.c, l.m, l.n, l.k, \
+                     l.a_off, l.b_off, l.as, l.bs, l.splits, l.kps, l.part, l.tm, l.tn, 1)
+  if (mode == LOAD_EVEN) RG_GEMM(LOAD_EVEN);
+  else if (mode == LOAD_VEC) RG_GEMM(LOAD_VEC);
+  else RG_GEMM(LOAD_SCALAR);
 #undef RG_GEMM
 }
 
+template <int BM, int BN, int BK, int WM, int WN>
+void launch_flags(hipStream_t s, bool ta, bool tb, int mode, const Launch& l) {
+  if (!ta && !tb) launch_mode<BM, BN, BK, WM, WN, false, false>(s, mode, l);
+  else if (ta && !tb) launch_mode<BM, BN, BK, WM, WN, true, false>(s, mode, l);
+  else if (!ta && tb) launch_mode<BM, BN, BK, WM, WN, false, true>(s, mode, l);
+  else launch_mode<BM, BN, BK, WM, WN, true, true>(s, mode, l);
+}
+
 // Instantiates the tile shapes pick_tile can return.
-void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, dim3 grid, const float* A, const float* B, float* C, int M, int N,
-                 int K, const int64_t* a_off, const int64_t* b_off, uint64_t as, uint64_t bs, int splits, int kps, float* part, bool va,
-                 bool vb, uint32_t tm, uint32_t tn, int swizzle) {
-#define RG_TILE(BM_, BN_, BK_, WM_, WN_)                                                                                      \
-  if (t.bm == BM_ && t.bn == BN_ && t.bk == BK_)                                                                               \
-    return launch_flags<BM_, BN_, BK_, WM_, WN_>(s, ta, tb, grid, A, B, C, M, N, K, a_off, b_off, as, bs, splits, kps, part, va, vb, \
-                                                 tm, tn, swizzle)
+void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, const Launch& l) {
+#define RG_TILE(BM_, BN_, BK_, WM_, WN_) \
+  if (t.bm == BM_ && t.bn == BN_ && t.bk == BK_) return launch_flags<BM_, BN_, BK_, WM_, WN_>(s, ta, tb, mode, l)
   RG_TILE(128, 128, 16, 2, 2);
   RG_TILE(128, 64, 16, 2, 2);
-  RG_TILE(64, 128, 16, 2, 2);
-  RG_TILE(64, 64, 16, 2, 2);
-  RG_TILE(128, 32, 16, 4, 1);
-  RG_TILE(32, 128, 16, 1, 4);
-  RG_TILE(128, 128, 32, 2, 2);
-  RG_TILE(128, 64, 32, 2, 2);
   RG_TILE(64, 128, 32, 2, 2);
   RG_TILE(64, 64, 32, 2, 2);
   RG_TILE(128, 32, 32, 4, 1);
@@ -298,20 +377,34 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     int splits = split_count(t, g.m, g.n, g.k, g.batch);
     int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
     splits = (int)((g.k + kps - 1) / kps);
+    // 16-byte vector loads need 16-byte aligned operand rows: aligned bases, leading dimensions
+    // (K, or M / N for the contiguous-column layouts) and batch offsets that are multiples of 4.
     auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-    bool offs_ok_a = g.a_off == nullptr && g.a_stride % 4 == 0;
-    bool offs_ok_b = g.b_off == nullptr && g.b_stride % 4 == 0;
-    // Vector loads run along K for A (untransposed) or M (transposed); likewise for B.
-    bool vec_a = aligned(g.a) && offs_ok_a && ((g.ta ? g.m : g.k) % 4 == 0);
-    bool vec_b = aligned(g.b) && offs_ok_b && ((g.tb ? g.k : g.n) % 4 == 0);
-    uint32_t tiles_m = (uint32_t)((g.m + t.bm - 1) / t.bm), tiles_n = (uint32_t)((g.n + t.bn - 1) / t.bn);
-    dim3 grid((uint32_t)(tiles_m * tiles_n * g.batch * splits));
-    float* part = splits > 1 ? (float*)g.workspace : nullptr;
-    launch_mfma(s, t, g.ta, g.tb, grid, (const float*)g.a, (const float*)g.b, (float*)g.c, (int)g.m, (int)g.n, (int)g.k, g.a_off,
-                g.b_off, g.a_stride, g.b_stride, splits, kps, part, vec_a, vec_b, tiles_m, tiles_n, 1);
+    bool vec = aligned(g.a) && aligned(g.b) && g.k % 4 == 0 && (!g.ta || g.m % 4 == 0) && (g.tb || g.n % 4 == 0) &&
+               (g.a_off ? g.a_off4 : g.a_stride % 4 == 0) && (g.b_off ? g.b_off4 : g.b_stride % 4 == 0);
+    bool even = g.m % t.bm == 0 && g.n % t.bn == 0 && g.k % t.bk == 0 && kps % t.bk == 0;
+    int mode = !vec ? LOAD_SCALAR : even ? LOAD_EVEN : LOAD_VEC;
+    Launch l;
+    l.tm = (uint32_t)((g.m + t.bm - 1) / t.bm);
+    l.tn = (uint32_t)((g.n + t.bn - 1) / t.bn);
+    l.grid = dim3((uint32_t)(l.tm * l.tn * g.batch * splits));
+    l.a = (const float*)g.a;
+    l.b = (const float*)g.b;
+    l.c = (float*)g.c;
+    l.m = (int)g.m;
+    l.n = (int)g.n;
+    l.k = (int)g.k;
+    l.a_off = g.a_off;
+    l.b_off = g.b_off;
+    l.as = g.a_stride;
+    l.bs = g.b_stride;
+    l.splits = splits;
+    l.kps = kps;
+    l.part = splits > 1 ? (float*)g.workspace : nullptr;
+    launch_mfma(s, t, g.ta, g.tb, mode, l);
     if (splits > 1) {
       uint64_t mn = g.m * g.n;
-      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 255) / 256), (uint32_t)g.batch), dim3(256), 0, s, (const float*)part,
+      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 255) / 256), (uint32_t)g.batch), dim3(256), 0, s, (const float*)l.part,
                          (float*)g.c, mn, splits);
     }
     return;

@@ -92,10 +92,37 @@ struct GemmArgs {
   void* c;
   const int64_t* a_off;  // device arrays of per-batch element offsets, or nullptr
   const int64_t* b_off;
+  bool a_off4, b_off4;          // every offset in the array is a multiple of 4 elements
   uint64_t a_stride, b_stride;  // per-batch element strides when the offset arrays are null
   void* workspace;              // split-K partial sums
   uint64_t workspace_bytes;
 };
+// Fused attention (attention.hip) over bh = batch * heads independent (tq x hd, tk x hd)
+// problems in row-major [bh][t][hd] slots. The mask, when present, is read at
+// b * s0 + h * s1 + q * s2 + k * s3 (zero strides for broadcast dimensions); the forward packs it
+// into `mask_bits` (attention_mask_words words), which the backward reads.
+constexpr int ATTN_MAX_KEYS = 256;
+struct AttnArgs {
+  uint32_t bh, heads;
+  int tq, tk, hd;
+  const float *q, *k, *v;
+  const float* mask;
+  int64_t mask_strides[4];
+  uint32_t* mask_bits;
+  float div, fill;  // scores are divided by `div`; masked scores are `fill`
+  float* o;         // forward output
+  // Per-query statistics, [bh][tq] each: the row max and sum (forward) and rowsum(dO * O)
+  // (backward's query pass).
+  float *stat_m, *stat_z, *stat_dd;
+  const float* o_in;  // backward inputs: the forward output and its cotangent
+  const float* d_o;
+  float *dq, *dk, *dv;
+};
+bool attention_supported(int dtype, int64_t hd, int64_t tq, int64_t tk);
+uint64_t attention_mask_words(const AttnArgs& a);
+void attention_forward(hipStream_t s, const AttnArgs& a);
+void attention_backward(hipStream_t s, const AttnArgs& a);
+
 // Workspace bytes the product needs for its split-K partials.
 uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch);
 void gemm(hipStream_t s, const GemmArgs& g);

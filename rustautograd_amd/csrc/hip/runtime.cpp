@@ -152,8 +152,17 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
       prog.device_tables.push_back(d);
       return (const int64_t*)d;
     };
-    if (!affine(ao, &base.a_stride)) base.a_off = upload(ao);
-    if (!affine(bo, &base.b_stride)) base.b_off = upload(bo);
+    auto all4 = [](const std::vector<int64_t>& o) {
+      return std::all_of(o.begin(), o.end(), [](int64_t x) { return x % 4 == 0; });
+    };
+    if (!affine(ao, &base.a_stride)) {
+      base.a_off = upload(ao);
+      base.a_off4 = all4(ao);
+    }
+    if (!affine(bo, &base.b_stride)) {
+      base.b_off = upload(bo);
+      base.b_off4 = all4(bo);
+    }
   }
   uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch);
   prog.workspace_bytes = std::max(prog.workspace_bytes, ws);
@@ -377,6 +386,60 @@ StepFn lower_instr(Program& prog, const Instr& i) {
   }
 }
 
+// A fused attention step (attention.hip). The statistics slot holds the per-query max, sum and
+// rowsum(dO * O), then the packed mask bits.
+StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
+  if (!rgk::attention_supported(at.dtype, at.hd, at.tq, at.tk))
+    throw std::runtime_error("attention step of unsupported shape (hd " + std::to_string(at.hd) + ", t " + std::to_string(at.tq) + "x" +
+                             std::to_string(at.tk) + ")");
+  rgk::AttnArgs base{};
+  base.bh = (uint32_t)at.bh;
+  base.heads = (uint32_t)at.heads;
+  base.tq = (int)at.tq;
+  base.tk = (int)at.tk;
+  base.hd = (int)at.hd;
+  base.div = (float)at.div;
+  base.fill = (float)at.fill;
+  for (int k = 0; k < 4; k++) base.mask_strides[k] = at.mask_strides[k];
+  const uint64_t rows = (uint64_t)at.bh * at.tq;
+  const uint64_t need = 3 * rows + (at.mask_slot >= 0 ? [&] {
+    rgk::AttnArgs t = base;
+    t.mask = (const float*)1;
+    return rgk::attention_mask_words(t);
+  }() : 0);
+  const auto& ss = prog.plan.slots[(size_t)at.stats_slot];
+  if ((uint64_t)ss.cap < need || esize(ss.dtype) != 4)
+    throw std::runtime_error("attention statistics slot holds " + std::to_string(ss.cap) + " words, needs " + std::to_string(need));
+  const int64_t mask = at.mask_slot, stats = at.stats_slot;
+  const std::vector<int64_t> in = at.in, out = at.out;
+  const bool bwd = at.backward;
+  return [=](hipStream_t s, void* const* sl, void*) {
+    rgk::AttnArgs a = base;
+    a.q = (const float*)sl[in[0]];
+    a.k = (const float*)sl[in[1]];
+    a.v = (const float*)sl[in[2]];
+    float* st = (float*)sl[stats];
+    a.stat_m = st;
+    a.stat_z = st + rows;
+    a.stat_dd = st + 2 * rows;
+    if (mask >= 0) {
+      a.mask = (const float*)sl[mask];
+      a.mask_bits = (uint32_t*)(st + 3 * rows);
+    }
+    if (!bwd) {
+      a.o = (float*)sl[out[0]];
+      rgk::attention_forward(s, a);
+    } else {
+      a.o_in = (const float*)sl[in[3]];
+      a.d_o = (const float*)sl[in[4]];
+      a.dq = (float*)sl[out[0]];
+      a.dk = (float*)sl[out[1]];
+      a.dv = (float*)sl[out[2]];
+      rgk::attention_backward(s, a);
+    }
+  };
+}
+
 void build_program(Program& prog) {
   std::ostringstream src;
   std::vector<rgjit::FusedKernel*> kernels;
@@ -412,6 +475,8 @@ void build_program(Program& prog) {
         for (size_t j = 0; j < q; j++) args[j] = &ptrs[j];
         hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, rgjit::TPB, 1, 1, 0, s, args, nullptr);
       });
+    } else if (st.kind == RG_STEP_ATTN) {
+      prog.steps.push_back(lower_attention(prog, st.attn));
     } else {
       const Instr& in = st.instr;
       prog.steps.push_back(lower_instr(prog, in));

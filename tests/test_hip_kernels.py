@@ -152,6 +152,15 @@ def test_mfma_products_with_transpose_flags(m, k, n, ta, tb):
     close(hip, want, 1e-4, f"gemm {m}x{k}x{n} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("a,b", [((5, 1, 96, 64), (1, 4, 64, 96)), ((3, 67, 129), (3, 129, 65)), ((2, 3, 128, 64), (3, 64, 256))])
+def test_batched_products_with_broadcast_and_odd_strides(a, b):
+    """Per-batch offset tables (broadcast batches) and batch strides that are not multiples of 4."""
+    rng = np.random.default_rng(sum(a) + sum(b))
+    x, y = rng.normal(size=a).astype(np.float32), rng.normal(size=b).astype(np.float32)
+    hip = run_graph("hip", lambda g, i: op(g, "matmul", [i[0], i[1]]), [t(x), t(y)], optimize="standard")[0]
+    close(hip, x.astype(np.float64) @ y.astype(np.float64), 1e-4, f"matmul {a} {b}")
+
+
 def test_batched_attention_products():
     rng = np.random.default_rng(5)
     q = rng.normal(size=(4, 8, 256, 32)).astype(np.float32)
