@@ -6,6 +6,8 @@
 
 #include <algorithm>
 #include <cstring>
+#include <iterator>
+#include <map>
 #include <queue>
 #include <set>
 
@@ -531,6 +533,77 @@ std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const 
   return items;
 }
 
+// Recomputation instead of storage. A plain fused group C that reads values X of an earlier plain
+// group G of its shape, where C is X's only other reader, recomputes X from G's own inputs: the
+// members of G that X depends on are added to C (a node may then run in two kernels). G stops
+// writing what nobody else reads, and C reads G's inputs instead of X. Done when it lowers C's
+// full-size reads, e.g. an activation's backward that would read every intermediate of its
+// forward. Members stay sorted by node id.
+void rematerialize(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, std::vector<Item>& items,
+                   size_t max_bindings) {
+  const size_t total = g.nodes.size();
+  std::vector<bool> is_out(total, false);
+  for (uint32_t o : outputs) is_out[o] = true;
+  std::vector<std::vector<uint32_t>> users(total);
+  for (size_t i = 0; i < total; i++)
+    if (keep[i])
+      for (uint32_t x : g.nodes[i].inputs) users[x].push_back((uint32_t)i);
+  std::vector<int64_t> item_of(total, -1);  // the plain group that first computes a node
+  auto plain = [&](const Item& it) { return it.group && !it.rows && it.attn < 0; };
+  auto in = [](const std::vector<size_t>& v, size_t x) { return std::binary_search(v.begin(), v.end(), x); };
+  for (size_t ci = 0; ci < items.size(); ci++) {
+    Item& C = items[ci];
+    if (plain(C)) {
+      const Node& c0 = g.nodes[C.members[0]];
+      std::map<size_t, std::vector<uint32_t>> cand;  // producer group -> values C would recompute
+      for (size_t u : C.members)
+        for (uint32_t x : g.nodes[u].inputs) {
+          if (in(C.members, x) || item_of[x] < 0 || is_out[x]) continue;
+          const Item& G = items[(size_t)item_of[x]];
+          const Node& n = g.nodes[x];
+          if (n.shape != c0.shape || n.dtype != c0.dtype || g.nodes[G.members[0]].shape != c0.shape) continue;
+          bool only = true;
+          for (uint32_t w : users[x]) only &= in(G.members, w) || in(C.members, w);
+          auto& v = cand[(size_t)item_of[x]];
+          if (only && std::find(v.begin(), v.end(), x) == v.end()) v.push_back(x);
+        }
+      for (auto& [gi, xs] : cand) {
+        const Item& G = items[gi];
+        // X's ancestors within G.
+        std::vector<size_t> closure;
+        std::vector<uint32_t> stack(xs.begin(), xs.end());
+        while (!stack.empty()) {
+          uint32_t x = stack.back();
+          stack.pop_back();
+          if (std::find(closure.begin(), closure.end(), (size_t)x) != closure.end()) continue;
+          closure.push_back(x);
+          for (uint32_t y : g.nodes[x].inputs)
+            if (in(G.members, y)) stack.push_back(y);
+        }
+        std::sort(closure.begin(), closure.end());
+        // Full-size values C would newly read, against the values it no longer reads.
+        std::set<uint32_t> ext_c, fresh;
+        for (size_t u : C.members)
+          for (uint32_t y : g.nodes[u].inputs)
+            if (!in(C.members, y)) ext_c.insert(y);
+        for (size_t m : closure)
+          for (uint32_t y : g.nodes[m].inputs)
+            if (!in(closure, y) && !in(C.members, y) && !ext_c.count(y)) fresh.insert(y);
+        size_t full = 0;
+        for (uint32_t y : fresh) full += numel(g.shape(y)) == numel(c0.shape);
+        if (full >= xs.size() || closure.size() > 64 || ext_c.size() + fresh.size() + C.members.size() + closure.size() > max_bindings)
+          continue;
+        std::vector<size_t> merged;
+        std::set_union(C.members.begin(), C.members.end(), closure.begin(), closure.end(), std::back_inserter(merged));
+        C.members = std::move(merged);
+      }
+    }
+    if (plain(C))
+      for (size_t m : C.members)
+        if (item_of[m] < 0) item_of[m] = (int64_t)ci;
+  }
+}
+
 Fused compile_group(const Graph& g, const std::vector<size_t>& members, const std::vector<size_t>& slot_of,
                     const std::vector<std::pair<size_t, size_t>>& out_slots, const std::vector<bool>& abs, bool rows) {
   const Node& first = g.nodes[members[0]];
@@ -608,10 +681,6 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   std::vector<bool> keep = g.reachable(outputs);
   size_t total = g.nodes.size();
   std::vector<uint32_t> uses(total, 0);
-  for (size_t i = 0; i < total; i++)
-    if (keep[i])
-      for (uint32_t x : g.nodes[i].inputs) uses[x]++;
-  for (uint32_t o : outputs) uses[o]++;  // outputs stay live past the last instruction
 
   Allocator a;
   a.reuse = reuse;
@@ -649,14 +718,9 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   };
   for (size_t k = 0; k < regions.size(); k++) {
     const AttnRegion& r = regions[k];
-    for (int b = 0; b < 2; b++) {
-      if (b && !r.has_bwd) continue;
-      for (uint32_t m : b ? r.bwd : r.fwd) {
-        claimed[m] = (int64_t)(2 * k + b);
-        for (uint32_t x : g.nodes[m].inputs) uses[x]--;
-      }
-      for (uint32_t x : region_inputs(r, b)) uses[x]++;
-    }
+    for (int b = 0; b < 2; b++)
+      if (!b || r.has_bwd)
+        for (uint32_t m : b ? r.bwd : r.fwd) claimed[m] = (int64_t)(2 * k + b);
   }
   std::vector<size_t> stats_slot(regions.size(), SIZE_MAX);
 
@@ -671,6 +735,27 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
     for (size_t i = 0; i < total; i++)
       if (keep[i] && !leaf(g.nodes[i])) items.push_back({false, i, {}});
   }
+  for (auto& item : items)
+    if (item.group) std::sort(item.members.begin(), item.members.end());  // node order is topological
+  if (fuse && fuse->remat) rematerialize(g, keep, outputs, items, fuse->max_bindings);
+
+  // Reads of each value by later plan steps: a group's reads of its own members are registers,
+  // an attention step reads its region's operands, an absorbed broadcast reads its source (as an
+  // alias, on first use); plan outputs stay live past the last step.
+  for (const auto& item : items) {
+    if (item.attn >= 0) {
+      for (uint32_t x : region_inputs(regions[(size_t)item.attn], item.attn_bwd)) uses[x]++;
+    } else if (item.group) {
+      for (size_t m : item.members)
+        for (uint32_t x : g.nodes[m].inputs)
+          if (!std::binary_search(item.members.begin(), item.members.end(), (size_t)x)) uses[x]++;
+    } else {
+      for (uint32_t x : g.nodes[item.node].inputs) uses[x]++;
+    }
+  }
+  for (size_t i = 0; i < total; i++)
+    if (keep[i] && abs[i] && claimed[i] < 0) uses[g.nodes[i].inputs[0]]++;
+  for (uint32_t o : outputs) uses[o]++;
 
   for (auto& item : items) {
     if (item.attn >= 0) {
@@ -718,10 +803,9 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       for (size_t m : members) {
         p.naive_bytes += g.nodes[m].n() * dsize(g.nodes[m].dtype);
         for (uint32_t x : g.nodes[m].inputs) {
+          if (std::binary_search(members.begin(), members.end(), (size_t)x)) continue;
           uses[x]--;
-          if (std::find(members.begin(), members.end(), (size_t)x) == members.end() &&
-              std::find(external.begin(), external.end(), x) == external.end())
-            external.push_back(x);
+          if (std::find(external.begin(), external.end(), x) == external.end()) external.push_back(x);
         }
       }
       // Destinations come first so they can never share a buffer with an input.

@@ -44,12 +44,17 @@ struct Fuse {
   // Level order only: scaled, masked softmax attention and its backward form become fused
   // attention steps (attention.cpp).
   bool attention;
+  // A fused group recomputes elementwise values of an earlier group it alone reads instead of
+  // reading them back from memory (plan.cpp rematerialize).
+  bool remat;
 
-  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false, false, false, false}; }
-  static Fuse metal() { return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false, false, false, false}; }
+  static Fuse cpu() { return {200000.0, false, false, 0, false, false, 0, 30000.0, 0.1, false, false, false, false, false, false}; }
+  static Fuse metal() {
+    return {0.0, true, true, 28, true, false, size_t(2) << 30, 30000.0, 0.1, false, false, false, false, false, false};
+  }
   // MI355X: ~4 us per dispatch inside a captured graph, ~0.001 ns per fp32 element written at
   // HBM speed, and 288 GB of HBM so level order is capped far higher.
-  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true, true, true, true}; }
+  static Fuse hip() { return {0.0, true, true, 64, false, true, size_t(64) << 30, 4000.0, 0.001, true, true, true, true, true, true}; }
 };
 
 // An attention region of the graph (attention.cpp): the nodes a fused forward step computes

@@ -286,3 +286,31 @@ def test_row_groups_agree_on_random_row_programs(chunk):
         plan = tw.g.compile([tw.ids[k] for k in outs], inputs, device=DEVPLAN, optimize="standard").plan_summary()
         row_groups += sum(s["kind"] == "fused" and s["row_len"] > 0 for s in plan)
     assert row_groups >= 15, f"row groups formed: {row_groups}"
+
+
+def test_activation_backward_recomputes_its_forward():
+    """A tanh-GELU layer trained through the device planner: the backward group recomputes the
+    forward's intermediates from the pre-activation instead of reading them back, so the forward
+    group writes only what other steps read, and results equal the CPU plan's."""
+    from rustautograd_amd import nn
+    r = np.random.default_rng(0)
+    x = rg.tensor(r.normal(size=(64, 48)).astype(np.float32))
+    w1 = rg.tensor(r.normal(size=(48, 96)).astype(np.float32) * 0.2)
+    b1 = rg.tensor(r.normal(size=(96,)).astype(np.float32))
+    w2 = rg.tensor(r.normal(size=(96, 8)).astype(np.float32) * 0.2)
+
+    def loss(w1, b1, w2):
+        y = nn.gelu(x @ w1 + b1) @ w2
+        return (y * y).sum()  # the activation's cotangent depends on its output: a later level
+    fn = rg.value_and_grad(loss, argnums=(0, 1, 2))
+    dev = rg.compile(fn, (w1, b1, w2), device=DEVPLAN, validate="none")
+    cpu = rg.compile(fn, (w1, b1, w2), device="cpu", validate="none")
+    groups = [s for s in dev._n.plan_summary() if s["kind"] == "fused" and s["n"] == 64 * 96 and "tanh" in s["ops"]]
+    assert len(groups) == 2, groups
+    fwd, bwd = groups
+    assert fwd["n_outputs"] <= 2, fwd
+    assert sum(k == "full" for k in bwd["input_kinds"]) <= 3, bwd
+    (v1, g1), (v2, g2) = dev(w1, b1, w2), cpu(w1, b1, w2)
+    np.testing.assert_allclose(float(v1), float(v2), rtol=1e-5)
+    for a, b in zip(g1, g2):
+        np.testing.assert_allclose(a.numpy(), b.numpy(), rtol=1e-5, atol=1e-5)
