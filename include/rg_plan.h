@@ -33,9 +33,11 @@
  *                    row-level registers hold one value per row.
  *     RG_STEP_ATTN   dtype, backward (0/1), bh, heads, tq, tk, hd, div (f64 bits), fill (f64 bits),
  *                    mask_slot (-1: none), mask strides (4 words), stats_slot,
- *                    n_in, in slots, n_out, out slots, node
+ *                    n_in, per in: slot, offset, sb, sh, st,  n_out, per out: the same,  node
  *                    Fused attention (no reference counterpart; device plans only) over bh
- *                    independent problems with row-major [bh][t][hd] operands:
+ *                    independent problems b * heads + h; row t, column d of an operand lies at
+ *                    offset + b * sb + h * sh + t * st + d in its slot (so operands may be
+ *                    slices and transposes of other values, and outputs may share a slot):
  *                      forward   in q, k, v        out O = softmax(where(mask, q k^T / div, fill)) v
  *                      backward  in q, k, v, O, dO out dq, dk, dv (the gradients of O's graph)
  *                    The softmax is over keys; the mask (f32, nonzero = visible) is read at
@@ -138,6 +140,9 @@ struct Fused {
 };
 
 /* RG_STEP_ATTN */
+struct AttnView {
+  int64_t slot, offset, sb, sh, st;
+};
 struct Attn {
   int32_t dtype;
   bool backward;
@@ -146,7 +151,7 @@ struct Attn {
   int64_t mask_slot;
   int64_t mask_strides[4];
   int64_t stats_slot;
-  std::vector<int64_t> in, out;
+  std::vector<AttnView> in, out;
   int64_t node;
 };
 
@@ -306,8 +311,19 @@ inline Plan parse(const int64_t* w, size_t nw) {
       a.mask_slot = next();
       for (int k = 0; k < 4; k++) a.mask_strides[k] = next();
       a.stats_slot = next();
-      a.in = vec(next());
-      a.out = vec(next());
+      for (int side = 0; side < 2; side++) {
+        int64_t n = next();
+        if (n < 0 || n > 8) throw std::runtime_error("malformed attention step");
+        for (int64_t k = 0; k < n; k++) {
+          AttnView v;
+          v.slot = next();
+          v.offset = next();
+          v.sb = next();
+          v.sh = next();
+          v.st = next();
+          (side ? a.out : a.in).push_back(v);
+        }
+      }
       a.node = next();
       if (a.in.size() != (a.backward ? 5u : 3u) || a.out.size() != (a.backward ? 3u : 1u) || a.bh <= 0 || a.heads <= 0 ||
           a.bh % a.heads != 0)

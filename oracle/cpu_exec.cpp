@@ -866,15 +866,27 @@ void run_attention(const Attn& a, std::vector<Buf>& s) {
   const float div = (float)a.div, fill = (float)a.fill;
   auto ptr = [&](int64_t slot) { return s[(size_t)slot].as<float>(); };
   const float* mask = a.mask_slot >= 0 ? ptr(a.mask_slot) : nullptr;
+  // Operand views: row t of problem b at offset + (b / heads) sb + (b % heads) sh + t st.
+  auto row = [&](const AttnView& v, size_t b, size_t t) {
+    return ptr(v.slot) + v.offset + (int64_t)(b / heads) * v.sb + (int64_t)(b % heads) * v.sh + (int64_t)t * v.st;
+  };
+  auto gather = [&](const AttnView& v, size_t b, size_t t_n, std::vector<float>& out) {
+    out.resize(t_n * hd);
+    for (size_t t = 0; t < t_n; t++) memcpy(&out[t * hd], row(v, b, t), hd * sizeof(float));
+  };
+  auto scatter = [&](const AttnView& v, size_t b, size_t t_n, const std::vector<float>& in) {
+    for (size_t t = 0; t < t_n; t++) memcpy(row(v, b, t), &in[t * hd], hd * sizeof(float));
+  };
 #pragma omp parallel for schedule(static)
   for (size_t b = 0; b < bh; b++) {
-    const float* q = ptr(a.in[0]) + b * tq * hd;
-    const float* k = ptr(a.in[1]) + b * tk * hd;
-    const float* v = ptr(a.in[2]) + b * tk * hd;
+    std::vector<float> q, k, v;
+    gather(a.in[0], b, tq, q);
+    gather(a.in[1], b, tk, k);
+    gather(a.in[2], b, tk, v);
     const float* mb = mask ? mask + (b / heads) * a.mask_strides[0] + (b % heads) * a.mask_strides[1] : nullptr;
     auto visible = [&](size_t i, size_t j) { return !mb || mb[(int64_t)i * a.mask_strides[2] + (int64_t)j * a.mask_strides[3]] != 0.0f; };
     std::vector<float> S(tq * tk), E(tq * tk), Z(tq), P(tq * tk);
-    gemm<float>(tq, hd, tk, q, false, k, true, S.data());
+    gemm<float>(tq, hd, tk, q.data(), false, k.data(), true, S.data());
     for (size_t i = 0; i < tq; i++) {
       float* y = &S[i * tk];
       float m = -INFINITY;
@@ -887,13 +899,15 @@ void run_attention(const Attn& a, std::vector<Buf>& s) {
       for (size_t j = 0; j < tk; j++) P[i * tk + j] = E[i * tk + j] / Z[i];
     }
     if (!a.backward) {
-      gemm<float>(tq, tk, hd, P.data(), false, v, false, ptr(a.out[0]) + b * tq * hd);
+      std::vector<float> o(tq * hd);
+      gemm<float>(tq, tk, hd, P.data(), false, v.data(), false, o.data());
+      scatter(a.out[0], b, tq, o);
       continue;
     }
-    const float* d_o = ptr(a.in[4]) + b * tq * hd;
-    std::vector<float> dP(tq * tk), dS(tq * tk), t(tk);
-    gemm<float>(tq, hd, tk, d_o, false, v, true, dP.data());
-    gemm<float>(tk, tq, hd, P.data(), true, d_o, false, ptr(a.out[2]) + b * tk * hd);
+    std::vector<float> d_o, dP(tq * tk), dS(tq * tk), t(tk), dq(tq * hd), dk(tk * hd), dv(tk * hd);
+    gather(a.in[4], b, tq, d_o);
+    gemm<float>(tq, hd, tk, d_o.data(), false, v.data(), true, dP.data());
+    gemm<float>(tk, tq, hd, P.data(), true, d_o.data(), false, dv.data());
     for (size_t i = 0; i < tq; i++) {
       const float z = Z[i], zz = z * z;
       for (size_t j = 0; j < tk; j++) t[j] = -dP[i * tk + j] * E[i * tk + j] / zz;
@@ -903,8 +917,11 @@ void run_attention(const Attn& a, std::vector<Buf>& s) {
         dS[i * tk + j] = (visible(i, j) ? h : 0.0f) / div;
       }
     }
-    gemm<float>(tq, tk, hd, dS.data(), false, k, false, ptr(a.out[0]) + b * tq * hd);
-    gemm<float>(tk, tq, hd, dS.data(), true, q, false, ptr(a.out[1]) + b * tk * hd);
+    gemm<float>(tq, tk, hd, dS.data(), false, k.data(), false, dq.data());
+    gemm<float>(tk, tq, hd, dS.data(), true, q.data(), false, dk.data());
+    scatter(a.out[0], b, tq, dq);
+    scatter(a.out[1], b, tk, dk);
+    scatter(a.out[2], b, tk, dv);
   }
 }
 

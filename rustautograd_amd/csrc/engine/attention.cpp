@@ -390,6 +390,211 @@ AttnShape attn_shape(const AttnRegion& r, const Graph& g) {
   return a;
 }
 
+namespace {
+
+std::vector<int64_t> contiguous(const Shape& s) {
+  std::vector<int64_t> st(s.size(), 1);
+  for (size_t d = s.size(); d-- > 1;) st[d - 1] = st[d] * (int64_t)s[d];
+  return st;
+}
+
+// Strides of a reshape of a strided view, when it needs no copy: groups of old dimensions that
+// multiply to groups of new ones must be contiguous relative to each other.
+bool reshape_strides(const Shape& os, const std::vector<int64_t>& ost, const Shape& ns, std::vector<int64_t>* nst) {
+  std::vector<size_t> od;
+  std::vector<int64_t> ostr;
+  for (size_t i = 0; i < os.size(); i++)
+    if (os[i] != 1) {
+      od.push_back(os[i]);
+      ostr.push_back(ost[i]);
+    }
+  nst->assign(ns.size(), 0);
+  size_t oi = 0, ni = 0;
+  while (ni < ns.size() && oi < od.size()) {
+    if (ns[ni] == 1) {
+      ni++;
+      continue;
+    }
+    size_t np = ns[ni], op = od[oi], nj = ni + 1, oj = oi + 1;
+    while (np != op) {
+      if (np < op) {
+        if (nj >= ns.size()) return false;
+        np *= ns[nj++];
+      } else {
+        if (oj >= od.size()) return false;
+        op *= od[oj++];
+      }
+    }
+    for (size_t k = oi; k + 1 < oj; k++)
+      if (ostr[k] != ostr[k + 1] * (int64_t)od[k + 1]) return false;
+    int64_t st = ostr[oj - 1];
+    for (size_t k = nj; k-- > ni;)
+      if (ns[k] != 1) {
+        (*nst)[k] = st;
+        st *= (int64_t)ns[k];
+      }
+    ni = nj;
+    oi = oj;
+  }
+  for (; ni < ns.size(); ni++)
+    if (ns[ni] != 1) return false;
+  return oi == od.size();
+}
+
+bool layout_op(const Node& n) {
+  return n.op.kind == RG_OP_RESHAPE || n.op.kind == RG_OP_TRANSPOSE || n.op.kind == RG_OP_SLICE;
+}
+
+// The operand (b, h, t, d) strides of a [batch..., t, d] view, for the steps' (batch, heads)
+// split of the problems: rank 3 puts every problem in the heads' place; ranks above 4 only
+// when the leading batch dimensions merge.
+bool operand_of(uint32_t node, int64_t offset, const Shape& shape, const std::vector<int64_t>& st, AttnOperand* out) {
+  const size_t r = shape.size();
+  if (r < 3 || st[r - 1] != 1) return false;
+  AttnOperand o;
+  o.node = node;
+  o.offset = offset;
+  o.st = st[r - 2];
+  o.sh = st[r - 3];
+  o.sb = 0;
+  if (r >= 4) {
+    o.sb = st[r - 4];
+    for (size_t d = 0; d + 4 < r; d++)
+      if (st[d] != st[d + 1] * (int64_t)shape[d + 1]) return false;
+  }
+  // 16-byte vectors along d.
+  if (o.offset % 4 || o.st % 4 || o.sh % 4 || o.sb % 4) return false;
+  *out = o;
+  return true;
+}
+
+// Reads of node x: through unclaimed reshapes, transposes and slices back to the buffer of a
+// materialized node. Falls back to x's own buffer.
+AttnOperand read_view(const Graph& g, uint32_t x, const std::vector<bool>& claimed) {
+  std::vector<uint32_t> chain;
+  uint32_t cur = x;
+  while (layout_op(g.nodes[cur]) && !claimed[cur]) {
+    chain.push_back(cur);
+    cur = g.nodes[cur].inputs[0];
+  }
+  AttnOperand own;
+  operand_of(x, 0, g.shape(x), contiguous(g.shape(x)), &own);
+  if (chain.empty() || g.nodes[cur].op.kind == RG_OP_BROADCAST_TO) return own;
+  Shape shape = g.shape(cur);
+  std::vector<int64_t> st = contiguous(shape);
+  int64_t off = 0;
+  for (size_t j = chain.size(); j-- > 0;) {
+    const Node& n = g.nodes[chain[j]];
+    if (n.op.kind == RG_OP_TRANSPOSE) {
+      Shape s2(shape.size());
+      std::vector<int64_t> t2(shape.size());
+      for (size_t d = 0; d < shape.size(); d++) {
+        s2[d] = shape[n.op.v[d]];
+        t2[d] = st[n.op.v[d]];
+      }
+      shape = s2;
+      st = t2;
+    } else if (n.op.kind == RG_OP_SLICE) {
+      for (size_t d = 0; d < shape.size(); d++) {
+        off += (int64_t)n.op.v[d] * st[d];
+        shape[d] = n.op.w[d] - n.op.v[d];
+      }
+    } else {
+      std::vector<int64_t> t2;
+      if (!reshape_strides(shape, st, n.shape, &t2)) return own;
+      shape = n.shape;
+      st = t2;
+    }
+  }
+  AttnOperand v;
+  return operand_of(cur, off, shape, st, &v) ? v : own;
+}
+
+// Results written straight into the layout their readers want. The forward writes O into the
+// one transpose that alone reads it (the heads merged back). The backward writes dq, dk and dv
+// into the transpose of their sum after each is padded into its slice of one tensor (the
+// gradient of the slices that split q, k and v from one projection): the sum holds each value
+// once, the zeros elsewhere add nothing. Nodes already claimed or returned by the program are
+// not folded.
+void fold_outputs(const Matcher& mt, const std::set<uint32_t>& taken, AttnRegion& r) {
+  const Graph& g = mt.g;
+  auto free_node = [&](uint32_t x) { return !taken.count(x) && !mt.is_out[x]; };
+  operand_of(r.o, 0, g.shape(r.o), contiguous(g.shape(r.o)), &r.out_o);
+  r.fwd_out = {r.o};
+  uint32_t t;
+  if (!mt.is_out[r.o] && mt.only_user(r.o, &t) && free_node(t) && mt.is(t, RG_OP_TRANSPOSE) &&
+      g.nodes[t].op.v.back() == g.shape(t).size() - 1) {
+    const Shape& ts = g.shape(t);
+    std::vector<int64_t> ct = contiguous(ts), st(ts.size());
+    for (size_t j = 0; j < ts.size(); j++) st[g.nodes[t].op.v[j]] = ct[j];
+    AttnOperand w;
+    if (operand_of(t, 0, g.shape(r.o), st, &w)) {
+      r.out_o = w;
+      r.fwd.push_back(t);
+      r.fwd_out = {t};
+    }
+  }
+  if (!r.has_bwd) return;
+  const uint32_t grads[3] = {r.dq, r.dk, r.dv};
+  AttnOperand* outs[3] = {&r.out_dq, &r.out_dk, &r.out_dv};
+  for (int i = 0; i < 3; i++) operand_of(grads[i], 0, g.shape(grads[i]), contiguous(g.shape(grads[i])), outs[i]);
+  r.bwd_out = {r.dq, r.dk, r.dv};
+  // gradient -> reshape [1, ...] -> pad to [3, ...] at slice i.
+  uint32_t re[3], pad[3], user[3];
+  int64_t at[3];
+  const Shape& gs = g.shape(r.dq);
+  for (int i = 0; i < 3; i++) {
+    if (mt.is_out[grads[i]] || g.shape(grads[i]) != gs) return;
+    if (!mt.only_user(grads[i], &re[i]) || !free_node(re[i]) || !mt.is(re[i], RG_OP_RESHAPE)) return;
+    if (!mt.only_user(re[i], &pad[i]) || !free_node(pad[i]) || !mt.is(pad[i], RG_OP_PAD)) return;
+    const Shape& rs = g.shape(re[i]);
+    const Node& pn = g.nodes[pad[i]];
+    if (rs.size() != gs.size() + 1 || rs[0] != 1 || pn.op.w.size() != rs.size() || pn.op.w[0] != 3) return;
+    for (size_t d = 1; d < rs.size(); d++)
+      if (rs[d] != gs[d - 1] || pn.op.v[d] != 0 || pn.op.w[d] != rs[d]) return;
+    at[i] = (int64_t)pn.op.v[0];
+    if (!mt.only_user(pad[i], &user[i]) || !free_node(user[i]) || !mt.is(user[i], RG_OP_ADD)) return;
+  }
+  if (at[0] == at[1] || at[0] == at[2] || at[1] == at[2]) return;
+  // Two adds: `inner` joins two pads, `outer` joins the third pad and `inner`.
+  int64_t inner = -1;
+  for (int i = 0; i < 3; i++)
+    for (int j = i + 1; j < 3; j++)
+      if (user[i] == user[j]) inner = user[i];
+  if (inner < 0) return;
+  uint32_t outer = 0;
+  for (int i = 0; i < 3; i++)
+    if (user[i] != (uint32_t)inner) outer = user[i];
+  uint32_t u;
+  if (!mt.only_user((uint32_t)inner, &u) || u != outer) return;
+  // The sum, or the one transpose that alone reads it.
+  uint32_t fin = outer;
+  const Shape& ss = g.shape(outer);
+  std::vector<int64_t> sst = contiguous(ss);  // strides of the [3, batch..., t, d] layout
+  if (mt.only_user(outer, &u) && free_node(u) && !mt.is_out[outer] && mt.is(u, RG_OP_TRANSPOSE) &&
+      g.nodes[u].op.v.back() == ss.size() - 1) {
+    const Shape& ts = g.shape(u);
+    std::vector<int64_t> ct = contiguous(ts);
+    for (size_t j = 0; j < ts.size(); j++) sst[g.nodes[u].op.v[j]] = ct[j];
+    fin = u;
+  }
+  std::vector<int64_t> gst(sst.begin() + 1, sst.end());
+  AttnOperand w[3];
+  for (int i = 0; i < 3; i++)
+    if (!operand_of(fin, at[i] * sst[0], gs, gst, &w[i])) return;
+  for (int i = 0; i < 3; i++) {
+    *outs[i] = w[i];
+    r.bwd.push_back(re[i]);
+    r.bwd.push_back(pad[i]);
+  }
+  r.bwd.push_back((uint32_t)inner);
+  r.bwd.push_back(outer);
+  if (fin != outer) r.bwd.push_back(fin);
+  r.bwd_out = {fin};
+}
+
+}  // namespace
+
 std::vector<AttnRegion> match_attention(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs) {
   Matcher mt(g, keep, outputs);
   std::vector<AttnRegion> out;
@@ -413,9 +618,19 @@ std::vector<AttnRegion> match_attention(const Graph& g, const std::vector<bool>&
     for (uint32_t m : pick->fwd) clash |= taken.count(m) > 0;
     for (uint32_t m : pick->bwd) clash |= taken.count(m) > 0;
     if (clash) continue;
+    fold_outputs(mt, taken, *pick);
     taken.insert(pick->fwd.begin(), pick->fwd.end());
     taken.insert(pick->bwd.begin(), pick->bwd.end());
     out.push_back(*pick);
+  }
+  // Operand views, once every region's nodes are known: a walk stops at claimed nodes.
+  std::vector<bool> claimed(g.nodes.size(), false);
+  for (uint32_t m : taken) claimed[m] = true;
+  for (auto& r : out) {
+    r.in_q = read_view(g, r.q, claimed);
+    r.in_k = read_view(g, r.k, claimed);
+    r.in_v = read_view(g, r.v, claimed);
+    if (r.has_bwd) r.in_do = read_view(g, r.d_o, claimed);
   }
   return out;
 }

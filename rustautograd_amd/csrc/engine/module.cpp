@@ -256,8 +256,11 @@ PYBIND11_MODULE(_rg, m) {
                  d["hd"] = a.shape.hd;
                  d["masked"] = a.mask_slot >= 0;
                  d["n"] = a.shape.bh * a.shape.tq * a.shape.hd;
-                 d["input_slots"] = a.in;
-                 d["output_slots"] = a.out;
+                 py::list ins, outs;
+                 for (auto& v : a.in) ins.append(v.slot);
+                 for (auto& v : a.out) outs.append(v.slot);
+                 d["input_slots"] = ins;
+                 d["output_slots"] = outs;
                } else if (s.fused) {
                  d["kind"] = "fused";
                  py::list ops;

@@ -343,8 +343,13 @@ std::vector<std::vector<size_t>> row_groups(const Graph& g, const std::vector<bo
   return out;
 }
 
-std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
-                                  const std::vector<bool>& abs, const std::vector<int64_t>& claimed, size_t n_attn_units) {
+// `keep`: the nodes to schedule; `keep_all`: every node the outputs reach in the graph, including
+// the reshapes and transposes attention steps read through, which carry the row groups'
+// dependence tracking.
+std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep, const std::vector<bool>& keep_all,
+                                  const std::vector<uint32_t>& outputs, const Fuse& cfg, const std::vector<bool>& abs,
+                                  const std::vector<int64_t>& claimed, const std::vector<std::vector<uint32_t>>& attn_inputs) {
+  const size_t n_attn_units = attn_inputs.size();
   std::vector<bool> up = cfg.hoist ? hoisted(g, keep) : std::vector<bool>(g.nodes.size(), false);
   std::vector<Item> items;
   for (size_t i = 0; i < g.nodes.size(); i++)
@@ -360,7 +365,7 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   if (cfg.row_groups) {
     std::vector<bool> excluded(total, false);
     for (size_t i = 0; i < total; i++) excluded[i] = up[i] || tail[i] || claimed[i] >= 0;
-    rgs = row_groups(g, keep, abs, excluded, dev_fusable, cfg.max_bindings);
+    rgs = row_groups(g, keep_all, abs, excluded, dev_fusable, cfg.max_bindings);
     for (size_t k = 0; k < rgs.size(); k++)
       for (size_t m : rgs[k]) rg_of[m] = (int64_t)k;
   }
@@ -387,6 +392,19 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
       indeg[u]++;
     }
   }
+  // An attention unit reads its operands through views of other values: those are its inputs.
+  for (size_t k = 0; k < n_attn_units; k++) {
+    size_t u = total + rgs.size() + k;
+    if (first[u] == SIZE_MAX) continue;
+    std::set<size_t> deps;
+    for (uint32_t x : attn_inputs[k])
+      if (active(x) && unit_of(x) != u) deps.insert(unit_of(x));
+    for (size_t d : deps)
+      if (std::find(unit_users[d].begin(), unit_users[d].end(), u) == unit_users[d].end()) {
+        unit_users[d].push_back(u);
+        indeg[u]++;
+      }
+  }
   std::priority_queue<std::pair<size_t, size_t>, std::vector<std::pair<size_t, size_t>>, std::greater<>> ready;
   for (size_t u = 0; u < n_units; u++)
     if (first[u] != SIZE_MAX && indeg[u] == 0) ready.push({first[u], u});
@@ -398,6 +416,9 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     for (size_t v : unit_users[u])
       if (--indeg[v] == 0) ready.push({first[v], v});
   }
+  size_t n_real = 0;
+  for (size_t u = 0; u < n_units; u++) n_real += first[u] != SIZE_MAX;
+  if (order.size() != n_real) throw std::logic_error("planner: scheduling units depend on each other in a cycle");
   std::vector<size_t> sunk;
   std::vector<size_t> level(total, 0);
   // Members of each attention unit, in node order.
@@ -412,6 +433,8 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
       for (size_t m : members)
         for (uint32_t x : g.nodes[m].inputs)
           if (unit_of(x) != u) deepest = std::max(deepest, level[x]);
+      if (u >= total + rgs.size())
+        for (uint32_t x : attn_inputs[u - total - rgs.size()]) deepest = std::max(deepest, level[x]);
       for (size_t m : members) level[m] = deepest + 1;
       if (by_level.size() <= deepest + 1) by_level.resize(deepest + 2);
       by_level[deepest + 1].push_back(u);
@@ -496,9 +519,10 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
 
 // Greedy fusion: one open group. Instructions independent of the group are emitted first; one
 // that reads a member closes the group, which keeps the group free of cycles (plan.rs:311-350).
-std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, const Fuse& cfg,
-                           const std::vector<bool>& abs, const std::vector<int64_t>& claimed, size_t n_attn_units) {
-  if (cfg.device && cfg.levels) return schedule_levels(g, keep, outputs, cfg, abs, claimed, n_attn_units);
+std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const std::vector<bool>& keep_all,
+                           const std::vector<uint32_t>& outputs, const Fuse& cfg, const std::vector<bool>& abs,
+                           const std::vector<int64_t>& claimed, const std::vector<std::vector<uint32_t>>& attn_inputs) {
+  if (cfg.device && cfg.levels) return schedule_levels(g, keep, keep_all, outputs, cfg, abs, claimed, attn_inputs);
   std::vector<Item> items;
   std::vector<size_t> open;
   auto close = [&]() {
@@ -678,7 +702,8 @@ rg_mode binary_mode(const Op& op, const Shape& shape, const std::vector<Shape>& 
 }
 
 Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse, const Fuse* fuse) {
-  std::vector<bool> keep = g.reachable(outputs);
+  std::vector<bool> keep = g.reachable(outputs);  // narrowed below when attention steps replace nodes
+  const std::vector<bool> keep_all = keep;
   size_t total = g.nodes.size();
   std::vector<uint32_t> uses(total, 0);
 
@@ -707,12 +732,19 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   std::vector<AttnRegion> regions;
   std::vector<int64_t> claimed(total, -1);  // attention unit: 2 * region (+ 1 for the backward)
   if (fuse && fuse->attention && fuse->device && fuse->levels) regions = match_attention(g, keep, outputs);
-  auto region_inputs = [&](const AttnRegion& r, bool bwd) {
-    std::vector<uint32_t> in = {r.q, r.k, r.v};
+  // The operand views each step reads (q, k, v; the backward also O and dO), in that order,
+  // then the mask.
+  auto region_views = [&](const AttnRegion& r, bool bwd) {
+    std::vector<AttnOperand> in = {r.in_q, r.in_k, r.in_v};
     if (bwd) {
-      in.push_back(r.o);
-      in.push_back(r.d_o);
+      in.push_back(r.out_o);
+      in.push_back(r.in_do);
     }
+    return in;
+  };
+  auto region_inputs = [&](const AttnRegion& r, bool bwd) {
+    std::vector<uint32_t> in;
+    for (const AttnOperand& v : region_views(r, bwd)) in.push_back(v.node);
     if (r.mask >= 0) in.push_back((uint32_t)r.mask);
     return in;
   };
@@ -722,6 +754,31 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       if (!b || r.has_bwd)
         for (uint32_t m : b ? r.bwd : r.fwd) claimed[m] = (int64_t)(2 * k + b);
   }
+  if (!regions.empty()) {
+    // Values only the replaced nodes read (e.g. the transposes that split the heads, now read
+    // through views) are no longer computed.
+    std::vector<bool> live(total, false);
+    std::vector<uint32_t> stack(outputs.begin(), outputs.end());
+    std::vector<bool> region_done(2 * regions.size(), false);
+    while (!stack.empty()) {
+      uint32_t x = stack.back();
+      stack.pop_back();
+      if (live[x]) continue;
+      live[x] = true;
+      if (claimed[x] >= 0) {
+        size_t u = (size_t)claimed[x];
+        if (region_done[u]) continue;
+        region_done[u] = true;
+        const AttnRegion& r = regions[u / 2];
+        for (uint32_t y : region_inputs(r, u % 2)) stack.push_back(y);  // the backward's include the forward's O
+        for (uint32_t m : u % 2 ? r.bwd : r.fwd) live[m] = true;
+        continue;
+      }
+      for (uint32_t y : g.nodes[x].inputs) stack.push_back(y);
+    }
+    for (size_t i = 0; i < total; i++)
+      if (claimed[i] < 0) keep[i] = keep[i] && live[i];
+  }
   std::vector<size_t> stats_slot(regions.size(), SIZE_MAX);
 
   std::vector<Item> items;
@@ -730,7 +787,12 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   if (fuse && fuse->exact_outputs)
     for (uint32_t o : outputs) exact[o] = true;
   if (fuse) {
-    items = schedule(g, keep, outputs, *fuse, abs, claimed, 2 * regions.size());
+    std::vector<std::vector<uint32_t>> attn_inputs(2 * regions.size());
+    for (size_t k = 0; k < regions.size(); k++) {
+      attn_inputs[2 * k] = region_inputs(regions[k], false);
+      if (regions[k].has_bwd) attn_inputs[2 * k + 1] = region_inputs(regions[k], true);
+    }
+    items = schedule(g, keep, keep_all, outputs, *fuse, abs, claimed, attn_inputs);
   } else {
     for (size_t i = 0; i < total; i++)
       if (keep[i] && !leaf(g.nodes[i])) items.push_back({false, i, {}});
@@ -770,16 +832,18 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       at.fill = r.fill;
       std::vector<uint32_t> ins = region_inputs(r, bwd);
       at.mask_slot = r.mask >= 0 ? (int64_t)value_slot[(size_t)r.mask] : -1;
-      for (size_t j = 0; j < (bwd ? 5u : 3u); j++) at.in.push_back(value_slot[ins[j]]);
+      auto view = [&](const AttnOperand& o) { return AttnView{value_slot[o.node], o.offset, o.sb, o.sh, o.st}; };
+      for (const AttnOperand& o : region_views(r, bwd)) at.in.push_back(view(o));
       if (!bwd) stats_slot[(size_t)item.attn] = a.new_slot(DType::F32, attn_stats_words(r, g), true);
       at.stats_slot = stats_slot[(size_t)item.attn];
-      std::vector<uint32_t> outs = bwd ? std::vector<uint32_t>{r.dq, r.dk, r.dv} : std::vector<uint32_t>{r.o};
-      for (uint32_t o : outs) {
-        size_t sl = a.alloc(g.nodes[o].dtype, g.nodes[o].n(), exact[o]);
-        value_slot[o] = sl;
-        at.out.push_back(sl);
+      for (uint32_t o : bwd ? r.bwd_out : r.fwd_out) {
+        value_slot[o] = a.alloc(g.nodes[o].dtype, g.nodes[o].n(), exact[o]);
         p.naive_bytes += g.nodes[o].n() * dsize(g.nodes[o].dtype);
       }
+      if (bwd)
+        for (const AttnOperand* o : {&r.out_dq, &r.out_dk, &r.out_dv}) at.out.push_back(view(*o));
+      else
+        at.out.push_back(view(r.out_o));
       at.node = bwd ? r.dq : r.o;
       p.steps.push_back(std::move(st));
       for (uint32_t x : ins)
@@ -1010,10 +1074,18 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
       w.push_back(at.mask_slot);
       for (int k = 0; k < 4; k++) w.push_back(at.shape.mask_strides[k]);
       w.push_back((int64_t)at.stats_slot);
-      w.push_back((int64_t)at.in.size());
-      for (size_t x : at.in) w.push_back((int64_t)x);
-      w.push_back((int64_t)at.out.size());
-      for (size_t x : at.out) w.push_back((int64_t)x);
+      auto views = [&](const std::vector<AttnView>& vs) {
+        w.push_back((int64_t)vs.size());
+        for (const AttnView& v : vs) {
+          w.push_back((int64_t)v.slot);
+          w.push_back(v.offset);
+          w.push_back(v.sb);
+          w.push_back(v.sh);
+          w.push_back(v.st);
+        }
+      };
+      views(at.in);
+      views(at.out);
       w.push_back(at.node);
       continue;
     }

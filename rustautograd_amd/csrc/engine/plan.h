@@ -60,6 +60,12 @@ struct Fuse {
 // An attention region of the graph (attention.cpp): the nodes a fused forward step computes
 // (`fwd`, with O = node `o` its one output) and, when the graph differentiates O, the nodes a
 // fused backward step computes (`bwd`, outputs dq, dk, dv for the cotangent node `d_o`).
+// One operand of an attention step: element (b, h, t, d) of a problem lies at
+// offset + b sb + h sh + t st + d in the buffer of node `node` (d is contiguous).
+struct AttnOperand {
+  uint32_t node = 0;
+  int64_t offset = 0, sb = 0, sh = 0, st = 0;
+};
 struct AttnRegion {
   uint32_t q = 0, k = 0, v = 0, o = 0, s = 0, e = 0, z = 0, p = 0, y = 0;
   int64_t mask = -1, mask_bcast = -1;  // the mask's source node and its broadcast
@@ -68,6 +74,11 @@ struct AttnRegion {
   std::vector<uint32_t> fwd, bwd, optional;
   bool has_bwd = false;
   uint32_t d_o = 0, dq = 0, dk = 0, dv = 0;
+  // Where the steps read their operands (through reshapes, transposes and slices of other
+  // values) and write their results (into the one transpose that reads O, or into the transposed
+  // sum of dq, dk and dv padded into one tensor); the nodes those results materialize.
+  AttnOperand in_q, in_k, in_v, in_do, out_o, out_dq, out_dk, out_dv;
+  std::vector<uint32_t> fwd_out, bwd_out;
 };
 // Problem sizes of a region: bh = batch * heads independent (tq x hd, tk x hd) problems, the
 // mask's element strides over (batch, heads, query, key) and its number of distinct slices.
@@ -121,6 +132,10 @@ struct Fused {
 };
 
 // A fused attention step (include/rg_plan.h RG_STEP_ATTN; device plans only).
+struct AttnView {
+  size_t slot = 0;
+  int64_t offset = 0, sb = 0, sh = 0, st = 0;
+};
 struct Attn {
   bool backward = false;
   DType dtype = DType::F32;
@@ -128,8 +143,8 @@ struct Attn {
   double div = 1.0, fill = 0.0;
   int64_t mask_slot = -1;
   size_t stats_slot = 0;
-  std::vector<size_t> in, out;  // forward: q, k, v -> O; backward: q, k, v, O, dO -> dq, dk, dv
-  uint32_t node = 0;            // the O node (forward) or the dq node (backward)
+  std::vector<AttnView> in, out;  // forward: q, k, v -> O; backward: q, k, v, O, dO -> dq, dk, dv
+  uint32_t node = 0;              // the O node (forward) or the dq node (backward)
 };
 
 struct Step {

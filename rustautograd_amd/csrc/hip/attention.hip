@@ -7,6 +7,10 @@
 // [batch, heads, T, T] tensors; here they live in registers, 16x16 tiles at a time, and only q, k,
 // v, O, their gradients and three per-row statistics touch HBM.
 //
+// Operands are strided views (AttnOperand): row t of problem b * heads + h starts at
+// p + b sb + h sh + t st, so q, k and v are read straight out of the projection that produced them
+// and O, dq, dk, dv are written into the layouts their readers use.
+//
 // Every kernel runs four wave64s per block; each wave owns 16 rows (queries in the forward and
 // the dq pass, keys in the dk/dv pass) and walks the other side in tiles of 16 with
 // v_mfma_f32_16x16x4f32. A score tile is formed either as S^T (K supplies the MFMA rows) so that
@@ -82,6 +86,14 @@ __device__ __forceinline__ MaskTables mask_tables(const AttnArgs& a, uint32_t bh
 
 constexpr uint64_t ALL_LANES = ~0ull;
 
+// Row t of problem bh of an operand.
+__device__ __forceinline__ const float* row_of(const AttnOperand& x, const AttnArgs& a, uint32_t bh, int t) {
+  return x.p + (int64_t)(bh / a.heads) * x.sb + (int64_t)(bh % a.heads) * x.sh + (int64_t)t * x.st;
+}
+__device__ __forceinline__ float* out_row(const AttnOperand& x, const AttnArgs& a, uint32_t bh, int t) {
+  return const_cast<float*>(row_of(x, a, bh, t));
+}
+
 // Builds the packed mask tables: one thread per word.
 __global__ void __launch_bounds__(256) k_attn_mask_bits(AttnArgs a, uint32_t slices_h, uint64_t n_words) {
   const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
@@ -116,13 +128,12 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
   const uint32_t bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int tq = a.tq, tk = a.tk, nkt = tk / 16;
-  const float* Qb = a.q + (uint64_t)bh * tq * HD;
-  const float* Kb = a.k + (uint64_t)bh * tk * HD;
-  const float* Vb = a.v + (uint64_t)bh * tk * HD;
+  const float* Kb = row_of(a.k, a, bh, 0);
+  const float* Vb = row_of(a.v, a, bh, 0);
   for (int i = tid; i < tk * HD / 4; i += NT) {
     const int key = i / (HD / 4), d = (i % (HD / 4)) * 4;
-    *(float4*)&Ks[key * KP + d] = *(const float4*)(Kb + key * HD + d);
-    const float4 v = *(const float4*)(Vb + key * HD + d);
+    *(float4*)&Ks[key * KP + d] = *(const float4*)(Kb + key * a.k.st + d);
+    const float4 v = *(const float4*)(Vb + key * a.v.st + d);
     Vt[(d + 0) * TKP + key] = v.x;
     Vt[(d + 1) * TKP + key] = v.y;
     Vt[(d + 2) * TKP + key] = v.z;
@@ -137,7 +148,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
   float4 qf[ND];
 #pragma unroll
   for (int n = 0; n < ND; n++) {
-    const float4 x = *(const float4*)(Qb + q * HD + n * 16 + g4);
+    const float4 x = *(const float4*)(row_of(a.q, a, bh, q) + n * 16 + g4);
     qf[n] = make_float4(x.x * sc, x.y * sc, x.z * sc, x.w * sc);
   }
 
@@ -233,11 +244,12 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
       for (int n = 0; n < ND; n++)
         oacc[kt & 1][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j], Vt[(n * 16 + l16) * TKP + kt * 16 + g4 + j], oacc[kt & 1][n], 0, 0, 0);
   }
-  float* Ob = a.o + (uint64_t)bh * tq * HD;
 #pragma unroll
-  for (int n = 0; n < ND; n++)
+  for (int r = 0; r < 4; r++) {
+    float* orow = out_row(a.o, a, bh, q0 + g4 + r);
 #pragma unroll
-    for (int r = 0; r < 4; r++) Ob[(q0 + g4 + r) * HD + n * 16 + l16] = oacc[0][n][r] + oacc[1][n][r];
+    for (int n = 0; n < ND; n++) orow[n * 16 + l16] = oacc[0][n][r] + oacc[1][n][r];
+  }
 }
 
 // Backward, query side: one block per 16 * WAVES queries; dq = dS k, and rowsum(dO * O) per query.
@@ -249,28 +261,28 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
   const uint32_t bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int tq = a.tq, tk = a.tk, nkt = tk / 16;
-  const float* Kb = a.k + (uint64_t)bh * tk * HD;
-  const float* Vb = a.v + (uint64_t)bh * tk * HD;
+  const float* Kb = row_of(a.k, a, bh, 0);
+  const float* Vb = row_of(a.v, a, bh, 0);
   for (int i = tid; i < tk * HD / 4; i += NT) {
     const int key = i / (HD / 4), d = (i % (HD / 4)) * 4;
-    *(float4*)&Ks[key * KP + d] = *(const float4*)(Kb + key * HD + d);
-    *(float4*)&Vs[key * KP + d] = *(const float4*)(Vb + key * HD + d);
+    *(float4*)&Ks[key * KP + d] = *(const float4*)(Kb + key * a.k.st + d);
+    *(float4*)&Vs[key * KP + d] = *(const float4*)(Vb + key * a.v.st + d);
   }
   __syncthreads();
   const int q0 = blockIdx.x * 16 * WAVES + w * 16;
   if (q0 >= tq) return;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
   const int q = q0 + l16;
-  const uint64_t qoff = ((uint64_t)bh * tq + q) * HD;
+  const float *qrow = row_of(a.q, a, bh, q), *grow = row_of(a.d_o, a, bh, q), *orow = row_of(a.o_in, a, bh, q);
   const float sc = LOG2E / a.div, fill = a.fill * LOG2E, rdiv = 1.0f / a.div;
   float4 qf[ND], gf[ND];
   float dd = 0.0f;
 #pragma unroll
   for (int n = 0; n < ND; n++) {
-    const float4 x = *(const float4*)(a.q + qoff + n * 16 + g4);
+    const float4 x = *(const float4*)(qrow + n * 16 + g4);
     qf[n] = make_float4(x.x * sc, x.y * sc, x.z * sc, x.w * sc);
-    gf[n] = *(const float4*)(a.d_o + qoff + n * 16 + g4);
-    const float4 o = *(const float4*)(a.o_in + qoff + n * 16 + g4);
+    gf[n] = *(const float4*)(grow + n * 16 + g4);
+    const float4 o = *(const float4*)(orow + n * 16 + g4);
     dd += gf[n].x * o.x + gf[n].y * o.y + gf[n].z * o.z + gf[n].w * o.w;
   }
   dd = row_sum(dd);
@@ -325,11 +337,12 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
       for (int n = 0; n < ND; n++)
         dacc[kt & 1][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[j], Ks[(kt * 16 + g4 + j) * KP + n * 16 + l16], dacc[kt & 1][n], 0, 0, 0);
   }
-  float* dqb = a.dq + (uint64_t)bh * tq * HD;
 #pragma unroll
-  for (int n = 0; n < ND; n++)
+  for (int r = 0; r < 4; r++) {
+    float* drow = out_row(a.dq, a, bh, q0 + g4 + r);
 #pragma unroll
-    for (int r = 0; r < 4; r++) dqb[(q0 + g4 + r) * HD + n * 16 + l16] = dacc[0][n][r] + dacc[1][n][r];
+    for (int n = 0; n < ND; n++) drow[n * 16 + l16] = dacc[0][n][r] + dacc[1][n][r];
+  }
 }
 
 // Backward, key side: one block per 16 * WAVES keys; dv = P^T dO and dk = dS^T q over all queries.
@@ -343,12 +356,12 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   const uint32_t bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int tq = a.tq, tk = a.tk, nqt = tq / 16;
-  const float* Qb = a.q + (uint64_t)bh * tq * HD;
-  const float* Gb = a.d_o + (uint64_t)bh * tq * HD;
+  const float* Qb = row_of(a.q, a, bh, 0);
+  const float* Gb = row_of(a.d_o, a, bh, 0);
   for (int i = tid; i < tq * HD / 4; i += NT) {
     const int qq = i / (HD / 4), d = (i % (HD / 4)) * 4;
-    *(float4*)&Qs[qq * KP + d] = *(const float4*)(Qb + qq * HD + d);
-    *(float4*)&Gs[qq * KP + d] = *(const float4*)(Gb + qq * HD + d);
+    *(float4*)&Qs[qq * KP + d] = *(const float4*)(Qb + qq * a.q.st + d);
+    *(float4*)&Gs[qq * KP + d] = *(const float4*)(Gb + qq * a.d_o.st + d);
   }
   const uint64_t srow = (uint64_t)bh * tq;
   MaskTables mt{nullptr, nullptr, nullptr};
@@ -367,9 +380,9 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   float4 kf[ND], vf[ND];
 #pragma unroll
   for (int n = 0; n < ND; n++) {
-    const float4 x = *(const float4*)(a.k + ((uint64_t)bh * tk + key) * HD + n * 16 + g4);
+    const float4 x = *(const float4*)(row_of(a.k, a, bh, key) + n * 16 + g4);
     kf[n] = make_float4(x.x * sc, x.y * sc, x.z * sc, x.w * sc);
-    vf[n] = *(const float4*)(a.v + ((uint64_t)bh * tk + key) * HD + n * 16 + g4);
+    vf[n] = *(const float4*)(row_of(a.v, a, bh, key) + n * 16 + g4);
   }
   // The lane's key column of the mask, 32 queries per word.
   uint32_t cb[NW];
@@ -423,15 +436,16 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
         ka[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[j], Qs[(qt * 16 + g4 + j) * KP + n * 16 + l16], ka[n], 0, 0, 0);
       }
   }
-  float* dkb = a.dk + (uint64_t)bh * tk * HD;
-  float* dvb = a.dv + (uint64_t)bh * tk * HD;
 #pragma unroll
-  for (int n = 0; n < ND; n++)
+  for (int r = 0; r < 4; r++) {
+    float* krow = out_row(a.dk, a, bh, k0 + g4 + r);
+    float* vrow = out_row(a.dv, a, bh, k0 + g4 + r);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      dkb[(k0 + g4 + r) * HD + n * 16 + l16] = kacc[0][n][r] + kacc[1][n][r];
-      dvb[(k0 + g4 + r) * HD + n * 16 + l16] = vacc[0][n][r] + vacc[1][n][r];
+    for (int n = 0; n < ND; n++) {
+      krow[n * 16 + l16] = kacc[0][n][r] + kacc[1][n][r];
+      vrow[n * 16 + l16] = vacc[0][n][r] + vacc[1][n][r];
     }
+  }
 }
 
 // Four waves per block unless the launch would still give every CU two blocks with eight.

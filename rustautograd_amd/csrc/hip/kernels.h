@@ -98,25 +98,29 @@ struct GemmArgs {
   uint64_t workspace_bytes;
 };
 // Fused attention (attention.hip) over bh = batch * heads independent (tq x hd, tk x hd)
-// problems in row-major [bh][t][hd] slots. The mask, when present, is read at
-// b * s0 + h * s1 + q * s2 + k * s3 (zero strides for broadcast dimensions); the forward packs it
-// into `mask_bits` (attention_mask_words words), which the backward reads.
+// problems. Operands are strided views: row t of problem b * heads + h starts at
+// p + b * sb + h * sh + t * st, with hd contiguous floats (16-byte aligned). The mask, when
+// present, is read at b * s0 + h * s1 + q * s2 + k * s3 (zero strides for broadcast dimensions);
+// the forward packs it into `mask_bits` (attention_mask_words words), which the backward reads.
 constexpr int ATTN_MAX_KEYS = 256;
+struct AttnOperand {
+  const float* p;
+  int64_t sb, sh, st;
+};
 struct AttnArgs {
   uint32_t bh, heads;
   int tq, tk, hd;
-  const float *q, *k, *v;
+  AttnOperand q, k, v;
   const float* mask;
   int64_t mask_strides[4];
   uint32_t* mask_bits;
   float div, fill;  // scores are divided by `div`; masked scores are `fill`
-  float* o;         // forward output
+  AttnOperand o;    // forward output
   // Per-query statistics, [bh][tq] each: the row max and sum (forward) and rowsum(dO * O)
   // (backward's query pass).
   float *stat_m, *stat_z, *stat_dd;
-  const float* o_in;  // backward inputs: the forward output and its cotangent
-  const float* d_o;
-  float *dq, *dk, *dv;
+  AttnOperand o_in, d_o;  // backward inputs: the forward output and its cotangent
+  AttnOperand dq, dk, dv;
 };
 bool attention_supported(int dtype, int64_t hd, int64_t tq, int64_t tk);
 uint64_t attention_mask_words(const AttnArgs& a);

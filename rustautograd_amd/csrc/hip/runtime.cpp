@@ -411,13 +411,20 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
   if ((uint64_t)ss.cap < need || esize(ss.dtype) != 4)
     throw std::runtime_error("attention statistics slot holds " + std::to_string(ss.cap) + " words, needs " + std::to_string(need));
   const int64_t mask = at.mask_slot, stats = at.stats_slot;
-  const std::vector<int64_t> in = at.in, out = at.out;
+  const std::vector<rgplan::AttnView> in = at.in, out = at.out;
+  for (const auto* vs : {&in, &out})
+    for (const auto& v : *vs)
+      if (v.offset % 4 || v.sb % 4 || v.sh % 4 || v.st % 4 || esize(prog.plan.slots[(size_t)v.slot].dtype) != 4)
+        throw std::runtime_error("attention operand view is not 16-byte aligned");
   const bool bwd = at.backward;
   return [=](hipStream_t s, void* const* sl, void*) {
     rgk::AttnArgs a = base;
-    a.q = (const float*)sl[in[0]];
-    a.k = (const float*)sl[in[1]];
-    a.v = (const float*)sl[in[2]];
+    auto op = [&](const rgplan::AttnView& v) {
+      return rgk::AttnOperand{(const float*)sl[v.slot] + v.offset, v.sb, v.sh, v.st};
+    };
+    a.q = op(in[0]);
+    a.k = op(in[1]);
+    a.v = op(in[2]);
     float* st = (float*)sl[stats];
     a.stat_m = st;
     a.stat_z = st + rows;
@@ -427,14 +434,14 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
       a.mask_bits = (uint32_t*)(st + 3 * rows);
     }
     if (!bwd) {
-      a.o = (float*)sl[out[0]];
+      a.o = op(out[0]);
       rgk::attention_forward(s, a);
     } else {
-      a.o_in = (const float*)sl[in[3]];
-      a.d_o = (const float*)sl[in[4]];
-      a.dq = (float*)sl[out[0]];
-      a.dk = (float*)sl[out[1]];
-      a.dv = (float*)sl[out[2]];
+      a.o_in = op(in[3]);
+      a.d_o = op(in[4]);
+      a.dq = op(out[0]);
+      a.dk = op(out[1]);
+      a.dv = op(out[2]);
       rgk::attention_backward(s, a);
     }
   };

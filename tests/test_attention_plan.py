@@ -128,6 +128,15 @@ def test_multi_head_attention_module_and_gpt_layers():
     dev = rg.compile(step, (state,), device=DEVPLAN, validate="none")
     kinds = [s["backward"] for s in _steps(dev)]
     assert kinds.count(False) == 2 and kinds.count(True) == 2, kinds
+    # q, k and v are read in place from the projection that produced them, O is written with its
+    # heads merged, and dq, dk, dv go straight into one gradient tensor: the transposes, slices
+    # and pads around attention are gone.
+    for s in _steps(dev):
+        assert len(set(s["input_slots"][:3])) == 1, s
+        if s["backward"]:
+            assert len(set(s["output_slots"])) == 1, s
+    ops = [s["op"] for s in dev._n.plan_summary() if s["kind"] == "instr"]
+    assert "pad" not in ops and ops.count("transpose") <= 2, ops
     cpu = rg.compile(step, (state,), device="cpu", validate="none")
     a = rg.run(dev, state, steps=2)
     b = rg.run(cpu, state, steps=2)
