@@ -32,7 +32,8 @@
  *                    Broadcast input whose last dimension is 1 is row level. Outputs of
  *                    row-level registers hold one value per row.
  *     RG_STEP_ATTN   dtype, backward (0/1), bh, heads, tq, tk, hd, div (f64 bits), fill (f64 bits),
- *                    mask_slot (-1: none), mask strides (4 words), stats_slot,
+ *                    mask_slot (-1: none), mask strides (4 words), mask_bits_slot, build_bits (0/1),
+ *                    stats_slot,
  *                    n_in, per in: slot, offset, sb, sh, st,  n_out, per out: the same,  node
  *                    Fused attention (no reference counterpart; device plans only) over bh
  *                    independent problems b * heads + h; row t, column d of an operand lies at
@@ -43,10 +44,12 @@
  *                    The softmax is over keys; the mask (f32, nonzero = visible) is read at
  *                    b * s0 + h * s1 + q * s2 + k * s3 for problem b * heads + h. The stats
  *                    slot holds 3 * bh * tq words of per-query statistics (written by the
- *                    forward, read by the backward) followed, with a mask, by
+ *                    forward, read by the backward). With a mask, mask_bits_slot holds
  *                    slices * (2 * tq * tk / 32 + tq) words of packed mask bits, slices being
- *                    (s0 ? bh / heads : 1) * (s1 ? heads : 1). Planned only for hd in
- *                    {16, 32, 64} and tq, tk multiples of 32 up to RG_ATTN_MAX_T.
+ *                    (s0 ? bh / heads : 1) * (s1 ? heads : 1); the step with build_bits set
+ *                    packs them, and later steps reading the same mask reuse them. Planned
+ *                    only for hd in {16, 32, 64} and tq, tk multiples of 32 up to
+ *                    RG_ATTN_MAX_T.
  *
  * Attribute words per op:
  *   MATMUL_T       ta, tb
@@ -150,6 +153,8 @@ struct Attn {
   double div, fill;
   int64_t mask_slot;
   int64_t mask_strides[4];
+  int64_t mask_bits_slot;
+  bool build_bits;
   int64_t stats_slot;
   std::vector<AttnView> in, out;
   int64_t node;
@@ -310,6 +315,8 @@ inline Plan parse(const int64_t* w, size_t nw) {
       memcpy(&a.fill, &bits, 8);
       a.mask_slot = next();
       for (int k = 0; k < 4; k++) a.mask_strides[k] = next();
+      a.mask_bits_slot = next();
+      a.build_bits = next() != 0;
       a.stats_slot = next();
       for (int side = 0; side < 2; side++) {
         int64_t n = next();

@@ -349,9 +349,13 @@ bool Matcher::closed(AttnRegion& r) const {
 
 size_t attn_stats_words(const AttnRegion& r, const Graph& g) {
   AttnShape a = attn_shape(r, g);
-  size_t words = 3 * a.bh * a.tq;
-  if (r.mask >= 0) words += a.mask_slices * (2 * a.tq * a.tk / 32 + a.tq);
-  return words;
+  return 3 * a.bh * a.tq;
+}
+
+size_t attn_mask_words(const AttnRegion& r, const Graph& g) {
+  if (r.mask < 0) return 0;
+  AttnShape a = attn_shape(r, g);
+  return a.mask_slices * (2 * a.tq * a.tk / 32 + a.tq);
 }
 
 AttnShape attn_shape(const AttnRegion& r, const Graph& g) {

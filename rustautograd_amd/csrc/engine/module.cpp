@@ -255,6 +255,8 @@ PYBIND11_MODULE(_rg, m) {
                  d["tk"] = a.shape.tk;
                  d["hd"] = a.shape.hd;
                  d["masked"] = a.mask_slot >= 0;
+                 d["mask_bits_slot"] = a.mask_bits_slot;
+                 d["builds_mask_bits"] = a.build_mask_bits;
                  d["n"] = a.shape.bh * a.shape.tq * a.shape.hd;
                  py::list ins, outs;
                  for (auto& v : a.in) ins.append(v.slot);

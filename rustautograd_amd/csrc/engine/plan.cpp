@@ -780,6 +780,8 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       if (claimed[i] < 0) keep[i] = keep[i] && live[i];
   }
   std::vector<size_t> stats_slot(regions.size(), SIZE_MAX);
+  // One packed copy of each mask (node and broadcast shape), built by the first forward reading it.
+  std::map<std::vector<int64_t>, size_t> mask_tables;
 
   std::vector<Item> items;
   std::vector<bool> abs = fuse ? absorbed_broadcasts(g, keep, outputs, *fuse) : std::vector<bool>(total, false);
@@ -836,6 +838,17 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       for (const AttnOperand& o : region_views(r, bwd)) at.in.push_back(view(o));
       if (!bwd) stats_slot[(size_t)item.attn] = a.new_slot(DType::F32, attn_stats_words(r, g), true);
       at.stats_slot = stats_slot[(size_t)item.attn];
+      if (r.mask >= 0) {
+        const AttnShape& sh = at.shape;
+        std::vector<int64_t> key = {(int64_t)r.mask, (int64_t)sh.bh, (int64_t)sh.heads, (int64_t)sh.tq, (int64_t)sh.tk};
+        key.insert(key.end(), sh.mask_strides, sh.mask_strides + 4);
+        auto it = mask_tables.find(key);
+        if (it == mask_tables.end()) {
+          it = mask_tables.emplace(key, a.new_slot(DType::F32, attn_mask_words(r, g), true)).first;
+          at.build_mask_bits = true;  // items run in plan order: this is the first reader
+        }
+        at.mask_bits_slot = (int64_t)it->second;
+      }
       for (uint32_t o : bwd ? r.bwd_out : r.fwd_out) {
         value_slot[o] = a.alloc(g.nodes[o].dtype, g.nodes[o].n(), exact[o]);
         p.naive_bytes += g.nodes[o].n() * dsize(g.nodes[o].dtype);
@@ -1073,6 +1086,8 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
       w.push_back(bits);
       w.push_back(at.mask_slot);
       for (int k = 0; k < 4; k++) w.push_back(at.shape.mask_strides[k]);
+      w.push_back(at.mask_bits_slot);
+      w.push_back(at.build_mask_bits ? 1 : 0);
       w.push_back((int64_t)at.stats_slot);
       auto views = [&](const std::vector<AttnView>& vs) {
         w.push_back((int64_t)vs.size());

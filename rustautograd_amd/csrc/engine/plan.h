@@ -88,8 +88,10 @@ struct AttnShape {
 };
 std::vector<AttnRegion> match_attention(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs);
 AttnShape attn_shape(const AttnRegion& r, const Graph& g);
-// 32-bit words of the statistics slot a region's steps share (include/rg_plan.h RG_STEP_ATTN).
+// 32-bit words of the statistics slot a region's steps share, and of the packed mask tables
+// (include/rg_plan.h RG_STEP_ATTN).
 size_t attn_stats_words(const AttnRegion& r, const Graph& g);
+size_t attn_mask_words(const AttnRegion& r, const Graph& g);
 
 struct Instr {
   Op op;
@@ -142,6 +144,8 @@ struct Attn {
   AttnShape shape;
   double div = 1.0, fill = 0.0;
   int64_t mask_slot = -1;
+  int64_t mask_bits_slot = -1;  // packed mask tables, shared by the steps of one mask
+  bool build_mask_bits = false;  // this step packs them (the first forward that reads the mask)
   size_t stats_slot = 0;
   std::vector<AttnView> in, out;  // forward: q, k, v -> O; backward: q, k, v, O, dO -> dq, dk, dv
   uint32_t node = 0;              // the O node (forward) or the dq node (backward)

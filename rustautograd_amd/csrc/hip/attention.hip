@@ -25,12 +25,15 @@
 // per-element divisions and exp by rounding-level amounts (1e-6 relative at most on P), the same
 // order as the MFMA's own reduction differences, well inside the products' 1e-4 tolerance. The
 // forward keeps a whole row of scores in registers (keys <= 256), so P comes from the final max
-// and sum, not from online rescaling. The backward recomputes P from the saved max and sum and
-// uses rowsum(P dP) = rowsum(dO * O).
+// and sum, as the backward recomputes it; the backward uses rowsum(P dP) = rowsum(dO * O), and
+// its tile loops keep the next tile's score products in flight on the matrix cores while the
+// vector units finish the current tile.
 //
-// Causal-style masks: a 16x16 tile whose mask entries are all zero is skipped, which is exact
-// when every row of the tile has some visible key: its probabilities underflow to exactly zero
-// (exp(fill - max) with fill = -1e9). Waves with a fully masked row skip nothing.
+// Causal-style masks: the forward skips 16x16 tiles whose mask entries are all zero; the backward
+// walks only the tiles between the first and the last key (or query) any row of the wave can
+// see. Both are exact when every row has some visible key: the skipped probabilities underflow
+// to exactly zero (exp(fill - max) with fill = -1e9), and hidden tiles inside the range
+// contribute exact zeros. Waves with a fully masked row skip nothing.
 #include <hip/hip_runtime.h>
 
 #include "kernels.h"
@@ -94,28 +97,69 @@ __device__ __forceinline__ float* out_row(const AttnOperand& x, const AttnArgs& 
   return const_cast<float*>(row_of(x, a, bh, t));
 }
 
-// Builds the packed mask tables: one thread per word.
-__global__ void __launch_bounds__(256) k_attn_mask_bits(AttnArgs a, uint32_t slices_h, uint64_t n_words) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n_words) return;
+// Builds the packed mask tables: one wave per query row (its row bits and visible flag) or per key
+// column (its column bits) of one mask slice, 64 mask entries per ballot.
+__global__ void __launch_bounds__(256) k_attn_mask_bits(AttnArgs a, uint32_t slices_h, uint32_t n_waves) {
+  const uint32_t wv = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (wv >= n_waves) return;
   const int tq = a.tq, tk = a.tk;
-  const uint64_t per = slice_words(tq, tk), n = (uint64_t)tq * tk / 32;
-  const uint32_t slice = (uint32_t)(i / per), b = slice / slices_h, h = slice % slices_h;
-  const uint64_t t = i % per;
+  const uint32_t per = (uint32_t)(tq + tk), slice = wv / per, t = wv % per;
+  const uint32_t b = slice / slices_h, h = slice % slices_h;
   const float* m = a.mask + (int64_t)b * a.mask_strides[0] + (int64_t)h * a.mask_strides[1];
   const int64_t sq = a.mask_strides[2], sk = a.mask_strides[3];
-  uint32_t word = 0;
-  if (t < n) {  // row bits
-    const int q = (int)(t / (tk / 32)), w = (int)(t % (tk / 32));
-    for (int j = 0; j < 32; j++) word |= (m[q * sq + (int64_t)(32 * w + j) * sk] != 0.0f ? 1u : 0u) << j;
-  } else if (t < 2 * n) {  // column bits
-    const int k = (int)((t - n) / (tq / 32)), w = (int)((t - n) % (tq / 32));
-    for (int j = 0; j < 32; j++) word |= (m[(int64_t)(32 * w + j) * sq + k * sk] != 0.0f ? 1u : 0u) << j;
-  } else {  // some key visible in row q
-    const int q = (int)(t - 2 * n);
-    for (int k = 0; k < tk && !word; k++) word = m[q * sq + k * sk] != 0.0f;
+  const uint64_t n = (uint64_t)tq * tk / 32;
+  uint32_t* base = a.mask_bits + (uint64_t)slice * (2 * n + tq);
+  if (t < (uint32_t)tq) {  // row t: bits over keys, and whether any is set
+    uint64_t any = 0;
+    for (int c = 0; c < tk; c += 64) {
+      const uint64_t bits = __ballot(c + (int)lane < tk && m[(int64_t)t * sq + (int64_t)(c + lane) * sk] != 0.0f);
+      any |= bits;
+      if (lane < 2 && c + 32 * (int)lane < tk) base[(uint64_t)t * (tk / 32) + c / 32 + lane] = (uint32_t)(bits >> (32 * lane));
+    }
+    if (lane == 0) base[2 * n + t] = any != 0;
+  } else {  // column k: bits over queries
+    const int k = (int)(t - tq);
+    for (int c = 0; c < tq; c += 64) {
+      const uint64_t bits = __ballot(c + (int)lane < tq && m[(int64_t)(c + lane) * sq + (int64_t)k * sk] != 0.0f);
+      if (lane < 2 && c + 32 * (int)lane < tq) base[n + (uint64_t)k * (tq / 32) + c / 32 + lane] = (uint32_t)(bits >> (32 * lane));
+    }
   }
-  a.mask_bits[i] = word;
+}
+
+__device__ __forceinline__ int wave_min(int x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = min(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = max(x, __shfl_xor(x, o));
+  return x;
+}
+
+// Tiles [lo, hi) of 16 holding every set bit of each lane's bit row (`nw` words): the first and
+// last set bits over the wave. With `skip` false (a row of the wave sees nothing, so its masked
+// entries are not exactly zero), every tile.
+__device__ __forceinline__ void tile_range(const uint32_t* words, int nw, bool skip, int n_tiles, int* lo, int* hi) {
+  *lo = 0;
+  *hi = n_tiles;
+  if (!skip) return;
+  int first = 1 << 30, last = -1;
+  for (int i = 0; i < nw; i++) {
+    const uint32_t w = words[i];
+    if (w) {
+      if (first == 1 << 30) first = 32 * i + __builtin_ctz(w);
+      last = 32 * i + 31 - __builtin_clz(w);
+    }
+  }
+  first = wave_min(first);
+  last = wave_max(last);
+  if (last < 0) {
+    *hi = 0;
+    return;
+  }
+  *lo = first / 16;
+  *hi = last / 16 + 1;
 }
 
 // Forward: one block per 16 * WAVES queries of one (batch, head); wave w owns queries
@@ -252,7 +296,9 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
   }
 }
 
-// Backward, query side: one block per 16 * WAVES queries; dq = dS k, and rowsum(dO * O) per query.
+// Backward, query side: one block per 16 * WAVES queries; dq = dS k, and rowsum(dO * O) per
+// query. The next key tile's scores and dP are in flight while the current tile's dS is formed
+// and multiplied into dq.
 template <int HD, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
   constexpr int KP = HD + 4, ND = HD / 16, NT = 64 * WAVES;
@@ -287,7 +333,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
   }
   dd = row_sum(dd);
   const uint64_t row = (uint64_t)bh * tq + q;
-  const float mx = a.stat_m[row], z = a.stat_z[row];
+  const float mx = a.stat_m[row], rz = 1.0f / a.stat_z[row];
   if (g4 == 0) a.stat_dd[row] = dd;
   const uint32_t* mr = nullptr;
   bool row_vis = true;
@@ -296,63 +342,60 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
     mr = mt.rows + (uint64_t)q * (tk / 32);
     row_vis = mt.vis[q] != 0;
   }
-  const bool all_vis = __ballot(row_vis) == ALL_LANES;
-  const float rz = 1.0f / z;
-
-  floatx4 dacc[2][ND];
-#pragma unroll
-  for (int n = 0; n < ND; n++) dacc[0][n] = dacc[1][n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int kt = 0; kt < nkt; kt++) {
-    uint32_t bits = 0xF;
-    if (mr) {
-      bits = mr[kt >> 1] >> (((kt & 1) << 4) + g4) & 0xF;
-      if (all_vis && __ballot(bits != 0) == 0) continue;
-    }
-    floatx4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+  int lo = 0, hi = nkt;
+  if (mr) tile_range(mr, tk / 32, __ballot(row_vis) == ALL_LANES, nkt, &lo, &hi);
+  auto scores = [&](int kt, floatx4& sacc, floatx4& pacc) {
+    sacc = pacc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < ND; n++) {
       const float4 kk = *(const float4*)&Ks[(kt * 16 + l16) * KP + n * 16 + g4];
       const float4 vv = *(const float4*)&Vs[(kt * 16 + l16) * KP + n * 16 + g4];
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qf[n].x, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, gf[n].x, pacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qf[n].y, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, gf[n].y, pacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qf[n].z, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, gf[n].z, pacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qf[n].w, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, gf[n].w, pacc, 0, 0, 0);
+      sacc = mfma4(sacc, kk, qf[n]);
+      pacc = mfma4(pacc, vv, gf[n]);
     }
-    // sacc[r] = S[q][key], pacc[r] = dP[q][key] for key = kt * 16 + g4 + r.
+  };
+  floatx4 dacc[ND];
+#pragma unroll
+  for (int n = 0; n < ND; n++) dacc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 s_cur = {0.f, 0.f, 0.f, 0.f}, p_cur = s_cur;
+  if (lo < hi) scores(lo, s_cur, p_cur);
+  for (int kt = lo; kt < hi; kt++) {
+    floatx4 s_nxt = s_cur, p_nxt = p_cur;
+    if (kt + 1 < hi) scores(kt + 1, s_nxt, p_nxt);
+    // s_cur[r] = S'[q][key], p_cur[r] = dP[q][key] for key = kt * 16 + g4 + r.
+    const uint32_t bits = mr ? (mr[kt >> 1] >> (((kt & 1) << 4) + g4)) & 0xF : 0xF;
     float ds[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const bool vis = bits >> r & 1;
-      const float p = exp2_hw((vis ? sacc[r] : fill) - mx) * rz;
-      ds[r] = vis ? p * (pacc[r] - dd) * rdiv : 0.0f;
+      const float p = exp2_hw((vis ? s_cur[r] : fill) - mx) * rz;
+      ds[r] = vis ? p * (p_cur[r] - dd) * rdiv : 0.0f;
     }
     // dq += dS K: A = dS (query l16, keys g4 + j), B = K rows g4 + j of the tile, column n*16 + l16.
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int n = 0; n < ND; n++)
-        dacc[kt & 1][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[j], Ks[(kt * 16 + g4 + j) * KP + n * 16 + l16], dacc[kt & 1][n], 0, 0, 0);
+        dacc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[j], Ks[(kt * 16 + g4 + j) * KP + n * 16 + l16], dacc[n], 0, 0, 0);
+    s_cur = s_nxt;
+    p_cur = p_nxt;
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     float* drow = out_row(a.dq, a, bh, q0 + g4 + r);
 #pragma unroll
-    for (int n = 0; n < ND; n++) drow[n * 16 + l16] = dacc[0][n][r] + dacc[1][n][r];
+    for (int n = 0; n < ND; n++) drow[n * 16 + l16] = dacc[n][r];
   }
 }
 
-// Backward, key side: one block per 16 * WAVES keys; dv = P^T dO and dk = dS^T q over all queries.
+// Backward, key side: one block per 16 * WAVES keys; dv = P^T dO and dk = dS^T q over the query
+// tiles that see the wave's keys, the next tile's scores and dP in flight as in the query pass.
 template <int HD, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   constexpr int KP = HD + 4, ND = HD / 16, NT = 64 * WAVES, NW = ATTN_MAX_KEYS / 32;
   __shared__ float Qs[ATTN_MAX_KEYS * KP];
   __shared__ float Gs[ATTN_MAX_KEYS * KP];
   __shared__ float4 St[ATTN_MAX_KEYS];  // per query: row max, row sum, rowsum(dO * O), 1 / row sum
-  __shared__ uint32_t Rv[ATTN_MAX_KEYS];  // per query: some key visible
   const uint32_t bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int tq = a.tq, tk = a.tk, nqt = tq / 16;
@@ -366,12 +409,14 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   const uint64_t srow = (uint64_t)bh * tq;
   MaskTables mt{nullptr, nullptr, nullptr};
   if (a.mask_bits) mt = mask_tables(a, bh);
+  int vis_all = 1;
   for (int i = tid; i < tq; i += NT) {
     const float zz = a.stat_z[srow + i];
     St[i] = make_float4(a.stat_m[srow + i], zz, a.stat_dd[srow + i], 1.0f / zz);
-    Rv[i] = mt.vis ? mt.vis[i] : 1u;
+    if (mt.vis && !mt.vis[i]) vis_all = 0;
   }
-  __syncthreads();
+  // Every query row sees some key: then masked entries are exactly zero and may be skipped.
+  const bool all_vis = __syncthreads_and(vis_all);
   const int k0 = blockIdx.x * 16 * WAVES + w * 16;
   if (k0 >= tk) return;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
@@ -388,53 +433,51 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   uint32_t cb[NW];
 #pragma unroll
   for (int i = 0; i < NW; i++) cb[i] = (mt.cols && i < tq / 32) ? mt.cols[(uint64_t)key * (tq / 32) + i] : ~0u;
-  floatx4 kacc[2][ND], vacc[2][ND];
+  int lo = 0, hi = nqt;
+  if (mt.cols) tile_range(cb, tq / 32, all_vis, nqt, &lo, &hi);
+  auto scores = [&](int qt, floatx4& sacc, floatx4& pacc) {
+    sacc = pacc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int n = 0; n < ND; n++) kacc[0][n] = kacc[1][n] = vacc[0][n] = vacc[1][n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int qt = 0; qt < nqt; qt++) {
+    for (int n = 0; n < ND; n++) {
+      const float4 qq = *(const float4*)&Qs[(qt * 16 + l16) * KP + n * 16 + g4];
+      const float4 gg = *(const float4*)&Gs[(qt * 16 + l16) * KP + n * 16 + g4];
+      sacc = mfma4(sacc, qq, kf[n]);
+      pacc = mfma4(pacc, gg, vf[n]);
+    }
+  };
+  floatx4 kacc[ND], vacc[ND];
+#pragma unroll
+  for (int n = 0; n < ND; n++) kacc[n] = vacc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 s_cur = {0.f, 0.f, 0.f, 0.f}, p_cur = s_cur;
+  if (lo < hi) scores(lo, s_cur, p_cur);
+  for (int qt = lo; qt < hi; qt++) {
+    floatx4 s_nxt = s_cur, p_nxt = p_cur;
+    if (qt + 1 < hi) scores(qt + 1, s_nxt, p_nxt);
     const int qb = qt * 16 + g4;  // the lane's four queries qb .. qb + 3
     uint32_t word = cb[0];
 #pragma unroll
     for (int i = 1; i < NW; i++)
       if (qt >> 1 == i) word = cb[i];
     const uint32_t bits = word >> (((qt & 1) << 4) + g4) & 0xF;
-    if (mt.cols) {
-      const bool vis4 = Rv[qb] && Rv[qb + 1] && Rv[qb + 2] && Rv[qb + 3];
-      if (__ballot(vis4) == ALL_LANES && __ballot(bits != 0) == 0) continue;
-    }
-    floatx4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int n = 0; n < ND; n++) {
-      const float4 qq = *(const float4*)&Qs[(qt * 16 + l16) * KP + n * 16 + g4];
-      const float4 gg = *(const float4*)&Gs[(qt * 16 + l16) * KP + n * 16 + g4];
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qq.x, kf[n].x, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gg.x, vf[n].x, pacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qq.y, kf[n].y, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gg.y, vf[n].y, pacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qq.z, kf[n].z, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gg.z, vf[n].z, pacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qq.w, kf[n].w, sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gg.w, vf[n].w, pacc, 0, 0, 0);
-    }
-    // sacc[r] = S[qb + r][key], pacc[r] = dP[qb + r][key].
+    // s_cur[r] = S'[qb + r][key], p_cur[r] = dP[qb + r][key].
     float p[4], ds[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const bool vis = bits >> r & 1;
       const float4 st = St[qb + r];
-      p[r] = exp2_hw((vis ? sacc[r] : fill) - st.x) * st.w;
-      ds[r] = vis ? p[r] * (pacc[r] - st.z) * rdiv : 0.0f;
+      p[r] = exp2_hw((vis ? s_cur[r] : fill) - st.x) * st.w;
+      ds[r] = vis ? p[r] * (p_cur[r] - st.z) * rdiv : 0.0f;
     }
     // dv += P^T dO, dk += dS^T q: A = P^T / dS^T (key l16, queries g4 + j), B = rows g4 + j of the tile.
-    floatx4* va = vacc[qt & 1];
-    floatx4* ka = kacc[qt & 1];
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int n = 0; n < ND; n++) {
-        va[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j], Gs[(qt * 16 + g4 + j) * KP + n * 16 + l16], va[n], 0, 0, 0);
-        ka[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[j], Qs[(qt * 16 + g4 + j) * KP + n * 16 + l16], ka[n], 0, 0, 0);
+        vacc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j], Gs[(qt * 16 + g4 + j) * KP + n * 16 + l16], vacc[n], 0, 0, 0);
+        kacc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[j], Qs[(qt * 16 + g4 + j) * KP + n * 16 + l16], kacc[n], 0, 0, 0);
       }
+    s_cur = s_nxt;
+    p_cur = p_nxt;
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
@@ -442,8 +485,8 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
     float* vrow = out_row(a.dv, a, bh, k0 + g4 + r);
 #pragma unroll
     for (int n = 0; n < ND; n++) {
-      krow[n * 16 + l16] = kacc[0][n][r] + kacc[1][n][r];
-      vrow[n * 16 + l16] = vacc[0][n][r] + vacc[1][n][r];
+      krow[n * 16 + l16] = kacc[n][r];
+      vrow[n * 16 + l16] = vacc[n][r];
     }
   }
 }
@@ -484,10 +527,11 @@ uint64_t attention_mask_words(const AttnArgs& a) {
   return slices * (2 * (uint64_t)a.tq * a.tk / 32 + a.tq);
 }
 
-void attention_forward(hipStream_t s, const AttnArgs& a) {
-  if (a.mask) {
-    const uint64_t n = attention_mask_words(a);
-    hipLaunchKernelGGL(k_attn_mask_bits, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, a, a.mask_strides[1] ? a.heads : 1u, n);
+void attention_forward(hipStream_t s, const AttnArgs& a, bool build_mask_bits) {
+  if (a.mask && build_mask_bits) {
+    const uint64_t slices = (a.mask_strides[0] ? a.bh / a.heads : 1) * (a.mask_strides[1] ? a.heads : 1);
+    const uint32_t waves = (uint32_t)(slices * (uint64_t)(a.tq + a.tk));
+    hipLaunchKernelGGL(k_attn_mask_bits, dim3((waves + 3) / 4), dim3(256), 0, s, a, a.mask_strides[1] ? a.heads : 1u, waves);
   }
   if (a.hd == 16) forward_hd<16>(s, a);
   else if (a.hd == 32) forward_hd<32>(s, a);

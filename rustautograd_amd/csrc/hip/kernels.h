@@ -101,7 +101,8 @@ struct GemmArgs {
 // problems. Operands are strided views: row t of problem b * heads + h starts at
 // p + b * sb + h * sh + t * st, with hd contiguous floats (16-byte aligned). The mask, when
 // present, is read at b * s0 + h * s1 + q * s2 + k * s3 (zero strides for broadcast dimensions);
-// the forward packs it into `mask_bits` (attention_mask_words words), which the backward reads.
+// the forward packs it into `mask_bits` (attention_mask_words words), which the backward and
+// later forwards over the same mask read.
 constexpr int ATTN_MAX_KEYS = 256;
 struct AttnOperand {
   const float* p;
@@ -124,7 +125,8 @@ struct AttnArgs {
 };
 bool attention_supported(int dtype, int64_t hd, int64_t tq, int64_t tk);
 uint64_t attention_mask_words(const AttnArgs& a);
-void attention_forward(hipStream_t s, const AttnArgs& a);
+// `build_mask_bits`: pack the mask into `mask_bits` first (else they hold it already).
+void attention_forward(hipStream_t s, const AttnArgs& a, bool build_mask_bits = true);
 void attention_backward(hipStream_t s, const AttnArgs& a);
 
 // Workspace bytes the product needs for its split-K partials.

@@ -402,14 +402,19 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
   base.fill = (float)at.fill;
   for (int k = 0; k < 4; k++) base.mask_strides[k] = at.mask_strides[k];
   const uint64_t rows = (uint64_t)at.bh * at.tq;
-  const uint64_t need = 3 * rows + (at.mask_slot >= 0 ? [&] {
+  const auto& ss = prog.plan.slots[(size_t)at.stats_slot];
+  if ((uint64_t)ss.cap < 3 * rows || esize(ss.dtype) != 4)
+    throw std::runtime_error("attention statistics slot holds " + std::to_string(ss.cap) + " words, needs " + std::to_string(3 * rows));
+  if (at.mask_slot >= 0) {
     rgk::AttnArgs t = base;
     t.mask = (const float*)1;
-    return rgk::attention_mask_words(t);
-  }() : 0);
-  const auto& ss = prog.plan.slots[(size_t)at.stats_slot];
-  if ((uint64_t)ss.cap < need || esize(ss.dtype) != 4)
-    throw std::runtime_error("attention statistics slot holds " + std::to_string(ss.cap) + " words, needs " + std::to_string(need));
+    const uint64_t need = rgk::attention_mask_words(t);
+    const auto& ms = prog.plan.slots[(size_t)at.mask_bits_slot];
+    if (at.mask_bits_slot < 0 || (uint64_t)ms.cap < need || esize(ms.dtype) != 4)
+      throw std::runtime_error("attention mask table slot too small: needs " + std::to_string(need) + " words");
+  }
+  const int64_t bits_slot = at.mask_bits_slot;
+  const bool build_bits = at.build_bits;
   const int64_t mask = at.mask_slot, stats = at.stats_slot;
   const std::vector<rgplan::AttnView> in = at.in, out = at.out;
   for (const auto* vs : {&in, &out})
@@ -431,11 +436,11 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
     a.stat_dd = st + 2 * rows;
     if (mask >= 0) {
       a.mask = (const float*)sl[mask];
-      a.mask_bits = (uint32_t*)(st + 3 * rows);
+      a.mask_bits = (uint32_t*)sl[bits_slot];
     }
     if (!bwd) {
       a.o = op(out[0]);
-      rgk::attention_forward(s, a);
+      rgk::attention_forward(s, a, build_bits);
     } else {
       a.o_in = op(in[3]);
       a.d_o = op(in[4]);

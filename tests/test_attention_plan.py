@@ -137,6 +137,11 @@ def test_multi_head_attention_module_and_gpt_layers():
             assert len(set(s["output_slots"])) == 1, s
     ops = [s["op"] for s in dev._n.plan_summary() if s["kind"] == "instr"]
     assert "pad" not in ops and ops.count("transpose") <= 2, ops
+    # Every layer reads the same causal mask: the first forward packs it, the rest reuse it.
+    steps = _steps(dev)
+    assert len({s["mask_bits_slot"] for s in steps}) == 1, steps
+    assert [s["builds_mask_bits"] for s in steps].count(True) == 1
+    assert steps[0]["builds_mask_bits"] and not steps[0]["backward"]
     cpu = rg.compile(step, (state,), device="cpu", validate="none")
     a = rg.run(dev, state, steps=2)
     b = rg.run(cpu, state, steps=2)
