@@ -193,7 +193,7 @@ def main():
                     "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4)}
         roof["traffic"] = measured_traffic(dom_name)
         roof.update({"kernel": dom_name, "launches_per_step": dom["launches"], "algorithmic_per_launch": round(per_launch),
-                     "avg_launch_us": round(avg_s * 1e6, 2)})
+                     "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]), "avg_launch_us": round(avg_s * 1e6, 2)})
         kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
                        "unit": v["unit"],
                        "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4)}
