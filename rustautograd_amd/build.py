@@ -28,7 +28,10 @@ ENGINE_SOURCES = ["graph.cpp", "autodiff.cpp", "optimize.cpp", "egraph.cpp", "pl
 HIP_SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "runtime.cpp", "jit.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result"]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result",
+             # MFMA accumulators in ordinary VGPRs: without it the GEMM's pipelined loop copies every
+             # accumulator out of and back into AGPRs on each iteration.
+             "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def _run(cmd):

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -137,13 +138,15 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
   const int kbeg = sp * k_per_split, kend = min(K, kbeg + k_per_split);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
-  Stager<AK ? BM : BK, AK ? BK : BM, NT, MODE> sa;
-  Stager<BKC ? BN : BK, BKC ? BK : BN, NT, MODE> sb;
-  auto load_tiles = [&](int k0) {
-    if (AK) sa.load(Ab, K, m0, k0, M, kend, tid);
-    else sa.load(Ab, M, k0, m0, kend, M, tid);
-    if (BKC) sb.load(Bb, K, n0, k0, N, kend, tid);
-    else sb.load(Bb, N, k0, n0, kend, N, tid);
+  // Two register stages: the global loads of tile t + 2 are issued while tile t is multiplied
+  // out of LDS and tile t + 1 waits in registers, so each load has two iterations to arrive.
+  Stager<AK ? BM : BK, AK ? BK : BM, NT, MODE> sa[2];
+  Stager<BKC ? BN : BK, BKC ? BK : BN, NT, MODE> sb[2];
+  auto load_tiles = [&](int k0, int set) {
+    if (AK) sa[set].load(Ab, K, m0, k0, M, kend, tid);
+    else sa[set].load(Ab, M, k0, m0, kend, M, tid);
+    if (BKC) sb[set].load(Bb, K, n0, k0, N, kend, tid);
+    else sb[set].load(Bb, N, k0, n0, kend, N, tid);
   };
 
   floatx4 acc[TM][TN];
@@ -152,21 +155,17 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+  if (nk > 0) load_tiles(kbeg, 0);
+  if (nk > 1) load_tiles(kbeg + BK, 1);
   if (nk > 0) {
-    load_tiles(kbeg);
-    sa.store(As[0], LDA, tid);
-    sb.store(Bs[0], LDB, tid);
+    sa[0].store(As[0], LDA, tid);
+    sb[0].store(Bs[0], LDB, tid);
   }
   __syncthreads();
   // MFMA 16x16x4 lane roles: lane l supplies row (A) / column (B) l % 16 at k = l / 16. Within a
   // group of 16 k the four k-steps j give lane l the k index 4 * (l / 16) + j in both operands.
   const int l16 = lane & 15, q4 = (lane >> 4) * 4;
-  for (int t = 0; t < nk; t++) {
-    const int buf = t & 1;
-    const bool more = t + 1 < nk;
-    if (more) load_tiles(kbeg + (t + 1) * BK);
-    const float* as = As[buf];
-    const float* bs = Bs[buf];
+  auto multiply = [&](const float* as, const float* bs) {
 #pragma unroll
     for (int kg = 0; kg < BK; kg += 16) {
       float a[4][TM], bv[4][TN];  // [k-step][tile]
@@ -206,11 +205,23 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
             else acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][i], bv[j][n], acc[i][n], 0, 0, 0);
           }
     }
-    if (more) {
-      sa.store(As[buf ^ 1], LDA, tid);
-      sb.store(Bs[buf ^ 1], LDB, tid);
+  };
+  // Iteration t multiplies LDS buffer t % 2, whose register stage t % 2 is then free for tile
+  // t + 2; tile t + 1 goes from register stage (t + 1) % 2 into the other LDS buffer, which every
+  // wave finished reading before the previous barrier.
+  auto iteration = [&](int t, auto parity) {
+    constexpr int P = decltype(parity)::value;
+    if (t + 2 < nk) load_tiles(kbeg + (t + 2) * BK, P);
+    multiply(As[P], Bs[P]);
+    if (t + 1 < nk) {
+      sa[P ^ 1].store(As[P ^ 1], LDA, tid);
+      sb[P ^ 1].store(Bs[P ^ 1], LDB, tid);
     }
     __syncthreads();
+  };
+  for (int t = 0; t < nk; t += 2) {
+    iteration(t, std::integral_constant<int, 0>());
+    if (t + 1 < nk) iteration(t + 1, std::integral_constant<int, 1>());
   }
   // Accumulator register r of lane l holds MFMA row 4 * (l / 16) + r, column l % 16 (for the
   // transposed form: output row l % 16, column 4 * (l / 16) + r). MFMA tile i row rho is block row
