@@ -48,7 +48,7 @@ std::string expr(int op, const std::vector<std::string>& a) {
 
 }  // namespace
 
-std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k) {
+std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k, bool device_fn) {
   const bool dbl = f.dtype == RG_F64;
   const char* T = dbl ? "double" : "float";
   const int V = dbl ? 2 : 4;
@@ -65,13 +65,14 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
   for (auto& o : f.outputs)
     for (auto& in : f.inputs) alias |= in.slot == o.second;
   const char* R = alias ? "" : "__restrict__ ";
-  s << "extern \"C\" __global__ void __launch_bounds__(" << TPB << ") " << name << "(";
+  if (device_fn) s << "static __device__ __forceinline__ void " << name << "(const unsigned int bid, ";
+  else s << "extern \"C\" __global__ void __launch_bounds__(" << TPB << ") " << name << "(";
   for (size_t j = 0; j < f.inputs.size(); j++) s << (j ? ", " : "") << "const " << T << "* " << R << "in" << j;
   for (size_t j = 0; j < f.outputs.size(); j++) s << ", " << T << "* " << R << "out" << j;
   s << ") {\n";
   s << "  typedef " << I << " I;\n";
   s << "  const I n = " << n << "ull;\n";
-  s << "  const I i0 = ((I)blockIdx.x * " << TPB << "u + (I)threadIdx.x) * " << V << "u;\n";
+  s << "  const I i0 = ((I)" << (device_fn ? "bid" : "blockIdx.x") << " * " << TPB << "u + (I)threadIdx.x) * " << V << "u;\n";
   s << "  if (i0 >= n) return;\n";
   s << "  const bool full = i0 + " << V << "u <= n;\n";
   const char* VT = dbl ? "double2" : "float4";
@@ -146,6 +147,32 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
       << "[i0 + v] = o" << j << "[v]; }\n";
   }
   s << "}\n";
+  return s.str();
+}
+
+std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, const std::string& name, FusedKernel* k) {
+  std::ostringstream s, params, body;
+  uint32_t start = 0;
+  body << "  const unsigned int b = blockIdx.x;\n";
+  for (size_t j = 0; j < parts.size(); j++) {
+    const rgplan::Fused& f = *parts[j];
+    const std::string part = name + "_" + std::to_string(j);
+    FusedKernel pk;
+    s << generate(f, part, &pk, true);
+    const char* T = f.dtype == RG_F64 ? "double" : "float";
+    std::string call = part + "(b - " + std::to_string(start) + "u";
+    for (size_t q = 0; q < f.inputs.size() + f.outputs.size(); q++) {
+      const std::string a = "p" + std::to_string(j) + "_" + std::to_string(q);
+      params << (params.tellp() > 0 ? ", " : "") << (q < f.inputs.size() ? "const " : "") << T << "* " << a;
+      call += ", " + a;
+    }
+    start += pk.grid;
+    body << "  if (b < " << start << "u) { " << call << "); return; }\n";
+  }
+  k->name = name;
+  k->grid = start;
+  k->vec = 1;
+  s << "extern \"C\" __global__ void __launch_bounds__(" << TPB << ") " << name << "(" << params.str() << ") {\n" << body.str() << "}\n";
   return s.str();
 }
 

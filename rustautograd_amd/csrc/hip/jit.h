@@ -21,9 +21,16 @@ struct FusedKernel {
   hipFunction_t fn = nullptr;
 };
 
-// Source of one kernel named `name` computing group `f`. `inplace` lists outputs whose slot is
-// also an input slot (the kernel then reads each element before writing it).
-std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k);
+// Source of one kernel named `name` computing group `f` (`k->grid` blocks). Outputs whose slot is
+// also an input slot are written in place (each element is read before it is written). With
+// `device_fn`, the source is instead a device function `name(block, inputs..., outputs...)` that
+// computes the elements of block `block`.
+std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k, bool device_fn = false);
+
+// Source of one kernel computing several independent groups side by side (horizontal fusion):
+// blocks [start_j, start_j + grid_j) compute part j, and the parameters are each part's inputs
+// then outputs, part after part. For groups too small to fill the device on their own.
+std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, const std::string& name, FusedKernel* k);
 
 // Source of one row-group kernel (RG_STEP_ROWS): `k->grid` blocks of four rows each.
 std::string generate_rows(const rgplan::Fused& f, const std::string& name, FusedKernel* k);

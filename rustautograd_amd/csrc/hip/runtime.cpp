@@ -12,6 +12,7 @@
 #include <functional>
 #include <memory>
 #include <mutex>
+#include <set>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -59,6 +60,15 @@ struct Program {
   std::vector<uint8_t> blob;
   std::vector<StepFn> steps;
   std::vector<std::unique_ptr<rgjit::FusedKernel>> fused;
+  // Runs of consecutive small, independent fused groups launched as one kernel (merge_sets):
+  // merged[m] replaces steps first..last when all of them run; merged_at[k] is the run starting
+  // at step k, or -1. The single-step functions stay for partial ranges and per-step timing.
+  struct Merged {
+    size_t first, last;
+    StepFn fn;
+  };
+  std::vector<Merged> merged;
+  std::vector<int64_t> merged_at;
   std::vector<void*> device_tables;  // per-batch GEMM offset tables
   uint64_t workspace_bytes = 0;
   std::vector<uint64_t> slot_bytes;
@@ -452,6 +462,55 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
   };
 }
 
+// Horizontal fusion. Fused groups of at most MERGE_MAX_GRID blocks leave most of the 256 CUs idle
+// and cost about a launch each (C4's AdamW updates: one group per parameter shape). Maximal runs
+// of consecutive such groups that are independent (no group writes a slot another group of the
+// run reads or writes; a group's own in-place update is fine) become one kernel, up to
+// MERGE_MAX_ARGS pointer arguments.
+constexpr uint32_t MERGE_MAX_GRID = 256;
+constexpr size_t MERGE_MAX_ARGS = 120;
+
+uint32_t fused_grid(const rgplan::Fused& f) {
+  const uint64_t per = (uint64_t)rgjit::TPB * (f.dtype == RG_F64 ? 2 : 4);
+  return (uint32_t)(((uint64_t)f.n + per - 1) / per);
+}
+
+std::vector<std::pair<size_t, size_t>> merge_sets(const Plan& plan) {
+  std::vector<std::pair<size_t, size_t>> sets;
+  auto small = [&](size_t k) {
+    const Step& st = plan.steps[k];
+    if (st.kind != RG_STEP_FUSED) return false;
+    uint32_t g = fused_grid(st.fused);
+    return g > 0 && g <= MERGE_MAX_GRID;
+  };
+  size_t k = 0;
+  while (k < plan.steps.size()) {
+    if (!small(k)) {
+      k++;
+      continue;
+    }
+    std::set<int64_t> reads, writes;
+    size_t args = 0, last = k;
+    for (size_t j = k; j < plan.steps.size() && small(j); j++) {
+      const auto& f = plan.steps[j].fused;
+      std::set<int64_t> r, w;
+      for (auto& in : f.inputs) r.insert(in.slot);
+      for (auto& o : f.outputs) w.insert(o.second);
+      bool clash = args + f.inputs.size() + f.outputs.size() > MERGE_MAX_ARGS;
+      for (int64_t x : w) clash |= reads.count(x) || writes.count(x);
+      for (int64_t x : r) clash |= writes.count(x) > 0;
+      if (clash) break;
+      reads.insert(r.begin(), r.end());
+      writes.insert(w.begin(), w.end());
+      args += f.inputs.size() + f.outputs.size();
+      last = j;
+    }
+    if (last > k) sets.push_back({k, last});
+    k = last + 1;
+  }
+  return sets;
+}
+
 void build_program(Program& prog) {
   std::ostringstream src;
   std::vector<rgjit::FusedKernel*> kernels;
@@ -465,7 +524,39 @@ void build_program(Program& prog) {
       prog.fused.push_back(std::move(fk));
     }
   }
+  const auto sets = merge_sets(prog.plan);
+  std::vector<rgjit::FusedKernel*> merged_kernels;
+  for (auto [first, last] : sets) {
+    std::vector<const rgplan::Fused*> parts;
+    for (size_t j = first; j <= last; j++) parts.push_back(&prog.plan.steps[j].fused);
+    auto fk = std::make_unique<rgjit::FusedKernel>();
+    src << rgjit::generate_merged(parts, "rgm" + std::to_string(first), fk.get());
+    kernels.push_back(fk.get());
+    merged_kernels.push_back(fk.get());
+    prog.fused.push_back(std::move(fk));
+  }
   rgjit::compile(src.str(), kernels);
+  prog.merged_at.assign(prog.plan.steps.size(), -1);
+  for (size_t m = 0; m < sets.size(); m++) {
+    auto [first, last] = sets[m];
+    std::vector<int64_t> slots;
+    for (size_t j = first; j <= last; j++) {
+      const auto& f = prog.plan.steps[j].fused;
+      for (auto& in : f.inputs) slots.push_back(in.slot);
+      for (auto& o : f.outputs) slots.push_back(o.second);
+    }
+    rgjit::FusedKernel* fk = merged_kernels[m];
+    prog.merged_at[first] = (int64_t)m;
+    prog.merged.push_back({first, last, [fk, slots](hipStream_t s, void* const* sl, void*) {
+                             void* ptrs[MERGE_MAX_ARGS];
+                             void* args[MERGE_MAX_ARGS];
+                             for (size_t j = 0; j < slots.size(); j++) {
+                               ptrs[j] = sl[slots[j]];
+                               args[j] = &ptrs[j];
+                             }
+                             hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, rgjit::TPB, 1, 1, 0, s, args, nullptr);
+                           }});
+  }
   size_t fi = 0;
   for (size_t k = 0; k < prog.plan.steps.size(); k++) {
     const Step& st = prog.plan.steps[k];
@@ -531,6 +622,43 @@ bool latch(Exec* e, hipError_t err, const char* what) {
   return true;
 }
 
+// Enqueues plan steps begin..end-1, taking each merged run that lies wholly inside the range as
+// its one kernel.
+void enqueue_range(const Program& p, hipStream_t s, void* const* slots, void* ws, size_t begin, size_t end) {
+  for (size_t k = begin; k < end;) {
+    int64_t m = p.merged_at.empty() ? -1 : p.merged_at[k];
+    if (m >= 0 && p.merged[(size_t)m].last < end) {
+      p.merged[(size_t)m].fn(s, slots, ws);
+      k = p.merged[(size_t)m].last + 1;
+    } else {
+      p.steps[k](s, slots, ws);
+      k++;
+    }
+  }
+}
+
+// Enqueues the listed steps in order, taking a merged run as its one kernel where the list holds
+// all of its steps consecutively.
+void enqueue_list(const Program& p, hipStream_t s, void* const* slots, void* ws, const int64_t* steps, size_t n) {
+  for (size_t q = 0; q < n;) {
+    size_t k = (size_t)steps[q];
+    int64_t m = p.merged_at.empty() ? -1 : p.merged_at[k];
+    if (m >= 0) {
+      const auto& mr = p.merged[(size_t)m];
+      size_t len = mr.last - mr.first + 1;
+      bool whole = q + len <= n;
+      for (size_t i = 0; whole && i < len; i++) whole = (size_t)steps[q + i] == k + i;
+      if (whole) {
+        mr.fn(s, slots, ws);
+        q += len;
+        continue;
+      }
+    }
+    p.steps[k](s, slots, ws);
+    q++;
+  }
+}
+
 void run_steps(Exec* e, size_t begin, size_t end) {
   if (!e->failure.empty()) return;
   if (e->prog->inject.exchange(false)) {
@@ -539,7 +667,7 @@ void run_steps(Exec* e, size_t begin, size_t end) {
   }
   Frame* f = e->frame;
   try {
-    for (size_t k = begin; k < end; k++) e->prog->steps[k](f->stream, f->slot.data(), f->workspace);
+    enqueue_range(*e->prog, f->stream, f->slot.data(), f->workspace, begin, end);
   } catch (std::exception& ex) {
     e->failure = ex.what();
     return;
@@ -613,6 +741,13 @@ int rg_hip_compile_check(const int64_t* words, size_t n_words, char* err, size_t
       rgjit::FusedKernel fk;
       if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), &fk);
       else src << rgjit::generate(st.fused, "rgf" + std::to_string(k), &fk);
+      count++;
+    }
+    for (auto [first, last] : merge_sets(plan)) {
+      std::vector<const rgplan::Fused*> parts;
+      for (size_t j = first; j <= last; j++) parts.push_back(&plan.steps[j].fused);
+      rgjit::FusedKernel fk;
+      src << rgjit::generate_merged(parts, "rgm" + std::to_string(first), &fk);
       count++;
     }
     if (count) rgjit::compile_code(src.str());
@@ -751,8 +886,7 @@ int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, in
   // Hold the stream while the launches are enqueued, so the device never waits on the host.
   rgk::hold_stream(f->stream, 2000.0 + 4.0 * (double)(n_steps * repeats));
   hipEventRecord(a, f->stream);
-  for (int64_t r = 0; r < repeats; r++)
-    for (int64_t k = 0; k < n_steps; k++) e->prog->steps[steps[k]](f->stream, f->slot.data(), f->workspace);
+  for (int64_t r = 0; r < repeats; r++) enqueue_list(*e->prog, f->stream, f->slot.data(), f->workspace, steps, (size_t)n_steps);
   hipEventRecord(b, f->stream);
   if (!latch(e, hipEventSynchronize(b), "time_steps")) {
     float ms = 0;
@@ -774,7 +908,7 @@ int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len) {
   double t0 = now();
   hipEventRecord(a, f->stream);
   for (int64_t r = 0; r < repeats && e->failure.empty(); r++)
-    for (auto& st : e->prog->steps) st(f->stream, f->slot.data(), f->workspace);
+    enqueue_range(*e->prog, f->stream, f->slot.data(), f->workspace, 0, e->prog->steps.size());
   hipEventRecord(b, f->stream);
   latch(e, hipEventSynchronize(b), "breakdown");
   double wall = now() - t0;
@@ -785,8 +919,11 @@ int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len) {
   size_t fused = 0;
   for (auto& st : e->prog->plan.steps) fused += st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS;
   std::ostringstream s;
+  size_t launches = e->prog->steps.size();
+  for (auto& m : e->prog->merged) launches -= m.last - m.first;
   s << "{\"wall_ms\":" << wall / repeats * 1e3 << ",\"gpu_ms\":" << ms / repeats << ",\"per_step\":{\"dispatches\":"
-    << e->prog->steps.size() << ",\"fused_kernels\":" << fused << ",\"cpu_steps\":0}}";
+    << e->prog->steps.size() << ",\"fused_kernels\":" << fused << ",\"merged_launches\":" << e->prog->merged.size()
+    << ",\"launches\":" << launches << ",\"cpu_steps\":0}}";
   put(json, len, s.str());
   return e->failure.empty() ? 0 : -1;
 }
@@ -857,7 +994,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       const std::vector<void*>& t = table[g];
       for (int64_t j = 0; j < (int64_t)batch_bufs.size(); j++)
         rgk::load_batch(f->stream, t[(size_t)d->data_slots[j]], batch_bufs[j], d->data_bytes[j], d->n_batches, counter);
-      for (auto& st : p->steps) st(f->stream, t.data(), f->workspace);
+      enqueue_range(*p, f->stream, t.data(), f->workspace, 0, p->steps.size());
       for (int64_t h = 0; h < d->n_history; h++) {
         int64_t s = d->history_slots[h];
         rgk::record_history(f->stream, p->plan.slots[(size_t)s].dtype, t[(size_t)s], hist + h * chunk, counter, chunk);

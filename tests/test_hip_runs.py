@@ -152,3 +152,22 @@ def test_small_gpt_loss_curve_overlays_cpu():
     close(np.array(a.history["aux"]), np.array(b.history["aux"]), 1e-4, "loss curve")
     # Uniform random tokens carry no structure: the loss stays near ln(vocab).
     assert abs(np.mean(a.history["aux"]) - np.log(cfg.vocab)) < 0.1
+
+
+def test_small_independent_groups_run_as_one_launch():
+    """AdamW over a small MLP: one update group per parameter shape, each far too small to fill
+    the device. The runtime launches runs of such independent groups as one kernel; the training
+    run must equal the oracle's, and the launch count per pass must drop."""
+    import json
+    step, state = workloads.mlp_train_step(workloads.MLPConfig(batch=64, d_in=16, hidden=32))
+    hip = rg.compile(step, (state,), device="hip", validate="none")
+    cpu = rg.compile(step, (state,), device="cpu", validate="none")
+    bd = hip.profile(state, repeats=1)["breakdown"]
+    per = (json.loads(bd) if isinstance(bd, str) else bd)["per_step"]
+    assert per["merged_launches"] >= 1 and per["launches"] < per["dispatches"], per
+    a = rg.run(hip, state, steps=20)
+    b = rg.run(cpu, state, steps=20)
+    close(np.array(a.history["aux"]), np.array(b.history["aux"]), 1e-4, "loss curve")
+    from rustautograd_amd import tree as rtree
+    for (name, u), (_, v) in zip(rtree.paths(a.state["params"]), rtree.paths(b.state["params"])):
+        close(u.numpy(), v.numpy(), 1e-4, name)
