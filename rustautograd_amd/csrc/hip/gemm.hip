@@ -140,13 +140,27 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
 
   // Two register stages: the global loads of tile t + 2 are issued while tile t is multiplied
   // out of LDS and tile t + 1 waits in registers, so each load has two iterations to arrive.
-  Stager<AK ? BM : BK, AK ? BK : BM, NT, MODE> sa[2];
-  Stager<BKC ? BN : BK, BKC ? BK : BN, NT, MODE> sb[2];
-  auto load_tiles = [&](int k0, int set) {
-    if (AK) sa[set].load(Ab, K, m0, k0, M, kend, tid);
-    else sa[set].load(Ab, M, k0, m0, kend, M, tid);
-    if (BKC) sb[set].load(Bb, K, n0, k0, N, kend, tid);
-    else sb[set].load(Bb, N, k0, n0, kend, N, tid);
+  Stager<AK ? BM : BK, AK ? BK : BM, NT, MODE> sa0, sa1;
+  Stager<BKC ? BN : BK, BKC ? BK : BN, NT, MODE> sb0, sb1;
+  // The register stage SET (a constant): two variables rather than an array, so that no stage is
+  // ever indexed and both stay in registers.
+  auto stage_a = [&](auto set) -> auto& {
+    if constexpr (decltype(set)::value == 0) return sa0;
+    else return sa1;
+  };
+  auto stage_b = [&](auto set) -> auto& {
+    if constexpr (decltype(set)::value == 0) return sb0;
+    else return sb1;
+  };
+  // Tile t of this block's K range into register stage `stage`.
+  auto load_tiles = [&](int t, auto stage) __attribute__((always_inline)) {
+    auto& xa = stage_a(stage);
+    auto& xb = stage_b(stage);
+    const int k0 = kbeg + t * BK;
+    if (AK) xa.load(Ab, K, m0, k0, M, kend, tid);
+    else xa.load(Ab, M, k0, m0, kend, M, tid);
+    if (BKC) xb.load(Bb, K, n0, k0, N, kend, tid);
+    else xb.load(Bb, N, k0, n0, kend, N, tid);
   };
 
   floatx4 acc[TM][TN];
@@ -155,17 +169,17 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  if (nk > 0) load_tiles(kbeg, 0);
-  if (nk > 1) load_tiles(kbeg + BK, 1);
   if (nk > 0) {
-    sa[0].store(As[0], LDA, tid);
-    sb[0].store(Bs[0], LDB, tid);
+    load_tiles(0, std::integral_constant<int, 0>());
+    load_tiles(min(1, nk - 1), std::integral_constant<int, 1>());
+    sa0.store(As[0], LDA, tid);
+    sb0.store(Bs[0], LDB, tid);
   }
   __syncthreads();
   // MFMA 16x16x4 lane roles: lane l supplies row (A) / column (B) l % 16 at k = l / 16. Within a
   // group of 16 k the four k-steps j give lane l the k index 4 * (l / 16) + j in both operands.
   const int l16 = lane & 15, q4 = (lane >> 4) * 4;
-  auto multiply = [&](const float* as, const float* bs) {
+  auto multiply = [&](const float* as, const float* bs) __attribute__((always_inline)) {
 #pragma unroll
     for (int kg = 0; kg < BK; kg += 16) {
       float a[4][TM], bv[4][TN];  // [k-step][tile]
@@ -208,21 +222,23 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
   };
   // Iteration t multiplies LDS buffer t % 2, whose register stage t % 2 is then free for tile
   // t + 2; tile t + 1 goes from register stage (t + 1) % 2 into the other LDS buffer, which every
-  // wave finished reading before the previous barrier.
-  auto iteration = [&](int t, auto parity) {
+  // wave finished reading before the previous barrier. The body has no branches, so the compiler
+  // can interleave the loads and address arithmetic with the MFMAs: past the end of the range the
+  // last tile is loaded again and stored into the idle buffer, and never read.
+  auto iteration = [&](int t, auto parity) __attribute__((always_inline)) {
     constexpr int P = decltype(parity)::value;
-    if (t + 2 < nk) load_tiles(kbeg + (t + 2) * BK, P);
+    load_tiles(min(t + 2, nk - 1), parity);
     multiply(As[P], Bs[P]);
-    if (t + 1 < nk) {
-      sa[P ^ 1].store(As[P ^ 1], LDA, tid);
-      sb[P ^ 1].store(Bs[P ^ 1], LDB, tid);
-    }
+    stage_a(std::integral_constant<int, P ^ 1>()).store(As[P ^ 1], LDA, tid);
+    stage_b(std::integral_constant<int, P ^ 1>()).store(Bs[P ^ 1], LDB, tid);
     __syncthreads();
   };
-  for (int t = 0; t < nk; t += 2) {
+  int t = 0;
+  for (; t + 1 < nk; t += 2) {
     iteration(t, std::integral_constant<int, 0>());
-    if (t + 1 < nk) iteration(t + 1, std::integral_constant<int, 1>());
+    iteration(t + 1, std::integral_constant<int, 1>());
   }
+  if (t < nk) iteration(t, std::integral_constant<int, 0>());
   // Accumulator register r of lane l holds MFMA row 4 * (l / 16) + r, column l % 16 (for the
   // transposed form: output row l % 16, column 4 * (l / 16) + r). MFMA tile i row rho is block row
   // 16 i + rho (K-contiguous A) or TM rho + i (M-contiguous A); tile n column gamma is block column
@@ -309,22 +325,27 @@ struct TileCfg {
 
 // Block tile, from measurements of C4's products on MI355X: 32-wide tiles for outputs 32..96 wide
 // or 32 tall (attention heads, the vocabulary); 128x128 when that still yields two blocks per CU
-// (512), then 128x64 at two blocks per CU, 64x128 at one, else 64x64 (split over K later when even
-// that leaves the CUs idle).
-TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t batch) {
+// (512), then 128x64 at two blocks per CU; 128x64 with eight waves (two per SIMD) at one block per
+// CU, and for long-K products with at least 32 such tiles (split over K to 256 blocks); 64x128 at
+// one block per CU; else 64x64 (split over K when that leaves the CUs idle).
+TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
   auto blocks = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
   if (n <= 96 && n % 32 == 0) return {128, 32, 32, 4, 1};
   if (m <= 32) return {32, 128, 32, 1, 4};
   if (blocks(128, 128) >= 512) return {128, 128, 16, 2, 2};
   if (blocks(128, 64) >= 512) return {128, 64, 16, 2, 2};
+  if (blocks(128, 64) >= 256 || (blocks(128, 64) >= 32 && k >= 4096)) return {128, 64, 32, 2, 4};
   if (blocks(64, 128) >= 256) return {64, 128, 32, 2, 2};
   return {64, 64, 32, 2, 2};
 }
 
+// K splits for products with too few tiles: about 256 blocks of eight waves or 768 of four, each
+// split at least 512 deep, at most 16.
 int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
   uint64_t tiles = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn) * batch;
   if (tiles >= 256 || k < 1024) return 1;
-  uint64_t want = (512 + tiles - 1) / tiles;
+  uint64_t target = t.wm * t.wn == 8 ? 256 : 768;
+  uint64_t want = (target + tiles - 1) / tiles;
   uint64_t most = k / 512;
   return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 16));
 }
@@ -366,6 +387,7 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
   if (t.bm == BM_ && t.bn == BN_ && t.bk == BK_) return launch_flags<BM_, BN_, BK_, WM_, WN_>(s, ta, tb, mode, l)
   RG_TILE(128, 128, 16, 2, 2);
   RG_TILE(128, 64, 16, 2, 2);
+  RG_TILE(128, 64, 32, 2, 4);
   RG_TILE(64, 128, 32, 2, 2);
   RG_TILE(64, 64, 32, 2, 2);
   RG_TILE(128, 32, 32, 4, 1);
@@ -377,14 +399,14 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
 
 uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
   if (!use_mfma(dtype, m, n, k)) return 0;
-  int s = split_count(pick_tile(m, n, batch), m, n, k, batch);
+  int s = split_count(pick_tile(m, n, k, batch), m, n, k, batch);
   return s > 1 ? (uint64_t)s * batch * m * n * sizeof(float) : 0;
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m == 0 || g.n == 0 || g.batch == 0) return;
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
-    TileCfg t = pick_tile(g.m, g.n, g.batch);
+    TileCfg t = pick_tile(g.m, g.n, g.k, g.batch);
     int splits = split_count(t, g.m, g.n, g.k, g.batch);
     int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
     splits = (int)((g.k + kps - 1) / kps);

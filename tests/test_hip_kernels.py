@@ -6,6 +6,8 @@ magnitude.
 """
 
 import numpy as np
+import rustautograd_amd as rg
+from rustautograd_amd import _rg
 import pytest
 
 from helpers import agree, close, op, run_graph, seq, t
@@ -119,6 +121,30 @@ def test_reductions_at_model_shapes(shape, axes):
         hip, cpu = run_graph("hip", lambda g, i: op(g, kind, [i[0]], axes=axes, keepdims=False), [x]), \
             run_graph("cpu", lambda g, i: op(g, kind, [i[0]], axes=axes, keepdims=False), [x])
         close(hip[0], cpu[0], 1e-4, f"{kind} {shape} {axes}")
+
+
+@pytest.mark.parametrize("shape,axes", [((3, 5000, 64), [1]), ((40, 8192), [0]), ((1000, 100), [0]), ((257, 12), [0]), ((8, 4), [0])])
+def test_column_reductions_repeat_exactly(shape, axes):
+    """Leading-axis reductions: chunk partials folded in a fixed order by a second launch. Shapes
+    cover a batch, partial column tiles, uneven chunks and a single chunk. Three calls in a row on
+    one compiled program must each match the oracle and repeat bit for bit."""
+    rng = np.random.default_rng(5)
+    for kind in ("sum", "max", "min"):
+        g = _rg.Graph()
+        i = g.input(list(shape), "float32")
+        outs = [op(g, kind, [i], axes=axes, keepdims=False)]
+        xs = [t(rng.normal(size=shape).astype(np.float32)) for _ in range(2)]
+        hip = _rg.compile(g, outs, [xs[0]._t], "none", "hip", "none")
+        cpu = _rg.compile(g, outs, [xs[0]._t], "none", "cpu", "none")
+        first = None
+        for x in (xs[0], xs[1], xs[0]):
+            got = rg.Tensor(hip.call([x._t])[0]).numpy()
+            close(got, rg.Tensor(cpu.call([x._t])[0]).numpy(), 1e-4, f"{kind} {shape} {axes}")
+            if x is xs[0]:
+                if first is None:
+                    first = got
+                else:
+                    assert np.array_equal(got, first), f"{kind} {shape}: repeated call differs"
 
 
 MATMUL_CASES = [((3,), (3,)), ((2, 3), (3,)), ((3,), (3, 2)), ((2, 3), (3, 4)), ((5, 2, 3), (3, 4)), ((5, 2, 3), (5, 3, 4)),
