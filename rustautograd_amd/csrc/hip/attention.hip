@@ -162,6 +162,19 @@ __device__ __forceinline__ void tile_range(const uint32_t* words, int nw, bool s
   *hi = last / 16 + 1;
 }
 
+// The 16-row tile of wave w. With 16 waves a block covers a whole 256-row problem, and under a
+// causal mask the work of a tile grows with its index; waves are dealt to the four SIMDs in
+// turn, so SIMD s gets tiles s, 7 - s, 8 + s and 15 - s: equal work on every SIMD.
+template <int WAVES>
+__device__ __forceinline__ int wave_tile(int w) {
+  if constexpr (WAVES == 16) {
+    const int j = w >> 2, s = w & 3;
+    return j == 0 ? s : j == 1 ? 7 - s : j == 2 ? 8 + s : 15 - s;
+  } else {
+    return w;
+  }
+}
+
 // Forward: one block per 16 * WAVES queries of one (batch, head); wave w owns queries
 // q0 .. q0 + 15. Writes O and, per query, the row max (of the base-2 scores) and the row sum.
 template <int HD, int NKT, int WAVES>
@@ -184,7 +197,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
     Vt[(d + 3) * TKP + key] = v.w;
   }
   __syncthreads();
-  const int q0 = blockIdx.x * 16 * WAVES + w * 16;
+  const int q0 = blockIdx.x * 16 * WAVES + wave_tile<WAVES>(w) * 16;
   if (q0 >= tq) return;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
   const int q = q0 + l16;  // the lane's query in score tiles
@@ -315,7 +328,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
     *(float4*)&Vs[key * KP + d] = *(const float4*)(Vb + key * a.v.st + d);
   }
   __syncthreads();
-  const int q0 = blockIdx.x * 16 * WAVES + w * 16;
+  const int q0 = blockIdx.x * 16 * WAVES + wave_tile<WAVES>(w) * 16;
   if (q0 >= tq) return;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
   const int q = q0 + l16;
@@ -417,7 +430,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   }
   // Every query row sees some key: then masked entries are exactly zero and may be skipped.
   const bool all_vis = __syncthreads_and(vis_all);
-  const int k0 = blockIdx.x * 16 * WAVES + w * 16;
+  const int k0 = blockIdx.x * 16 * WAVES + wave_tile<WAVES>(w) * 16;
   if (k0 >= tk) return;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
   const int key = k0 + l16;  // the lane's key in score tiles
@@ -491,27 +504,39 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   }
 }
 
-// Four waves per block unless the launch would still give every CU two blocks with eight.
-int waves_for(const AttnArgs& a, int rows) { return (uint64_t)a.bh * ((rows + 127) / 128) >= 512 ? 8 : 4; }
+// Sixteen waves (a whole 256-row problem per block: its K and V, or q and dO, are staged once)
+// when there are problems for every CU; else four waves per block unless the launch would still
+// give every CU two blocks with eight.
+int waves_for(const AttnArgs& a, int rows) {
+  if (rows == 256 && a.bh >= 256) return 16;
+  return (uint64_t)a.bh * ((rows + 127) / 128) >= 512 ? 8 : 4;
+}
 
 template <int HD>
 void forward_hd(hipStream_t s, const AttnArgs& a) {
-  if (waves_for(a, a.tq) == 8)
-    hipLaunchKernelGGL((k_attn_fwd<HD, ATTN_MAX_KEYS / 16, 8>), dim3((uint32_t)((a.tq + 127) / 128), a.bh), dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_attn_fwd<HD, ATTN_MAX_KEYS / 16, 4>), dim3((uint32_t)((a.tq + 63) / 64), a.bh), dim3(256), 0, s, a);
+  const int wv = waves_for(a, a.tq);
+  const dim3 grid((uint32_t)((a.tq + 16 * wv - 1) / (16 * wv)), a.bh);
+  if (wv == 16) hipLaunchKernelGGL((k_attn_fwd<HD, ATTN_MAX_KEYS / 16, 16>), grid, dim3(1024), 0, s, a);
+  else if (wv == 8) hipLaunchKernelGGL((k_attn_fwd<HD, ATTN_MAX_KEYS / 16, 8>), grid, dim3(512), 0, s, a);
+  else hipLaunchKernelGGL((k_attn_fwd<HD, ATTN_MAX_KEYS / 16, 4>), grid, dim3(256), 0, s, a);
 }
 
 template <int HD>
 void backward_hd(hipStream_t s, const AttnArgs& a) {
-  if (waves_for(a, a.tq) == 8)
-    hipLaunchKernelGGL((k_attn_bwd_q<HD, 8>), dim3((uint32_t)((a.tq + 127) / 128), a.bh), dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_attn_bwd_q<HD, 4>), dim3((uint32_t)((a.tq + 63) / 64), a.bh), dim3(256), 0, s, a);
-  if (waves_for(a, a.tk) == 8)
-    hipLaunchKernelGGL((k_attn_bwd_kv<HD, 8>), dim3((uint32_t)((a.tk + 127) / 128), a.bh), dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_attn_bwd_kv<HD, 4>), dim3((uint32_t)((a.tk + 63) / 64), a.bh), dim3(256), 0, s, a);
+  {
+    const int wv = waves_for(a, a.tq);
+    const dim3 grid((uint32_t)((a.tq + 16 * wv - 1) / (16 * wv)), a.bh);
+    if (wv == 16) hipLaunchKernelGGL((k_attn_bwd_q<HD, 16>), grid, dim3(1024), 0, s, a);
+    else if (wv == 8) hipLaunchKernelGGL((k_attn_bwd_q<HD, 8>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_attn_bwd_q<HD, 4>), grid, dim3(256), 0, s, a);
+  }
+  {
+    const int wv = waves_for(a, a.tk);
+    const dim3 grid((uint32_t)((a.tk + 16 * wv - 1) / (16 * wv)), a.bh);
+    if (wv == 16) hipLaunchKernelGGL((k_attn_bwd_kv<HD, 16>), grid, dim3(1024), 0, s, a);
+    else if (wv == 8) hipLaunchKernelGGL((k_attn_bwd_kv<HD, 8>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_attn_bwd_kv<HD, 4>), grid, dim3(256), 0, s, a);
+  }
 }
 
 }  // namespace
