@@ -1,9 +1,11 @@
 // Dense products for MatMul / MatMulT (reference src/plan.rs:1453-1493, flags from
 // src/optimize.rs:338-350).
 //
-// fp32: block tiles from 128x128 down to 128x32 / 32x128, four wave64s per block, each wave
-// owning a grid of 16x16 MFMA tiles (v_mfma_f32_16x16x4f32). Operands are staged through
-// double-buffered LDS in their own global layout, so no operand is transposed while staging:
+// fp32: block tiles from 128x128 down to 128x32 / 32x128, four or eight wave64s per block, each
+// wave owning a grid of 16x16 MFMA tiles (v_mfma_f32_16x16x4f32), or of 32x32 ones
+// (v_mfma_f32_32x32x2f32) for some shapes. Global loads run two K steps ahead through two register
+// stages, and operands are staged through double-buffered LDS in their own global layout, so no
+// operand is transposed while staging:
 //  - a K-contiguous operand (A, or B when transposed) sits in LDS as [rows][BK + 4]; one 16-byte
 //    LDS read gives a lane four consecutive k of one tile row, feeding four MFMA k-steps;
 //  - an M- or N-contiguous operand sits as [BK][cols]; one read gives a lane T consecutive
@@ -53,6 +55,26 @@ __device__ __forceinline__ TileIndex tile_of(uint32_t tiles_m, uint32_t tiles_n,
   uint32_t in = t % span;
   return {first + in % rows, in / rows, z};
 }
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// One MFMA step of shape MS x MS (16x16x4 or 32x32x2 f32): lane l supplies row (A) / column (B)
+// l % MS at k = l / MS, and register r of its accumulator holds row 8 (r / 4) + 4 (l / MS) + r % 4,
+// column l % MS.
+template <int MS>
+struct Mfma;
+template <>
+struct Mfma<16> {
+  typedef floatx4 acc_t;
+  static constexpr int REGS = 4;
+  static __device__ __forceinline__ acc_t step(float a, float b, acc_t c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+};
+template <>
+struct Mfma<32> {
+  typedef floatx16 acc_t;
+  static constexpr int REGS = 16;
+  static __device__ __forceinline__ acc_t step(float a, float b, acc_t c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
+};
 
 // Load modes: every vector inside the operand (no checks), checked 16-byte vectors, or checked
 // scalar loads (operands whose rows are not 16-byte aligned).
@@ -114,15 +136,18 @@ __device__ __forceinline__ void lds_read(const float* p, float* v) {
 // C = op(A) op(B) for one BM x BN block tile; WM x WN wave64s, each owning (BM/WM) x (BN/WN) as
 // TM x TN MFMA tiles of 16x16. The grid is one-dimensional: tiles_m * tiles_n * batch * splits
 // blocks (tile_of); split `sp` covers K range [sp * k_per_split, (sp + 1) * k_per_split).
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE>
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE, int MS>
 __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                                                            int M, int N, int K, const int64_t* a_off, const int64_t* b_off,
                                                            uint64_t a_stride, uint64_t b_stride, int splits, int k_per_split,
                                                            float* __restrict__ partial, uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
   constexpr int NT = 64 * WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16;
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / MS, TN = WTN / MS;
   static_assert(TM >= 1 && TN >= 1 && TM <= 4 && TN <= 4 && (TM & (TM - 1)) == 0 && (TN & (TN - 1)) == 0, "wave tiles");
-  static_assert(BK % 16 == 0, "K step");
+  // A group of KG k: four MFMA steps, lane l taking k = 4 (l / MS) + j at step j in both operands.
+  constexpr int KG = 4 * (64 / MS);
+  static_assert(BK % KG == 0, "K step");
+  typedef Mfma<MS> MF;
   constexpr bool AK = !TA, BKC = TB;  // K-contiguous operands
   constexpr int LDA = AK ? BK + 4 : BM, LDB = BKC ? BK + 4 : BN;
   constexpr int SA = AK ? BM * LDA : BK * LDA, SB = BKC ? BN * LDB : BK * LDB;
@@ -163,11 +188,13 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
     else xb.load(Bb, N, k0, n0, kend, N, tid);
   };
 
-  floatx4 acc[TM][TN];
+  typename MF::acc_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < MF::REGS; r++) acc[i][j][r] = 0.0f;
 
   if (nk > 0) {
     load_tiles(0, std::integral_constant<int, 0>());
@@ -176,36 +203,34 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
     sb0.store(Bs[0], LDB, tid);
   }
   __syncthreads();
-  // MFMA 16x16x4 lane roles: lane l supplies row (A) / column (B) l % 16 at k = l / 16. Within a
-  // group of 16 k the four k-steps j give lane l the k index 4 * (l / 16) + j in both operands.
-  const int l16 = lane & 15, q4 = (lane >> 4) * 4;
+  const int li = lane % MS, q4 = (lane / MS) * 4;
   auto multiply = [&](const float* as, const float* bs) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kg = 0; kg < BK; kg += 16) {
+    for (int kg = 0; kg < BK; kg += KG) {
       float a[4][TM], bv[4][TN];  // [k-step][tile]
       if (AK) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           float v[4];
-          lds_read<4>(as + (wm * WTM + i * 16 + l16) * LDA + kg + q4, v);
+          lds_read<4>(as + (wm * WTM + i * MS + li) * LDA + kg + q4, v);
 #pragma unroll
           for (int j = 0; j < 4; j++) a[j][i] = v[j];
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++) lds_read<TM>(as + (kg + q4 + j) * LDA + wm * WTM + TM * l16, a[j]);
+        for (int j = 0; j < 4; j++) lds_read<TM>(as + (kg + q4 + j) * LDA + wm * WTM + TM * li, a[j]);
       }
       if (BKC) {
 #pragma unroll
         for (int i = 0; i < TN; i++) {
           float v[4];
-          lds_read<4>(bs + (wn * WTN + i * 16 + l16) * LDB + kg + q4, v);
+          lds_read<4>(bs + (wn * WTN + i * MS + li) * LDB + kg + q4, v);
 #pragma unroll
           for (int j = 0; j < 4; j++) bv[j][i] = v[j];
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++) lds_read<TN>(bs + (kg + q4 + j) * LDB + wn * WTN + TN * l16, bv[j]);
+        for (int j = 0; j < 4; j++) lds_read<TN>(bs + (kg + q4 + j) * LDB + wn * WTN + TN * li, bv[j]);
       }
 #pragma unroll
       for (int j = 0; j < 4; j++)
@@ -215,8 +240,8 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
           for (int n = 0; n < TN; n++) {
             // With a K-contiguous B the product is formed transposed (B supplies the MFMA rows), so
             // that each lane ends up with four adjacent output columns.
-            if constexpr (BKC) acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j][n], a[j][i], acc[i][n], 0, 0, 0);
-            else acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][i], bv[j][n], acc[i][n], 0, 0, 0);
+            if constexpr (BKC) acc[i][n] = MF::step(bv[j][n], a[j][i], acc[i][n]);
+            else acc[i][n] = MF::step(a[j][i], bv[j][n], acc[i][n]);
           }
     }
   };
@@ -239,41 +264,45 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
     iteration(t + 1, std::integral_constant<int, 1>());
   }
   if (t < nk) iteration(t, std::integral_constant<int, 0>());
-  // Accumulator register r of lane l holds MFMA row 4 * (l / 16) + r, column l % 16 (for the
-  // transposed form: output row l % 16, column 4 * (l / 16) + r). MFMA tile i row rho is block row
-  // 16 i + rho (K-contiguous A) or TM rho + i (M-contiguous A); tile n column gamma is block column
-  // 16 n + gamma (K-contiguous B) or TN gamma + n (N-contiguous B). Either way a lane holds
-  // adjacent output columns: four in one tile (K-contiguous B) or one in each of its TN tiles.
+  // Accumulator register r of lane l holds MFMA row rho(r) = 8 (r / 4) + 4 (l / MS) + r % 4, column
+  // l % MS (for the transposed form: output row l % MS, column rho(r)). MFMA tile i row rho is
+  // block row MS i + rho (K-contiguous A) or TM rho + i (M-contiguous A); tile n column gamma is
+  // block column MS n + gamma (K-contiguous B) or TN gamma + n (N-contiguous B). Either way a lane
+  // holds adjacent output columns: four per group of four registers in one tile (K-contiguous B)
+  // or one in each of its TN tiles.
   float* out = splits > 1 ? partial + ((uint64_t)b * splits + sp) * (uint64_t)M * N : C + (uint64_t)b * M * N;
   const bool vec_out = MODE != LOAD_SCALAR && N % 4 == 0;
   if constexpr (BKC) {
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-      const int row = m0 + wm * WTM + (AK ? i * 16 + l16 : TM * l16 + i);
+      const int row = m0 + wm * WTM + (AK ? i * MS + li : TM * li + i);
       if (row >= M) continue;
       float* crow = out + (uint64_t)row * N;
 #pragma unroll
-      for (int n = 0; n < TN; n++) {
-        const int col = n0 + wn * WTN + n * 16 + q4;
-        if (vec_out && col + 4 <= N) {
-          *(float4*)(crow + col) = make_float4(acc[i][n][0], acc[i][n][1], acc[i][n][2], acc[i][n][3]);
-        } else {
+      for (int n = 0; n < TN; n++)
 #pragma unroll
-          for (int r = 0; r < 4; r++)
-            if (col + r < N) crow[col + r] = acc[i][n][r];
+        for (int g = 0; g < MF::REGS / 4; g++) {
+          const int col = n0 + wn * WTN + n * MS + 8 * g + q4;
+          const auto& c = acc[i][n];
+          if (vec_out && col + 4 <= N) {
+            *(float4*)(crow + col) = make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              if (col + r < N) crow[col + r] = c[4 * g + r];
+          }
         }
-      }
     }
   } else {
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int rho = q4 + r;
-        const int row = m0 + wm * WTM + (AK ? i * 16 + rho : TM * rho + i);
+      for (int r = 0; r < MF::REGS; r++) {
+        const int rho = 8 * (r / 4) + q4 + r % 4;
+        const int row = m0 + wm * WTM + (AK ? i * MS + rho : TM * rho + i);
         if (row >= M) continue;
         float* crow = out + (uint64_t)row * N;
-        const int col = n0 + wn * WTN + TN * l16;
+        const int col = n0 + wn * WTN + TN * li;
         if (TN > 1 && vec_out && col + TN <= N) {
           if constexpr (TN == 4) *(float4*)(crow + col) = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
           else if constexpr (TN == 2) *(float2*)(crow + col) = make_float2(acc[i][0][r], acc[i][1][r]);
@@ -320,7 +349,7 @@ bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
 }
 
 struct TileCfg {
-  int bm, bn, bk, wm, wn;
+  int bm, bn, bk, wm, wn, ms = 16;
 };
 
 // Block tile, from measurements of C4's products on MI355X: 32-wide tiles for outputs 32..96 wide
@@ -328,12 +357,14 @@ struct TileCfg {
 // (512), then 128x64 at two blocks per CU; 128x64 with eight waves (two per SIMD) at one block per
 // CU, and for long-K products with at least 32 such tiles (split over K to 256 blocks); 64x128 at
 // one block per CU; else 64x64 (split over K when that leaves the CUs idle).
-TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
+TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
   auto blocks = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
   if (n <= 96 && n % 32 == 0) return {128, 32, 32, 4, 1};
   if (m <= 32) return {32, 128, 32, 1, 4};
   if (blocks(128, 128) >= 512) return {128, 128, 16, 2, 2};
   if (blocks(128, 64) >= 512) return {128, 64, 16, 2, 2};
+  // With a K-contiguous B, 32x32 MFMAs on 64x64 tiles (two blocks per CU) do slightly better.
+  if (tb && blocks(128, 64) >= 256) return {64, 64, 32, 2, 2, 32};
   if (blocks(128, 64) >= 256 || (blocks(128, 64) >= 32 && k >= 4096)) return {128, 64, 32, 2, 4};
   if (blocks(64, 128) >= 256) return {64, 128, 32, 2, 2};
   return {64, 64, 32, 2, 2};
@@ -362,29 +393,29 @@ struct Launch {
   uint32_t tm, tn;
 };
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MS>
 void launch_mode(hipStream_t s, int mode, const Launch& l) {
-#define RG_GEMM(MODE_)                                                                                                             \
-  hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, TA, TB, MODE_>), l.grid, dim3(64 * WM * WN), 0, s, l.a, l.b, l.c, l.m, l.n, l.k, \
-                     l.a_off, l.b_off, l.as, l.bs, l.splits, l.kps, l.part, l.tm, l.tn, 1)
+#define RG_GEMM(MODE_)                                                                                                       \
+  hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, TA, TB, MODE_, MS>), l.grid, dim3(64 * WM * WN), 0, s, l.a, l.b, l.c, l.m, l.n, \
+                     l.k, l.a_off, l.b_off, l.as, l.bs, l.splits, l.kps, l.part, l.tm, l.tn, 1)
   if (mode == LOAD_EVEN) RG_GEMM(LOAD_EVEN);
   else if (mode == LOAD_VEC) RG_GEMM(LOAD_VEC);
   else RG_GEMM(LOAD_SCALAR);
 #undef RG_GEMM
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int MS = 16>
 void launch_flags(hipStream_t s, bool ta, bool tb, int mode, const Launch& l) {
-  if (!ta && !tb) launch_mode<BM, BN, BK, WM, WN, false, false>(s, mode, l);
-  else if (ta && !tb) launch_mode<BM, BN, BK, WM, WN, true, false>(s, mode, l);
-  else if (!ta && tb) launch_mode<BM, BN, BK, WM, WN, false, true>(s, mode, l);
-  else launch_mode<BM, BN, BK, WM, WN, true, true>(s, mode, l);
+  if (!ta && !tb) launch_mode<BM, BN, BK, WM, WN, false, false, MS>(s, mode, l);
+  else if (ta && !tb) launch_mode<BM, BN, BK, WM, WN, true, false, MS>(s, mode, l);
+  else if (!ta && tb) launch_mode<BM, BN, BK, WM, WN, false, true, MS>(s, mode, l);
+  else launch_mode<BM, BN, BK, WM, WN, true, true, MS>(s, mode, l);
 }
 
 // Instantiates the tile shapes pick_tile can return.
 void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, const Launch& l) {
 #define RG_TILE(BM_, BN_, BK_, WM_, WN_) \
-  if (t.bm == BM_ && t.bn == BN_ && t.bk == BK_) return launch_flags<BM_, BN_, BK_, WM_, WN_>(s, ta, tb, mode, l)
+  if (t.bm == BM_ && t.bn == BN_ && t.bk == BK_ && t.wm == WM_ && t.wn == WN_ && t.ms == 16) return launch_flags<BM_, BN_, BK_, WM_, WN_>(s, ta, tb, mode, l)
   RG_TILE(128, 128, 16, 2, 2);
   RG_TILE(128, 64, 16, 2, 2);
   RG_TILE(128, 64, 32, 2, 4);
@@ -393,20 +424,21 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
   RG_TILE(128, 32, 32, 4, 1);
   RG_TILE(32, 128, 32, 1, 4);
 #undef RG_TILE
+  if (t.bm == 64 && t.bn == 64 && t.bk == 32 && t.wm == 2 && t.wn == 2 && t.ms == 32) return launch_flags<64, 64, 32, 2, 2, 32>(s, ta, tb, mode, l);
 }
 
 }  // namespace
 
 uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
   if (!use_mfma(dtype, m, n, k)) return 0;
-  int s = split_count(pick_tile(m, n, k, batch), m, n, k, batch);
+  int s = split_count(pick_tile(m, n, k, batch, false), m, n, k, batch);
   return s > 1 ? (uint64_t)s * batch * m * n * sizeof(float) : 0;
 }
 
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m == 0 || g.n == 0 || g.batch == 0) return;
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
-    TileCfg t = pick_tile(g.m, g.n, g.k, g.batch);
+    TileCfg t = pick_tile(g.m, g.n, g.k, g.batch, g.tb);
     int splits = split_count(t, g.m, g.n, g.k, g.batch);
     int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
     splits = (int)((g.k + kps - 1) / kps);
