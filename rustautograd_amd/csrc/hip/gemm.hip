@@ -315,13 +315,31 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
   }
 }
 
+// Sums the K-split partial products in split order. Four outputs per thread (16-byte loads when
+// M N is a multiple of 4), all splits' loads issued before the adds.
 __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ partial, float* __restrict__ C, uint64_t mn, int splits) {
-  uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  uint32_t b = blockIdx.y;
+  const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const uint32_t b = blockIdx.y;
   if (i >= mn) return;
-  float acc = partial[((uint64_t)b * splits) * mn + i];
-  for (int s = 1; s < splits; s++) acc += partial[((uint64_t)b * splits + s) * mn + i];
-  C[(uint64_t)b * mn + i] = acc;
+  const float* p = partial + (uint64_t)b * splits * mn + i;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (mn % 4 == 0) {
+    float4 v[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++)
+      if (s < splits) v[s] = *(const float4*)(p + (uint64_t)s * mn);
+    acc = v[0];
+#pragma unroll
+    for (int s = 1; s < 16; s++)
+      if (s < splits) acc = make_float4(acc.x + v[s].x, acc.y + v[s].y, acc.z + v[s].z, acc.w + v[s].w);
+    *(float4*)(C + (uint64_t)b * mn + i) = acc;
+    return;
+  }
+  for (uint64_t e = i; e < i + 4 && e < mn; e++) {
+    float x = partial[(uint64_t)b * splits * mn + e];
+    for (int s = 1; s < splits; s++) x += partial[((uint64_t)b * splits + s) * mn + e];
+    C[(uint64_t)b * mn + e] = x;
+  }
 }
 
 // One output element per thread; k ascending.
@@ -469,7 +487,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     launch_mfma(s, t, g.ta, g.tb, mode, l);
     if (splits > 1) {
       uint64_t mn = g.m * g.n;
-      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 255) / 256), (uint32_t)g.batch), dim3(256), 0, s, (const float*)l.part,
+      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 1023) / 1024), (uint32_t)g.batch), dim3(256), 0, s, (const float*)l.part,
                          (float*)g.c, mn, splits);
     }
     return;
