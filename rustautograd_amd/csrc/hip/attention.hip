@@ -21,7 +21,8 @@
 //
 // The softmax runs in base 2 with the score scale folded into one operand: the kernels form
 // S' = (q k^T) log2(e) / c by scaling q (or k) once, then P = exp2(Y' - max Y') / sum, with
-// v_exp_f32 and a multiplication by the reciprocal row sum. This reassociates the graph's
+// v_exp_f32 and a multiplication by the reciprocal row sum (in the forward, applied to each row
+// of O = exp2(...) v rather than to every probability). This reassociates the graph's
 // per-element divisions and exp by rounding-level amounts (1e-6 relative at most on P), the same
 // order as the MFMA's own reduction differences, well inside the products' 1e-4 tolerance. The
 // forward keeps a whole row of scores in registers (keys <= 256), so P comes from the final max
@@ -235,6 +236,13 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
   for (int kt = 0; kt < NKT; kt++)
     if (kt < nkt && (!all_vis || __ballot(bits[kt] != 0) != 0)) live |= 1u << kt;
 
+  // Tiles every lane of the wave sees in full need no masking (all but the diagonal of a causal
+  // mask).
+  uint32_t full = 0;
+#pragma unroll
+  for (int kt = 0; kt < NKT; kt++)
+    if (__ballot(bits[kt] != 0xF) == 0) full |= 1u << kt;
+
   // Scores, masked, and the row max; tiles in pairs for two independent MFMA chains.
   float s[NKT][4];
   float mx = -__builtin_huge_valf();
@@ -257,13 +265,12 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const float y0 = (bits[kt] >> r & 1) ? acc0[r] : fill;
-      const float y1 = (bits[kt + 1] >> r & 1) ? acc1[r] : fill;
-      s[kt][r] = y0;
-      s[kt + 1][r] = y1;
-      if (live >> kt & 1) mx = fmaxf(mx, y0);
-      if (live >> (kt + 1) & 1) mx = fmaxf(mx, y1);
+      s[kt][r] = (full >> kt & 1) || (bits[kt] >> r & 1) ? acc0[r] : fill;
+      s[kt + 1][r] = (full >> (kt + 1) & 1) || (bits[kt + 1] >> r & 1) ? acc1[r] : fill;
     }
+    // The max of each tile's four scores first, then one step into the running max.
+    if (live >> kt & 1) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+    if (live >> (kt + 1) & 1) mx = fmaxf(mx, fmaxf(fmaxf(s[kt + 1][0], s[kt + 1][1]), fmaxf(s[kt + 1][2], s[kt + 1][3])));
   }
   mx = row_max(mx);
   float z = 0.0f;
@@ -283,29 +290,30 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
     a.stat_m[row] = mx;
     a.stat_z[row] = z;
   }
-  // O = P V: P from registers (A operand: query l16, keys g4 + j), V^T rows from LDS; even and
-  // odd tiles accumulate separately (independent MFMA chains) and are added at the end.
-  const float rz = 1.0f / z;
+  // O = P V with P = e / z: the exponentials from registers (A operand: query l16, keys g4 + j),
+  // V^T rows from LDS, and the division by the row sum applied once to each output; even and odd
+  // tiles accumulate separately (independent MFMA chains) and are added at the end.
   floatx4 oacc[2][ND];
 #pragma unroll
   for (int n = 0; n < ND; n++) oacc[0][n] = oacc[1][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kt = 0; kt < NKT; kt++) {
     if (!(live >> kt & 1)) continue;
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) p[r] = s[kt][r] * rz;
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int n = 0; n < ND; n++)
-        oacc[kt & 1][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j], Vt[(n * 16 + l16) * TKP + kt * 16 + g4 + j], oacc[kt & 1][n], 0, 0, 0);
+        oacc[kt & 1][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kt][j], Vt[(n * 16 + l16) * TKP + kt * 16 + g4 + j], oacc[kt & 1][n], 0, 0, 0);
   }
+  // Output row g4 + r belongs to query q0 + g4 + r, whose row sum lanes with l16 = g4 + r hold.
+  float rzr[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) rzr[r] = 1.0f / __shfl(z, g4 + r);
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     float* orow = out_row(a.o, a, bh, q0 + g4 + r);
 #pragma unroll
-    for (int n = 0; n < ND; n++) orow[n * 16 + l16] = oacc[0][n][r] + oacc[1][n][r];
+    for (int n = 0; n < ND; n++) orow[n * 16 + l16] = (oacc[0][n][r] + oacc[1][n][r]) * rzr[r];
   }
 }
 
