@@ -30,7 +30,11 @@
  *                    micro-ops reduce an element-level register over the row, `aux` being the
  *                    rg_reduce_kind. Inputs are read per element like a fused group's; a
  *                    Broadcast input whose last dimension is 1 is row level. Outputs of
- *                    row-level registers hold one value per row.
+ *                    row-level registers hold one value per row. An RG_OP_REDUCE whose `aux`
+ *                    has RG_ROWS_COLUMN added reduces an element-level register over all the
+ *                    rows instead (every axis but the last): its register is column level, one
+ *                    value per position of the row, read by no other micro-op, and its outputs
+ *                    hold row_len values.
  *     RG_STEP_ATTN   dtype, backward (0/1), bh, heads, tq, tk, hd, div (f64 bits), fill (f64 bits),
  *                    mask_slot (-1: none), mask strides (4 words), mask_bits_slot, build_bits (0/1),
  *                    stats_slot,
@@ -91,6 +95,8 @@ enum rg_op {
 };
 
 enum rg_reduce_kind { RG_REDUCE_SUM = 0, RG_REDUCE_MAX = 1, RG_REDUCE_MIN = 2 };
+/* Added to a row group's RG_OP_REDUCE `aux`: the reduction runs over the rows (a column reduction). */
+#define RG_ROWS_COLUMN 4
 /* Input kinds of a fused group (plan.rs:75-83). */
 enum rg_arg_kind { RG_ARG_FULL = 0, RG_ARG_SPLAT = 1, RG_ARG_ROW = 2, RG_ARG_BROADCAST = 3 };
 /* Binary broadcast modes of a single elementwise instruction (plan.rs:119-125). */

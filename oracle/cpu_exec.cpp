@@ -304,13 +304,28 @@ void run_fused(const Fused& f, std::vector<Buf>& s) {
   }
 }
 
+template <class T>
+void reduce(const Instr& i, std::vector<Buf>& s);
+
 // A row group of a device plan (include/rg_plan.h RG_STEP_ROWS; no reference counterpart): each
 // row computed on its own. Every register is held as a full row; a row-level register (per-row
 // inputs, reductions, ops on row-level values) has the same value at every position and is
-// stored as one value per row. Reductions fold the row in element order.
+// stored as one value per row. Reductions fold the row in element order. A column reduction
+// (RG_ROWS_COLUMN) collects its element-level operand for every row, then reduces it over the
+// leading axes exactly as the standalone reduction instruction it replaces does.
 template <class T>
 void run_rows(const Fused& f, std::vector<Buf>& s) {
   const size_t L = (size_t)f.row_len, n = (size_t)f.n, rows = n / L, rank = f.shape.size();
+  std::vector<bool> col_op(f.ops.size(), false), col_reg((size_t)f.regs, false);
+  std::vector<Buf> col_src(f.ops.size());
+  for (size_t q = 0; q < f.ops.size(); q++)
+    if (f.ops[q].op == RG_OP_REDUCE && (f.ops[q].aux & RG_ROWS_COLUMN)) {
+      col_op[q] = col_reg[(size_t)f.ops[q].reg] = true;
+      col_src[q].bytes.resize(n * sizeof(T));
+    }
+  for (auto& m : f.ops)
+    for (auto& a : m.args)
+      if (a.first && col_reg[(size_t)a.second]) throw std::runtime_error("row group reads a column reduction");
   std::vector<bool> row_level((size_t)f.regs, false);
   std::vector<std::vector<size_t>> bst(f.inputs.size());
   auto ds = strides(f.shape);
@@ -347,12 +362,15 @@ void run_rows(const Fused& f, std::vector<Buf>& s) {
           d[j] = ins[k][src];
         }
       }
-      for (auto& m : f.ops) {
+      for (size_t oq = 0; oq < f.ops.size(); oq++) {
+        const auto& m = f.ops[oq];
         T* d = reg.data() + (size_t)m.reg * L;
         const T* a[3];
         for (size_t q = 0; q < m.args.size(); q++)
           a[q] = m.args[q].first ? reg.data() + (size_t)m.args[q].second * L : ins[(size_t)m.args[q].second] + r * L;
-        if (m.op == RG_OP_REDUCE) {
+        if (col_op[oq]) {
+          memcpy(col_src[oq].as<T>() + r * L, a[0], L * sizeof(T));
+        } else if (m.op == RG_OP_REDUCE) {
           T acc = a[0][0];
           for (size_t j = 1; j < L; j++)
             acc = m.aux == RG_REDUCE_SUM ? acc + a[0][j] : binary_op<T>(m.aux == RG_REDUCE_MAX ? RG_OP_MAX : RG_OP_MIN, acc, a[0][j]);
@@ -366,11 +384,30 @@ void run_rows(const Fused& f, std::vector<Buf>& s) {
         }
       }
       for (size_t k = 0; k < f.outputs.size(); k++) {
+        if (col_reg[(size_t)f.outputs[k].first]) continue;
         const T* v = reg.data() + (size_t)f.outputs[k].first * L;
         if (row_level[(size_t)f.outputs[k].first]) outs[k][r] = v[0];
         else memcpy(outs[k] + r * L, v, L * sizeof(T));
       }
     }
+  }
+  for (size_t q = 0; q < f.ops.size(); q++) {
+    if (!col_op[q]) continue;
+    Instr red;
+    red.op = RG_OP_REDUCE;
+    red.dtype = f.dtype;
+    red.dst = 1;
+    red.n = (int64_t)L;
+    red.shape = {(int64_t)L};
+    red.args = {Arg{0, f.shape}};
+    red.attr = {f.ops[q].aux & ~(int64_t)RG_ROWS_COLUMN, 0, (int64_t)rank - 1};
+    for (size_t ax = 0; ax + 1 < rank; ax++) red.attr.push_back((int64_t)ax);
+    std::vector<Buf> tmp(2);
+    tmp[0] = std::move(col_src[q]);
+    tmp[1].bytes.resize(L * sizeof(T));
+    reduce<T>(red, tmp);
+    for (size_t k = 0; k < f.outputs.size(); k++)
+      if (f.outputs[k].first == f.ops[q].reg) memcpy(outs[k], tmp[1].as<T>(), L * sizeof(T));
   }
 }
 

@@ -273,6 +273,10 @@ PYBIND11_MODULE(_rg, m) {
                  d["inputs"] = s.group.input_shapes;
                  d["n_outputs"] = s.group.outputs.size();
                  d["row_len"] = s.group.row_len;  // > 0: a row group
+                 size_t cols = 0;  // reductions over the rows (every axis but the last)
+                 for (auto& m : s.group.ops)
+                   cols += m.op.kind == RG_OP_REDUCE && std::find(m.op.v.begin(), m.op.v.end(), (int64_t)s.group.shape.size() - 1) == m.op.v.end();
+                 d["column_reductions"] = cols;
                  static const char* kinds[] = {"full", "splat", "row", "broadcast"};
                  py::list in_kinds, in_slots, out_slots;
                  for (auto& in : s.group.inputs) {

@@ -337,6 +337,87 @@ std::vector<std::vector<size_t>> row_groups(const Graph& g, const std::vector<bo
     for (uint32_t y : n.inputs) G.external.insert(y);
     gid[i] = k;
   }
+  // Column reductions: a reduction over every axis but the last of a value of a kept group's full
+  // shape joins that group, folded from the rows the group walks anyway (e.g. a layer norm's
+  // scale and shift gradients beside its input gradient). The value is a member, a value the
+  // group reads, or an ungrouped elementwise node read only by such reductions that shares an
+  // input with the group (it joins too). Nothing the group computes may depend on the reduction,
+  // and no value it reads may depend on the group through a non-member.
+  auto leading_reduce = [&](size_t i) {
+    const Node& n = g.nodes[i];
+    if (n.op.kind != RG_OP_REDUCE || n.dtype == DType::I32) return false;
+    const Shape& s = g.shape(n.inputs[0]);
+    if (s.size() < 2 || s.back() > (int64_t)ROW_MAX || n.op.v.size() + 1 != s.size()) return false;
+    Shape ax = n.op.v;
+    std::sort(ax.begin(), ax.end());
+    for (size_t q = 0; q < ax.size(); q++)
+      if (ax[q] != (int64_t)q) return false;
+    return true;
+  };
+  auto reaches_group = [&](size_t from, int64_t k) {  // a member of group k depends on `from`
+    size_t last = groups[(size_t)k].members.back();
+    std::vector<size_t> stack = {from};
+    std::set<size_t> seen;
+    while (!stack.empty()) {
+      size_t x = stack.back();
+      stack.pop_back();
+      for (uint32_t u : users[x]) {
+        if (u > last || !seen.insert(u).second) continue;
+        if (gid[u] == k) return true;
+        stack.push_back(u);
+      }
+    }
+    return false;
+  };
+  for (size_t i = 0; i < total; i++) {
+    if (!keep[i] || gid[i] >= 0 || excluded[i] || abs[i] || !leading_reduce(i)) continue;
+    const Node& n = g.nodes[i];
+    const uint32_t x = n.inputs[0];
+    const Shape& xs = g.shape(x);
+    auto fits = [&](int64_t k) { return kept(k) && groups[(size_t)k].full == xs && groups[(size_t)k].dtype == n.dtype; };
+    int64_t k = -1;
+    bool pull = false;
+    if (fits(gid[x])) {
+      k = gid[x];
+    } else {
+      for (size_t q = 0; q < groups.size() && k < 0; q++)
+        if (fits((int64_t)q) && groups[q].external.count(x) && !tainted(x, (int64_t)q)) k = (int64_t)q;
+      const Node& xn = g.nodes[x];
+      bool pullable = k < 0 && !kept(gid[x]) && keep[x] && !leaf(xn) && !excluded[x] && !abs[x] && !is_alias(g, x) && dev_fusable(x);
+      for (uint32_t u : users[x]) pullable = pullable && leading_reduce(u) && g.shape(g.nodes[u].inputs[0]) == xs;
+      for (size_t q = 0; q < groups.size() && pullable && k < 0; q++) {
+        if (!fits((int64_t)q)) continue;
+        bool ok = true, shared = false;
+        for (uint32_t y : xn.inputs) {
+          ok = ok && !tainted(y, (int64_t)q);
+          shared = shared || gid[y] == (int64_t)q || groups[q].external.count(y);
+        }
+        if (ok && shared) {
+          k = (int64_t)q;
+          pull = true;
+        }
+      }
+    }
+    if (k < 0 || reaches_group(i, k)) continue;
+    RG& G = groups[(size_t)k];
+    std::set<uint32_t> ext = G.external;
+    if (pull)
+      for (uint32_t y : g.nodes[x].inputs)
+        if (gid[y] != k) ext.insert(y);
+    if (!pull && gid[x] != k) ext.insert(x);
+    if (ext.size() + G.members.size() + 2 > max_bindings) continue;
+    G.external = std::move(ext);
+    if (pull) {
+      if (gid[x] >= 0) {  // leave its dropped group
+        auto& old = groups[(size_t)gid[x]].members;
+        old.erase(std::remove(old.begin(), old.end(), (size_t)x), old.end());
+      }
+      G.members.insert(std::lower_bound(G.members.begin(), G.members.end(), (size_t)x), (size_t)x);
+      gid[x] = k;
+    }
+    G.members.insert(std::lower_bound(G.members.begin(), G.members.end(), i), i);
+    gid[i] = k;
+  }
   std::vector<std::vector<size_t>> out;
   for (auto& G : groups)
     if (G.reduces && G.members.size() >= 2) out.push_back(G.members);
@@ -1144,7 +1225,12 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
       for (auto& m : f.ops) {
         w.push_back(m.op.kind);
         w.push_back((int64_t)m.reg);
-        if (rows) w.push_back(m.op.kind == RG_OP_REDUCE ? (int64_t)m.op.rk : 0);
+        if (rows) {
+          // A reduction over the leading axes (a column reduction) is flagged with RG_ROWS_COLUMN.
+          const bool col = m.op.kind == RG_OP_REDUCE &&
+                           std::find(m.op.v.begin(), m.op.v.end(), (int64_t)f.shape.size() - 1) == m.op.v.end();
+          w.push_back(m.op.kind == RG_OP_REDUCE ? (int64_t)m.op.rk + (col ? RG_ROWS_COLUMN : 0) : 0);
+        }
         w.push_back((int64_t)m.args.size());
         for (auto& [is_reg, idx] : m.args) {
           w.push_back(is_reg ? 1 : 0);

@@ -199,6 +199,19 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   k->name = name;
   k->vec = 1;
   k->grid = (uint32_t)((rows + 3) / 4);
+  // Column reductions (RG_ROWS_COLUMN): the waves walk rows grid-stride, accumulating them.
+  std::vector<bool> col_reg((size_t)f.regs, false);
+  bool has_col = false;
+  for (auto& m : f.ops)
+    if (m.op == RG_OP_REDUCE && (m.aux & RG_ROWS_COLUMN)) col_reg[(size_t)m.reg] = has_col = true;
+  k->col_kind.assign(f.outputs.size(), -1);
+  k->row_len = (uint32_t)L;
+  if (has_col) {
+    k->grid = (uint32_t)std::min<int64_t>((rows + 3) / 4, COL_BLOCKS);
+    for (size_t j = 0; j < f.outputs.size(); j++)
+      for (auto& m : f.ops)
+        if (m.reg == f.outputs[j].first && col_reg[(size_t)m.reg]) k->col_kind[j] = (int)(m.aux & ~(int64_t)RG_ROWS_COLUMN);
+  }
 
   // Levels: true for row-level registers.
   std::vector<int> level((size_t)f.regs, 0);
@@ -225,8 +238,25 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   for (size_t j = 0; j < f.outputs.size(); j++) s << ", " << T << "* " << R << "out" << j;
   s << ") {\n";
   s << "  const unsigned lane = threadIdx.x & 63u;\n";
-  s << "  const unsigned long long row = (unsigned long long)blockIdx.x * 4ull + (threadIdx.x >> 6);\n";
-  s << "  if (row >= " << rows << "ull) return;\n";
+  auto col_init = [&](int64_t aux) {
+    const int64_t kind = aux & ~(int64_t)RG_ROWS_COLUMN;
+    return kind == RG_REDUCE_SUM ? std::string("0") : kind == RG_REDUCE_MAX ? std::string("-__builtin_huge_val()") : std::string("__builtin_huge_val()");
+  };
+  auto col_comb = [&](int64_t aux, const std::string& x, const std::string& y) {
+    const int64_t kind = aux & ~(int64_t)RG_ROWS_COLUMN;
+    return kind == RG_REDUCE_SUM ? x + " + " + y : std::string(kind == RG_REDUCE_MAX ? "rg_max(" : "rg_min(") + x + ", " + y + ")";
+  };
+  if (has_col) {
+    for (auto& m : f.ops)
+      if (col_reg[(size_t)m.reg])
+        s << "  " << T << " c" << m.reg << "[" << E << "];\n  for (int e = 0; e < " << E << "; e++) c" << m.reg << "[e] = (" << T << ")"
+          << col_init(m.aux) << ";\n";
+    s << "  for (unsigned long long row = (unsigned long long)blockIdx.x * 4ull + (threadIdx.x >> 6); row < " << rows
+      << "ull; row += (unsigned long long)gridDim.x * 4ull) {\n";
+  } else {
+    s << "  const unsigned long long row = (unsigned long long)blockIdx.x * 4ull + (threadIdx.x >> 6);\n";
+    s << "  if (row >= " << rows << "ull) return;\n";
+  }
   // Element e of this lane sits at column J(e) of the row.
   auto col = [&](int64_t e) {
     return std::to_string((e / V) * 64 * V + e % V) + "u + lane * " + std::to_string(V) + "u";
@@ -304,6 +334,20 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   };
   for (auto& m : f.ops) {
     std::string rn = "r" + std::to_string(m.reg);
+    if (col_reg[(size_t)m.reg]) {  // fold this row into the lane's column accumulators
+      std::string is_row;
+      std::string a = operand(m.args[0], false, &is_row);
+      if (is_row == "1") throw std::runtime_error("column reduction of a row-level value");
+      for (int64_t e = 0; e < E; e++) {
+        std::string acc = "c" + std::to_string(m.reg) + "[" + std::to_string(e) + "]";
+        std::string v = a + "[" + std::to_string(e) + "]";
+        if (exact) s << "  " << acc << " = " << col_comb(m.aux, acc, v) << ";\n";
+        else s << "  if (" << valid(e) << ") " << acc << " = " << col_comb(m.aux, acc, v) << ";\n";
+      }
+      continue;
+    }
+    for (auto& a : m.args)
+      if (a.first && col_reg[(size_t)a.second]) throw std::runtime_error("row group reads a column reduction");
     if (m.op == RG_OP_REDUCE) {
       std::string is_row;
       std::string a = operand(m.args[0], false, &is_row);
@@ -348,6 +392,7 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   }
   for (size_t j = 0; j < f.outputs.size(); j++) {
     int64_t r = f.outputs[j].first;
+    if (col_reg[(size_t)r]) continue;
     std::string rn = reg_name[(size_t)r].empty() ? "r" + std::to_string(r) : reg_name[(size_t)r];
     std::string o = "out" + std::to_string(j);
     if (level[(size_t)r]) {
@@ -363,6 +408,30 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
       }
     } else {
       for (int64_t e = 0; e < E; e++) s << "  if (" << valid(e) << ") " << base << "[" << col(e) << "] = " << rn << "[" << e << "];\n";
+    }
+  }
+  if (has_col) {
+    s << "  }\n";  // end of the row loop
+    // The four waves' accumulators, combined in wave order through LDS: one partial row per block.
+    s << "  __shared__ " << T << " cl[4 * " << L << "];\n";
+    for (size_t j = 0; j < f.outputs.size(); j++) {
+      int64_t r = f.outputs[j].first;
+      if (!col_reg[(size_t)r]) continue;
+      int64_t aux = 0;
+      for (auto& m : f.ops)
+        if (m.reg == r) aux = m.aux;
+      const std::string c = "c" + std::to_string(r);
+      s << "  __syncthreads();\n";
+      for (int64_t e = 0; e < E; e++) {
+        std::string w = "  cl[(threadIdx.x >> 6) * " + std::to_string(L) + "u + " + col(e) + "] = " + c + "[" + std::to_string(e) + "];\n";
+        s << (exact ? w : "  if (" + valid(e) + ") " + w.substr(2));
+      }
+      s << "  __syncthreads();\n";
+      s << "  for (unsigned q = threadIdx.x; q < " << L << "u; q += " << TPB << "u) {\n";
+      s << "    " << T << " v = cl[q];\n";
+      s << "    for (int w = 1; w < 4; w++) v = " << col_comb(aux, "v", "cl[w * " + std::to_string(L) + "u + q]") << ";\n";
+      s << "    out" << j << "[(unsigned long long)blockIdx.x * " << L << "ull + q] = v;\n";
+      s << "  }\n";
     }
   }
   s << "}\n";

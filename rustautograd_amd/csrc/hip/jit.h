@@ -19,7 +19,14 @@ struct FusedKernel {
   uint32_t grid = 0;     // blocks of TPB threads
   int vec = 1;           // elements per thread
   hipFunction_t fn = nullptr;
+  // Row groups with column reductions: per output, the reduce kind of a column output (-1 for
+  // the others), which the kernel writes as `grid` partial rows of row_len values to be folded.
+  std::vector<int> col_kind;
+  uint32_t row_len = 0;
 };
+
+// Blocks of a row group with column reductions (each folds its rows into one partial row).
+constexpr int64_t COL_BLOCKS = 256;
 
 // Source of one kernel named `name` computing group `f` (`k->grid` blocks). Outputs whose slot is
 // also an input slot are written in place (each element is read before it is written). With

@@ -69,6 +69,8 @@ void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
 void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k,
                  void* partial, uint64_t chunks);
 uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k);
+// d[c] = the fold over rows 0 .. rows - 1 of partial[row][c], c < k, rows in order.
+void fold_rows(hipStream_t s, int dtype, int kind, const void* partial, void* d, uint64_t rows, uint64_t k);
 void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer,
                     const Strided& inner, uint64_t red_n);
 

@@ -788,6 +788,20 @@ void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
   });
 }
 
+void fold_rows(hipStream_t s, int dtype, int kind, const void* partial, void* d, uint64_t rows, uint64_t k) {
+  // The combining pass of reduce_cols: 16 row lanes per column, rows folded in order.
+  dim3 g((uint32_t)blocks_for(k, 64), 1, 1);
+  with_kind(kind, [&](auto K) {
+    constexpr int KIND = decltype(K)::value;
+    if (dtype == RG_F32)
+      hipLaunchKernelGGL((k_reduce_cols<float, 16, KIND>), g, dim3(1024), 0, s, (const float*)partial, (float*)d, (uint32_t)rows, (uint32_t)k,
+                         (uint32_t)rows, 1u);
+    else
+      hipLaunchKernelGGL((k_reduce_cols<double, 16, KIND>), g, dim3(1024), 0, s, (const double*)partial, (double*)d, (uint32_t)rows,
+                         (uint32_t)k, (uint32_t)rows, 1u);
+  });
+}
+
 void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer, const Strided& inner,
                     uint64_t red_n) {
   with_kind(kind, [&](auto K) {

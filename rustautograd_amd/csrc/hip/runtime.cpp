@@ -569,14 +569,27 @@ void build_program(Program& prog) {
         prog.steps.push_back([](hipStream_t, void* const*, void*) {});
         continue;
       }
-      prog.steps.push_back([fk, ins, outs](hipStream_t s, void* const* sl, void*) {
+      // Column outputs of a row group: partial rows in the workspace, folded after the kernel.
+      std::vector<uint64_t> col_off(outs.size(), UINT64_MAX);
+      uint64_t col_bytes = 0;
+      const int dtype = st.fused.dtype;
+      for (size_t j = 0; j < outs.size() && !fk->col_kind.empty(); j++)
+        if (fk->col_kind[j] >= 0) {
+          col_off[j] = col_bytes;
+          col_bytes += (uint64_t)fk->grid * fk->row_len * esize(dtype);
+        }
+      prog.workspace_bytes = std::max(prog.workspace_bytes, col_bytes);
+      if (ins.size() + outs.size() > 160) throw std::runtime_error("fused group with more than 160 operands");
+      prog.steps.push_back([fk, ins, outs, col_off, dtype](hipStream_t s, void* const* sl, void* ws) {
         void* ptrs[160];
         void* args[160];
         size_t q = 0;
         for (auto x : ins) ptrs[q++] = sl[x];
-        for (auto x : outs) ptrs[q++] = sl[x];
+        for (size_t j = 0; j < outs.size(); j++) ptrs[q++] = col_off[j] == UINT64_MAX ? sl[outs[j]] : (char*)ws + col_off[j];
         for (size_t j = 0; j < q; j++) args[j] = &ptrs[j];
         hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, rgjit::TPB, 1, 1, 0, s, args, nullptr);
+        for (size_t j = 0; j < outs.size(); j++)
+          if (col_off[j] != UINT64_MAX) rgk::fold_rows(s, dtype, fk->col_kind[j], (char*)ws + col_off[j], sl[outs[j]], fk->grid, fk->row_len);
       });
     } else if (st.kind == RG_STEP_ATTN) {
       prog.steps.push_back(lower_attention(prog, st.attn));

@@ -50,6 +50,9 @@ def test_layer_norm_forward_and_backward(rows, d):
     gx, gs, gb = g.grad(loss, [x, s, b])
     n = _both(g, [y, gx, gs, gb], [xv, sv, bv, wv], what=f"layernorm {rows}x{d}")
     assert n >= 2, "forward and backward should each form a row group"
+    plan = g.compile([y, gx, gs, gb], [xv, sv, bv, wv], device="hip", optimize="standard").plan_summary()
+    cols = sum(s.get("column_reductions", 0) for s in plan if s["kind"] == "fused")
+    assert cols == 2, f"the scale and shift gradients should fold inside the backward row group: {cols}"
 
 
 @pytest.mark.parametrize("shape", [(32, 8, 256), (16, 4, 96), (3, 300)])

@@ -1,0 +1,65 @@
+"""Row groups in device plans, on the CPU oracle.
+
+The HIP planner fuses a last-axis reduction with the row-wise work around it into a row group,
+and folds into the same group the reductions over every other axis (column reductions) of values
+it walks, such as a layer norm's scale and shift gradients. The oracle runs a device plan
+("cpu_devplan") with the operations of the nodes it replaces; a row group folds each row in
+element order (the CPU plan's eight-lane order differs by rounding), and a column reduction
+exactly as the standalone reduction it replaces. Results agree with the unfused CPU plan to
+rounding (1e-5 relative).
+"""
+
+import numpy as np
+import pytest
+
+from conftest import DEVPLAN
+from helpers import G
+from test_hip_rows import _layer_norm
+
+
+def _plans(g, outs, inputs):
+    dev = g.compile(outs, inputs, device=DEVPLAN, optimize="standard")
+    cpu = g.compile(outs, inputs, device="cpu", optimize="standard")
+    return dev, cpu
+
+
+@pytest.mark.parametrize("shape", [(64, 256), (3, 40, 96), (9, 7)])
+def test_layer_norm_parameter_gradients_fold_into_the_backward_row_group(shape):
+    d = shape[-1]
+    r = np.random.default_rng(d)
+    xv = r.normal(size=shape).astype(np.float32)
+    sv = (1 + 0.1 * r.normal(size=d)).astype(np.float32)
+    bv = (0.1 * r.normal(size=d)).astype(np.float32)
+    wv = r.normal(size=shape).astype(np.float32)
+    g = G()
+    x, s, b, w = g.input(shape, "float32"), g.input((d,), "float32"), g.input((d,), "float32"), g.input(shape, "float32")
+    y = _layer_norm(g, x, s, b, d)
+    loss = g.sum_all(g.bin("mul", y, w))
+    gx, gs, gb = g.grad(loss, [x, s, b])
+    outs, inputs = [y, gx, gs, gb], [xv, sv, bv, wv]
+    dev, cpu = _plans(g, outs, inputs)
+    steps = dev.plan_summary()
+    assert sum(st.get("column_reductions", 0) for st in steps if st["kind"] == "fused") == 2, steps
+    assert not any(st["kind"] == "instr" and st["op"] == "sum" for st in steps), [st.get("op") for st in steps]
+    a = g.eval(outs, inputs, device=DEVPLAN, optimize="standard")
+    b2 = g.eval(outs, inputs, device="cpu", optimize="standard")
+    for k, (u, v) in enumerate(zip(a, b2)):
+        np.testing.assert_allclose(u, v, rtol=1e-5, atol=1e-5 * np.abs(v).max(), err_msg=f"output {k}")
+
+
+def test_column_reduction_of_a_value_computed_after_the_group_stays_outside():
+    """A reduction whose value depends on the group's result through another reduction cannot
+    join it (the fold would need the finished group)."""
+    r = np.random.default_rng(3)
+    xv = r.normal(size=(32, 64)).astype(np.float32)
+    g = G()
+    x = g.input((32, 64), "float32")
+    m = g.op("max", [x], axes=[1], keepdims=True)
+    e = g.un("exp", g.bin("sub", x, m))
+    tot = g.op("sum", [e], axes=[0, 1], keepdims=True)  # every axis: a full reduction, not a column one
+    z = g.bin("div", e, tot)
+    col = g.op("sum", [z], axes=[0], keepdims=False)
+    outs, inputs = [col], [xv]
+    a = g.eval(outs, inputs, device=DEVPLAN, optimize="standard")
+    b = g.eval(outs, inputs, device="cpu", optimize="standard")
+    np.testing.assert_allclose(a[0], b[0], rtol=1e-5, atol=1e-5 * np.abs(b[0]).max())
