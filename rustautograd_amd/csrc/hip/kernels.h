@@ -71,6 +71,19 @@ void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
 uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k);
 // d[c] = the fold over rows 0 .. rows - 1 of partial[row][c], c < k, rows in order.
 void fold_rows(hipStream_t s, int dtype, int kind, const void* partial, void* d, uint64_t rows, uint64_t k);
+// Up to FOLD_JOBS f32 folds of that form in one launch of `tiles` blocks (job j covers blocks
+// [first_tile, next job's first_tile), one per 64 columns).
+constexpr int FOLD_JOBS = 48;
+struct FoldJob {
+  const float* part;
+  float* out;
+  uint32_t rows, k, kind, first_tile;
+};
+struct FoldJobs {
+  FoldJob job[FOLD_JOBS];
+  uint32_t n;
+};
+void fold_jobs(hipStream_t s, const FoldJobs& jobs, uint32_t tiles);
 void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer,
                     const Strided& inner, uint64_t red_n);
 

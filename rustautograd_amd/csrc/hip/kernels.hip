@@ -788,6 +788,42 @@ void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
   });
 }
 
+// Several f32 folds in one launch: block b folds 64 columns of the job whose column tiles it
+// falls in, 16 row lanes each folding a run of rows in order, the lanes then combined in order
+// (the same order as k_reduce_cols' combining pass).
+__global__ void __launch_bounds__(1024) k_fold_jobs(FoldJobs jobs) {
+  __shared__ float part[16][64];
+  uint32_t j = 0;
+  while (j + 1 < jobs.n && blockIdx.x >= jobs.job[j + 1].first_tile) j++;
+  const FoldJob& f = jobs.job[j];
+  const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const uint32_t c = (blockIdx.x - f.first_tile) * 64 + tx;
+  float acc = Red<float>::init(f.kind);
+  if (c < f.k) {
+    uint32_t r = ty;
+    for (; r + 7 * 16 < f.rows; r += 8 * 16) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) v[q] = f.part[(uint64_t)(r + q * 16) * f.k + c];
+#pragma unroll
+      for (int q = 0; q < 8; q++) acc = combine(f.kind, acc, v[q]);
+    }
+    for (; r < f.rows; r += 16) acc = combine(f.kind, acc, f.part[(uint64_t)r * f.k + c]);
+  }
+  part[ty][tx] = acc;
+  __syncthreads();
+  if (ty == 0 && c < f.k) {
+    float v = part[0][tx];
+#pragma unroll
+    for (int l = 1; l < 16; l++) v = combine(f.kind, v, part[l][tx]);
+    f.out[c] = v;
+  }
+}
+
+void fold_jobs(hipStream_t s, const FoldJobs& jobs, uint32_t tiles) {
+  if (jobs.n) hipLaunchKernelGGL(k_fold_jobs, dim3(tiles), dim3(1024), 0, s, jobs);
+}
+
 void fold_rows(hipStream_t s, int dtype, int kind, const void* partial, void* d, uint64_t rows, uint64_t k) {
   // The combining pass of reduce_cols: 16 row lanes per column, rows folded in order.
   dim3 g((uint32_t)blocks_for(k, 64), 1, 1);

@@ -69,6 +69,20 @@ struct Program {
   };
   std::vector<Merged> merged;
   std::vector<int64_t> merged_at;
+  // Column outputs of row groups: each kernel writes partial rows into its own range of the fold
+  // area (after the workspace); the folds run together, one launch, just before the first step
+  // that reads one of their outputs (folds_due[k]: the folds to run before step k; k = number of
+  // steps: at the end).
+  struct Fold {
+    uint64_t offset;
+    int64_t out_slot;
+    uint32_t rows, k;
+    int kind, dtype;
+  };
+  std::vector<Fold> folds;
+  std::vector<std::vector<size_t>> folds_due;
+  uint64_t fold_bytes = 0;
+  uint64_t fold_base() const { return (workspace_bytes + 255) / 256 * 256; }
   std::vector<void*> device_tables;  // per-batch GEMM offset tables
   uint64_t workspace_bytes = 0;
   std::vector<uint64_t> slot_bytes;
@@ -511,7 +525,24 @@ std::vector<std::pair<size_t, size_t>> merge_sets(const Plan& plan) {
   return sets;
 }
 
+// Slots a plan step reads.
+std::vector<int64_t> step_reads(const Step& st) {
+  std::vector<int64_t> r;
+  if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
+    for (auto& in : st.fused.inputs) r.push_back(in.slot);
+  } else if (st.kind == RG_STEP_ATTN) {
+    for (auto& v : st.attn.in) r.push_back(v.slot);
+    r.push_back(st.attn.mask_slot);
+    r.push_back(st.attn.mask_bits_slot);
+    r.push_back(st.attn.stats_slot);
+  } else {
+    for (auto& a : st.instr.args) r.push_back(a.slot);
+  }
+  return r;
+}
+
 void build_program(Program& prog) {
+  std::vector<size_t> fold_producer;  // per fold: the step of the row group that writes its partials
   std::ostringstream src;
   std::vector<rgjit::FusedKernel*> kernels;
   for (size_t k = 0; k < prog.plan.steps.size(); k++) {
@@ -569,27 +600,27 @@ void build_program(Program& prog) {
         prog.steps.push_back([](hipStream_t, void* const*, void*) {});
         continue;
       }
-      // Column outputs of a row group: partial rows in the workspace, folded after the kernel.
+      // Column outputs of a row group: partial rows in the fold area, folded later (folds_due).
       std::vector<uint64_t> col_off(outs.size(), UINT64_MAX);
-      uint64_t col_bytes = 0;
       const int dtype = st.fused.dtype;
       for (size_t j = 0; j < outs.size() && !fk->col_kind.empty(); j++)
         if (fk->col_kind[j] >= 0) {
-          col_off[j] = col_bytes;
-          col_bytes += (uint64_t)fk->grid * fk->row_len * esize(dtype);
+          col_off[j] = prog.fold_bytes;
+          prog.folds.push_back({prog.fold_bytes, outs[j], fk->grid, fk->row_len, fk->col_kind[j], dtype});
+          fold_producer.push_back(k);
+          prog.fold_bytes += ((uint64_t)fk->grid * fk->row_len * esize(dtype) + 255) / 256 * 256;
         }
-      prog.workspace_bytes = std::max(prog.workspace_bytes, col_bytes);
       if (ins.size() + outs.size() > 160) throw std::runtime_error("fused group with more than 160 operands");
-      prog.steps.push_back([fk, ins, outs, col_off, dtype](hipStream_t s, void* const* sl, void* ws) {
+      const Program* pp = &prog;
+      prog.steps.push_back([fk, ins, outs, col_off, pp](hipStream_t s, void* const* sl, void* ws) {
         void* ptrs[160];
         void* args[160];
         size_t q = 0;
         for (auto x : ins) ptrs[q++] = sl[x];
-        for (size_t j = 0; j < outs.size(); j++) ptrs[q++] = col_off[j] == UINT64_MAX ? sl[outs[j]] : (char*)ws + col_off[j];
+        for (size_t j = 0; j < outs.size(); j++)
+          ptrs[q++] = col_off[j] == UINT64_MAX ? sl[outs[j]] : (char*)ws + pp->fold_base() + col_off[j];
         for (size_t j = 0; j < q; j++) args[j] = &ptrs[j];
         hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, rgjit::TPB, 1, 1, 0, s, args, nullptr);
-        for (size_t j = 0; j < outs.size(); j++)
-          if (col_off[j] != UINT64_MAX) rgk::fold_rows(s, dtype, fk->col_kind[j], (char*)ws + col_off[j], sl[outs[j]], fk->grid, fk->row_len);
       });
     } else if (st.kind == RG_STEP_ATTN) {
       prog.steps.push_back(lower_attention(prog, st.attn));
@@ -599,6 +630,20 @@ void build_program(Program& prog) {
     }
   }
   for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));
+  // Each fold runs before the first later step reading its output, or right after its producer.
+  const size_t n = prog.plan.steps.size();
+  prog.folds_due.assign(n + 1, {});
+  for (size_t f = 0; f < prog.folds.size(); f++) {
+    size_t due = fold_producer[f] + 1;
+    for (size_t j = fold_producer[f] + 1; j < n; j++) {
+      auto r = step_reads(prog.plan.steps[j]);
+      if (std::find(r.begin(), r.end(), prog.folds[f].out_slot) != r.end()) {
+        due = j;
+        break;
+      }
+    }
+    prog.folds_due[due].push_back(f);
+  }
 }
 
 Frame* new_frame(Program& p) {
@@ -610,7 +655,7 @@ Frame* new_frame(Program& p) {
     total += (b + ALIGN - 1) / ALIGN * ALIGN;
   }
   uint64_t ws_off = total;
-  total += (p.workspace_bytes + ALIGN - 1) / ALIGN * ALIGN;
+  total += p.fold_base() + (p.fold_bytes + ALIGN - 1) / ALIGN * ALIGN;
   total = std::max<uint64_t>(total, ALIGN);
   hipError_t e = hipMalloc(&f->arena, total);
   if (e != hipSuccess) {
@@ -635,19 +680,47 @@ bool latch(Exec* e, hipError_t err, const char* what) {
   return true;
 }
 
+// Runs the folds due before steps first..last: f32 ones together, FOLD_JOBS per launch.
+void flush_folds(const Program& p, hipStream_t s, void* const* slots, void* ws, size_t first, size_t last) {
+  if (p.folds.empty()) return;
+  rgk::FoldJobs jobs;
+  jobs.n = 0;
+  uint32_t tiles = 0;
+  char* base = (char*)ws + p.fold_base();
+  for (size_t k = first; k <= last && k < p.folds_due.size(); k++)
+    for (size_t f : p.folds_due[k]) {
+      const auto& fd = p.folds[f];
+      if (fd.dtype != RG_F32) {
+        rgk::fold_rows(s, fd.dtype, fd.kind, base + fd.offset, slots[fd.out_slot], fd.rows, fd.k);
+        continue;
+      }
+      jobs.job[jobs.n++] = {(const float*)(base + fd.offset), (float*)slots[fd.out_slot], fd.rows, fd.k, (uint32_t)fd.kind, tiles};
+      tiles += (fd.k + 63) / 64;
+      if (jobs.n == rgk::FOLD_JOBS) {
+        rgk::fold_jobs(s, jobs, tiles);
+        jobs.n = 0;
+        tiles = 0;
+      }
+    }
+  rgk::fold_jobs(s, jobs, tiles);
+}
+
 // Enqueues plan steps begin..end-1, taking each merged run that lies wholly inside the range as
-// its one kernel.
+// its one kernel, and the folds due before each step.
 void enqueue_range(const Program& p, hipStream_t s, void* const* slots, void* ws, size_t begin, size_t end) {
   for (size_t k = begin; k < end;) {
     int64_t m = p.merged_at.empty() ? -1 : p.merged_at[k];
     if (m >= 0 && p.merged[(size_t)m].last < end) {
+      flush_folds(p, s, slots, ws, k, p.merged[(size_t)m].last);
       p.merged[(size_t)m].fn(s, slots, ws);
       k = p.merged[(size_t)m].last + 1;
     } else {
+      flush_folds(p, s, slots, ws, k, k);
       p.steps[k](s, slots, ws);
       k++;
     }
   }
+  if (end == p.steps.size()) flush_folds(p, s, slots, ws, end, end);
 }
 
 // Enqueues the listed steps in order, taking a merged run as its one kernel where the list holds
@@ -662,11 +735,13 @@ void enqueue_list(const Program& p, hipStream_t s, void* const* slots, void* ws,
       bool whole = q + len <= n;
       for (size_t i = 0; whole && i < len; i++) whole = (size_t)steps[q + i] == k + i;
       if (whole) {
+        flush_folds(p, s, slots, ws, mr.first, mr.last);
         mr.fn(s, slots, ws);
         q += len;
         continue;
       }
     }
+    flush_folds(p, s, slots, ws, k, k);
     p.steps[k](s, slots, ws);
     q++;
   }
@@ -868,7 +943,9 @@ int rg_hip_exec_step_timed(void* exec, double* seconds) {
   rgk::hold_stream(f->stream, 3000.0 + 15.0 * (double)n);
   hipEventRecord(ev[0], f->stream);
   for (size_t k = 0; k < n; k++) {
+    flush_folds(*e->prog, f->stream, f->slot.data(), f->workspace, k, k);
     e->prog->steps[k](f->stream, f->slot.data(), f->workspace);
+    if (k + 1 == n) flush_folds(*e->prog, f->stream, f->slot.data(), f->workspace, n, n);
     hipEventRecord(ev[k + 1], f->stream);
   }
   if (!latch(e, hipEventSynchronize(ev[n]), "timed step")) {
