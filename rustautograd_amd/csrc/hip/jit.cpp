@@ -207,7 +207,8 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   k->col_kind.assign(f.outputs.size(), -1);
   k->row_len = (uint32_t)L;
   if (has_col) {
-    k->grid = (uint32_t)std::min<int64_t>((rows + 3) / 4, COL_BLOCKS);
+    k->grid = (uint32_t)std::min<int64_t>((rows + COL_WAVES - 1) / COL_WAVES, COL_BLOCKS);
+    k->block = 64 * COL_WAVES;
     for (size_t j = 0; j < f.outputs.size(); j++)
       for (auto& m : f.ops)
         if (m.reg == f.outputs[j].first && col_reg[(size_t)m.reg]) k->col_kind[j] = (int)(m.aux & ~(int64_t)RG_ROWS_COLUMN);
@@ -233,7 +234,8 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   for (auto& o : f.outputs)
     for (auto& in : f.inputs) alias |= in.slot == o.second;
   const char* R = alias ? "" : "__restrict__ ";
-  s << "extern \"C\" __global__ void __launch_bounds__(" << TPB << ") " << name << "(";
+  const int waves = has_col ? COL_WAVES : TPB / 64;
+  s << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << name << "(";
   for (size_t j = 0; j < f.inputs.size(); j++) s << (j ? ", " : "") << "const " << T << "* " << R << "in" << j;
   for (size_t j = 0; j < f.outputs.size(); j++) s << ", " << T << "* " << R << "out" << j;
   s << ") {\n";
@@ -251,8 +253,8 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
       if (col_reg[(size_t)m.reg])
         s << "  " << T << " c" << m.reg << "[" << E << "];\n  for (int e = 0; e < " << E << "; e++) c" << m.reg << "[e] = (" << T << ")"
           << col_init(m.aux) << ";\n";
-    s << "  for (unsigned long long row = (unsigned long long)blockIdx.x * 4ull + (threadIdx.x >> 6); row < " << rows
-      << "ull; row += (unsigned long long)gridDim.x * 4ull) {\n";
+    s << "  for (unsigned long long row = (unsigned long long)blockIdx.x * " << waves << "ull + (threadIdx.x >> 6); row < " << rows
+      << "ull; row += (unsigned long long)gridDim.x * " << waves << "ull) {\n";
   } else {
     s << "  const unsigned long long row = (unsigned long long)blockIdx.x * 4ull + (threadIdx.x >> 6);\n";
     s << "  if (row >= " << rows << "ull) return;\n";
@@ -412,8 +414,8 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   }
   if (has_col) {
     s << "  }\n";  // end of the row loop
-    // The four waves' accumulators, combined in wave order through LDS: one partial row per block.
-    s << "  __shared__ " << T << " cl[4 * " << L << "];\n";
+    // The waves' accumulators, combined in wave order through LDS: one partial row per block.
+    s << "  __shared__ " << T << " cl[" << waves << " * " << L << "];\n";
     for (size_t j = 0; j < f.outputs.size(); j++) {
       int64_t r = f.outputs[j].first;
       if (!col_reg[(size_t)r]) continue;
@@ -427,9 +429,9 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
         s << (exact ? w : "  if (" + valid(e) + ") " + w.substr(2));
       }
       s << "  __syncthreads();\n";
-      s << "  for (unsigned q = threadIdx.x; q < " << L << "u; q += " << TPB << "u) {\n";
+      s << "  for (unsigned q = threadIdx.x; q < " << L << "u; q += " << 64 * waves << "u) {\n";
       s << "    " << T << " v = cl[q];\n";
-      s << "    for (int w = 1; w < 4; w++) v = " << col_comb(aux, "v", "cl[w * " + std::to_string(L) + "u + q]") << ";\n";
+      s << "    for (int w = 1; w < " << waves << "; w++) v = " << col_comb(aux, "v", "cl[w * " + std::to_string(L) + "u + q]") << ";\n";
       s << "    out" << j << "[(unsigned long long)blockIdx.x * " << L << "ull + q] = v;\n";
       s << "  }\n";
     }

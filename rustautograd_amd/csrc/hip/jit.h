@@ -23,10 +23,13 @@ struct FusedKernel {
   // the others), which the kernel writes as `grid` partial rows of row_len values to be folded.
   std::vector<int> col_kind;
   uint32_t row_len = 0;
+  uint32_t block = TPB;  // threads per block
 };
 
-// Blocks of a row group with column reductions (each folds its rows into one partial row).
+// A row group with column reductions: COL_BLOCKS blocks of COL_WAVES waves (one block per CU,
+// four waves per SIMD), each folding the rows it walks into one partial row.
 constexpr int64_t COL_BLOCKS = 256;
+constexpr int COL_WAVES = 16;
 
 // Source of one kernel named `name` computing group `f` (`k->grid` blocks). Outputs whose slot is
 // also an input slot are written in place (each element is read before it is written). With
@@ -39,7 +42,9 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
 // then outputs, part after part. For groups too small to fill the device on their own.
 std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, const std::string& name, FusedKernel* k);
 
-// Source of one row-group kernel (RG_STEP_ROWS): `k->grid` blocks of four rows each.
+// Source of one row-group kernel (RG_STEP_ROWS): `k->grid` blocks of four rows each, or, with
+// column reductions, COL_BLOCKS blocks of COL_WAVES waves walking the rows grid-stride and writing
+// one partial row per block for each column output (see col_kind).
 std::string generate_rows(const rgplan::Fused& f, const std::string& name, FusedKernel* k);
 
 // Compiles all sources into one code object for gfx950 and resolves each kernel. Modules are

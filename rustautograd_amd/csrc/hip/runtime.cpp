@@ -620,7 +620,7 @@ void build_program(Program& prog) {
         for (size_t j = 0; j < outs.size(); j++)
           ptrs[q++] = col_off[j] == UINT64_MAX ? sl[outs[j]] : (char*)ws + pp->fold_base() + col_off[j];
         for (size_t j = 0; j < q; j++) args[j] = &ptrs[j];
-        hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, rgjit::TPB, 1, 1, 0, s, args, nullptr);
+        hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, fk->block, 1, 1, 0, s, args, nullptr);
       });
     } else if (st.kind == RG_STEP_ATTN) {
       prog.steps.push_back(lower_attention(prog, st.attn));
