@@ -65,10 +65,11 @@ void cumsum(hipStream_t s, int dtype, const void* a, void* d, uint64_t rows, uin
 
 // Reductions over a canonical pattern; see runtime.cpp for how shapes map onto them.
 void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t rows, uint64_t len);
-// With chunks > 1, `partial` holds batch*chunks*k elements.
+// With chunks > 1, `partial` holds batch*chunks*k elements; with d == nullptr only the chunk
+// partials are written, to be folded by fold_rows or fold_jobs.
 void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k,
                  void* partial, uint64_t chunks);
-uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k);
+uint64_t reduce_cols_chunks(int dtype, uint64_t batch, uint64_t r, uint64_t k);
 // d[c] = the fold over rows 0 .. rows - 1 of partial[row][c], c < k, rows in order.
 void fold_rows(hipStream_t s, int dtype, int kind, const void* partial, void* d, uint64_t rows, uint64_t k);
 // Up to FOLD_JOBS f32 folds of that form in one launch of `tiles` blocks (job j covers blocks

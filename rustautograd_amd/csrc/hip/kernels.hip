@@ -473,6 +473,55 @@ __global__ void __launch_bounds__(64 * LANES) k_reduce_cols(const T* __restrict_
   }
 }
 
+// The same reduction with 16-byte loads: a lane owns V = 16 / sizeof(T) adjacent columns, so one
+// wave covers 64 * V columns (a 1 KiB row segment) and four waves are the row lanes. Eight row
+// loads in flight per lane; per column the rows are combined in the same lane-strided order as
+// k_reduce_cols. Needs k % V == 0 and a 16-byte aligned base.
+template <class T, int KIND>
+__global__ void __launch_bounds__(256) k_reduce_cols_vec(const T* __restrict__ a, T* __restrict__ out, uint32_t r, uint32_t k,
+                                                         uint32_t chunk_rows, uint32_t chunks) {
+  constexpr int V = 16 / sizeof(T), LANES = 4;
+  using Vec = T __attribute__((ext_vector_type(V)));
+  __shared__ T part[LANES][64 * V];
+  const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const uint32_t c = (blockIdx.x * 64 + tx) * V;
+  const uint32_t b = blockIdx.y, s = blockIdx.z;
+  const uint32_t r0 = s * chunk_rows, r1 = min(r, r0 + chunk_rows);
+  Vec acc;
+#pragma unroll
+  for (int e = 0; e < V; e++) acc[e] = Red<T>::init(KIND);
+  if (c < k) {
+    const T* x = a + (uint64_t)b * r * k + c;
+    uint32_t row = r0 + ty;
+    for (; row + 7 * LANES < r1; row += 8 * LANES) {
+      Vec v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) v[q] = *(const Vec*)(x + (uint64_t)(row + q * LANES) * k);
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+#pragma unroll
+        for (int e = 0; e < V; e++) acc[e] = combine(KIND, acc[e], v[q][e]);
+    }
+    for (; row < r1; row += LANES) {
+      Vec v = *(const Vec*)(x + (uint64_t)row * k);
+#pragma unroll
+      for (int e = 0; e < V; e++) acc[e] = combine(KIND, acc[e], v[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < V; e++) part[ty][tx * V + e] = acc[e];
+  __syncthreads();
+  // Each thread finishes 64 * V / 256 columns of the block's tile.
+  for (uint32_t j = threadIdx.x; j < 64 * V; j += 256) {
+    const uint32_t col = blockIdx.x * 64 * V + j;
+    if (col >= k) continue;
+    T v = part[0][j];
+#pragma unroll
+    for (int l = 1; l < LANES; l++) v = combine(KIND, v, part[l][j]);
+    out[((uint64_t)b * chunks + s) * k + col] = v;
+  }
+}
+
 template <class T, int KIND>
 __global__ void __launch_bounds__(TPB) k_reduce_general(const T* __restrict__ a, T* __restrict__ d, uint32_t out_n, Strided outer,
                                                         Strided inner, uint32_t red_n) {
@@ -753,29 +802,47 @@ void reduce_rows(hipStream_t s, int dtype, int kind, const void* a, void* d, uin
   });
 }
 
-uint64_t reduce_cols_chunks(uint64_t batch, uint64_t r, uint64_t k) {
-  // About 512 blocks in the first pass (2 per CU), at least 64 rows per chunk, and at most 256
-  // chunks so the combining pass stays one round of loads per thread.
-  uint64_t col_blocks = (k + 63) / 64 * batch;
+static bool reduce_cols_vector(int dtype, const void* a, uint64_t k) {
+  const uint64_t v = dtype == RG_F32 ? 4 : 2;
+  return k % v == 0 && ((uintptr_t)a & 15) == 0;
+}
+
+uint64_t reduce_cols_chunks(int dtype, uint64_t batch, uint64_t r, uint64_t k) {
+  // About 512 blocks in the first pass (2 per CU), at least 32 rows per chunk (one round of eight
+  // loads per row lane), and at most 256 chunks so the combining pass stays one round of loads per
+  // thread. The column tile is 64 lanes of 16 bytes when k allows vector loads, else 64 columns.
+  const uint64_t tile = k % (dtype == RG_F32 ? 4 : 2) == 0 ? (dtype == RG_F32 ? 256 : 128) : 64;
+  uint64_t col_blocks = (k + tile - 1) / tile * batch;
   uint64_t want = (512 + col_blocks - 1) / col_blocks;
-  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 64));
+  uint64_t chunks = std::max<uint64_t>(1, std::min<uint64_t>(want, r / 32));
   return std::min<uint64_t>(chunks, 256);
 }
 
 void reduce_cols(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t batch, uint64_t r, uint64_t k, void* partial,
                  uint64_t chunks) {
   uint32_t chunk_rows = (uint32_t)((r + chunks - 1) / chunks);
-  dim3 grid(blocks_for(k, 64), (uint32_t)batch, (uint32_t)chunks);
   void* out = chunks == 1 ? d : partial;
+  const bool vec = reduce_cols_vector(dtype, a, k);
   with_kind(kind, [&](auto K) {
     constexpr int KIND = decltype(K)::value;
-    if (dtype == RG_F32)
-      hipLaunchKernelGGL((k_reduce_cols<float, 4, KIND>), grid, dim3(256), 0, s, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k,
-                         chunk_rows, (uint32_t)chunks);
-    else
-      hipLaunchKernelGGL((k_reduce_cols<double, 4, KIND>), grid, dim3(256), 0, s, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k,
-                         chunk_rows, (uint32_t)chunks);
-    if (chunks > 1) {
+    if (vec) {
+      dim3 grid(blocks_for(k, dtype == RG_F32 ? 256 : 128), (uint32_t)batch, (uint32_t)chunks);
+      if (dtype == RG_F32)
+        hipLaunchKernelGGL((k_reduce_cols_vec<float, KIND>), grid, dim3(256), 0, s, (const float*)a, (float*)out, (uint32_t)r,
+                           (uint32_t)k, chunk_rows, (uint32_t)chunks);
+      else
+        hipLaunchKernelGGL((k_reduce_cols_vec<double, KIND>), grid, dim3(256), 0, s, (const double*)a, (double*)out, (uint32_t)r,
+                           (uint32_t)k, chunk_rows, (uint32_t)chunks);
+    } else {
+      dim3 grid(blocks_for(k, 64), (uint32_t)batch, (uint32_t)chunks);
+      if (dtype == RG_F32)
+        hipLaunchKernelGGL((k_reduce_cols<float, 4, KIND>), grid, dim3(256), 0, s, (const float*)a, (float*)out, (uint32_t)r, (uint32_t)k,
+                           chunk_rows, (uint32_t)chunks);
+      else
+        hipLaunchKernelGGL((k_reduce_cols<double, 4, KIND>), grid, dim3(256), 0, s, (const double*)a, (double*)out, (uint32_t)r, (uint32_t)k,
+                           chunk_rows, (uint32_t)chunks);
+    }
+    if (chunks > 1 && d != nullptr) {
       // The partials [batch, chunks, k] are themselves a leading-axis reduction: 16 row lanes.
       dim3 g2(blocks_for(k, 64), (uint32_t)batch, 1);
       if (dtype == RG_F32)

@@ -69,10 +69,10 @@ struct Program {
   };
   std::vector<Merged> merged;
   std::vector<int64_t> merged_at;
-  // Column outputs of row groups: each kernel writes partial rows into its own range of the fold
-  // area (after the workspace); the folds run together, one launch, just before the first step
-  // that reads one of their outputs (folds_due[k]: the folds to run before step k; k = number of
-  // steps: at the end).
+  // Column outputs of row groups and chunked leading-axis reductions: each kernel writes partial
+  // rows into its own range of the fold area (after the workspace); the folds run together, one
+  // launch, just before the first step that reads one of their outputs (folds_due[k]: the folds to
+  // run before step k; k = number of steps: at the end).
   struct Fold {
     uint64_t offset;
     int64_t out_slot;
@@ -240,7 +240,17 @@ StepFn lower_reduce(Program& prog, const Instr& i) {
   if ((pat.size() == 2 && pat[0].second && !pat[1].second) || (pat.size() == 3 && !pat[0].second && pat[1].second && !pat[2].second)) {
     uint64_t batch = pat.size() == 3 ? pat[0].first : 1;
     uint64_t r = pat[pat.size() - 2].first, k = pat.back().first;
-    uint64_t chunks = rgk::reduce_cols_chunks(batch, r, k);
+    uint64_t chunks = rgk::reduce_cols_chunks(dtype, batch, r, k);
+    if (chunks > 1 && batch == 1) {
+      // The chunk partials go to the fold area and are folded with the other deferred folds.
+      const uint64_t off = prog.fold_bytes;
+      prog.folds.push_back({off, dst, (uint32_t)chunks, (uint32_t)k, kind, dtype});
+      prog.fold_bytes += (chunks * k * esize(dtype) + 255) / 256 * 256;
+      const Program* pp = &prog;
+      return [=](hipStream_t s, void* const* sl, void* ws) {
+        rgk::reduce_cols(s, dtype, kind, sl[a], nullptr, 1, r, k, (char*)ws + pp->fold_base() + off, chunks);
+      };
+    }
     if (chunks > 1) prog.workspace_bytes = std::max<uint64_t>(prog.workspace_bytes, batch * chunks * k * esize(dtype));
     return [=](hipStream_t s, void* const* sl, void* ws) { rgk::reduce_cols(s, dtype, kind, sl[a], sl[dst], batch, r, k, ws, chunks); };
   }
@@ -627,6 +637,7 @@ void build_program(Program& prog) {
     } else {
       const Instr& in = st.instr;
       prog.steps.push_back(lower_instr(prog, in));
+      while (fold_producer.size() < prog.folds.size()) fold_producer.push_back(k);
     }
   }
   for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));

@@ -123,10 +123,11 @@ def test_reductions_at_model_shapes(shape, axes):
         close(hip[0], cpu[0], 1e-4, f"{kind} {shape} {axes}")
 
 
-@pytest.mark.parametrize("shape,axes", [((3, 5000, 64), [1]), ((40, 8192), [0]), ((1000, 100), [0]), ((257, 12), [0]), ((8, 4), [0])])
+@pytest.mark.parametrize("shape,axes", [((3, 5000, 64), [1]), ((40, 8192), [0]), ((1000, 100), [0]), ((1000, 101), [0]), ((257, 12), [0]), ((8, 4), [0])])
 def test_column_reductions_repeat_exactly(shape, axes):
     """Leading-axis reductions: chunk partials folded in a fixed order by a second launch. Shapes
-    cover a batch, partial column tiles, uneven chunks and a single chunk. Three calls in a row on
+    cover a batch, partial column tiles, uneven chunks, a single chunk, and column counts that do
+    and do not allow 16-byte loads. Three calls in a row on
     one compiled program must each match the oracle and repeat bit for bit."""
     rng = np.random.default_rng(5)
     for kind in ("sum", "max", "min"):
