@@ -447,9 +447,16 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
 
 }  // namespace
 
-uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
-  if (!use_mfma(dtype, m, n, k)) return 0;
-  int s = split_count(pick_tile(m, n, k, batch, false), m, n, k, batch);
+int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
+  if (m == 0 || n == 0 || batch == 0 || !use_mfma(dtype, m, n, k)) return 1;
+  TileCfg t = pick_tile(m, n, k, batch, tb);
+  int splits = split_count(t, m, n, k, batch);
+  uint64_t kps = ((k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk;
+  return (int)((k + kps - 1) / kps);
+}
+
+uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
+  int s = gemm_splits(dtype, m, n, k, batch, tb);
   return s > 1 ? (uint64_t)s * batch * m * n * sizeof(float) : 0;
 }
 
@@ -485,7 +492,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     l.kps = kps;
     l.part = splits > 1 ? (float*)g.workspace : nullptr;
     launch_mfma(s, t, g.ta, g.tb, mode, l);
-    if (splits > 1) {
+    if (splits > 1 && !g.defer_split) {
       uint64_t mn = g.m * g.n;
       hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 1023) / 1024), (uint32_t)g.batch), dim3(256), 0, s, (const float*)l.part,
                          (float*)g.c, mn, splits);

@@ -85,6 +85,21 @@ struct FoldJobs {
   uint32_t n;
 };
 void fold_jobs(hipStream_t s, const FoldJobs& jobs, uint32_t tiles);
+// Up to FOLD_JOBS f32 sums over a few long rows in one launch: out[i] = part[0][i] + part[1][i]
+// + ... + part[rows - 1][i], rows in order, i < n (a multiple of 4; 16-byte aligned part and out),
+// 1024 elements per block (job j covers blocks [first_block, next job's first_block)). The form
+// of K-split partial products.
+struct WideFold {
+  const float* part;
+  float* out;
+  uint64_t n;
+  uint32_t rows, first_block;
+};
+struct WideFolds {
+  WideFold job[FOLD_JOBS];
+  uint32_t n;
+};
+void fold_wide(hipStream_t s, const WideFolds& jobs, uint32_t blocks);
 void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, uint64_t out_n, const Strided& outer,
                     const Strided& inner, uint64_t red_n);
 
@@ -110,8 +125,9 @@ struct GemmArgs {
   const int64_t* b_off;
   bool a_off4, b_off4;          // every offset in the array is a multiple of 4 elements
   uint64_t a_stride, b_stride;  // per-batch element strides when the offset arrays are null
-  void* workspace;              // split-K partial sums
+  void* workspace;              // split-K partial sums, [batch][splits][M N]
   uint64_t workspace_bytes;
+  bool defer_split = false;  // leave the partials for fold_wide instead of summing them into C
 };
 // Fused attention (attention.hip) over bh = batch * heads independent (tq x hd, tk x hd)
 // problems. Operands are strided views: row t of problem b * heads + h starts at
@@ -145,8 +161,10 @@ uint64_t attention_mask_words(const AttnArgs& a);
 void attention_forward(hipStream_t s, const AttnArgs& a, bool build_mask_bits = true);
 void attention_backward(hipStream_t s, const AttnArgs& a);
 
-// Workspace bytes the product needs for its split-K partials.
-uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch);
+// The number of K splits the product runs with (1: none), and the workspace bytes its split-K
+// partials need.
+int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb);
+uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb);
 void gemm(hipStream_t s, const GemmArgs& g);
 
 }  // namespace rgk

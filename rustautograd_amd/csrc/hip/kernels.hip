@@ -891,6 +891,34 @@ void fold_jobs(hipStream_t s, const FoldJobs& jobs, uint32_t tiles) {
   if (jobs.n) hipLaunchKernelGGL(k_fold_jobs, dim3(tiles), dim3(1024), 0, s, jobs);
 }
 
+// Eight rows' loads in flight per thread, added in row order (the order of k_split_sum).
+__global__ void __launch_bounds__(256) k_fold_wide(WideFolds jobs) {
+  uint32_t j = 0;
+  while (j + 1 < jobs.n && blockIdx.x >= jobs.job[j + 1].first_block) j++;
+  const WideFold& f = jobs.job[j];
+  const uint64_t i = ((uint64_t)(blockIdx.x - f.first_block) * 256 + threadIdx.x) * 4;
+  if (i >= f.n) return;
+  const float* p = f.part + i;
+  float4 acc = *(const float4*)p;
+  uint32_t r = 1;
+  for (; r + 7 < f.rows; r += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = *(const float4*)(p + (uint64_t)(r + q) * f.n);
+#pragma unroll
+    for (int q = 0; q < 8; q++) acc = make_float4(acc.x + v[q].x, acc.y + v[q].y, acc.z + v[q].z, acc.w + v[q].w);
+  }
+  for (; r < f.rows; r++) {
+    const float4 v = *(const float4*)(p + (uint64_t)r * f.n);
+    acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+  }
+  *(float4*)(f.out + i) = acc;
+}
+
+void fold_wide(hipStream_t s, const WideFolds& jobs, uint32_t blocks) {
+  if (jobs.n) hipLaunchKernelGGL(k_fold_wide, dim3(blocks), dim3(256), 0, s, jobs);
+}
+
 void fold_rows(hipStream_t s, int dtype, int kind, const void* partial, void* d, uint64_t rows, uint64_t k) {
   // The combining pass of reduce_cols: 16 row lanes per column, rows folded in order.
   dim3 g((uint32_t)blocks_for(k, 64), 1, 1);

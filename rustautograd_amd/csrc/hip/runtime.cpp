@@ -78,6 +78,7 @@ struct Program {
     int64_t out_slot;
     uint32_t rows, k;
     int kind, dtype;
+    bool wide = false;  // a sum over a few long rows (K-split partials): fold_wide
   };
   std::vector<Fold> folds;
   std::vector<std::vector<size_t>> folds_due;
@@ -188,10 +189,30 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
       base.b_off4 = all4(bo);
     }
   }
-  uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch);
+  if (i.n == 0) return [](hipStream_t, void* const*, void*) {};
+  const int splits = rgk::gemm_splits(dtype, base.m, base.n, base.k, base.batch, tb);
+  const uint64_t mn = base.m * base.n;
+  if (splits > 1 && base.batch == 1 && mn % 4 == 0 && mn < (1ull << 32)) {
+    // K-split partials go to the fold area; their sum joins the deferred folds (fold_wide).
+    const uint64_t off = prog.fold_bytes;
+    Program::Fold fd{off, dst, (uint32_t)splits, (uint32_t)mn, RG_REDUCE_SUM, dtype};
+    fd.wide = true;
+    prog.folds.push_back(fd);
+    prog.fold_bytes += ((uint64_t)splits * mn * sizeof(float) + 255) / 256 * 256;
+    base.defer_split = true;
+    const Program* pp = &prog;
+    return [base, as, bs, dst, off, pp](hipStream_t s, void* const* sl, void* wsp) {
+      rgk::GemmArgs g = base;
+      g.a = sl[as];
+      g.b = sl[bs];
+      g.c = sl[dst];
+      g.workspace = (char*)wsp + pp->fold_base() + off;
+      rgk::gemm(s, g);
+    };
+  }
+  uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch, tb);
   prog.workspace_bytes = std::max(prog.workspace_bytes, ws);
   base.workspace_bytes = ws;
-  if (i.n == 0) return [](hipStream_t, void* const*, void*) {};
   return [base, as, bs, dst](hipStream_t s, void* const* sl, void* wsp) {
     rgk::GemmArgs g = base;
     g.a = sl[as];
@@ -697,10 +718,23 @@ void flush_folds(const Program& p, hipStream_t s, void* const* slots, void* ws, 
   rgk::FoldJobs jobs;
   jobs.n = 0;
   uint32_t tiles = 0;
+  rgk::WideFolds wide;
+  wide.n = 0;
+  uint32_t blocks = 0;
   char* base = (char*)ws + p.fold_base();
   for (size_t k = first; k <= last && k < p.folds_due.size(); k++)
     for (size_t f : p.folds_due[k]) {
       const auto& fd = p.folds[f];
+      if (fd.wide) {
+        wide.job[wide.n++] = {(const float*)(base + fd.offset), (float*)slots[fd.out_slot], fd.k, fd.rows, blocks};
+        blocks += (fd.k + 1023) / 1024;
+        if (wide.n == rgk::FOLD_JOBS) {
+          rgk::fold_wide(s, wide, blocks);
+          wide.n = 0;
+          blocks = 0;
+        }
+        continue;
+      }
       if (fd.dtype != RG_F32) {
         rgk::fold_rows(s, fd.dtype, fd.kind, base + fd.offset, slots[fd.out_slot], fd.rows, fd.k);
         continue;
@@ -714,6 +748,7 @@ void flush_folds(const Program& p, hipStream_t s, void* const* slots, void* ws, 
       }
     }
   rgk::fold_jobs(s, jobs, tiles);
+  rgk::fold_wide(s, wide, blocks);
 }
 
 // Enqueues plan steps begin..end-1, taking each merged run that lies wholly inside the range as

@@ -180,6 +180,25 @@ def test_mfma_products_with_transpose_flags(m, k, n, ta, tb):
     close(hip, want, 1e-4, f"gemm {m}x{k}x{n} ta={ta} tb={tb}")
 
 
+def test_split_products_feed_later_steps():
+    """K-split products whose partial sums are folded later, just before the first step that
+    reads the product: an elementwise group, another product and a program output."""
+    rng = np.random.default_rng(11)
+    a = rng.normal(size=(8192, 256)).astype(np.float32)
+    b = rng.normal(size=(8192, 768)).astype(np.float32)
+    c = rng.normal(size=(768, 64)).astype(np.float32)
+
+    def build(g, i):
+        y = op(g, "matmul", [_swap(g, i[0], 2), i[1]])
+        z = op(g, "mul", [y, y])
+        return [z, op(g, "matmul", [y, i[2]]), y]
+    hip = run_graph("hip", build, [t(a), t(b), t(c)], optimize="standard")
+    y = a.T.astype(np.float64) @ b.astype(np.float64)
+    close(hip[0], y * y, 2e-4, "square of a split product")
+    close(hip[1], y @ c.astype(np.float64), 1e-4, "product of a split product")
+    close(hip[2], y, 1e-4, "split product")
+
+
 @pytest.mark.parametrize("a,b", [((5, 1, 96, 64), (1, 4, 64, 96)), ((3, 67, 129), (3, 129, 65)), ((2, 3, 128, 64), (3, 64, 256))])
 def test_batched_products_with_broadcast_and_odd_strides(a, b):
     """Per-batch offset tables (broadcast batches) and batch strides that are not multiples of 4."""
