@@ -1,5 +1,6 @@
 // Graph optimizer: single forward rewrite with identities, folding, broadcast elision,
-// transpose flags, the device split of full sums and CSE, then rematerialization.
+// transpose flags, the device split of full sums and CSE, then rematerialization (followed, for
+// device plans, by a merge of identical nodes).
 // Follows the reference's src/optimize.rs:8-15 (constants), 42-77 (splat, identity),
 // 79-166 (rematerialize), 172-285 (modes), 287-403 (simplify).
 #include "optimize.h"
@@ -271,12 +272,53 @@ Simplified simplify(const Graph& g, const std::vector<uint32_t>& outputs, bool d
   return r;
 }
 
-Optimized finish(const Simplified& s, OptStats st) {
+// A rematerialized value whose original also stays in the forward pass has a clone with the
+// same inputs; level-order device plans compute both in the same group, so the clone only adds
+// a second output of the same value. On the device, identical nodes are merged after
+// rematerialization (the same keying as simplify's CSE).
+Simplified merge_identical(const Graph& g, const std::vector<uint32_t>& outputs, OptStats& st) {
+  std::vector<bool> keep = g.reachable(outputs);
+  Simplified r;
+  Graph& h = r.g;
+  std::vector<uint32_t> map(g.nodes.size(), UINT32_MAX);
+  std::unordered_map<std::string, uint32_t> seen;
+  for (size_t i = 0; i < g.nodes.size(); i++) {
+    const Node& n = g.nodes[i];
+    h.cur_source = n.source;
+    if (n.op.kind == RG_OP_INPUT) {
+      map[i] = h.input(n.shape, n.dtype);
+      h.nodes[map[i]].op = n.op;
+      continue;
+    }
+    if (!keep[i]) continue;
+    std::vector<uint32_t> ins;
+    for (uint32_t x : n.inputs) ins.push_back(map[x]);
+    const bool big_const = n.op.kind == RG_OP_CONST && n.op.t->n() > CSE_CONST_LIMIT;
+    std::string key;
+    if (!big_const) {
+      key = n.op.key() + "|";
+      for (uint32_t x : ins) key += std::to_string(x) + ",";
+      auto it = seen.find(key);
+      if (it != seen.end()) {
+        map[i] = it->second;
+        st.cse++;
+        continue;
+      }
+    }
+    map[i] = n.op.kind == RG_OP_CONST ? h.constant(*n.op.t) : h.add(n.op, ins);
+    if (!big_const) seen[key] = map[i];
+  }
+  for (uint32_t o : outputs) r.out.push_back(map[o]);
+  return r;
+}
+
+Optimized finish(const Simplified& s, OptStats st, bool device) {
   Simplified h = rematerialize(s.g, s.out, s.backward, REMAT_MIN, false, st);
   if (build_plan(h.g, h.out, true).peak_live_bytes > COSTLY_REMAT_ABOVE_BYTES) {
     st.rematerialized = 0;
     h = rematerialize(s.g, s.out, s.backward, REMAT_MIN, true, st);
   }
+  if (device) h = merge_identical(h.g, h.out, st);
   size_t kept = 0;
   for (bool k : h.g.reachable(h.out)) kept += k;
   st.nodes_after = kept;
@@ -359,7 +401,7 @@ Optimized optimize_mode(const Graph& g, const std::vector<uint32_t>& outputs, bo
     if (mode == OptMode::SearchLinear && !has_matrix_structure(first.g, first.out)) {
       OptStats st = baseline.st;
       st.nodes_before = count_kept(g, outputs);
-      return finish(baseline, st);
+      return finish(baseline, st, device);
     }
     CostModel model = device ? CostModel::Device : CostModel::Cpu;
     SearchStats ss;
@@ -377,10 +419,10 @@ Optimized optimize_mode(const Graph& g, const std::vector<uint32_t>& outputs, bo
     st.searched = true;
     st.accepted = accepted;
     st.search = ss;
-    return finish(chosen, st);
+    return finish(chosen, st, device);
   }
   Simplified s = simplify(g, outputs, device, true);
-  return finish(s, s.st);
+  return finish(s, s.st, device);
 }
 
 }  // namespace rg

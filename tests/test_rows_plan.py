@@ -9,6 +9,8 @@ exactly as the standalone reduction it replaces. Results agree with the unfused 
 rounding (1e-5 relative).
 """
 
+import json
+
 import numpy as np
 import pytest
 
@@ -63,3 +65,34 @@ def test_column_reduction_of_a_value_computed_after_the_group_stays_outside():
     a = g.eval(outs, inputs, device=DEVPLAN, optimize="standard")
     b = g.eval(outs, inputs, device="cpu", optimize="standard")
     np.testing.assert_allclose(a[0], b[0], rtol=1e-5, atol=1e-5 * np.abs(b[0]).max())
+
+
+def test_rematerialized_copies_merge_with_their_originals_in_device_plans():
+    """An activation kept for the backward pass is rematerialized (a clone with the same inputs)
+    while its original still feeds the forward pass; level-order device plans would compute both
+    in one group and write the value twice, so device plans merge identical nodes afterwards.
+    The CPU plan keeps the clone. Results agree to rounding."""
+    r = np.random.default_rng(7)
+    xv = r.normal(size=(64, 128)).astype(np.float32)
+    w1v = (0.1 * r.normal(size=(128, 512))).astype(np.float32)
+    bv = (0.1 * r.normal(size=(512,))).astype(np.float32)
+    w2v = (0.1 * r.normal(size=(512, 128))).astype(np.float32)
+    tv = r.normal(size=(64, 128)).astype(np.float32)
+    g = G()
+    x, w1, b, w2, t = (g.input(v.shape, "float32") for v in (xv, w1v, bv, w2v, tv))
+    u = g.bin("add", g.op("matmul", [x, w1]), b)
+    a = g.bin("mul", u, g.un("tanh", u))  # an activation the backward pass needs
+    y = g.op("matmul", [a, w2])
+    loss = g.sum_all(g.bin("mul", y, t))
+    gw1, gb, gw2 = g.grad(loss, [w1, b, w2])
+    outs, inputs = [y, gw1, gb, gw2], [xv, w1v, bv, w2v, tv]
+    dev, cpu = _plans(g, outs, inputs)
+    st_dev = json.loads(dev.report_json)["graph"]["optimization"]
+    st_cpu = json.loads(cpu.report_json)["graph"]["optimization"]
+    assert st_cpu["rematerialized"] >= 1, st_cpu
+    assert st_dev["cse_merged"] > st_cpu["cse_merged"], (st_dev, st_cpu)
+    assert st_dev["nodes_after"] < st_cpu["nodes_after"], (st_dev, st_cpu)
+    got = g.eval(outs, inputs, device=DEVPLAN, optimize="standard")
+    want = g.eval(outs, inputs, device="cpu", optimize="standard")
+    for k, (p, q) in enumerate(zip(got, want)):
+        np.testing.assert_allclose(p, q, rtol=1e-5, atol=1e-5 * np.abs(q).max(), err_msg=f"output {k}")
