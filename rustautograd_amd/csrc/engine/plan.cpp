@@ -638,12 +638,14 @@ std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const 
   return items;
 }
 
-// Recomputation instead of storage. A plain fused group C that reads values X of an earlier plain
-// group G of its shape, where C is X's only other reader, recomputes X from G's own inputs: the
-// members of G that X depends on are added to C (a node may then run in two kernels). G stops
-// writing what nobody else reads, and C reads G's inputs instead of X. Done when it lowers C's
-// full-size reads, e.g. an activation's backward that would read every intermediate of its
-// forward. Members stay sorted by node id.
+// Recomputation instead of storage. A group C that reads values X of an earlier group G walking
+// the same elements (two fused groups of one shape, or two row groups over the same rows), where
+// C is X's only other reader, recomputes X: the members of G that X depends on, back to values C
+// reads anyway, are added to C (a node may then run in two kernels; a row group recomputes per-row
+// reductions such as a layer norm's mean and variance). G stops writing what nobody else reads.
+// Done when C reads no more full-size values than before (G then writes fewer), e.g. an
+// activation's backward that would read every intermediate of its forward, or a layer norm's
+// backward reading the centred input and the normalised values. Members stay sorted by node id.
 void rematerialize(const Graph& g, const std::vector<bool>& keep, const std::vector<uint32_t>& outputs, std::vector<Item>& items,
                    size_t max_bindings) {
   const size_t total = g.nodes.size();
@@ -653,20 +655,36 @@ void rematerialize(const Graph& g, const std::vector<bool>& keep, const std::vec
   for (size_t i = 0; i < total; i++)
     if (keep[i])
       for (uint32_t x : g.nodes[i].inputs) users[x].push_back((uint32_t)i);
-  std::vector<int64_t> item_of(total, -1);  // the plain group that first computes a node
-  auto plain = [&](const Item& it) { return it.group && !it.rows && it.attn < 0; };
+  std::vector<int64_t> item_of(total, -1);  // the group that first computes a node
+  auto eligible = [&](const Item& it) { return it.group && it.attn < 0; };
   auto in = [](const std::vector<size_t>& v, size_t x) { return std::binary_search(v.begin(), v.end(), x); };
+  // The shape a group walks: a row group's reduction input, a fused group's members' shape.
+  auto walk_of = [&](const Item& it) -> Shape {
+    if (it.rows)
+      for (size_t m : it.members)
+        if (g.nodes[m].op.kind == RG_OP_REDUCE) return g.shape(g.nodes[m].inputs[0]);
+    return g.nodes[it.members[0]].shape;
+  };
+  auto last_axis_reduce = [&](size_t m) {
+    const Node& n = g.nodes[m];
+    return n.op.kind == RG_OP_REDUCE && n.op.v.size() == 1 && n.op.v[0] + 1 == (int64_t)g.shape(n.inputs[0]).size();
+  };
   for (size_t ci = 0; ci < items.size(); ci++) {
     Item& C = items[ci];
-    if (plain(C)) {
-      const Node& c0 = g.nodes[C.members[0]];
+    if (eligible(C)) {
+      const Shape cf = walk_of(C);
+      const size_t cn = numel(cf), rows = cf.empty() || cf.back() == 0 ? cn : cn / (size_t)cf.back();
+      const DType cdt = g.nodes[C.members[0]].dtype;
       std::map<size_t, std::vector<uint32_t>> cand;  // producer group -> values C would recompute
       for (size_t u : C.members)
         for (uint32_t x : g.nodes[u].inputs) {
           if (in(C.members, x) || item_of[x] < 0 || is_out[x]) continue;
           const Item& G = items[(size_t)item_of[x]];
           const Node& n = g.nodes[x];
-          if (n.shape != c0.shape || n.dtype != c0.dtype || g.nodes[G.members[0]].shape != c0.shape) continue;
+          // Same walk: a fused group's values from a fused group of its shape; a row group's full
+          // or per-row values from a row group over the same rows.
+          if (G.rows != C.rows || walk_of(G) != cf || n.dtype != cdt) continue;
+          if (!(n.shape == cf || (C.rows && numel(n.shape) == rows && (n.op.kind != RG_OP_REDUCE || last_axis_reduce(x))))) continue;
           bool only = true;
           for (uint32_t w : users[x]) only &= in(G.members, w) || in(C.members, w);
           auto& v = cand[(size_t)item_of[x]];
@@ -674,36 +692,43 @@ void rematerialize(const Graph& g, const std::vector<bool>& keep, const std::vec
         }
       for (auto& [gi, xs] : cand) {
         const Item& G = items[gi];
-        // X's ancestors within G.
+        std::set<uint32_t> ext_c;
+        for (size_t u : C.members)
+          for (uint32_t y : g.nodes[u].inputs)
+            if (!in(C.members, y)) ext_c.insert(y);
+        // X's ancestors within G, up to the values C reads anyway.
         std::vector<size_t> closure;
         std::vector<uint32_t> stack(xs.begin(), xs.end());
+        bool ok = true;
         while (!stack.empty()) {
           uint32_t x = stack.back();
           stack.pop_back();
           if (std::find(closure.begin(), closure.end(), (size_t)x) != closure.end()) continue;
           closure.push_back(x);
+          // Only reductions a row group folds per row may be recomputed.
+          if (g.nodes[x].op.kind == RG_OP_REDUCE && !(C.rows && last_axis_reduce(x))) ok = false;
           for (uint32_t y : g.nodes[x].inputs)
-            if (in(G.members, y)) stack.push_back(y);
+            if (in(G.members, y) && (!ext_c.count(y) || std::find(xs.begin(), xs.end(), y) != xs.end())) stack.push_back(y);
         }
         std::sort(closure.begin(), closure.end());
-        // Full-size values C would newly read, against the values it no longer reads.
-        std::set<uint32_t> ext_c, fresh;
-        for (size_t u : C.members)
-          for (uint32_t y : g.nodes[u].inputs)
-            if (!in(C.members, y)) ext_c.insert(y);
+        // Full-size values C would newly read, against the full-size values it no longer reads
+        // (and G no longer writes): a trade of equal reads still saves G's writes.
+        std::set<uint32_t> fresh;
         for (size_t m : closure)
           for (uint32_t y : g.nodes[m].inputs)
             if (!in(closure, y) && !in(C.members, y) && !ext_c.count(y)) fresh.insert(y);
-        size_t full = 0;
-        for (uint32_t y : fresh) full += numel(g.shape(y)) == numel(c0.shape);
-        if (full >= xs.size() || closure.size() > 64 || ext_c.size() + fresh.size() + C.members.size() + closure.size() > max_bindings)
+        size_t full = 0, saved = 0;
+        for (uint32_t y : fresh) full += numel(g.shape(y)) == cn;
+        for (uint32_t x : xs) saved += numel(g.shape(x)) == cn;
+        if (!ok || saved == 0 || full > saved || closure.size() > 64 ||
+            ext_c.size() + fresh.size() + C.members.size() + closure.size() > max_bindings)
           continue;
         std::vector<size_t> merged;
         std::set_union(C.members.begin(), C.members.end(), closure.begin(), closure.end(), std::back_inserter(merged));
         C.members = std::move(merged);
       }
     }
-    if (plain(C))
+    if (eligible(C))
       for (size_t m : C.members)
         if (item_of[m] < 0) item_of[m] = (int64_t)ci;
   }

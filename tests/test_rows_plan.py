@@ -96,3 +96,30 @@ def test_rematerialized_copies_merge_with_their_originals_in_device_plans():
     want = g.eval(outs, inputs, device="cpu", optimize="standard")
     for k, (p, q) in enumerate(zip(got, want)):
         np.testing.assert_allclose(p, q, rtol=1e-5, atol=1e-5 * np.abs(q).max(), err_msg=f"output {k}")
+
+
+@pytest.mark.parametrize("shape", [(64, 256), (3, 40, 96)])
+def test_layer_norm_backward_recomputes_the_forward_rows(shape):
+    """The backward row group of a layer norm recomputes the centred input and the normalised
+    values (with the row mean and variance) from the input it reads anyway, so the forward row
+    group writes only its output; results agree with the CPU plan to rounding."""
+    d = shape[-1]
+    r = np.random.default_rng(d + 1)
+    xv = r.normal(size=shape).astype(np.float32)
+    sv = (1 + 0.1 * r.normal(size=d)).astype(np.float32)
+    bv = (0.1 * r.normal(size=d)).astype(np.float32)
+    wv = r.normal(size=shape).astype(np.float32)
+    g = G()
+    x, s, b, w = g.input(shape, "float32"), g.input((d,), "float32"), g.input((d,), "float32"), g.input(shape, "float32")
+    y = _layer_norm(g, x, s, b, d)
+    loss = g.sum_all(g.bin("mul", y, w))
+    gx, gs, gb = g.grad(loss, [x, s, b])
+    outs, inputs = [y, gx, gs, gb], [xv, sv, bv, wv]
+    dev, _ = _plans(g, outs, inputs)
+    rows = [st for st in dev.plan_summary() if st["kind"] == "fused" and st["row_len"]]
+    assert len(rows) == 2, rows
+    assert rows[0]["n_outputs"] == 1, rows[0]
+    a = g.eval(outs, inputs, device=DEVPLAN, optimize="standard")
+    b2 = g.eval(outs, inputs, device="cpu", optimize="standard")
+    for k, (u, v) in enumerate(zip(a, b2)):
+        np.testing.assert_allclose(u, v, rtol=1e-5, atol=1e-5 * np.abs(v).max(), err_msg=f"output {k}")
