@@ -55,6 +55,10 @@
  *                    only for hd in {16, 32, 64} and tq, tk multiples of 32 up to
  *                    RG_ATTN_MAX_T.
  *
+ * Operands: MATMUL and MATMUL_T (f32, device plans) may carry a third argument, a vector of
+ * the product's column count added to every row of the finished product (a bias add folded
+ * into the product; no reference counterpart).
+ *
  * Attribute words per op:
  *   MATMUL_T       ta, tb
  *   REDUCE         kind, keepdims, n_axes, axes...

@@ -447,6 +447,17 @@ void binary(const Instr& i, std::vector<Buf>& s, F f) {
   }
 }
 
+// A product's optional third operand (device plans): a vector added to every row of the finished
+// product, the fp32 addition the fused group it replaces would do (include/rg_plan.h).
+template <class T>
+void add_bias(const Instr& i, std::vector<Buf>& s) {
+  if (i.args.size() != 3 || i.n == 0) return;
+  const T* bias = s[(size_t)i.args[2].slot].template as<T>();
+  T* dst = s[(size_t)i.dst].template as<T>();
+  const size_t n = (size_t)i.shape.back();
+  for (size_t e = 0; e < (size_t)i.n; e++) dst[e] = dst[e] + bias[e % n];
+}
+
 template <class T>
 void matmul(const Instr& i, std::vector<Buf>& s, bool ta, bool tb) {
   const Sh &sa = i.args[0].shape, &sb = i.args[1].shape;
@@ -682,8 +693,8 @@ void numeric(const Instr& i, std::vector<Buf>& s) {
   T* dst = s[(size_t)i.dst].as<T>();
   size_t n = (size_t)i.n;
   switch (i.op) {
-    case RG_OP_MATMUL: matmul<T>(i, s, false, false); break;
-    case RG_OP_MATMUL_T: matmul<T>(i, s, i.attr[0] != 0, i.attr[1] != 0); break;
+    case RG_OP_MATMUL: matmul<T>(i, s, false, false); add_bias<T>(i, s); break;
+    case RG_OP_MATMUL_T: matmul<T>(i, s, i.attr[0] != 0, i.attr[1] != 0); add_bias<T>(i, s); break;
     case RG_OP_REDUCE: reduce<T>(i, s); break;
     case RG_OP_TAKE_GRAD: {
       size_t axis = (size_t)i.attr[0];

@@ -1098,15 +1098,96 @@ Plan build_plan(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
   return build_with(g, outputs, reuse, nullptr);
 }
 
+namespace {
+
+std::vector<size_t> step_reads(const Step& st) {
+  std::vector<size_t> r;
+  if (st.attn) {
+    for (auto& v : st.att.in) r.push_back(v.slot);  // outputs are written whole (dq, dk, dv tile theirs)
+    if (st.att.mask_slot >= 0) r.push_back((size_t)st.att.mask_slot);
+    if (st.att.mask_bits_slot >= 0) r.push_back((size_t)st.att.mask_bits_slot);
+    r.push_back(st.att.stats_slot);
+  } else if (st.fused) {
+    for (auto& in : st.group.inputs) r.push_back(in.slot);
+  } else {
+    r = st.instr.args;
+  }
+  return r;
+}
+
+std::vector<size_t> step_writes(const Step& st) {
+  std::vector<size_t> w;
+  if (st.attn) {
+    for (auto& v : st.att.out) w.push_back(v.slot);
+    w.push_back(st.att.stats_slot);
+    if (st.att.mask_bits_slot >= 0) w.push_back((size_t)st.att.mask_bits_slot);
+  } else if (st.fused) {
+    for (auto& o : st.group.outputs) w.push_back(o.second);
+  } else {
+    w.push_back(st.instr.dst);
+  }
+  return w;
+}
+
+// Bias adds folded into products (device plans): a fused group whose only work is adding a
+// per-column vector to the rows of the product just before it, the product's only reader, goes
+// away; the vector becomes the product's third operand (include/rg_plan.h) and the product writes
+// the group's output slot. The sum is the same fp32 addition of the finished product and the bias.
+void fold_bias_into_products(Plan& p) {
+  std::set<size_t> out_slots;
+  for (auto& o : p.outputs) out_slots.insert(o.slot);
+  for (size_t k = 0; k + 1 < p.steps.size(); k++) {
+    Step& M = p.steps[k];
+    const Step& F = p.steps[k + 1];
+    if (M.fused || M.attn || F.attn || !F.fused || F.group.row_len != 0) continue;
+    const Instr& mi = M.instr;
+    if ((mi.op.kind != RG_OP_MATMUL && mi.op.kind != RG_OP_MATMUL_T) || mi.dtype != DType::F32 || mi.args.size() != 2 ||
+        mi.shape.empty() || mi.n == 0)
+      continue;
+    const Fused& f = F.group;
+    const size_t n = (size_t)mi.shape.back();
+    if (f.dtype != DType::F32 || f.n != mi.n || f.ops.size() != 1 || f.ops[0].op.kind != RG_OP_ADD || f.inputs.size() != 2 ||
+        f.outputs.size() != 1 || f.outputs[0].first != f.ops[0].reg)
+      continue;
+    int full = -1, row = -1;
+    for (int j = 0; j < 2; j++) {
+      const FusedIn& in = f.inputs[(size_t)j];
+      if (in.kind == RG_ARG_FULL && in.slot == mi.dst) full = j;
+      else if (in.kind == RG_ARG_ROW && in.row_len == n) row = j;
+    }
+    if (full < 0 || row < 0) continue;
+    const size_t bias = f.inputs[(size_t)row].slot, out = f.outputs[0].second;
+    // The group's output must not be an operand of the product, and the product's value must
+    // have no other reader before its slot is written again.
+    if (out == mi.args[0] || out == mi.args[1] || out == bias || bias == mi.dst || out_slots.count(mi.dst)) continue;
+    bool sole = true;
+    for (size_t j = k + 2; j < p.steps.size() && sole; j++) {
+      auto r = step_reads(p.steps[j]);
+      if (std::find(r.begin(), r.end(), mi.dst) != r.end()) sole = false;
+      auto w = step_writes(p.steps[j]);
+      if (std::find(w.begin(), w.end(), mi.dst) != w.end()) break;
+    }
+    if (!sole) continue;
+    M.instr.args.push_back(bias);
+    M.instr.arg_shapes.push_back(f.input_shapes[(size_t)row]);
+    M.instr.dst = out;
+    p.steps.erase(p.steps.begin() + (std::ptrdiff_t)(k + 1));
+  }
+}
+
+}  // namespace
+
 Plan build_fused(const Graph& g, const std::vector<uint32_t>& outputs, const Fuse& cfg) {
   Plan plan = build_with(g, outputs, true, &cfg);
-  if (!(cfg.device && cfg.levels)) return plan;
-  // Level order cuts dispatch dependencies but keeps values alive longer; keep the cheaper.
-  Fuse greedy_cfg = cfg;
-  greedy_cfg.levels = false;
-  Plan greedy = build_with(g, outputs, true, &greedy_cfg);
-  if (plan.peak_live_bytes > cfg.level_max_peak || greedy.gpu_cost_estimate(cfg) < plan.gpu_cost_estimate(cfg))
-    return greedy;
+  if (cfg.device && cfg.levels) {
+    // Level order cuts dispatch dependencies but keeps values alive longer; keep the cheaper.
+    Fuse greedy_cfg = cfg;
+    greedy_cfg.levels = false;
+    Plan greedy = build_with(g, outputs, true, &greedy_cfg);
+    if (plan.peak_live_bytes > cfg.level_max_peak || greedy.gpu_cost_estimate(cfg) < plan.gpu_cost_estimate(cfg))
+      plan = std::move(greedy);
+  }
+  if (cfg.device) fold_bias_into_products(plan);
   return plan;
 }
 

@@ -140,7 +140,8 @@ template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE, in
 __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                                                            int M, int N, int K, const int64_t* a_off, const int64_t* b_off,
                                                            uint64_t a_stride, uint64_t b_stride, int splits, int k_per_split,
-                                                           float* __restrict__ partial, uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
+                                                           float* __restrict__ partial, const float* __restrict__ bias, uint32_t tiles_m,
+                                                           uint32_t tiles_n, int swizzle) {
   constexpr int NT = 64 * WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / MS, TN = WTN / MS;
   static_assert(TM >= 1 && TN >= 1 && TM <= 4 && TN <= 4 && (TM & (TM - 1)) == 0 && (TN & (TN - 1)) == 0, "wave tiles");
@@ -272,6 +273,31 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
   // or one in each of its TN tiles.
   float* out = splits > 1 ? partial + ((uint64_t)b * splits + sp) * (uint64_t)M * N : C + (uint64_t)b * M * N;
   const bool vec_out = MODE != LOAD_SCALAR && N % 4 == 0;
+  // A per-column bias (unsplit products only) added to the finished sums, as one fp32 addition.
+  if (bias) {
+    if constexpr (BKC) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int n = 0; n < TN; n++)
+#pragma unroll
+          for (int g = 0; g < MF::REGS / 4; g++) {
+            const int col = n0 + wn * WTN + n * MS + 8 * g + q4;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              if (col + r < N) acc[i][n][4 * g + r] += bias[col + r];
+          }
+    } else {
+      const int col = n0 + wn * WTN + TN * li;
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < MF::REGS; r++)
+#pragma unroll
+          for (int n = 0; n < TN; n++)
+            if (col + n < N) acc[i][n][r] += bias[col + n];
+    }
+  }
   if constexpr (BKC) {
 #pragma unroll
     for (int i = 0; i < TM; i++) {
@@ -317,7 +343,8 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
 
 // Sums the K-split partial products in split order. Four outputs per thread (16-byte loads when
 // M N is a multiple of 4), all splits' loads issued before the adds.
-__global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ partial, float* __restrict__ C, uint64_t mn, int splits) {
+__global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ partial, float* __restrict__ C, uint64_t mn, int splits,
+                                                   const float* __restrict__ bias, uint64_t n) {
   const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   const uint32_t b = blockIdx.y;
   if (i >= mn) return;
@@ -332,14 +359,22 @@ __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ par
 #pragma unroll
     for (int s = 1; s < 16; s++)
       if (s < splits) acc = make_float4(acc.x + v[s].x, acc.y + v[s].y, acc.z + v[s].z, acc.w + v[s].w);
+    if (bias) acc = make_float4(acc.x + bias[i % n], acc.y + bias[(i + 1) % n], acc.z + bias[(i + 2) % n], acc.w + bias[(i + 3) % n]);
     *(float4*)(C + (uint64_t)b * mn + i) = acc;
     return;
   }
   for (uint64_t e = i; e < i + 4 && e < mn; e++) {
     float x = partial[(uint64_t)b * splits * mn + e];
     for (int s = 1; s < splits; s++) x += partial[((uint64_t)b * splits + s) * mn + e];
+    if (bias) x += bias[e % n];
     C[(uint64_t)b * mn + e] = x;
   }
+}
+
+// C[e] += bias[e mod n]: the bias of a product that does not run on the matrix cores.
+__global__ void __launch_bounds__(256) k_add_bias(float* __restrict__ C, const float* __restrict__ bias, uint64_t total, uint64_t n) {
+  const uint64_t e = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e < total) C[e] = C[e] + bias[e % n];
 }
 
 // One output element per thread; k ascending.
@@ -408,6 +443,7 @@ struct Launch {
   uint64_t as, bs;
   int splits, kps;
   float* part;
+  const float* bias;
   uint32_t tm, tn;
 };
 
@@ -415,7 +451,8 @@ template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MS>
 void launch_mode(hipStream_t s, int mode, const Launch& l) {
 #define RG_GEMM(MODE_)                                                                                                       \
   hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, TA, TB, MODE_, MS>), l.grid, dim3(64 * WM * WN), 0, s, l.a, l.b, l.c, l.m, l.n, \
-                     l.k, l.a_off, l.b_off, l.as, l.bs, l.splits, l.kps, l.part, l.tm, l.tn, 1)
+                     l.k, l.a_off, l.b_off, l.as, l.bs, l.splits, l.kps, l.part, l.bias, l.tm, \
+                     l.tn, 1)
   if (mode == LOAD_EVEN) RG_GEMM(LOAD_EVEN);
   else if (mode == LOAD_VEC) RG_GEMM(LOAD_VEC);
   else RG_GEMM(LOAD_SCALAR);
@@ -491,11 +528,12 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     l.splits = splits;
     l.kps = kps;
     l.part = splits > 1 ? (float*)g.workspace : nullptr;
+    l.bias = splits > 1 ? nullptr : (const float*)g.bias;
     launch_mfma(s, t, g.ta, g.tb, mode, l);
     if (splits > 1 && !g.defer_split) {
       uint64_t mn = g.m * g.n;
       hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 1023) / 1024), (uint32_t)g.batch), dim3(256), 0, s, (const float*)l.part,
-                         (float*)g.c, mn, splits);
+                         (float*)g.c, mn, splits, (const float*)g.bias, g.n);
     }
     return;
   }
@@ -506,6 +544,10 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   else
     hipLaunchKernelGGL(k_gemm_plain<double>, grid, dim3(256), 0, s, (const double*)g.a, (const double*)g.b, (double*)g.c, (uint32_t)g.m,
                        (uint32_t)g.n, (uint32_t)g.k, g.ta, g.tb, g.a_off, g.b_off, g.a_stride, g.b_stride);
+  if (g.bias && g.dtype == RG_F32) {
+    const uint64_t total = g.m * g.n * g.batch;
+    hipLaunchKernelGGL(k_add_bias, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, (float*)g.c, (const float*)g.bias, total, g.n);
+  }
 }
 
 }  // namespace rgk

@@ -128,6 +128,7 @@ struct GemmArgs {
   void* workspace;              // split-K partial sums, [batch][splits][M N]
   uint64_t workspace_bytes;
   bool defer_split = false;  // leave the partials for fold_wide instead of summing them into C
+  const void* bias = nullptr;  // f32 only: bias[c] added to column c of the finished product
 };
 // Fused attention (attention.hip) over bh = batch * heads independent (tq x hd, tk x hd)
 // problems. Operands are strided views: row t of problem b * heads + h starts at

@@ -190,9 +190,13 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
     }
   }
   if (i.n == 0) return [](hipStream_t, void* const*, void*) {};
+  // A third operand is a bias added to every row of the product (f32 plans only).
+  const int64_t bias = i.args.size() == 3 ? i.args[2].slot : -1;
+  if (bias >= 0 && (dtype != RG_F32 || i.args[2].shape.empty() || (uint64_t)i.args[2].shape.back() != n))
+    throw std::runtime_error("product bias operand does not match the product's columns");
   const int splits = rgk::gemm_splits(dtype, base.m, base.n, base.k, base.batch, tb);
   const uint64_t mn = base.m * base.n;
-  if (splits > 1 && base.batch == 1 && mn % 4 == 0 && mn < (1ull << 32)) {
+  if (splits > 1 && base.batch == 1 && mn % 4 == 0 && mn < (1ull << 32) && bias < 0) {
     // K-split partials go to the fold area; their sum joins the deferred folds (fold_wide).
     const uint64_t off = prog.fold_bytes;
     Program::Fold fd{off, dst, (uint32_t)splits, (uint32_t)mn, RG_REDUCE_SUM, dtype};
@@ -213,11 +217,12 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
   uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch, tb);
   prog.workspace_bytes = std::max(prog.workspace_bytes, ws);
   base.workspace_bytes = ws;
-  return [base, as, bs, dst](hipStream_t s, void* const* sl, void* wsp) {
+  return [base, as, bs, dst, bias](hipStream_t s, void* const* sl, void* wsp) {
     rgk::GemmArgs g = base;
     g.a = sl[as];
     g.b = sl[bs];
     g.c = sl[dst];
+    g.bias = bias >= 0 ? sl[bias] : nullptr;
     g.workspace = wsp;
     rgk::gemm(s, g);
   };

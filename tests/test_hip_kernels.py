@@ -180,6 +180,24 @@ def test_mfma_products_with_transpose_flags(m, k, n, ta, tb):
     close(hip, want, 1e-4, f"gemm {m}x{k}x{n} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("m,k,n,ta", [(8192, 256, 768, False), (256, 8192, 768, True), (1024, 8192, 256, True), (33, 17, 65, False),
+                                      (3, 5, 7, False), (300, 70, 132, True)])
+def test_products_with_a_bias_operand(m, k, n, ta):
+    """A bias add folded into the product before it: added in the MFMA kernel's epilogue, after
+    the split-K sum for split products, or by a separate pass for products off the matrix cores."""
+    rng = np.random.default_rng(m + 3 * k + 7 * n)
+    a = rng.normal(size=(k, m) if ta else (m, k)).astype(np.float32)
+    w = rng.normal(size=(k, n)).astype(np.float32)
+    b = rng.normal(size=(n,)).astype(np.float32)
+
+    def build(g, i):
+        x = _swap(g, i[0], 2) if ta else i[0]
+        return op(g, "add", [op(g, "matmul", [x, i[1]]), op(g, "broadcast_to", [i[2]], shape=[m, n])])
+    hip = run_graph("hip", build, [t(a), t(w), t(b)], optimize="standard")[0]
+    want = (a.T if ta else a).astype(np.float64) @ w.astype(np.float64) + b.astype(np.float64)
+    close(hip, want, 1e-4, f"biased product {m}x{k}x{n} ta={ta}")
+
+
 def test_split_products_feed_later_steps():
     """K-split products whose partial sums are folded later, just before the first step that
     reads the product: an elementwise group, another product and a program output."""

@@ -123,3 +123,26 @@ def test_layer_norm_backward_recomputes_the_forward_rows(shape):
     b2 = g.eval(outs, inputs, device="cpu", optimize="standard")
     for k, (u, v) in enumerate(zip(a, b2)):
         np.testing.assert_allclose(u, v, rtol=1e-5, atol=1e-5 * np.abs(v).max(), err_msg=f"output {k}")
+
+
+@pytest.mark.parametrize("m,k,n,ta", [(64, 32, 48, False), (40, 24, 16, True)])
+def test_bias_adds_fold_into_the_product(m, k, n, ta):
+    """A group that only adds a bias vector to the rows of the product before it (its only reader)
+    becomes the product's third operand in device plans; the oracle adds it to the finished
+    product, so results equal the CPU plan's exactly."""
+    r = np.random.default_rng(m + k + n)
+    av = r.normal(size=(k, m) if ta else (m, k)).astype(np.float32)
+    wv = r.normal(size=(k, n)).astype(np.float32)
+    bv = r.normal(size=(n,)).astype(np.float32)
+    g = G()
+    a, w, b = g.input(av.shape, "float32"), g.input(wv.shape, "float32"), g.input(bv.shape, "float32")
+    x = g.op("transpose", [a], perm=[1, 0]) if ta else a
+    y = g.bin("add", g.op("matmul", [x, w]), g.op("broadcast_to", [b], shape=[m, n]))
+    outs, inputs = [y], [av, wv, bv]
+    dev, _ = _plans(g, outs, inputs)
+    steps = dev.plan_summary()
+    prods = [st for st in steps if st["kind"] == "instr" and st["op"] in ("matmul", "matmul_t")]
+    assert len(prods) == 1 and len(prods[0]["args"]) == 3, steps
+    got = g.eval(outs, inputs, device=DEVPLAN, optimize="standard")[0]
+    want = g.eval(outs, inputs, device="cpu", optimize="standard")[0]
+    np.testing.assert_array_equal(got, want)
