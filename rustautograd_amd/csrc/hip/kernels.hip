@@ -221,28 +221,31 @@ __global__ void __launch_bounds__(TPB) k_take_grad(const T* __restrict__ ct, con
     for (uint32_t x = lo; x < hi; x++) c += clamp_index(idx[j0 + x], dim) == d;
     counts[threadIdx.x] = c;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t run = 0;
-      for (int t = 0; t < TPB; t++) {
-        uint32_t v = counts[t];
-        counts[t] = run;
-        run += v;
-      }
+    // Inclusive prefix sum of the counts (log2(TPB) steps), so each thread's matches land in
+    // increasing index order.
+    for (uint32_t off = 1; off < TPB; off <<= 1) {
+      const uint32_t v = threadIdx.x >= off ? counts[threadIdx.x - off] : 0u;
+      __syncthreads();
+      counts[threadIdx.x] += v;
+      __syncthreads();
     }
-    __syncthreads();
-    uint32_t at = counts[threadIdx.x];
+    uint32_t at = counts[threadIdx.x] - c;
+    const uint32_t len = counts[TPB - 1];
     for (uint32_t x = lo; x < hi; x++)
       if (clamp_index(idx[j0 + x], dim) == d) list[at++] = j0 + x;
     __syncthreads();
-    const uint32_t total = (threadIdx.x == TPB - 1) ? at : 0;
-    if (threadIdx.x == TPB - 1) counts[0] = at;  // last thread's end is the list length
-    __syncthreads();
-    const uint32_t len = counts[0];
-    (void)total;
     if (q < block) {
+      // Eight rows' loads in flight, added in list order.
       const T* base = ct + (uint64_t)o * n_idx * block + q;
-#pragma unroll 4
-      for (uint32_t e = 0; e < len; e++) acc = acc + base[(uint64_t)list[e] * block];
+      uint32_t e = 0;
+      for (; e + 8 <= len; e += 8) {
+        T v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = base[(uint64_t)list[e + u] * block];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = acc + v[u];
+      }
+      for (; e < len; e++) acc = acc + base[(uint64_t)list[e] * block];
     }
     __syncthreads();
   }
