@@ -296,3 +296,67 @@ def test_scatter_add_at_embedding_shapes_is_bit_exact():
     ct2 = t(rng.normal(size=(3, 9000, 5)).astype(np.float32))
     idx2 = t(rng.integers(-3, 12, size=(9000,)), "int32")
     agree(lambda g, i: op(g, "take_grad", [i[0], i[1]], axis=1, shape=[3, 10, 5]), [ct2, idx2], ulps=0)
+
+
+I32_MIN, I32_MAX = -2 ** 31, 2 ** 31 - 1
+INT_PAIRS = [(I32_MAX, 1), (I32_MIN, -1), (65536, 65536), (46341, 46341), (I32_MIN, I32_MIN), (I32_MAX, I32_MAX),
+             (I32_MIN, 1), (-1, I32_MIN), (0, I32_MIN), (123456789, -987654321), (-7, 3), (I32_MAX, I32_MIN)]
+
+
+def _wrap32(v):
+    v &= 0xFFFFFFFF
+    return v - 2 ** 32 if v >= 2 ** 31 else v
+
+
+INT_RULES = {"add": lambda a, b: _wrap32(a + b), "sub": lambda a, b: _wrap32(a - b), "mul": lambda a, b: _wrap32(a * b),
+             "gt": lambda a, b: int(a > b), "ge": lambda a, b: int(a >= b)}
+
+
+@pytest.mark.parametrize("name", sorted(INT_RULES))
+def test_int32_ops_wrap_and_compare_bit_exactly(name):
+    """int32 add/sub/mul wrap modulo 2^32 and comparisons hold at the bounds (src/plan.rs:1272-1287),
+    in every broadcast mode; checked against the oracle and against the closed form."""
+    a = t([p[0] for p in INT_PAIRS], "int32")
+    b = t([p[1] for p in INT_PAIRS], "int32")
+    hip, _ = agree(lambda g, i: op(g, name, [i[0], i[1]]), [a, b], what=name)
+    assert hip[0].tolist() == [INT_RULES[name](x, y) for x, y in INT_PAIRS]
+    s = t(I32_MAX, "int32")
+    hip, _ = agree(lambda g, i: op(g, name, [i[0], i[1]]), [s, b], what=f"{name} scalar lhs")
+    assert hip[0].tolist() == [INT_RULES[name](I32_MAX, y) for _, y in INT_PAIRS]
+    hip, _ = agree(lambda g, i: op(g, name, [i[0], i[1]]), [a, s], what=f"{name} scalar rhs")
+    assert hip[0].tolist() == [INT_RULES[name](x, I32_MAX) for x, _ in INT_PAIRS]
+    col = t(np.array([p[0] for p in INT_PAIRS], dtype=np.int32).reshape(12, 1), "int32")
+    row = t(np.array([p[1] for p in INT_PAIRS], dtype=np.int32).reshape(1, 12), "int32")
+    hip, _ = agree(lambda g, i: op(g, name, [i[0], i[1]]), [col, row], what=f"{name} general broadcast")
+    assert hip[0].tolist() == [[INT_RULES[name](x, y) for _, y in INT_PAIRS] for x, _ in INT_PAIRS]
+
+
+def _sweep(lo, hi, n, seed):
+    rng = np.random.default_rng(seed)
+    return np.concatenate([np.linspace(lo, hi, n // 2), rng.uniform(lo, hi, n - n // 2)]).astype(np.float32)
+
+
+WIDE = {
+    "exp": np.concatenate([_sweep(-104.0, 89.0, 4096, 1), np.float32([-87.33655, 88.72283, 88.72284, -103.97208])]),
+    "log": np.concatenate([_sweep(1e-6, 1e6, 4096, 2), np.float32([1e-45, 1e-40, 1.17549435e-38, 3.4028235e38])]),
+    "sin": np.concatenate([_sweep(-1e4, 1e4, 4096, 3), np.float32([1e5, -1e6, 1e-30, 3.1415927])]),
+    "cos": np.concatenate([_sweep(-1e4, 1e4, 4096, 4), np.float32([1e5, -1e6, 1e-30, 1.5707964])]),
+    "tanh": np.concatenate([_sweep(-12.0, 12.0, 4096, 5), np.float32([-10.0, 10.0, 9.01, -9.01, 1e-20])]),
+    "sqrt": np.concatenate([_sweep(0.0, 1e30, 4096, 6), np.float32([1e-45, 1e-40, 3.4028235e38])]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(WIDE))
+def test_fp32_unary_ops_over_wide_ranges_within_two_ulp(name):
+    """Near overflow and underflow of exp, large arguments of sin and cos, saturation of tanh, the
+    subnormal and huge ends of log and sqrt: the device's math stays within 2 ulp of glibc."""
+    agree(lambda g, i: op(g, name, [i[0]]), [t(WIDE[name])], what=f"wide {name}", ulps=2)
+    # The same values through a fused group (the JIT path) rather than the single-op kernel.
+    agree(lambda g, i: op(g, "add", [op(g, name, [i[0]]), i[1]]), [t(WIDE[name]), t(0.0)], what=f"wide fused {name}", ulps=2)
+
+
+def test_fp32_pow_over_wide_ranges_within_two_ulp():
+    rng = np.random.default_rng(7)
+    base = np.concatenate([rng.uniform(0.0, 4.0, 3000), rng.uniform(-3.0, 0.0, 500).round(), np.float32([2.0, 10.0, 0.5, 1.0001])])
+    expo = np.concatenate([rng.uniform(-40.0, 40.0, 3000), rng.integers(-9, 10, 500).astype(np.float64), np.float32([127.0, 38.0, 149.0, 80000.0])])
+    agree(lambda g, i: op(g, "pow", [i[0], i[1]]), [t(base.astype(np.float32)), t(expo.astype(np.float32))], what="wide pow", ulps=2)
