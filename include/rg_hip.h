@@ -69,6 +69,11 @@ void rg_hip_program_free(void* program);
 uint64_t rg_hip_program_allocated_bytes(void* program);
 /* metal.rs:525-529 `inject_failure_for_test()`: the next step fails as a device error would. */
 void rg_hip_program_inject_failure(void* program);
+/* Test hook next to `inject_failure_for_test` (metal.rs:525-529), with no reference counterpart:
+ * the next `steps` plan passes complete and the one after fails, as a device error would, so a
+ * test can check what a failure in the middle of a run hands back. The failure is latched on the
+ * host side; no device fault is involved. */
+void rg_hip_program_inject_failure_after(void* program, int64_t steps);
 
 /* metal.rs:505-523 `MetalProgram::exec`: a frame from the pool, or a new zeroed one with the
  * constants written. */
@@ -79,11 +84,18 @@ void rg_hip_exec_free(void* exec);
 int rg_hip_exec_write(void* exec, int64_t slot, const void* src, uint64_t bytes);
 /* `Exec::prefix` (plan.rs:35): the first bytes of a slot back to the host. */
 int rg_hip_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes);
+/* `Exec::load` for many slots at once (run_loop's state load, validate.rs:290-292): every copy is
+ * enqueued, then one wait. Returns 0, or -1 for a bad slot or size (nothing copied) or a failure. */
+int rg_hip_exec_write_slots(void* exec, int64_t n, const int64_t* slots, const void* const* srcs, const uint64_t* bytes);
+/* `Exec::prefix` for many slots at once (run_loop's final state read, validate.rs:361): every
+ * copy is enqueued, then one wait. Returns as rg_hip_exec_write_slots. */
+int rg_hip_exec_read_slots(void* exec, int64_t n, const int64_t* slots, void* const* dsts, const uint64_t* bytes);
 /* `Exec::scalar` (plan.rs:37): element 0 of a slot as a double. */
 double rg_hip_exec_scalar(void* exec, int64_t slot);
 /* `Exec::swap` (plan.rs:34): exchanges the buffers behind two slots. */
 void rg_hip_exec_swap(void* exec, int64_t a, int64_t b);
-/* `Exec::step` (plan.rs:32): runs every plan step once and waits for the device. */
+/* `Exec::step` (plan.rs:32): runs every plan step once and waits for the device (synchronous:
+ * a failure is visible to rg_hip_exec_failure when it returns). */
 void rg_hip_exec_step(void* exec);
 /* Runs plan steps [begin, end) and waits: what the instrumented check needs between steps. */
 void rg_hip_exec_steps(void* exec, int64_t begin, int64_t end);
@@ -101,7 +113,11 @@ int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, in
 /* The device-resident `run_loop` (validate.rs:289-363): steps captured in HIP graphs and
  * replayed, batches and history kept on the device, state handed off by buffer swaps and
  * copies. Semantics equal the host loop: a non-finite history value stops the run after that
- * step's state handoff. Returns 0, or -1 when the device failed (see rg_hip_exec_failure). */
+ * step's state handoff. Returns 0, or -1 when the device failed (see rg_hip_exec_failure); the
+ * state slots then hold the state after `out->done` steps, as in the host loop. The captured
+ * graphs and the loop's device buffers stay with the frame and are reused by the next run with
+ * the same description. `out->seconds` is the step loop alone (validate.rs:264-265): batch
+ * upload and graph capture are excluded. */
 int rg_hip_exec_run(void* exec, const rg_run_desc* desc, rg_run_result* out);
 
 #ifdef __cplusplus

@@ -244,7 +244,7 @@ struct Program {
   std::vector<uint8_t> blob;
   std::mutex mu;
   std::vector<Frame> pool;
-  bool inject = false;
+  int64_t fail_in = -1;  // test hook: the step pass that fails next (0: the next one), or -1
   uint64_t allocated = 0;
 };
 
@@ -1034,7 +1034,9 @@ uint64_t rg_cpu_program_allocated_bytes(void* program) {
   return p->allocated;
 }
 
-void rg_cpu_program_inject_failure(void* program) { ((Program*)program)->inject = true; }
+void rg_cpu_program_inject_failure(void* program) { ((Program*)program)->fail_in = 0; }
+
+void rg_cpu_program_inject_failure_after(void* program, int64_t steps) { ((Program*)program)->fail_in = steps < 0 ? 0 : steps; }
 
 void* rg_cpu_exec_new(void* program, char* err, size_t err_len) {
   auto* p = (Program*)program;
@@ -1083,6 +1085,18 @@ int rg_cpu_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes) {
   return 0;
 }
 
+int rg_cpu_exec_write_slots(void* exec, int64_t n, const int64_t* slots, const void* const* srcs, const uint64_t* bytes) {
+  for (int64_t k = 0; k < n; k++)
+    if (rg_cpu_exec_write(exec, slots[k], srcs[k], bytes[k]) != 0) return -1;
+  return 0;
+}
+
+int rg_cpu_exec_read_slots(void* exec, int64_t n, const int64_t* slots, void* const* dsts, const uint64_t* bytes) {
+  for (int64_t k = 0; k < n; k++)
+    if (rg_cpu_exec_read(exec, slots[k], dsts[k], bytes[k]) != 0) return -1;
+  return 0;
+}
+
 double rg_cpu_exec_scalar(void* exec, int64_t slot) {
   auto* e = (Exec*)exec;
   auto& b = e->frame.slots[(size_t)slot];
@@ -1098,11 +1112,12 @@ void rg_cpu_exec_swap(void* exec, int64_t a, int64_t b) {
 void rg_cpu_exec_steps(void* exec, int64_t begin, int64_t end) {
   auto* e = (Exec*)exec;
   if (!e->failure.empty()) return;
-  if (e->prog->inject) {
-    e->prog->inject = false;
+  if (e->prog->fail_in == 0) {
+    e->prog->fail_in = -1;
     e->failure = "injected failure";
     return;
   }
+  if (e->prog->fail_in > 0) e->prog->fail_in--;
   for (int64_t k = begin; k < end; k++) exec_step(e->prog, e->frame, (size_t)k);
 }
 

@@ -922,7 +922,7 @@ def run(compiled, state, data=None, steps=1, callback=None, every=None):
         else:
             offset = done % len(batches) if batches else 0
             part = batches[offset:] + batches[:offset]
-        new_state, outputs, hist, ran, bad, seconds = compiled._n.run(state_map, data_inputs, scalar, current, part, n)
+        new_state, outputs, hist, ran, bad, seconds = compiled._n.run(state_map, data_inputs, scalar, current, part, n, True)
         last = (current, part, ran, done)
         for k, h in zip(scalar, hist):
             history[names_of[k]].extend(h)

@@ -37,10 +37,13 @@ void register_backend(const std::string& name, const std::string& path, const st
   bind(*b, b->program_free, "program_free", true);
   bind(*b, b->program_allocated_bytes, "program_allocated_bytes", true);
   bind(*b, b->program_inject_failure, "program_inject_failure", true);
+  bind(*b, b->program_inject_failure_after, "program_inject_failure_after", false);
   bind(*b, b->exec_new, "exec_new", true);
   bind(*b, b->exec_free, "exec_free", true);
   bind(*b, b->exec_write, "exec_write", true);
   bind(*b, b->exec_read, "exec_read", true);
+  bind(*b, b->exec_write_slots, "exec_write_slots", false);
+  bind(*b, b->exec_read_slots, "exec_read_slots", false);
   bind(*b, b->exec_scalar, "exec_scalar", true);
   bind(*b, b->exec_swap, "exec_swap", true);
   bind(*b, b->exec_step, "exec_step", true);
@@ -99,6 +102,50 @@ std::unique_ptr<DeviceExec> DeviceProgram::exec() const {
   void* e = b_->exec_new(p_, err, sizeof err);
   if (!e) throw std::runtime_error(err[0] ? err : "device frame allocation failed");
   return std::make_unique<DeviceExec>(b_, e, plan_);
+}
+
+void DeviceProgram::inject_failure(int64_t after) const {
+  if (after > 0 && !b_->program_inject_failure_after) throw std::runtime_error(b_->name + " cannot delay an injected failure");
+  if (after > 0) b_->program_inject_failure_after(p_, after);
+  else b_->program_inject_failure(p_);
+}
+
+void DeviceExec::load_all(const std::vector<std::pair<size_t, const Tensor*>>& inputs) {
+  if (!b_->exec_write_slots) {
+    for (auto& [k, t] : inputs) load(k, *t);
+    return;
+  }
+  std::vector<int64_t> slots;
+  std::vector<const void*> srcs;
+  std::vector<uint64_t> bytes;
+  for (auto& [k, t] : inputs) {
+    size_t slot = plan_->input_slots[k];
+    slots.push_back((int64_t)slot);
+    srcs.push_back(t->data.data());
+    bytes.push_back(std::min<uint64_t>(plan_->input_ns[k] * dsize(plan_->slots[slot].first), t->data.size()));
+  }
+  b_->exec_write_slots(e_, (int64_t)slots.size(), slots.data(), srcs.data(), bytes.data());
+}
+
+std::vector<Tensor> DeviceExec::prefix_all(const std::vector<std::tuple<size_t, size_t, Shape>>& reads) const {
+  std::vector<Tensor> out(reads.size());
+  std::vector<int64_t> slots;
+  std::vector<void*> dsts;
+  std::vector<uint64_t> bytes;
+  for (size_t q = 0; q < reads.size(); q++) {
+    auto& [slot, n, shape] = reads[q];
+    out[q].shape = shape;
+    out[q].dtype = plan_->slots[slot].first;
+    out[q].data.resize(n * dsize(out[q].dtype));
+    slots.push_back((int64_t)slot);
+    dsts.push_back(out[q].data.data());
+    bytes.push_back(out[q].data.size());
+  }
+  if (b_->exec_read_slots) b_->exec_read_slots(e_, (int64_t)slots.size(), slots.data(), dsts.data(), bytes.data());
+  else
+    for (size_t q = 0; q < reads.size(); q++)
+      if (bytes[q]) b_->exec_read(e_, slots[q], dsts[q], bytes[q]);
+  return out;
 }
 
 void DeviceExec::load(size_t k, const Tensor& t) {

@@ -23,10 +23,13 @@ struct Backend {
   void (*program_free)(void*) = nullptr;
   uint64_t (*program_allocated_bytes)(void*) = nullptr;
   void (*program_inject_failure)(void*) = nullptr;
+  void (*program_inject_failure_after)(void*, int64_t) = nullptr;  // optional
   void* (*exec_new)(void*, char*, size_t) = nullptr;
   void (*exec_free)(void*) = nullptr;
   int (*exec_write)(void*, int64_t, const void*, uint64_t) = nullptr;
   int (*exec_read)(void*, int64_t, void*, uint64_t) = nullptr;
+  int (*exec_write_slots)(void*, int64_t, const int64_t*, const void* const*, const uint64_t*) = nullptr;  // optional
+  int (*exec_read_slots)(void*, int64_t, const int64_t*, void* const*, const uint64_t*) = nullptr;        // optional
   double (*exec_scalar)(void*, int64_t) = nullptr;
   void (*exec_swap)(void*, int64_t, int64_t) = nullptr;
   void (*exec_step)(void*) = nullptr;
@@ -59,6 +62,9 @@ class DeviceProgram {
   void* handle() const { return p_; }
   const Plan& plan() const { return *plan_; }
   std::unique_ptr<DeviceExec> exec() const;  // throws std::runtime_error
+  // Test hooks (metal.rs:385-388, 525-529): device bytes held, and a failure after `after` passes.
+  uint64_t allocated_bytes() const { return b_->program_allocated_bytes(p_); }
+  void inject_failure(int64_t after) const;
  private:
   Backend* b_;
   void* p_ = nullptr;
@@ -71,10 +77,14 @@ class DeviceExec {
   DeviceExec(Backend* b, void* e, const Plan* plan) : b_(b), e_(e), plan_(plan) {}
   ~DeviceExec() { b_->exec_free(e_); }
   void load(size_t k, const Tensor& t);
+  // `load` of several inputs (index, tensor), enqueued together with one wait.
+  void load_all(const std::vector<std::pair<size_t, const Tensor*>>& inputs);
   void step() { b_->exec_step(e_); }
   void steps(size_t begin, size_t end) { b_->exec_steps(e_, (int64_t)begin, (int64_t)end); }
   void swap(size_t a, size_t c) { b_->exec_swap(e_, (int64_t)a, (int64_t)c); }
   Tensor prefix(size_t slot, size_t n, const Shape& shape) const;
+  // `prefix` of several (slot, n, shape) at once, with one wait.
+  std::vector<Tensor> prefix_all(const std::vector<std::tuple<size_t, size_t, Shape>>& reads) const;
   void write_prefix(size_t slot, const Tensor& t);
   double scalar(size_t slot) const { return b_->exec_scalar(e_, (int64_t)slot); }
   std::optional<std::string> failure() const;

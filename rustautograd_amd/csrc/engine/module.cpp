@@ -381,11 +381,13 @@ PYBIND11_MODULE(_rg, m) {
              py::gil_scoped_release nogil;
              return c.c->profile(in, repeats).dump();
            })
+      .def("allocated_bytes", [](const PyCompiled& c) { return c.c->program->allocated_bytes(); })
+      .def("inject_failure", [](const PyCompiled& c, int64_t after) { c.c->program->inject_failure(after); }, py::arg("after") = 0)
       .def("run",
            [](const PyCompiled& c, const std::vector<std::pair<size_t, size_t>>& state_map, const std::vector<size_t>& data_inputs,
               const std::vector<size_t>& history, const std::vector<PyTensor>& state,
-              const std::vector<std::vector<PyTensor>>& batches, size_t steps) {
-             RunSpec spec{state_map, data_inputs, history};
+              const std::vector<std::vector<PyTensor>>& batches, size_t steps, bool skip_state_outputs) {
+             RunSpec spec{state_map, data_inputs, history, skip_state_outputs};
              c.c->validate_spec(spec);
              auto st = tensors(state);
              std::vector<std::vector<Tensor>> bs;
@@ -403,7 +405,9 @@ PYBIND11_MODULE(_rg, m) {
              std::optional<size_t> bad;
              if (out.nonfinite_step >= 0) bad = (size_t)out.nonfinite_step;
              return py::make_tuple(wrap(out.state), wrap(out.outputs), out.history, out.steps, bad, out.seconds);
-           })
+           },
+           py::arg("state_map"), py::arg("data_inputs"), py::arg("history"), py::arg("state"), py::arg("batches"), py::arg("steps"),
+           py::arg("skip_state_outputs") = false)
       .def("replay",
            [](const PyCompiled& c, const std::vector<std::pair<size_t, size_t>>& state_map, const std::vector<size_t>& data_inputs,
               const std::vector<size_t>& history, const std::vector<PyTensor>& state,

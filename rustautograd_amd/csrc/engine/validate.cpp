@@ -778,11 +778,34 @@ RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, cons
     return r;
   }
   const Plan& p = plan;
-  for (size_t k = 0; k < spec.state.size() && k < state.size(); k++) e->load(spec.state[k].first, state[k]);
   auto load_batch = [&](const std::vector<Tensor>& b) {
     for (size_t k = 0; k < spec.data.size() && k < b.size(); k++) e->load(spec.data[k], b[k]);
   };
-  if (batches.size() == 1) load_batch(batches[0]);
+  {
+    // The state (and a single batch) go over together, with one wait.
+    std::vector<std::pair<size_t, const Tensor*>> first;
+    for (size_t k = 0; k < spec.state.size() && k < state.size(); k++) first.push_back({spec.state[k].first, &state[k]});
+    if (batches.size() == 1)
+      for (size_t k = 0; k < spec.data.size() && k < batches[0].size(); k++) first.push_back({spec.data[k], &batches[0][k]});
+    e->load_all(first);
+  }
+  std::vector<bool> feeds_state(p.outputs.size(), false);
+  if (spec.skip_state_outputs)
+    for (auto& [i, o] : spec.state) feeds_state[o] = true;
+  auto read_outputs = [&](auto slot_of) {
+    std::vector<std::tuple<size_t, size_t, Shape>> reads;
+    std::vector<size_t> at;
+    r.outputs.assign(p.outputs.size(), Tensor{});
+    for (size_t q = 0; q < p.outputs.size(); q++) {
+      r.outputs[q].shape = p.outputs[q].shape;
+      r.outputs[q].dtype = p.slots[p.outputs[q].slot].first;
+      if (feeds_state[q]) continue;
+      reads.push_back({slot_of(p.outputs[q].slot), p.outputs[q].n, p.outputs[q].shape});
+      at.push_back(q);
+    }
+    auto got = e->prefix_all(reads);
+    for (size_t j = 0; j < at.size(); j++) r.outputs[at[j]] = std::move(got[j]);
+  };
   // State moves by swapping buffers when the output's slot is private and the same size.
   std::vector<size_t> out_slots;
   for (auto& [i, o] : spec.state) out_slots.push_back(p.outputs[o].slot);
@@ -854,17 +877,16 @@ RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, cons
       auto f = e->failure();
       r.device_error = f ? *f : std::string("device loop failed");
     }
-    bool read_outputs = !r.device_error && r.steps > 0 && (r.steps == steps || r.nonfinite_step >= 0);
-    if (read_outputs) {
+    bool want_outputs = !r.device_error && r.steps > 0 && (r.steps == steps || r.nonfinite_step >= 0);
+    if (want_outputs) {
       // After the handoff a swapped slot's pre-handoff value sits in its partner.
-      for (auto& o : p.outputs) {
-        size_t s = o.slot;
+      read_outputs([&](size_t s) {
         for (auto& [a, b] : swaps) {
-          if (s == b) { s = a; break; }
-          if (s == a) { s = b; break; }
+          if (s == b) return a;
+          if (s == a) return b;
         }
-        r.outputs.push_back(e->prefix(s, o.n, o.shape));
-      }
+        return s;
+      });
     }
   } else {
     auto started = Clock::now();
@@ -883,10 +905,7 @@ RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, cons
         r.history[h].push_back(v);
       }
       if (bad) r.nonfinite_step = (int64_t)k;
-      if (k + 1 == steps || bad) {
-        r.outputs.clear();
-        for (auto& o : p.outputs) r.outputs.push_back(e->prefix(o.slot, o.n, o.shape));
-      }
+      if (k + 1 == steps || bad) read_outputs([](size_t s) { return s; });
       std::vector<std::pair<size_t, Tensor>> temp;
       for (auto& [is, os, n] : copies) temp.push_back({is, e->prefix(os, n, {n})});
       for (auto& [is, os] : swaps) e->swap(is, os);
@@ -895,8 +914,9 @@ RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, cons
     }
     r.seconds = since(started);
   }
-  for (auto& [i, o] : spec.state)
-    r.state.push_back(e->prefix(p.input_slots[i], p.input_ns[i], p.outputs[o].shape));
+  std::vector<std::tuple<size_t, size_t, Shape>> reads;
+  for (auto& [i, o] : spec.state) reads.push_back({p.input_slots[i], p.input_ns[i], p.outputs[o].shape});
+  r.state = e->prefix_all(reads);
   return r;
 }
 

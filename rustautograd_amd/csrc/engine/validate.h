@@ -15,6 +15,9 @@ struct RunSpec {
   std::vector<std::pair<size_t, size_t>> state;  // (input index, output index) fed back
   std::vector<size_t> data;                      // data input indices
   std::vector<size_t> history;                   // scalar outputs recorded per step
+  // Outputs fed back into the state hold the same values as the final state: when set, `run`
+  // does not read them a second time and leaves them empty (shape kept, no data).
+  bool skip_state_outputs = false;
 };
 
 struct RunOut {

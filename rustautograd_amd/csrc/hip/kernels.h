@@ -108,6 +108,8 @@ void copy_bytes(hipStream_t s, void* dst, const void* src, uint64_t bytes);
 void record_history(hipStream_t s, int dtype, const void* slot, double* hist, const uint64_t* counter, uint64_t stride);
 void load_batch(hipStream_t s, void* dst, const void* batches, uint64_t bytes, uint64_t n_batches, const uint64_t* counter);
 void counter_inc(hipStream_t s, uint64_t* counter);
+// Sets the step counter with a one-thread kernel (no memset node where a caller may capture).
+void set_counter(hipStream_t s, uint64_t* counter, uint64_t value);
 // Keeps stream `s` busy for about `microseconds` (a bounded wait on the device wall clock).
 void hold_stream(hipStream_t s, double microseconds);
 void fill_zero(hipStream_t s, void* dst, uint64_t bytes);

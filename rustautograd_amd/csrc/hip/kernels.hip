@@ -575,6 +575,8 @@ __global__ void __launch_bounds__(TPB) k_load_batch(uint32_t* __restrict__ dst, 
 
 __global__ void k_counter_inc(uint64_t* counter) { *counter += 1; }
 
+__global__ void k_set_counter(uint64_t* counter, uint64_t value) { *counter = value; }
+
 // One thread waits until `ticks` of the constant-rate wall clock have passed: a bounded wait
 // that every launch leaves, used to hold a stream while the host enqueues timed work.
 __global__ void k_hold(uint64_t ticks) {
@@ -960,6 +962,8 @@ void load_batch(hipStream_t s, void* dst, const void* batches, uint64_t bytes, u
 }
 
 void counter_inc(hipStream_t s, uint64_t* counter) { hipLaunchKernelGGL(k_counter_inc, dim3(1), dim3(1), 0, s, counter); }
+
+void set_counter(hipStream_t s, uint64_t* counter, uint64_t value) { hipLaunchKernelGGL(k_set_counter, dim3(1), dim3(1), 0, s, counter, value); }
 
 void hold_stream(hipStream_t s, double microseconds) {
   static uint64_t khz = [] {

@@ -47,12 +47,49 @@ uint64_t prod(const std::vector<int64_t>& s) {
 // One launch of a plan step: (stream, slot pointer table, workspace).
 using StepFn = std::function<void(hipStream_t, void* const*, void*)>;
 
+// Device buffers and captured graphs of the step loop (rg_hip_exec_run), kept on the frame so
+// that a later run with the same description only uploads its batches and resets the counter.
+// `key` is the description (slot lists, sizes, batch count, chunk); `table` the two slot tables
+// the state handoff alternates between, each with its graph.
+struct RunCache {
+  std::vector<int64_t> key;
+  std::vector<void*> table[2];
+  int n_graphs = 0;
+  uint64_t chunk = 0;
+  void* mem = nullptr;  // one allocation holding everything below
+  uint64_t mem_bytes = 0;
+  uint64_t* counter = nullptr;
+  double* hist = nullptr;
+  std::vector<void*> batch_bufs, temps, snap;
+  std::vector<int64_t> state_slots;
+  std::vector<hipGraph_t> graphs;
+  std::vector<hipGraphExec_t> execs;
+  void clear_graphs() {
+    for (auto g : execs) hipGraphExecDestroy(g);
+    for (auto g : graphs) hipGraphDestroy(g);
+    execs.clear();
+    graphs.clear();
+  }
+  void release() {
+    clear_graphs();
+    if (mem) hipFree(mem);
+    mem = nullptr;
+    mem_bytes = 0;
+    key.clear();
+    batch_bufs.clear();
+    temps.clear();
+    snap.clear();
+    state_slots.clear();
+  }
+};
+
 struct Frame {
   void* arena = nullptr;
   uint64_t bytes = 0;
   std::vector<void*> slot;
   void* workspace = nullptr;
   hipStream_t stream = nullptr;
+  RunCache run;
 };
 
 struct Program {
@@ -89,10 +126,12 @@ struct Program {
   std::vector<uint64_t> slot_bytes;
   std::mutex mu;
   std::vector<Frame*> pool;
-  std::atomic<bool> inject{false};
+  // Test hook: the plan step pass that fails next, counted from now (0: the next one), or -1.
+  std::atomic<int64_t> fail_in{-1};
   int device = 0;
   ~Program() {
     for (auto* f : pool) {
+      f->run.release();
       hipStreamDestroy(f->stream);
       hipFree(f->arena);
       delete f;
@@ -798,9 +837,17 @@ void enqueue_list(const Program& p, hipStream_t s, void* const* slots, void* ws,
   }
 }
 
+// Consumes one pass of the failure countdown: true when this pass is the one that fails.
+bool injected_now(Program* p) {
+  int64_t f = p->fail_in.load();
+  while (f >= 0 && !p->fail_in.compare_exchange_weak(f, f - 1)) {
+  }
+  return f == 0;
+}
+
 void run_steps(Exec* e, size_t begin, size_t end) {
   if (!e->failure.empty()) return;
-  if (e->prog->inject.exchange(false)) {
+  if (injected_now(e->prog)) {
     e->failure = "injected failure";
     return;
   }
@@ -904,7 +951,9 @@ uint64_t rg_hip_program_allocated_bytes(void* program) {
   return total - free_b;
 }
 
-void rg_hip_program_inject_failure(void* program) { ((Program*)program)->inject = true; }
+void rg_hip_program_inject_failure(void* program) { ((Program*)program)->fail_in = 0; }
+
+void rg_hip_program_inject_failure_after(void* program, int64_t steps) { ((Program*)program)->fail_in = std::max<int64_t>(steps, 0); }
 
 void* rg_hip_exec_new(void* program, char* err, size_t err_len) {
   auto* p = (Program*)program;
@@ -943,6 +992,26 @@ int rg_hip_exec_write(void* exec, int64_t slot, const void* src, uint64_t bytes)
   if (!bytes) return 0;
   if (latch(e, hipMemcpyAsync(e->frame->slot[(size_t)slot], src, bytes, hipMemcpyHostToDevice, e->frame->stream), "write")) return -1;
   return latch(e, hipStreamSynchronize(e->frame->stream), "write") ? -1 : 0;
+}
+
+int rg_hip_exec_write_slots(void* exec, int64_t n, const int64_t* slots, const void* const* srcs, const uint64_t* bytes) {
+  auto* e = (Exec*)exec;
+  for (int64_t k = 0; k < n; k++)
+    if (slots[k] < 0 || (size_t)slots[k] >= e->frame->slot.size() || bytes[k] > e->prog->slot_bytes[(size_t)slots[k]]) return -1;
+  for (int64_t k = 0; k < n; k++)
+    if (bytes[k] && latch(e, hipMemcpyAsync(e->frame->slot[(size_t)slots[k]], srcs[k], bytes[k], hipMemcpyHostToDevice, e->frame->stream), "write"))
+      return -1;
+  return latch(e, hipStreamSynchronize(e->frame->stream), "write") ? -1 : 0;
+}
+
+int rg_hip_exec_read_slots(void* exec, int64_t n, const int64_t* slots, void* const* dsts, const uint64_t* bytes) {
+  auto* e = (Exec*)exec;
+  for (int64_t k = 0; k < n; k++)
+    if (slots[k] < 0 || (size_t)slots[k] >= e->frame->slot.size() || bytes[k] > e->prog->slot_bytes[(size_t)slots[k]]) return -1;
+  for (int64_t k = 0; k < n; k++)
+    if (bytes[k] && latch(e, hipMemcpyAsync(dsts[k], e->frame->slot[(size_t)slots[k]], bytes[k], hipMemcpyDeviceToHost, e->frame->stream), "read"))
+      return -1;
+  return latch(e, hipStreamSynchronize(e->frame->stream), "read") ? -1 : 0;
 }
 
 int rg_hip_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes) {
@@ -1072,8 +1141,11 @@ int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len) {
 // The step loop on the device (validate.rs:289-363 semantics). Each step is a replay of one of
 // two captured graphs: the swaps of the state handoff are disjoint pairs, so the slot table
 // alternates between two permutations and each has its graph. Batches, history and the step
-// counter live in device memory; history is read back once per chunk, and a non-finite value
-// re-runs that chunk from a snapshot to stop exactly after the bad step's handoff.
+// counter live in device memory; history is read back once per chunk. Every chunk starts from a
+// snapshot of the changing state slots: a non-finite value re-runs the chunk from it to stop
+// exactly after the bad step's handoff, and a device failure puts the state back to the chunk
+// start, so the state handed back always matches the completed steps. Graphs and buffers stay on
+// the frame (RunCache) for the next run with the same description.
 int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
   auto* e = (Exec*)exec;
   Program* p = e->prog;
@@ -1082,120 +1154,150 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
   out->nonfinite_step = -1;
   out->seconds = 0;
   if (!e->failure.empty()) return -1;
-  if (p->inject.exchange(false)) {
-    e->failure = "injected failure";
-    return -1;
-  }
-  std::vector<void*> owned;
-  auto dalloc = [&](uint64_t bytes) {
-    void* ptr = nullptr;
-    HIP_OK(hipMalloc(&ptr, std::max<uint64_t>(bytes, 16)));
-    owned.push_back(ptr);
-    return ptr;
-  };
-  std::vector<hipGraphExec_t> execs;
-  std::vector<hipGraph_t> graphs;
-  int rc = 0;
+  const int64_t fail_at = p->fail_in.exchange(-1);  // step index of an injected failure, or -1
+  RunCache& rc = f->run;
+  int result = 0;
   try {
     const int64_t steps = d->steps;
     const uint64_t chunk = d->n_history > 0 ? 64 : (uint64_t)std::max<int64_t>(steps, 1);
-    // Device-side run state.
-    auto* counter = (uint64_t*)dalloc(8);
-    double* hist = (double*)dalloc((uint64_t)std::max<int64_t>(d->n_history, 1) * std::max<uint64_t>(chunk, 1) * 8);
-    std::vector<void*> batch_bufs;
-    for (int64_t j = 0; j < d->n_data && d->n_batches > 1; j++) {
-      void* b = dalloc(d->data_bytes[j] * d->n_batches);
-      for (int64_t k = 0; k < d->n_batches; k++)
-        HIP_OK(hipMemcpy((char*)b + d->data_bytes[j] * k, d->batches[k * d->n_data + j], d->data_bytes[j], hipMemcpyHostToDevice));
-      batch_bufs.push_back(b);
+    const int n_graphs = d->n_swaps > 0 ? 2 : 1;
+    // The run description: a cached run with the same one can be replayed as it is.
+    std::vector<int64_t> key{d->n_swaps, d->n_copies, d->n_data, d->n_batches > 1 ? d->n_batches : 0, d->n_history, (int64_t)chunk};
+    key.insert(key.end(), d->swaps, d->swaps + 2 * d->n_swaps);
+    key.insert(key.end(), d->copies, d->copies + 3 * d->n_copies);
+    key.insert(key.end(), d->data_slots, d->data_slots + d->n_data);
+    for (int64_t j = 0; j < d->n_data; j++) key.push_back((int64_t)d->data_bytes[j]);
+    key.insert(key.end(), d->history_slots, d->history_slots + d->n_history);
+    auto tables_from = [&](const std::vector<void*>& start) {
+      rc.table[0] = start;
+      rc.table[1] = start;
+      for (int64_t k = 0; k < d->n_swaps; k++) std::swap(rc.table[1][(size_t)d->swaps[2 * k]], rc.table[1][(size_t)d->swaps[2 * k + 1]]);
+    };
+    if (rc.key != key) {
+      rc.release();
+      // One allocation: counter, history ring, batch tables, copy temporaries, snapshot.
+      std::vector<uint64_t> sizes{8, (uint64_t)std::max<int64_t>(d->n_history, 1) * chunk * 8};
+      const bool cycled = d->n_batches > 1;
+      for (int64_t j = 0; j < d->n_data && cycled; j++) sizes.push_back(d->data_bytes[j] * (uint64_t)d->n_batches);
+      for (int64_t c = 0; c < d->n_copies; c++) sizes.push_back(p->slot_bytes[(size_t)d->copies[3 * c + 1]]);
+      for (int64_t k = 0; k < d->n_swaps; k++) rc.state_slots.push_back(d->swaps[2 * k]);
+      for (int64_t k = 0; k < d->n_copies; k++) rc.state_slots.push_back(d->copies[3 * k]);
+      for (auto sl : rc.state_slots) sizes.push_back(p->slot_bytes[(size_t)sl]);
+      uint64_t total = 0;
+      std::vector<uint64_t> off;
+      for (auto b : sizes) {
+        off.push_back(total);
+        total += (b + ALIGN - 1) / ALIGN * ALIGN;
+      }
+      HIP_OK(hipMalloc(&rc.mem, total));
+      rc.mem_bytes = total;
+      char* base = (char*)rc.mem;
+      size_t q = 0;
+      rc.counter = (uint64_t*)(base + off[q++]);
+      rc.hist = (double*)(base + off[q++]);
+      for (int64_t j = 0; j < d->n_data && cycled; j++) rc.batch_bufs.push_back(base + off[q++]);
+      for (int64_t c = 0; c < d->n_copies; c++) rc.temps.push_back(base + off[q++]);
+      for (size_t k = 0; k < rc.state_slots.size(); k++) rc.snap.push_back(base + off[q++]);
+      rc.chunk = chunk;
+      rc.n_graphs = n_graphs;
+      tables_from(f->slot);
+      rc.key = key;
+    } else if (f->slot != rc.table[0] && (n_graphs < 2 || f->slot != rc.table[1])) {
+      // The frame's buffers were swapped outside a run: new tables, new graphs.
+      rc.clear_graphs();
+      tables_from(f->slot);
     }
-    std::vector<void*> temps;
-    for (int64_t c = 0; c < d->n_copies; c++) {
-      int64_t os = d->copies[3 * c + 1];
-      temps.push_back(dalloc(p->slot_bytes[(size_t)os]));
-    }
-    // State slots that change across steps, for the snapshot of a chunk.
-    std::vector<int64_t> state_slots;
-    for (int64_t k = 0; k < d->n_swaps; k++) state_slots.push_back(d->swaps[2 * k]);
-    for (int64_t k = 0; k < d->n_copies; k++) state_slots.push_back(d->copies[3 * k]);
-    std::vector<void*> snap;
-    if (d->n_history > 0)
-      for (auto s : state_slots) snap.push_back(dalloc(p->slot_bytes[(size_t)s]));
-
-    // The two slot tables and their graphs.
-    std::vector<void*> table[2];
-    table[0] = f->slot;
-    table[1] = f->slot;
-    for (int64_t k = 0; k < d->n_swaps; k++) std::swap(table[1][(size_t)d->swaps[2 * k]], table[1][(size_t)d->swaps[2 * k + 1]]);
-    int n_graphs = d->n_swaps > 0 ? 2 : 1;
+    // Step k (counted from this run's start) runs under table (parity + k) % n_graphs.
+    const int parity = f->slot == rc.table[0] ? 0 : 1;
     // Everything one step enqueues under slot table g: batch loads, the plan, history records,
     // the state copies (all sources read before any destination is written, validate.rs:349-355)
     // and the step counter.
     auto enqueue_step = [&](int g) {
-      const std::vector<void*>& t = table[g];
-      for (int64_t j = 0; j < (int64_t)batch_bufs.size(); j++)
-        rgk::load_batch(f->stream, t[(size_t)d->data_slots[j]], batch_bufs[j], d->data_bytes[j], d->n_batches, counter);
+      const std::vector<void*>& t = rc.table[g];
+      for (int64_t j = 0; j < (int64_t)rc.batch_bufs.size(); j++)
+        rgk::load_batch(f->stream, t[(size_t)d->data_slots[j]], rc.batch_bufs[(size_t)j], d->data_bytes[j], d->n_batches, rc.counter);
       enqueue_range(*p, f->stream, t.data(), f->workspace, 0, p->steps.size());
       for (int64_t h = 0; h < d->n_history; h++) {
-        int64_t s = d->history_slots[h];
-        rgk::record_history(f->stream, p->plan.slots[(size_t)s].dtype, t[(size_t)s], hist + h * chunk, counter, chunk);
+        int64_t sl = d->history_slots[h];
+        rgk::record_history(f->stream, p->plan.slots[(size_t)sl].dtype, t[(size_t)sl], rc.hist + h * chunk, rc.counter, chunk);
       }
       for (int64_t c = 0; c < d->n_copies; c++) {
         int64_t os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
-        rgk::copy_bytes(f->stream, temps[c], t[(size_t)os], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
+        rgk::copy_bytes(f->stream, rc.temps[(size_t)c], t[(size_t)os], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
       }
-      const std::vector<void*>& next = table[(g + 1) % n_graphs];
+      const std::vector<void*>& next = rc.table[(g + 1) % n_graphs];
       for (int64_t c = 0; c < d->n_copies; c++) {
         int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
-        rgk::copy_bytes(f->stream, next[(size_t)is], temps[c], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
+        rgk::copy_bytes(f->stream, next[(size_t)is], rc.temps[(size_t)c], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
       }
-      rgk::counter_inc(f->stream, counter);
+      rgk::counter_inc(f->stream, rc.counter);
     };
     // Each slot table is captured once as a HIP graph and replayed; RG_HIP_GRAPHS=0 launches the
     // same kernels directly instead (for tools that do not follow graph launches).
     const char* env = getenv("RG_HIP_GRAPHS");
     const bool use_graphs = !(env && env[0] == '0');
-    for (int g = 0; g < n_graphs && use_graphs; g++) {
-      HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));
-      enqueue_step(g);
-      hipGraph_t graph;
-      hipError_t ce = hipStreamEndCapture(f->stream, &graph);
-      if (ce != hipSuccess) throw std::runtime_error("graph capture failed: " + err_str(ce));
-      graphs.push_back(graph);
-      hipGraphExec_t ge;
-      HIP_OK(hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0));
-      execs.push_back(ge);
+    if (use_graphs && rc.execs.empty()) {
+      for (int g = 0; g < n_graphs; g++) {
+        HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));
+        enqueue_step(g);
+        hipGraph_t graph;
+        hipError_t ce = hipStreamEndCapture(f->stream, &graph);
+        if (ce != hipSuccess) throw std::runtime_error("graph capture failed: " + err_str(ce));
+        rc.graphs.push_back(graph);
+        hipGraphExec_t ge;
+        HIP_OK(hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0));
+        rc.execs.push_back(ge);
+      }
     }
+    // Batches for this run, uploaded together with one wait.
+    for (int64_t j = 0; j < (int64_t)rc.batch_bufs.size(); j++)
+      for (int64_t k = 0; k < d->n_batches; k++)
+        HIP_OK(hipMemcpyAsync((char*)rc.batch_bufs[(size_t)j] + d->data_bytes[j] * k, d->batches[k * d->n_data + j], d->data_bytes[j],
+                              hipMemcpyHostToDevice, f->stream));
+    auto table_of = [&](int64_t k) { return (int)((parity + k) % n_graphs); };
     auto launch = [&](int64_t k) -> hipError_t {
-      if (use_graphs) return hipGraphLaunch(execs[(size_t)(k % n_graphs)], f->stream);
-      enqueue_step((int)(k % n_graphs));
+      if (use_graphs) return hipGraphLaunch(rc.execs[(size_t)table_of(k)], f->stream);
+      enqueue_step(table_of(k));
       return hipGetLastError();
     };
-    HIP_OK(hipGetLastError());
-    auto set_counter = [&](uint64_t v) {
-      HIP_OK(hipStreamSynchronize(f->stream));
-      HIP_OK(hipMemcpy(counter, &v, 8, hipMemcpyHostToDevice));
+    auto snapshot = [&](int g, bool restore) {
+      for (size_t q = 0; q < rc.state_slots.size(); q++) {
+        void* live = rc.table[g][(size_t)rc.state_slots[q]];
+        uint64_t bytes = p->slot_bytes[(size_t)rc.state_slots[q]];
+        rgk::copy_bytes(f->stream, restore ? live : rc.snap[q], restore ? rc.snap[q] : live, bytes);
+      }
     };
-    set_counter(0);
+    HIP_OK(hipGetLastError());
+    rgk::set_counter(f->stream, rc.counter, 0);
+    HIP_OK(hipStreamSynchronize(f->stream));
     double t0 = now();
     int64_t done = 0;
     std::vector<double> hbuf((size_t)std::max<int64_t>(d->n_history, 1) * chunk);
     while (done < steps) {
       int64_t c0 = done, c1 = std::min<int64_t>(steps, done + (int64_t)chunk);
-      int parity0 = (int)(c0 % n_graphs);
-      if (d->n_history > 0) {
-        for (size_t q = 0; q < state_slots.size(); q++)
-          rgk::copy_bytes(f->stream, snap[q], table[parity0][(size_t)state_slots[q]], p->slot_bytes[(size_t)state_slots[q]]);
+      if (fail_at >= 0 && c0 >= fail_at) {
+        // The injected failure: a device error before step c0, with every earlier step complete.
+        e->failure = "injected failure";
+        result = -1;
+        break;
       }
-      for (int64_t k = c0; k < c1; k++)
-        if (latch(e, launch(k), "step launch")) break;
-      if (!e->failure.empty() || latch(e, hipStreamSynchronize(f->stream), "device execution")) {
-        rc = -1;
+      if (fail_at > c0) c1 = std::min<int64_t>(c1, fail_at);
+      const int g0 = table_of(c0);
+      snapshot(g0, false);
+      bool failed = false;
+      for (int64_t k = c0; k < c1 && !failed; k++) failed = latch(e, launch(k), "step launch");
+      if (failed || latch(e, hipStreamSynchronize(f->stream), "device execution")) {
+        // Back to the state before the chunk; if the device no longer runs copies, the state is
+        // lost and the failure message stands for it.
+        hipGetLastError();
+        snapshot(g0, true);
+        if (hipStreamSynchronize(f->stream) != hipSuccess) e->failure += " (state could not be restored)";
+        result = -1;
         break;
       }
       int64_t bad = -1;
       if (d->n_history > 0) {
-        HIP_OK(hipMemcpy(hbuf.data(), hist, (size_t)d->n_history * chunk * 8, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(hbuf.data(), rc.hist, (size_t)d->n_history * chunk * 8, hipMemcpyDeviceToHost));
         for (int64_t k = c0; k < c1 && bad < 0; k++)
           for (int64_t h = 0; h < d->n_history; h++)
             if (!std::isfinite(hbuf[(size_t)(h * chunk + (k - c0))])) bad = k;
@@ -1204,12 +1306,11 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       }
       if (bad >= 0) {
         // Back to the chunk start, then exactly through the bad step.
-        for (size_t q = 0; q < state_slots.size(); q++)
-          rgk::copy_bytes(f->stream, table[parity0][(size_t)state_slots[q]], snap[q], p->slot_bytes[(size_t)state_slots[q]]);
-        set_counter((uint64_t)c0);
+        snapshot(g0, true);
+        rgk::set_counter(f->stream, rc.counter, (uint64_t)c0);
         for (int64_t k = c0; k <= bad; k++) latch(e, launch(k), "step launch");
         if (latch(e, hipStreamSynchronize(f->stream), "device execution")) {
-          rc = -1;
+          result = -1;
           break;
         }
         done = bad + 1;
@@ -1221,16 +1322,13 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     out->seconds = now() - t0;
     out->done = done;
     // The frame's table reflects every handoff made.
-    f->slot = table[(size_t)(done % n_graphs)];
+    f->slot = rc.table[(size_t)table_of(done)];
   } catch (std::exception& ex) {
     if (e->failure.empty()) e->failure = ex.what();
-    rc = -1;
+    result = -1;
   }
   hipStreamSynchronize(f->stream);
-  for (auto g : execs) hipGraphExecDestroy(g);
-  for (auto g : graphs) hipGraphDestroy(g);
-  for (void* ptr : owned) hipFree(ptr);
-  return rc;
+  return result;
 }
 
 }  // extern "C"

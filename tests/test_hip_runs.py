@@ -2,6 +2,8 @@
 pooled frames, failure latching and the benchmark programs (tests/metal.rs:248-390 and
 test_framework.py:447-473 of the reference)."""
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -102,20 +104,156 @@ def test_nonfinite_stop_matches_the_host_loop():
     assert np.array_equal(a.state.numpy(), b.state.numpy())
 
 
-def test_device_failure_is_latched_reported_and_recovered():
+def test_repeated_runs_do_not_leak_device_memory():
+    """tests/metal.rs:278-301: frames come from the program's pool and the run loop's graphs and
+    buffers stay with the frame, so 200 cycles of calls and runs hold no more device memory."""
     g = _rg.Graph()
-    w = g.input([4], "float32")
-    m = op(g, "mul", [w, g.constant(rg.tensor(np.float32(0.5))._t)])
+    x = g.input([256, 256], "float32")
+    y = op(g, "tanh", [op(g, "matmul", [x, x])])
+    inp = seq((256, 256))
+    c = _rg.compile(g, [y], [inp._t], "none", "hip", "none")
+
+    def cycle():
+        for _ in range(5):
+            c.call([inp._t])
+        c.run([(0, 0)], [], [], [inp._t], [], 5, True)
+    cycle()
+    before = c.allocated_bytes()
+    for _ in range(200):
+        cycle()
+    after = c.allocated_bytes()
+    assert after < before + 32 * 1024 * 1024, f"device memory grew from {before} to {after}"
+
+
+def test_a_buffer_beyond_the_device_limit_is_refused_at_compile_time():
+    """tests/metal.rs:354-363: a 16 TiB float32 value is refused when the program is built,
+    before anything is allocated, as DEVICE_UNAVAILABLE naming the limit."""
+    g = _rg.Graph()
+    x = g.input([1], "float32")
+    y = op(g, "tanh", [op(g, "broadcast_to", [x], shape=[1 << 42])])
+    with pytest.raises(rg.DiagnosticError) as e:
+        _rg.compile(g, [y], [t([0.5])._t], "none", "hip", "none")
+    d = e.value.diagnostic
+    assert d["code"] == "DEVICE_UNAVAILABLE", d
+    assert "exceeds" in d["observation"]["detail"], d
+
+
+def test_device_failure_reaches_the_caller_and_the_program_recovers():
+    """tests/metal.rs:365-390: an injected failure surfaces as DEVICE_EXECUTION_FAILED from a
+    call and from a run (with no completed steps), and the next run on a recycled frame is right."""
     x = t([1.0, 2.0, 3.0, 4.0])
     c = rg.compile(lambda w: w * 0.5, (x,), validate="basic", device="hip")
-    import ctypes
+    c._n.inject_failure()
+    with pytest.raises(rg.DiagnosticError) as e:
+        c(x)
+    d = e.value.diagnostic
+    assert d["code"] == "DEVICE_EXECUTION_FAILED" and d["observation"]["detail"] == "injected failure", d
+    c._n.inject_failure()
+    with pytest.raises(rg.DiagnosticError) as e:
+        rg.run(c, x, steps=10)
+    d = e.value.diagnostic
+    assert d["code"] == "DEVICE_EXECUTION_FAILED" and d["observation"]["completed_steps"] == 0, d
+    assert d["observation"]["detail"] == "injected failure"
+    ok = rg.run(c, x, steps=1)
+    assert ok.status == "completed" and ok.state.numpy().tolist() == [0.5, 1.0, 1.5, 2.0]
+
+
+def test_a_failure_in_the_middle_of_a_run_reports_the_completed_steps():
+    """A failure after 5 of 10 steps reports 5 completed steps, with and without per-step history
+    (the device loop runs in chunks with and without history), and the next run is right."""
+    for with_aux in (False, True):
+        def step(w):
+            nw = w * 0.5
+            return (nw, nw.sum()) if with_aux else nw
+        x = t([1.0, 2.0, 3.0, 4.0])
+        c = rg.compile(step, (x,), validate="basic", device="hip")
+        c._n.inject_failure(after=5)
+        with pytest.raises(rg.DiagnosticError) as e:
+            rg.run(c, x, steps=10)
+        d = e.value.diagnostic
+        assert d["code"] == "DEVICE_EXECUTION_FAILED" and d["observation"]["completed_steps"] == 5, d
+        r = rg.run(c, x, steps=3)
+        assert r.state.numpy().tolist() == [0.125, 0.25, 0.375, 0.5]
+
+
+def _plan_io(words):
+    """Input and output slots of a flat plan (include/rg_plan.h: header, slots, consts, inputs, outputs)."""
+    k = 2
+    n = words[k]; k += 1 + 3 * n
+    n = words[k]; k += 1 + 3 * n
+    n = words[k]; inputs = [words[k + 1 + 2 * j] for j in range(n)]; k += 1 + 2 * n
+    n = words[k]; k += 1
+    outputs = []
+    for _ in range(n):
+        outputs.append(words[k])
+        k += 3 + words[k + 2]
+    return inputs, outputs
+
+
+class _RunDesc(ctypes.Structure):
+    _fields_ = [("n_swaps", ctypes.c_int64), ("swaps", ctypes.POINTER(ctypes.c_int64)),
+                ("n_copies", ctypes.c_int64), ("copies", ctypes.POINTER(ctypes.c_int64)),
+                ("n_data", ctypes.c_int64), ("data_slots", ctypes.POINTER(ctypes.c_int64)),
+                ("data_bytes", ctypes.POINTER(ctypes.c_uint64)), ("n_batches", ctypes.c_int64),
+                ("batches", ctypes.POINTER(ctypes.c_void_p)), ("n_history", ctypes.c_int64),
+                ("history_slots", ctypes.POINTER(ctypes.c_int64)), ("steps", ctypes.c_int64),
+                ("history", ctypes.POINTER(ctypes.c_double))]
+
+
+class _RunResult(ctypes.Structure):
+    _fields_ = [("done", ctypes.c_int64), ("nonfinite_step", ctypes.c_int64), ("seconds", ctypes.c_double)]
+
+
+def test_run_failure_leaves_the_state_of_the_completed_steps_at_the_abi():
+    """Through the C ABI: after a failure the state slot holds the state after `done` steps (as
+    the reference's host loop leaves it, validate.rs:329-335), not a half-run chunk."""
     from rustautograd_amd import _native
     lib = ctypes.CDLL(_native.HIP_LIBRARY)
-    # A program handle is not exposed to Python; failure injection is exercised through the ABI
-    # tests in test_zz_abi.py. Here: the run loop reports a completed run with the right values.
-    r = rg.run(c, x, steps=1)
-    assert r.state.numpy().tolist() == [0.5, 1.0, 1.5, 2.0]
-    del g, m, lib
+    lib.rg_hip_program_new.restype = ctypes.c_void_p
+    lib.rg_hip_program_new.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t,
+                                       ctypes.c_char_p, ctypes.c_size_t]
+    lib.rg_hip_exec_new.restype = ctypes.c_void_p
+    lib.rg_hip_exec_new.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    for name in ("rg_hip_exec_free", "rg_hip_program_free", "rg_hip_program_inject_failure"):
+        getattr(lib, name).argtypes = [ctypes.c_void_p]
+    lib.rg_hip_program_inject_failure_after.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    lib.rg_hip_exec_write.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_uint64]
+    lib.rg_hip_exec_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_uint64]
+    lib.rg_hip_exec_run.argtypes = [ctypes.c_void_p, ctypes.POINTER(_RunDesc), ctypes.POINTER(_RunResult)]
+    lib.rg_hip_exec_failure.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+
+    g = _rg.Graph()
+    w = g.input([4], "float32")
+    nw = op(g, "mul", [w, g.constant(rg.tensor(np.float32(0.5))._t)])
+    words, blob = _rg.plan_words(g, [nw, op(g, "sum", [nw], axes=[0], keepdims=False)], "hip", "none")
+    (win,), (wout, lout) = _plan_io(words)
+    arr = (ctypes.c_int64 * len(words))(*words)
+    err = ctypes.create_string_buffer(4096)
+    prog = lib.rg_hip_program_new(arr, len(words), blob, len(blob), err, len(err))
+    assert prog, err.value
+    try:
+        for history, fail_after in ((False, 5), (True, 70), (True, 0)):
+            e = lib.rg_hip_exec_new(prog, err, len(err))
+            assert e, err.value
+            x0 = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+            assert lib.rg_hip_exec_write(e, win, x0.ctypes.data, 16) == 0
+            swaps = (ctypes.c_int64 * 2)(win, wout)
+            hs = (ctypes.c_int64 * 1)(lout)
+            steps = 100
+            hist = (ctypes.c_double * steps)()
+            d = _RunDesc(n_swaps=1, swaps=swaps, n_history=1 if history else 0, history_slots=hs, steps=steps, history=hist)
+            lib.rg_hip_program_inject_failure_after(prog, fail_after)
+            out = _RunResult()
+            assert lib.rg_hip_exec_run(e, ctypes.byref(d), ctypes.byref(out)) == -1
+            assert out.done == fail_after, (history, out.done)
+            msg = ctypes.create_string_buffer(256)
+            assert lib.rg_hip_exec_failure(e, msg, 256) == 1 and msg.value == b"injected failure"
+            got = np.zeros(4, np.float32)
+            assert lib.rg_hip_exec_read(e, win, got.ctypes.data, 16) == 0
+            assert np.array_equal(got, x0 * np.float32(0.5) ** fail_after), (history, got)
+            lib.rg_hip_exec_free(e)
+    finally:
+        lib.rg_hip_program_free(prog)
 
 
 def test_linear_regression_converges_and_matches_cpu():
