@@ -195,8 +195,7 @@ def main():
     # events on the execution stream, after one full step has filled every slot.
     roof, kernels, total_s = None, None, None
     if args.timing_reps > 0:
-        from rustautograd_amd._core import _flatten
-        inputs = [rg.tensor(x)._t for x in _flatten((res.state,))[0]]
+        inputs = [rg.tensor(x)._t for x in rg.tree.leaves((res.state,))]
         classes = classify(compiled.plan_summary())
         time_classes(compiled, inputs, classes, 1)
         time_classes(compiled, inputs, classes, args.timing_reps)

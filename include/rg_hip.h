@@ -45,7 +45,7 @@ typedef struct rg_run_desc {
 typedef struct rg_run_result {
   int64_t done;                /* completed steps */
   int64_t nonfinite_step;      /* first step whose history held a non-finite value, or -1 */
-  double seconds;              /* time in the step loop, excluding one-time setup */
+  double seconds;              /* wall seconds of the loop itself; setup and transfers not counted */
 } rg_run_result;
 
 /* metal.rs:58-60 `available()`: 1 when a gfx950 device is present. */

@@ -57,7 +57,7 @@ std::vector<size_t> strides(const Sh& shape) {
   return out;
 }
 
-// Strides of `shape` right-aligned into `rank` dims, 0 on broadcast dims (plan.rs:1164-1169).
+// Element strides of `shape` laid out against `rank` output dims from the right; a broadcast dim gets stride 0 (plan.rs:1164-1169).
 std::vector<size_t> bstrides(const Sh& shape, size_t rank) {
   auto st = strides(shape);
   size_t lead = rank - shape.size();
@@ -67,7 +67,7 @@ std::vector<size_t> bstrides(const Sh& shape, size_t rank) {
   return out;
 }
 
-// Odometer over `shape`, tracking N flat offsets (plan.rs:1171-1192).
+// Walks every index of `shape` in row-major order, carrying one flat offset per operand (plan.rs:1171-1192).
 template <size_t N, class F>
 void walk(const Sh& shape, const std::vector<size_t>* st, F f) {
   size_t total = prod(shape);
@@ -209,7 +209,7 @@ T fast_sum(const T* a, size_t n) {
   return out;
 }
 
-// tensor.rs:238-251: out[m*n] = A[m*k] @ B[k*n], the naive i-p-j loop with no fused multiply-add.
+// tensor.rs:238-251: C (m x n) = A (m x k) times B (k x n), row-major, looping i, then p, then j, each term rounded on its own (no FMA).
 template <class T>
 void gemm(size_t m, size_t k, size_t n, const T* a, bool ta, const T* b, bool tb, T* out) {
   std::fill(out, out + m * n, (T)0);
@@ -480,7 +480,7 @@ void matmul(const Instr& i, std::vector<Buf>& s, bool ta, bool tb) {
   Sh ba(sa.begin(), sa.begin() + (ar >= 2 ? ar - 2 : 0)), bb(sb.begin(), sb.begin() + (br >= 2 ? br - 2 : 0));
   if (i.n == 0) return;
   if (bb.empty() && !ta) {
-    // Row-major batches of the left operand are one big matrix: a single gemm call.
+    // A 2-D right operand: the left operand's leading dims stack into rows of one matrix, so one gemm does it.
     size_t rows = prod(ba) * m;
     if (g_row_parallel_gemm && rows * k * n >= PARALLEL_FLOPS && rows >= 128) {
       // Checker-only speed-up (off by default, so the CPU baseline stays the reference's serial
@@ -544,7 +544,7 @@ void reduce(const Instr& i, std::vector<Buf>& s) {
   T init = kind == RG_REDUCE_SUM ? (T)0 : kind == RG_REDUCE_MAX ? (T)-INFINITY : (T)INFINITY;
   if (in_n >= (kind == RG_REDUCE_SUM ? PARALLEL_SUM : PARALLEL_MINMAX) && len > 0) {
     if (axes.size() == 1 && axes[0] == in_shape.size() - 1) {
-      // Each output owns one input row.
+      // One input row per output value.
 #pragma omp parallel for schedule(static)
       for (size_t o = 0; o < out_n; o++) {
         const T* row = a + o * len;
@@ -757,7 +757,7 @@ void arg_top_k(const Instr& i, std::vector<Buf>& s) {
   const T* a = s[(size_t)i.args[0].slot].as<T>();
   int32_t* dst = s[(size_t)i.dst].as<int32_t>();
   size_t rows = prod(i.args[0].shape) / v;
-  // A total order: larger first, ties by index, NaN last (plan.rs:838-848).
+  // Ordering used for the ranking: greater values rank first, equal values by position, NaN after everything (plan.rs:838-848).
   for (size_t r = 0; r < rows; r++) {
     const T* row = a + r * v;
     std::vector<int32_t> idx(v);

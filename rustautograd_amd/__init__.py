@@ -6,25 +6,21 @@ MI355X-native HIP execution backend.
     result = rg.run(step, state, data, steps=300)
 
 The engine (graph, autodiff, optimizer, planner, run loop) is C++ (`_rg`); every plan step runs
-as a hand-written CDNA4 kernel in librg_hip.so.
+as a hand-written CDNA4 kernel in librg_hip.so. The public names are those of the reference's
+python/rg/__init__.py.
 """
 
-from ._core import (
-    Compiled, DiagnosticError, Report, RunResult, Tensor, Tracer, _Ops,
-    abs, arange, argmax, argsort, broadcast_to, clip, compile, concatenate, cond, cos, cumsum, custom_vjp, devices, equal, exp,
-    expand_dims, eye, flip, floor, full, grad, hessian, inspect, jvp, linspace, log, matmul, maximum,
-    minimum, not_equal, ones, ones_like, reshape, run, sign, sin, sqrt, square, squeeze, stack, stop_gradient,
-    swapaxes, scan, sort, take, take_along_axis, tanh, tensor, top_k, transpose, tril, value_and_grad, where, while_loop, zeros,
+from ._native import DiagnosticError
+from .tensor import Tensor, Tracer, Value, tensor
+from .ops import (
+    abs, arange, argmax, argsort, broadcast_to, clip, concatenate, cos, cumsum, equal, exp, expand_dims, eye, flip, floor, full,
+    linspace, log, matmul, max, maximum, mean, min, minimum, not_equal, ones, ones_like, reshape, sign, sin, sort, sqrt, square,
+    squeeze, stack, std, stop_gradient, sum, swapaxes, take, take_along_axis, tanh, top_k, transpose, tril, var, where, zeros,
     zeros_like,
 )
+from .transforms import custom_vjp, grad, hessian, jvp, value_and_grad
+from .control import cond, scan, while_loop
+from .program import Compiled, Report, RunResult, compile, devices, inspect, run
 from . import nn, optim, random, tree
 
-__version__ = "0.1.0"
-
-
-def sum(x, axis=None, keepdims=False): return x.sum(axis, keepdims)
-def mean(x, axis=None, keepdims=False): return x.mean(axis, keepdims)
-def max(x, axis=None, keepdims=False): return x.max(axis, keepdims)
-def min(x, axis=None, keepdims=False): return x.min(axis, keepdims)
-def var(x, axis=None, keepdims=False): return x.var(axis, keepdims)
-def std(x, axis=None, keepdims=False): return x.std(axis, keepdims)
+__version__ = "0.2.0"

@@ -18,7 +18,7 @@ uint32_t reshape(Graph& g, uint32_t x, const Shape& s) {
   return g.add(o, {x});
 }
 
-// Sums `ct` back down to `target` after a broadcast (autodiff.rs:6-16).
+// Reduces a cotangent of the broadcast shape to the operand's own shape by summing the broadcast axes (autodiff.rs:6-16).
 uint32_t unbroadcast(Graph& g, uint32_t ct, Shape target) {  // by value: adding nodes moves g.nodes
   Shape shape = g.shape(ct);
   if (shape == target) return ct;
@@ -42,7 +42,7 @@ bool blocks_gradient(const Op& op) {
   }
 }
 
-// Transposes the last two axes.
+// Swap of the two innermost axes.
 uint32_t swap_last(Graph& g, uint32_t v) {
   size_t r = g.shape(v).size();
   Op o = mk(RG_OP_TRANSPOSE);
@@ -62,7 +62,7 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
   uint32_t y = node.inputs.size() > 1 ? node.inputs[1] : 0;
   std::vector<std::pair<uint32_t, uint32_t>> out;
 
-  // Unary rules: dy/dx times the cotangent.
+  // Single-input ops: the local derivative multiplied into the incoming cotangent.
   int64_t factor = -1;
   switch (node.op.kind) {
     case RG_OP_EXP: factor = me; break;
@@ -110,7 +110,7 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
           uint32_t f = bin(g, RG_OP_MUL, y, p);
           c = bin(g, RG_OP_MUL, ct, f);
         } else {
-          // Ties send the whole gradient to x, the convention `where(x >= y, x, y)` implies.
+          // On equality x receives all of it, as if the op were where(x >= y, x, y).
           uint32_t zero = g.scalar(d, 0.0);
           uint32_t m = k == RG_OP_MAX ? bin(g, RG_OP_GE, x, y) : bin(g, RG_OP_GE, y, x);
           c = g.add(mk(RG_OP_WHERE), {m, ct, zero});
@@ -148,7 +148,7 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
       break;
     }
     case RG_OP_MATMUL: {
-      // 1-D operands are promoted so one rule covers every rank, batched or not.
+      // Vectors are lifted to matrices first, so the same formulas serve every operand rank and batching.
       Shape sa = g.shape(x), sb = g.shape(y);
       uint32_t a2 = sa.size() == 1 ? reshape(g, x, {1, sa[0]}) : x;
       uint32_t b2 = sb.size() == 1 ? reshape(g, y, {sb[0], 1}) : y;
@@ -166,8 +166,8 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
       if (rel[y]) {
         uint32_t c;
         if (sa.size() > 2 && sb.size() == 2) {
-          // A shared matrix under a batched operand: flattening the batch gives the summed
-          // gradient in one multiply, instead of many followed by a reduction.
+          // The right operand is one matrix for every batch: stacking the batch into rows makes
+          // its gradient (the sum over batches) a single product, with no per-batch products to reduce.
           size_t k = sb[0], n = sb[1];
           size_t m_total = g.nodes[x].n() / k;
           uint32_t af = reshape(g, x, {m_total, k});
@@ -222,7 +222,7 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
       break;
     }
     case RG_OP_CUSTOM: {
-      // Re-instantiate the rule with the real cotangent in place of the placeholder.
+      // Copy the recorded rule's nodes, substituting the actual cotangent for its stand-in.
       std::map<uint32_t, uint32_t> memo{{node.op.placeholder, ct}};
       uint32_t last = node.op.placeholder;
       for (auto& r : node.op.rules) last = std::max(last, r.second);
@@ -261,7 +261,7 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
         b.v = in_shape;
         c = g.add(b, {ct_keep});
       } else {
-        // Ties share the gradient equally.
+        // Equal maxima (minima) split the cotangent evenly among them.
         uint32_t m = reshape(g, me, keep);
         uint32_t mask = node.op.rk == RK::Max ? bin(g, RG_OP_GE, x, m) : bin(g, RG_OP_GE, m, x);
         Op s = mk(RG_OP_REDUCE);
@@ -342,7 +342,7 @@ std::vector<uint32_t> grad(Graph& g, uint32_t y, const std::vector<uint32_t>& wr
     const Node& n = g.nodes[i];
     bool flows = false;
     if (n.op.kind == RG_OP_CUSTOM) {
-      // The rule, not the traced body, defines how gradients reach the inputs.
+      // Gradients flow through the user's rule only; the body it wraps is not differentiated.
       for (auto& r : n.op.rules) flows |= rel[r.first];
     } else if (!blocks_gradient(n.op)) {
       for (uint32_t x : n.inputs) flows |= rel[x];

@@ -96,7 +96,7 @@ class DeviceExec {
   const Plan* plan_;
 };
 
-// Runs a graph once with a fresh frame on `b` (plan.rs:997-1006 `eval`).
+// Plans `g`, builds it on backend `b`, executes it once and returns the outputs (plan.rs:997-1006 `eval`).
 std::vector<Tensor> eval_on(Backend* b, const Graph& g, const std::vector<uint32_t>& outputs,
                             const std::vector<const Tensor*>& inputs);
 

@@ -292,7 +292,7 @@ uint32_t Graph::add(const Op& op, const std::vector<uint32_t>& inputs) {
   for (uint32_t i : inputs) shapes.push_back(nodes[i].shape);
 
   if (op.kind == RG_OP_WHERE) {
-    // Materializing the broadcast keeps the Where kernel same-shape only (graph.rs:368-379).
+    // The condition is broadcast to the result shape up front, so the select itself only sees equal shapes (graph.rs:368-379).
     Shape target;
     bool ok = true;
     for (auto& s : shapes) {

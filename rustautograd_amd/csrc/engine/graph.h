@@ -112,7 +112,7 @@ struct Node {
   Shape shape;
   DType dtype = DType::F32;
   std::shared_ptr<const std::string> source;
-  int64_t origin = -1;  // backward nodes: the forward node whose VJP produced them
+  int64_t origin = -1;  // set on gradient nodes: which forward node's rule emitted them
   size_t n() const { return numel(shape); }
 };
 
@@ -150,7 +150,7 @@ class Graph {
   Shape infer(const Op& op, const std::vector<Shape>& s) const;
 };
 
-// Reverse-mode autodiff (src/autodiff.rs:245-326): appends d(y)/d(wrts) to the graph.
+// Reverse-mode autodiff (src/autodiff.rs:245-326): adds the nodes computing the gradient of y with respect to each of `wrts`.
 std::vector<uint32_t> grad(Graph& g, uint32_t y, const std::vector<uint32_t>& wrts);
 
 }  // namespace rg

@@ -1,6 +1,6 @@
-// Minimal JSON value for diagnostics and reports. Diagnostics are plain JSON documents: the
-// machine-readable form is the only form (the reference builds the same shapes with serde_json,
-// src/graph.rs:229-239).
+// Minimal JSON value for diagnostics and reports. Every diagnostic is a JSON document, for
+// programs and people alike; the reference builds the same document shapes with serde_json
+// (src/graph.rs:229-239).
 #pragma once
 #include <charconv>
 #include <cmath>
@@ -140,7 +140,7 @@ class Json {
   std::vector<std::pair<std::string, Json>> o_;
 };
 
-// JSON cannot carry Inf/NaN as numbers (src/validate.rs:28-39).
+// Non-finite doubles have no JSON number form; they are written as strings (src/validate.rs:28-39).
 inline Json num(double x) {
   if (std::isfinite(x)) return Json(x);
   if (std::isnan(x)) return Json("nan");

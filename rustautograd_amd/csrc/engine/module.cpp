@@ -219,7 +219,7 @@ PYBIND11_MODULE(_rg, m) {
       .def("dtype", [](const PyGraph& g, uint32_t id) { return std::string(dname(g.g.dtype(id))); })
       .def("__len__", [](const PyGraph& g) { return g.g.nodes.size(); })
       .def("eval", [](const PyGraph& g, const std::vector<uint32_t>& ids) {
-        // One-off evaluation for eager operations; the graph must have no inputs.
+        // Eager mode: a constant-only graph evaluated once on the eager backend.
         Backend* b = eager_backend();
         std::vector<Tensor> out;
         {

@@ -18,7 +18,7 @@ constexpr size_t CSE_CONST_LIMIT = 16;
 constexpr size_t REMAT_MIN = 1 << 14;
 constexpr size_t SPLIT_SUM_MIN = 4096;
 constexpr double SEARCH_MIN_GAIN = 0.9;
-// Peak memory above which recomputing costly functions beats storing them (optimize.rs:79-84).
+// Above this peak of live intermediates, even expensive elementwise values are recomputed in the backward pass rather than kept (optimize.rs:79-84).
 constexpr size_t COSTLY_REMAT_ABOVE_BYTES = size_t(2) << 30;
 
 bool splat(const Graph& g, uint32_t id, double* value) {
@@ -34,7 +34,7 @@ bool splat(const Graph& g, uint32_t id, double* value) {
   return true;
 }
 
-// An existing value equal to the node. Never rewrites `x * 0`: that would hide NaN/Inf in `x`.
+// A node already in the graph that computes the same value, if any. `x * 0` is left alone, since folding it to 0 would lose a NaN or Inf in x.
 int64_t identity(const Graph& g, const Op& op, const std::vector<uint32_t>& ins, const Shape& shape) {
   auto same = [&](uint32_t id) { return g.shape(id) == shape; };
   auto is = [&](uint32_t id, double c) {
@@ -68,7 +68,7 @@ int64_t identity(const Graph& g, const Op& op, const std::vector<uint32_t>& ins,
   }
 }
 
-// Elementwise and cheap enough to compute twice rather than store until the backward pass.
+// Elementwise ops cheap enough that redoing them later costs less than holding their result.
 bool recomputable(const Op& op, bool costly_too) {
   bool elementwise = op.is_unary_elementwise() || op.is_binary_elementwise() || op.kind == RG_OP_WHERE;
   bool costly = op.kind == RG_OP_EXP || op.kind == RG_OP_LOG || op.kind == RG_OP_SIN || op.kind == RG_OP_COS ||
@@ -108,7 +108,7 @@ Simplified rematerialize(const Graph& g, const std::vector<uint32_t>& outputs, c
       for (uint32_t x : n.inputs) retained[x] = true;
     }
   }
-  // Rebuild, cloning dropped values right where the backward pass first needs them.
+  // Emit the graph again; a value that was not kept is recomputed just before its first backward reader.
   Simplified r;
   Graph& h = r.g;
   std::vector<uint32_t> map(g.nodes.size(), UINT32_MAX);
@@ -179,7 +179,7 @@ Simplified simplify(const Graph& g, const std::vector<uint32_t>& outputs, bool d
       ins = {ins[0], ins[0]};
       r.st.simplified++;
     }
-    // Binary kernels broadcast by themselves, so a materialized broadcast is a wasted copy.
+    // Elementwise kernels read broadcast operands directly; an explicit broadcast copy is pure overhead.
     if (op.is_binary_elementwise()) {
       for (int k = 0; k < 2; k++) {
         const Node& n = ng.nodes[ins[k]];
@@ -194,7 +194,7 @@ Simplified simplify(const Graph& g, const std::vector<uint32_t>& outputs, bool d
         }
       }
     }
-    // A transposed operand is read through a flag; the copy then goes away with DCE.
+    // The product reads a transposed operand in place (the ta/tb flags); the transpose node then has no readers and dead-code elimination drops it.
     if (flip_transposes && op.kind == RG_OP_MATMUL) {
       auto flipped = [&](uint32_t id) -> int64_t {
         const Node& n = ng.nodes[id];
@@ -261,7 +261,7 @@ Simplified simplify(const Graph& g, const std::vector<uint32_t>& outputs, bool d
       }
     }
     uint32_t id = op.kind == RG_OP_CONST ? ng.constant(*op.t) : ng.add(op, ins);
-    ng.nodes[id].origin = node.origin;  // only presence is read after this point
+    ng.nodes[id].origin = node.origin;  // later passes only test whether it is set
     backward.resize(ng.nodes.size(), false);
     backward[id] = node.origin >= 0;
     if (!big_const) seen[key] = id;
@@ -325,7 +325,7 @@ Optimized finish(const Simplified& s, OptStats st, bool device) {
   return Optimized{std::move(h.g), std::move(h.out), st};
 }
 
-// Whether reassociating or factoring matrix products could apply at all (optimize.rs:259-281).
+// Cheap pre-check: does the graph contain a chain or sum of products the search could rewrite (optimize.rs:259-281).
 bool has_matrix_structure(const Graph& g, const std::vector<uint32_t>& outputs) {
   std::vector<bool> keep = g.reachable(outputs);
   auto is_product = [&](uint32_t id) {
@@ -406,7 +406,7 @@ Optimized optimize_mode(const Graph& g, const std::vector<uint32_t>& outputs, bo
     CostModel model = device ? CostModel::Device : CostModel::Cpu;
     SearchStats ss;
     auto found = matrix_search(first.g, first.out, model, mode, &ss);
-    // Compare final forms: both sides have folded constants and flagged transposes.
+    // Both graphs are compared after the same clean-up (constants folded, transposes turned into flags).
     ss.cost_before = graph_cost(model, baseline.g, baseline.out);
     std::optional<Simplified> candidate;
     if (found) candidate = simplify(found->first, found->second, device, true);

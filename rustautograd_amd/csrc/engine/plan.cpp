@@ -39,7 +39,7 @@ struct Allocator {
     return s;
   }
   size_t pick(DType d, size_t n, bool exact) {
-    // A small value in a big buffer would pin the big buffer for its whole lifetime.
+    // Reusing a large buffer for a small value would keep the large one busy for as long as the small one lives.
     int64_t best = -1;
     for (size_t k = 0; k < free.size(); k++) {
       size_t s = free[k];
@@ -90,7 +90,7 @@ bool arg_kind(const Shape& s, const Shape& shape, rg_arg_kind* k, size_t* row) {
   return true;
 }
 
-// Rough per-element cost in ns, used only to decide when CPU threads pay off (plan.rs:267-276).
+// Approximate nanoseconds per element; only the CPU plan's threading threshold uses it (plan.rs:267-276).
 double op_cost_ns(const Op& op) {
   switch (op.kind) {
     case RG_OP_EXP: case RG_OP_LOG: case RG_OP_SIN: case RG_OP_COS: case RG_OP_TANH: return 0.6;
@@ -564,9 +564,9 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
       }
       const Node& n = g.nodes[i];
       if (is_alias(g, i)) {
-        aliases.push_back(i);  // reads a value of this level, so it follows the groups
+        aliases.push_back(i);  // its input is produced in this level: emit it after the level's groups
       } else if (dev_fusable(i)) {
-        // The last group of this shape, which earlier members may feed.
+        // Most recent open group of this shape and dtype; its members may feed the node.
         int64_t found = -1;
         for (size_t k = groups.size(); k-- > 0;) {
           const Node& f = g.nodes[groups[k][0]];
@@ -598,8 +598,9 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   return items;
 }
 
-// Greedy fusion: one open group. Instructions independent of the group are emitted first; one
-// that reads a member closes the group, which keeps the group free of cycles (plan.rs:311-350).
+// Greedy fusion with a single open group: an instruction that does not depend on the group is
+// emitted ahead of it, and the first one reading a group member ends the group, so a group can
+// never wait on its own output (plan.rs:311-350).
 std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const std::vector<bool>& keep_all,
                            const std::vector<uint32_t>& outputs, const Fuse& cfg, const std::vector<bool>& abs,
                            const std::vector<int64_t>& claimed, const std::vector<std::vector<uint32_t>>& attn_inputs) {
@@ -991,7 +992,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
           if (std::find(external.begin(), external.end(), x) == external.end()) external.push_back(x);
         }
       }
-      // Destinations come first so they can never share a buffer with an input.
+      // Output buffers are assigned before the step's inputs are released, so an output never lands on an input's buffer.
       std::vector<std::pair<size_t, size_t>> out_slots;
       for (size_t m : members) {
         if (uses[m] > 0) {
@@ -1032,7 +1033,7 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       if (uses[x] == 0) dying.push_back(x);
     std::sort(dying.begin(), dying.end());
     dying.erase(std::unique(dying.begin(), dying.end()), dying.end());
-    // A dying same-shape argument of an elementwise op can be overwritten in place.
+    // An elementwise op may write over an argument of its own shape whose last reader it is.
     bool elementwise = node.op.is_unary_elementwise() || node.op.is_binary_elementwise();
     auto inplace = [&](uint32_t x) {
       return elementwise && in.mode != RG_MODE_GENERAL && g.shape(x) == node.shape && g.dtype(x) == node.dtype;

@@ -184,7 +184,7 @@ struct Plan {
   void serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) const;
 };
 
-// Linear-scan liveness; reuse=false gives every value its own buffer (plan.rs:462-465).
+// Buffer assignment by last use, scanning steps in order; with reuse=false no buffer is shared (plan.rs:462-465).
 Plan build_plan(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse);
 // Buffer reuse plus fused groups (plan.rs:466-479).
 Plan build_fused(const Graph& g, const std::vector<uint32_t>& outputs, const Fuse& cfg);

@@ -73,7 +73,7 @@ struct Classified {
   const char *code, *cause, *certainty;
 };
 
-// Root-cause rule given finite inputs and a non-finite output (validate.rs:95-128).
+// Classifies why an op turned finite inputs into a non-finite output (validate.rs:95-128).
 Classified classify(const Instr& i, const std::vector<Stats>& args, const Stats& out) {
   switch (i.op.kind) {
     case RG_OP_EXP: return {"NUMERIC_OVERFLOW", "exponential_overflow", "verified"};
@@ -196,8 +196,9 @@ std::vector<uint32_t> Compiled::raw_outputs() const {
   return all;
 }
 
-// Instrumented run of the unoptimized plan, so node ids and sources match the trace
-// (validate.rs:537-565, observer at 132-230). Runs on the compiled device, one step at a time.
+// Observes every node of the plan built from the traced graph as written (no optimization), so
+// each finding carries the node id and source line the user traced (validate.rs:537-565,
+// observer at 132-230). Runs on the compiled device, one step at a time.
 Compiled::Observed Compiled::observed(const std::vector<Tensor>& inputs) {
   Observed o;
   std::vector<bool> keep = raw.reachable(raw_outputs());
@@ -806,7 +807,7 @@ RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, cons
     auto got = e->prefix_all(reads);
     for (size_t j = 0; j < at.size(); j++) r.outputs[at[j]] = std::move(got[j]);
   };
-  // State moves by swapping buffers when the output's slot is private and the same size.
+  // Handoff by exchanging buffers where possible: the output slot must be unpinned, used by one state entry, and of the input's size; otherwise the values are copied.
   std::vector<size_t> out_slots;
   for (auto& [i, o] : spec.state) out_slots.push_back(p.outputs[o].slot);
   std::vector<std::pair<size_t, size_t>> swaps;
@@ -979,7 +980,7 @@ bool has_equivalence_failure(const Json& report) {
 std::unique_ptr<Compiled> compile_mode(const Graph& raw, const std::vector<uint32_t>& outputs, const std::vector<Tensor>& examples,
                                        Level level, Backend* device, OptMode mode) {
   if (mode == OptMode::Auto) {
-    // Lets the hardware decide between the plain plan and the rewritten one (validate.rs:437-473).
+    // optimize="auto": time the standard and the rewritten plan on the examples and keep the faster (validate.rs:437-473).
     auto standard = build(raw, outputs, examples, Level::None, device, OptMode::Standard);
     auto searched = compile_mode(raw, outputs, examples, Level::Basic, device, OptMode::SearchLinear);
     bool rewritten = searched->opt_stats.searched && searched->opt_stats.accepted;

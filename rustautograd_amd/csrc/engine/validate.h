@@ -14,7 +14,7 @@ bool parse_level(const std::string& s, Level* out);
 struct RunSpec {
   std::vector<std::pair<size_t, size_t>> state;  // (input index, output index) fed back
   std::vector<size_t> data;                      // data input indices
-  std::vector<size_t> history;                   // scalar outputs recorded per step
+  std::vector<size_t> history;                   // outputs whose single value is logged after each step
   // Outputs fed back into the state hold the same values as the final state: when set, `run`
   // does not read them a second time and leaves them empty (shape kept, no data).
   bool skip_state_outputs = false;
@@ -25,7 +25,7 @@ struct RunOut {
   std::vector<std::vector<double>> history;
   size_t steps = 0;
   int64_t nonfinite_step = -1;
-  double seconds = 0;  // time in the step loop, excluding one-time setup
+  double seconds = 0;  // seconds spent stepping; loading state and setup are not counted
   std::optional<std::string> device_error;
 };
 
@@ -49,7 +49,7 @@ class Compiled {
   void validate_spec(const RunSpec& spec) const;
   RunOut run(const RunSpec& spec, const std::vector<Tensor>& state, const std::vector<std::vector<Tensor>>& batches,
              size_t steps) const;
-  // First step at which the state or an output turns non-finite: (step, batch, state before).
+  // Replays one step at a time until the state or an output goes non-finite; returns that step, its batch index and the state it started from.
   std::optional<std::tuple<size_t, size_t, std::vector<Tensor>>> replay(const RunSpec& spec, const std::vector<Tensor>& state,
                                                                        const std::vector<std::vector<Tensor>>& batches,
                                                                        size_t steps) const;

@@ -38,7 +38,7 @@ struct Strided {
 // dims that are contiguous for every operand and dropping size-1 dims.
 Strided make_strided(const std::vector<int64_t>& shape, const std::vector<std::vector<int64_t>>& strides);
 std::vector<int64_t> row_strides(const std::vector<int64_t>& shape);
-// Strides of `shape` right-aligned to `rank` dims with 0 on broadcast dims.
+// Per-dimension element strides of an operand aligned to the output's trailing dims; broadcast dims read stride 0.
 std::vector<int64_t> bcast_strides(const std::vector<int64_t>& shape, size_t rank);
 
 void unary(hipStream_t s, int dtype, int op, const void* a, void* d, uint64_t n);

@@ -337,7 +337,7 @@ __global__ void __launch_bounds__(TPB) k_argmax(const T* __restrict__ a, int* __
   d[r] = (int)best;
 }
 
-// Rank order of src/plan.rs:838-848: larger first, ties by index, NaN last.
+// Ranking of src/plan.rs:838-848: a value ranks ahead when greater, or equal with a lower position; NaN ranks behind all.
 template <class T>
 __device__ __forceinline__ bool before(const T* row, uint32_t x, uint32_t y) {
   T p = row[x], q = row[y];

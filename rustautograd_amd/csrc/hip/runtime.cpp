@@ -172,7 +172,7 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
   base.n = n;
   base.k = k;
   if (bb.empty() && !ta) {
-    // Row-major batches of the left operand form one matrix: a single product (plan.rs:1471-1475).
+    // With a 2-D right operand and no transposed left one, the left operand's batch dims fold into its rows: one product (plan.rs:1471-1475).
     base.m = prod(ba) * m;
     base.batch = 1;
   } else {

@@ -1,112 +1,140 @@
-"""Optimizers as pure functions: `opt.init(params)` builds the state and
-`opt.update(grads, state, params)` returns `(new_params, new_state)`. Both trace like any other
-function, so the whole update compiles into the step (reference python/rg/optim.py).
+"""Optimizers as pairs of pure functions, traced into the compiled step like everything else.
+
+`opt = adamw(3e-4)`; `state = opt.init(params)`; `params, state = opt.update(grads, state, params)`.
+The state is a tree (a step counter plus per-parameter moments), so it lives in the run loop's
+state next to the parameters. Each update is written with the arithmetic, in the order, of the
+reference's python/rg/optim.py, so the same training run rounds the same way.
 """
 
 import math
-from typing import Callable, NamedTuple
+import typing
 
 from . import tree
-from ._core import cos, full, maximum, minimum, where, zeros_like
+from .ops import cos, full, maximum, minimum, where, zeros_like
 
 
-class Optimizer(NamedTuple):
-    init: Callable
-    update: Callable
+class Optimizer(typing.NamedTuple):
+    init: typing.Callable    # params -> state
+    update: typing.Callable  # (grads, state, params) -> (new params, new state)
 
+
+# ---- learning-rate schedules: count -> rate ----
 
 def constant(lr):
     return lambda count: lr
 
 
 def cosine_decay(lr, total_steps, warmup_steps=0, min_lr=0.0):
-    """Linear warmup, then a cosine from `lr` to `min_lr`."""
+    """A linear warm-up over `warmup_steps`, then half a cosine from `lr` down to `min_lr` at
+    `total_steps`."""
+    span = max(1, total_steps - warmup_steps)
 
-    def schedule(count):
-        t = minimum((count - warmup_steps) / max(1, total_steps - warmup_steps), 1.0)
-        decayed = min_lr + (lr - min_lr) * 0.5 * (1.0 + cos(math.pi * maximum(t, 0.0)))
-        if not warmup_steps:
-            return decayed
-        return where(count >= warmup_steps, decayed, lr * (count + 1.0) / warmup_steps)
-    return schedule
+    def rate(count):
+        progress = minimum((count - warmup_steps) / span, 1.0)
+        cosine = min_lr + (lr - min_lr) * 0.5 * (1.0 + cos(math.pi * maximum(progress, 0.0)))
+        if warmup_steps == 0:
+            return cosine
+        return where(count >= warmup_steps, cosine, lr * (count + 1.0) / warmup_steps)
+
+    return rate
 
 
-def _schedule(lr):
-    return lr if callable(lr) else constant(lr)
+def _as_schedule(lr):
+    if callable(lr):
+        return lr
+    return constant(lr)
 
+
+# ---- gradient transformations ----
 
 def clip_by_global_norm(grads, max_norm):
-    """Scales gradients down so their joint L2 norm is at most `max_norm`."""
-    norm = tree.global_norm(grads)
-    scale = max_norm / where(norm >= max_norm, norm, max_norm)
-    return tree.map(lambda g: g * scale, grads)
+    """`grads` scaled so that their joint L2 norm is at most `max_norm`."""
+    total = tree.global_norm(grads)
+    factor = max_norm / where(total >= max_norm, total, max_norm)
+    return tree.map(lambda g: g * factor, grads)
 
 
-def _dtype(params):
-    return tree.leaves(params)[0].dtype
+def _prepare(grads, max_grad_norm):
+    if not max_grad_norm:
+        return grads
+    return clip_by_global_norm(grads, max_grad_norm)
 
 
-def _clip(grads, max_grad_norm):
-    return clip_by_global_norm(grads, max_grad_norm) if max_grad_norm else grads
+def _counter(params):
+    """The step counter, a scalar of the parameters' dtype starting at 0."""
+    return full((), 0, tree.leaves(params)[0].dtype)
 
+
+def _zeros_like_tree(params):
+    return tree.map(zeros_like, params)
+
+
+# ---- optimizers ----
 
 def sgd(lr, momentum=0.0, max_grad_norm=None):
-    schedule = _schedule(lr)
+    """Gradient descent, with heavy-ball momentum when `momentum` > 0."""
+    schedule = _as_schedule(lr)
 
     def init(params):
-        return {"count": full((), 0, _dtype(params)), "velocity": tree.map(zeros_like, params)}
+        return {"count": _counter(params), "velocity": _zeros_like_tree(params)}
 
     def update(grads, state, params):
-        grads = _clip(grads, max_grad_norm)
-        rate = schedule(state["count"])
-        v = tree.map(lambda m, g: momentum * m + g, state["velocity"], grads) if momentum else grads
-        new = tree.map(lambda p, d: p - rate * d, params, v)
-        return new, {"count": state["count"] + 1.0, "velocity": v if momentum else state["velocity"]}
+        grads = _prepare(grads, max_grad_norm)
+        lr_now = schedule(state["count"])
+        velocity = tree.map(lambda v, g: momentum * v + g, state["velocity"], grads) if momentum else state["velocity"]
+        direction = velocity if momentum else grads
+        new_params = tree.map(lambda p, d: p - lr_now * d, params, direction)
+        return new_params, {"count": state["count"] + 1.0, "velocity": velocity}
 
-    return Optimizer(init, update)
+    return Optimizer(init=init, update=update)
 
 
 def rmsprop(lr, decay=0.9, eps=1e-8, max_grad_norm=None):
-    schedule = _schedule(lr)
+    """Steps scaled by a running average of squared gradients."""
+    schedule = _as_schedule(lr)
 
     def init(params):
-        return {"count": full((), 0, _dtype(params)), "square": tree.map(zeros_like, params)}
+        return {"count": _counter(params), "square": _zeros_like_tree(params)}
 
     def update(grads, state, params):
-        grads = _clip(grads, max_grad_norm)
-        rate = schedule(state["count"])
-        sq = tree.map(lambda s, g: decay * s + (1.0 - decay) * (g * g), state["square"], grads)
-        new = tree.map(lambda p, g, s: p - rate * g / (s.sqrt() + eps), params, grads, sq)
-        return new, {"count": state["count"] + 1.0, "square": sq}
+        grads = _prepare(grads, max_grad_norm)
+        lr_now = schedule(state["count"])
+        square = tree.map(lambda s, g: decay * s + (1.0 - decay) * (g * g), state["square"], grads)
+        new_params = tree.map(lambda p, g, s: p - lr_now * g / (s.sqrt() + eps), params, grads, square)
+        return new_params, {"count": state["count"] + 1.0, "square": square}
 
-    return Optimizer(init, update)
+    return Optimizer(init=init, update=update)
 
 
 def adamw(lr, b1=0.9, b2=0.999, eps=1e-8, weight_decay=0.01, decay_filter=None, max_grad_norm=None):
-    """Adam with decoupled weight decay; by default matrices decay, biases and norm scales do not."""
-    schedule = _schedule(lr)
-    decays = decay_filter or (lambda p: p.ndim >= 2)
+    """Adam with decoupled weight decay. `decay_filter(param)` says which parameters decay; by
+    default those with two or more dimensions (matrices), not biases or normalization scales."""
+    schedule = _as_schedule(lr)
+    decays = decay_filter if decay_filter is not None else (lambda param: param.ndim > 1)
 
     def init(params):
-        return {"count": full((), 0, _dtype(params)), "mu": tree.map(zeros_like, params), "nu": tree.map(zeros_like, params)}
+        return {"count": _counter(params), "mu": _zeros_like_tree(params), "nu": _zeros_like_tree(params)}
 
     def update(grads, state, params):
-        grads = _clip(grads, max_grad_norm)
+        grads = _prepare(grads, max_grad_norm)
         t = state["count"] + 1.0
-        rate = schedule(state["count"])
-        mu = tree.map(lambda m, g: b1 * m + (1.0 - b1) * g, state["mu"], grads)
-        nu = tree.map(lambda n, g: b2 * n + (1.0 - b2) * (g * g), state["nu"], grads)
-        c1, c2 = 1.0 - b1 ** t, 1.0 - b2 ** t
+        lr_now = schedule(state["count"])
+        first = lambda m, g: b1 * m + (1.0 - b1) * g
+        mu = tree.map(first, state["mu"], grads)
+        nu = tree.map(lambda v, g: b2 * v + (1.0 - b2) * (g * g), state["nu"], grads)
+        unbias1, unbias2 = 1.0 - b1 ** t, 1.0 - b2 ** t
 
-        def step(p, m, n):
-            d = (m / c1) / ((n / c2).sqrt() + eps)
-            if weight_decay and decays(p):
-                d = d + weight_decay * p
-            return p - rate * d
-        return tree.map(step, params, mu, nu), {"count": t, "mu": mu, "nu": nu}
+        def apply_one(p, m, v):
+            direction = (m / unbias1) / ((v / unbias2).sqrt() + eps)
+            if weight_decay != 0.0 and decays(p):
+                direction = direction + weight_decay * p
+            return p - lr_now * direction
 
-    return Optimizer(init, update)
+        return tree.map(apply_one, params, mu, nu), {"count": t, "mu": mu, "nu": nu}
+
+    return Optimizer(init=init, update=update)
 
 
 def adam(lr, b1=0.9, b2=0.999, eps=1e-8, max_grad_norm=None):
-    return adamw(lr, b1, b2, eps, weight_decay=0.0, max_grad_norm=max_grad_norm)
+    """adamw without weight decay."""
+    return adamw(lr, b1=b1, b2=b2, eps=eps, weight_decay=0.0, max_grad_norm=max_grad_norm)

@@ -1,54 +1,69 @@
-"""Explicit, splittable random numbers: every function is pure in its key.
+"""Counter-based random numbers with explicit keys.
 
-Keys are int32 pairs; streams are SplitMix64 of (key, index), so the same key gives the same
-numbers on every device and thread count (reference python/rg/random.py, src/plan.rs:1391-1435).
+A key is an int32 pair holding one 64-bit SplitMix64 state (high word first). Every draw is a
+pure function of its key and its shape: the same key gives the same numbers on any device and
+thread count, so a step that carries its key in the state can be replayed exactly. The engine's
+`random_uniform`, `random_normal` and `key_split` operations do the bit work; the key packing and
+the derived draws (integers, Bernoulli, Gumbel, categorical) are those of the reference's
+python/rg/random.py.
 """
 
-from ._core import _op, argmax, floor, log, maximum, tensor
+import numpy as np
 
-_GAMMA = 0x9E3779B97F4A7C15
+from .ops import argmax, floor, log, maximum
+from .tensor import apply, tensor
+
+_GOLDEN_GAMMA = 0x9E3779B97F4A7C15  # the SplitMix64 increment
 
 
 def key(seed):
-    """A key from an integer seed: seed * GAMMA mod 2**64, split into signed hi and lo words."""
-    mixed = seed * _GAMMA % (1 << 64)
-    signed = lambda v: v - (1 << 32) if v >= (1 << 31) else v
-    return tensor([signed(mixed >> 32), signed(mixed & 0xFFFFFFFF)], "int32")
+    """The key for an integer seed: seed * gamma mod 2^64, as (high, low) int32 words."""
+    state = (int(seed) * _GOLDEN_GAMMA) % (1 << 64)
+    words = np.array([state >> 32, state & 0xFFFFFFFF], dtype=np.uint32).view(np.int32)
+    return tensor(words, "int32")
 
 
 def split(k, n=2):
-    """`n` independent keys, as a tensor of shape (n, 2) that unpacks into keys."""
-    return _op("key_split", k, n=n)
+    """`n` new independent keys as an (n, 2) tensor; unpacking it gives the keys."""
+    return apply("key_split", k, n=n)
+
+
+def _unit(k, shape, dtype):
+    return apply("random_uniform", k, shape=list(shape), dtype=dtype)
 
 
 def uniform(k, shape=(), dtype="float32", low=0.0, high=1.0):
-    """Uniform floats in [low, high)."""
-    u = _op("random_uniform", k, shape=list(shape), dtype=dtype)
-    return u if low == 0.0 and high == 1.0 else low + (high - low) * u
+    """Uniform values in [low, high)."""
+    u = _unit(k, shape, dtype)
+    if (low, high) == (0.0, 1.0):
+        return u
+    return low + (high - low) * u
 
 
 def normal(k, shape=(), dtype="float32"):
-    """Standard normal floats (Box-Muller in float64, then rounded to `dtype`)."""
-    return _op("random_normal", k, shape=list(shape), dtype=dtype)
+    """Standard normal values (Box-Muller in float64, rounded to `dtype`)."""
+    return apply("random_normal", k, shape=list(shape), dtype=dtype)
 
 
 def randint(k, shape, low, high):
-    """Uniform int32 in [low, high). Drawn in float64 so every integer of a wide range is reachable."""
-    u = _op("random_uniform", k, shape=list(shape), dtype="float64")
-    return floor(low + (high - low) * u).cast("int32")
+    """Uniform int32 values in [low, high). The draw is made in float64, so every integer of a
+    range wider than 2^24 stays reachable."""
+    u64 = _unit(k, shape, "float64")
+    return floor(low + (high - low) * u64).cast("int32")
 
 
 def bernoulli(k, p=0.5, shape=(), dtype="float32"):
-    """1 with probability `p`, else 0, as floats."""
-    return _op("gt", tensor(float(p), dtype), _op("random_uniform", k, shape=list(shape), dtype=dtype))
+    """1 with probability `p` and 0 otherwise, in `dtype`."""
+    return apply("gt", tensor(float(p), dtype), _unit(k, shape, dtype))
 
 
 def gumbel(k, shape=(), dtype="float32"):
-    u = _op("random_uniform", k, shape=list(shape), dtype=dtype)
-    eps = 1e-7 if dtype == "float32" else 1e-15
-    return -log(-log(maximum(u, eps)))
+    """Standard Gumbel values, -log(-log(u)) with u kept away from 0."""
+    tiny = 1e-7 if dtype == "float32" else 1e-15
+    return -log(-log(maximum(_unit(k, shape, dtype), tiny)))
 
 
 def categorical(k, logits, axis=-1):
-    """Indices sampled from unnormalized log-probabilities with the Gumbel-max trick."""
-    return argmax(logits + gumbel(k, logits.shape, logits.dtype), axis)
+    """Indices drawn from the distribution softmax(logits) along `axis` (Gumbel-max)."""
+    noise = gumbel(k, logits.shape, logits.dtype)
+    return argmax(logits + noise, axis)

@@ -1,50 +1,61 @@
-"""Nested tuples, lists and dicts of tensors ("trees"): leaves, structure, map, names, sizes.
+"""Trees: nested tuples, lists and dicts of tensors, such as parameters and optimizer state.
 
-Same contract as the reference's python/rg/tree.py; dict keys flatten in sorted order.
+Leaves are visited in a fixed order (dict keys sorted), which is the order of a compiled
+program's inputs and of checkpoint entries. Names are dotted paths: `blocks.0.attn.qkv.w`.
 """
 
-from ._core import _flatten, _unflatten
+import builtins
+
+from . import _pytree
 
 
 def leaves(t):
-    """The tensors of a tree, in a stable order (dict keys sorted)."""
-    return _flatten(t)[0]
+    """The leaves of `t` in their fixed order."""
+    return _pytree.leaves(t)
 
 
 def structure(t):
-    """A comparable description of the tree's shape, ignoring its leaves."""
-    return _flatten(t)[1]
-
-
-def map(f, t, *rest):
-    """Applies `f` leaf by leaf across trees of the same structure."""
-    ls, d = _flatten(t)
-    others = [_flatten(r) for r in rest]
-    if any(o[1] != d for o in others):
-        raise ValueError("tree.map needs trees of the same structure")
-    return _unflatten(d, [f(*vals) for vals in zip(ls, *(o[0] for o in others))])
+    """A comparable description of `t` without its leaves."""
+    return _pytree.structure(t)
 
 
 def unflatten(structure_, values):
-    return _unflatten(structure_, values)
+    """The tree of `structure_` holding `values` in leaf order."""
+    return _pytree.unflatten(structure_, values)
+
+
+def map(f, t, *rest):
+    """`f` applied leaf by leaf to `t` and trees of the same structure."""
+    vals, treedef = _pytree.flatten(t)
+    columns = [vals]
+    for other in rest:
+        ov, od = _pytree.flatten(other)
+        if od != treedef:
+            raise ValueError("tree.map needs trees of the same structure")
+        columns.append(ov)
+    return _pytree.unflatten(treedef, [f(*row) for row in zip(*columns)])
 
 
 def paths(t, prefix=""):
-    """(dotted name, leaf) pairs."""
+    """(name, leaf) pairs in leaf order; `prefix` is put before every name."""
     if t is None:
         return []
-    if isinstance(t, dict):
-        return [p for k in sorted(t) for p in paths(t[k], f"{prefix}{k}.")]
-    if isinstance(t, (tuple, list)):
-        return [p for i, v in enumerate(t) for p in paths(v, f"{prefix}{i}.")]
-    return [(prefix[:-1], t)]
+    vals, treedef = _pytree.flatten(t)
+    names = treedef.paths()
+    if treedef.kind == "leaf":
+        return [(prefix[:-1] if prefix.endswith(".") else prefix, vals[0])]
+    return [(prefix + name, v) for name, v in zip(names, vals)]
 
 
 def size(t):
-    """Total number of elements."""
-    return sum(l.size for l in leaves(t))
+    """Number of elements over all leaves."""
+    return builtins.sum(leaf.size for leaf in leaves(t))
 
 
 def global_norm(t):
-    """L2 norm over all leaves together."""
-    return sum((l * l).sum() for l in leaves(t)).sqrt()
+    """The L2 norm of all leaves taken together."""
+    total = None
+    for leaf in leaves(t):
+        sq = (leaf * leaf).sum()
+        total = sq if total is None else total + sq
+    return total.sqrt()

@@ -62,8 +62,7 @@ def mlp_train_step(cfg=MLPConfig()):
         p, o = opt.update(grads, state["opt"], state["params"])
         return {"params": p, "opt": o, "key": k_next}, value
 
-    state = {"params": params, "opt": opt.init(params), "key": random.key(1)}
-    return step, state
+    return step, dict(params=params, opt=opt.init(params), key=random.key(1))
 
 
 # ---- C3 / C4: character-level GPT -------------------------------------------------------------
@@ -86,38 +85,40 @@ GPT_CONFIGS = {
 
 
 class GPT:
-    """examples/gpt.py:20-47 of the reference; `tied` reads the head from the token table."""
+    """The character-level GPT of the reference's examples/gpt.py:20-47: token and position
+    embeddings, pre-norm transformer blocks under a causal mask, a final layer norm and a linear
+    head (read from the token table when `tied`). `init` spends split keys in the example's
+    order: token table, position table, head, then one key per block."""
 
     def __init__(self, vocab, block, d=128, heads=4, layers=4, tied=False):
-        self.block = block
-        self.tied = tied
-        self.tok = nn.Embedding(vocab, d)
-        self.pos = nn.Embedding(block, d)
-        self.blocks = [nn.TransformerBlock(d, heads) for _ in range(layers)]
-        self.norm = nn.LayerNorm(d)
-        self.head = nn.Linear(d, vocab, bias=False)
-        self.mask = rg.tril(block)
+        self.block, self.tied = block, tied
+        self.layers = {
+            "tok": nn.Embedding(vocab, d),
+            "pos": nn.Embedding(block, d),
+            "norm": nn.LayerNorm(d),
+            "head": nn.Linear(d, vocab, bias=False),
+        }
+        self.stack = [nn.TransformerBlock(d, heads) for _ in range(layers)]
+        self.causal = rg.tril(block)
 
     def init(self, key):
-        keys = random.split(key, len(self.blocks) + 3)
-        p = {
-            "tok": self.tok.init(keys[0]),
-            "pos": self.pos.init(keys[1]),
-            "norm": self.norm.init(),
-            "blocks": [b.init(keys[3 + i]) for i, b in enumerate(self.blocks)],
-        }
+        k_tok, k_pos, k_head, *k_blocks = random.split(key, len(self.stack) + 3)
+        params = {"tok": self.layers["tok"].init(k_tok), "pos": self.layers["pos"].init(k_pos), "norm": self.layers["norm"].init(),
+                  "blocks": [blk.init(kb) for blk, kb in zip(self.stack, k_blocks)]}
         if not self.tied:
-            p["head"] = self.head.init(keys[2])
-        return p
+            params["head"] = self.layers["head"].init(k_head)
+        return params
 
-    def __call__(self, p, idx):
-        t = idx.shape[1]
-        x = self.tok(p["tok"], idx) + self.pos(p["pos"], rg.arange(t))
-        mask = self.mask[:t, :t]
-        for i, b in enumerate(self.blocks):
-            x = b(p["blocks"][i], x, mask)
-        h = self.norm(p["norm"], x)
-        return h @ p["tok"]["table"].T if self.tied else self.head(p["head"], h)
+    def __call__(self, params, idx):
+        length = idx.shape[1]
+        h = self.layers["tok"](params["tok"], idx) + self.layers["pos"](params["pos"], rg.arange(length))
+        visible = self.causal[:length, :length]
+        for blk, p_blk in zip(self.stack, params["blocks"]):
+            h = blk(p_blk, h, visible)
+        h = self.layers["norm"](params["norm"], h)
+        if self.tied:
+            return h @ params["tok"]["table"].T
+        return self.layers["head"](params["head"], h)
 
 
 def gpt_train_step(cfg):
@@ -139,8 +140,7 @@ def gpt_train_step(cfg):
         p, o = opt.update(grads, state["opt"], state["params"])
         return {"params": p, "opt": o, "key": k_next}, value
 
-    state = {"params": params, "opt": opt.init(params), "key": random.key(1)}
-    return step, state
+    return step, dict(params=params, opt=opt.init(params), key=random.key(1))
 
 
 def gpt_gemm_flops(cfg):

@@ -48,11 +48,11 @@ def pytest_configure(config):
 @pytest.fixture(autouse=True)
 def _default_device(request):
     """Tests without the gpu marker run the engine on the CPU oracle; gpu tests use "hip"."""
-    from rustautograd_amd import _core
-    saved = _core.DEFAULT_DEVICE
-    _core.DEFAULT_DEVICE = "hip" if "gpu" in request.keywords else "cpu"
+    from rustautograd_amd import program
+    saved = program.DEFAULT_DEVICE
+    program.DEFAULT_DEVICE = "hip" if "gpu" in request.keywords else "cpu"
     yield
-    _core.DEFAULT_DEVICE = saved
+    program.DEFAULT_DEVICE = saved
 
 
 def pytest_collection_modifyitems(config, items):

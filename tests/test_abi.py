@@ -117,16 +117,14 @@ def test_c3_program_compiles_for_gfx950():
     """Every fused kernel of a whole GPT training step (C3 at reduced depth) compiles."""
     cfg = workloads.GPT_CONFIGS["C3"]._replace(batch=2, block=16, layers=1)
     step, state = workloads.gpt_train_step(cfg)
-    from rustautograd_amd import _core
-    leaves, in_def = _core._as_tensors((state,))
+    from rustautograd_amd import _pytree
+    from rustautograd_amd.tensor import Tracer, lift, tracing
+    leaves, in_def = _pytree.flatten((state,))
     g = _rg.Graph()
-    tracers = [_core.Tracer(g, g.input(list(t.shape), t.dtype, None)) for t in leaves]
-    _core._traces.append(g)
-    try:
-        out = step(*_core._unflatten(in_def, tracers))
-        ids = [_core._node(g, leaf, "float32") for leaf in _core._flatten(out)[0]]
-    finally:
-        _core._traces.pop()
+    tracers = [Tracer(g, g.input(list(t.shape), t.dtype, None)) for t in leaves]
+    with tracing(g):
+        out = step(*_pytree.unflatten(in_def, tracers))
+        ids = [lift(g, leaf, "float32") for leaf in _pytree.leaves(out)]
     words, _ = _rg.plan_words(g, ids, "hip", "search-linear")
     n, err = _compile_check(words)
     assert n >= 10, err

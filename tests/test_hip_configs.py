@@ -13,7 +13,7 @@ import pytest
 import rustautograd_amd as rg
 from rustautograd_amd import workloads
 from rustautograd_amd import tree as rtree
-from rustautograd_amd._core import _paths
+
 from helpers import close
 
 pytestmark = pytest.mark.gpu
@@ -30,7 +30,7 @@ def _device_check(c, key_bias_d=None):
         assert c.report.ok, c.report["diagnostics"]
         return dev
     assert dev["detail"]["max_relative_error"] < 0.05, dev
-    names = _paths(c._out_def, "out")
+    names = c._out_def.paths("out")
     for d in c.report["diagnostics"]:
         assert d["code"] == "DEVICE_MISMATCH", d
         name, element = names[d["observation"]["output_index"]], d["observation"]["element"]

@@ -280,8 +280,8 @@ def test_small_gpt_loss_curve_overlays_cpu():
     # rounding noise that Adam scales to +-lr; a DEVICE_MISMATCH may only point there.
     dev = checks["device_equivalence"]
     assert dev["detail"]["max_relative_error"] < 0.05, dev
-    from rustautograd_amd._core import _paths
-    names = _paths(gpu._out_def, "out")
+
+    names = gpu._out_def.paths("out")
     for d in gpu.report["diagnostics"]:
         assert d["code"] == "DEVICE_MISMATCH", d
         name, element = names[d["observation"]["output_index"]], d["observation"]["element"]
