@@ -227,6 +227,44 @@ void gemm(size_t m, size_t k, size_t n, const T* a, bool ta, const T* b, bool tb
   }
 }
 
+// Checker-only form of `gemm` (row-parallel mode): rows [r0, r1) of the product, with the
+// right operand given as a contiguous k x n panel. Columns are taken 256 at a time and, for
+// each p, every row of the block adds its term, so a B row segment is loaded once per block of
+// rows; each output element still receives its terms in increasing p, one rounding per add
+// and per multiply, exactly as `gemm` does: the results are bit-identical.
+template <class T>
+void gemm_rows_blocked(size_t m, size_t k, size_t n, const T* a, bool ta, const T* bk, T* out, size_t r0, size_t r1) {
+  constexpr size_t JB = 256;
+  for (size_t i = r0; i < r1; i++) std::fill(out + i * n, out + i * n + n, (T)0);
+  for (size_t j0 = 0; j0 < n; j0 += JB) {
+    size_t j1 = std::min(n, j0 + JB);
+    for (size_t p = 0; p < k; p++) {
+      const T* bp = bk + p * n;
+      for (size_t i = r0; i < r1; i++) {
+        T x = ta ? a[p * m + i] : a[i * k + p];
+        T* row = out + i * n;
+        for (size_t j = j0; j < j1; j++) row[j] = row[j] + x * bp[j];
+      }
+    }
+  }
+}
+
+// The whole product on every thread, row blocks of 32 (checker-only; see gemm_rows_blocked).
+template <class T>
+void gemm_checker(size_t m, size_t k, size_t n, const T* a, bool ta, const T* b, bool tb, T* out) {
+  std::vector<T> panel;
+  const T* bk = b;
+  if (tb) {
+    panel.resize(k * n);
+    for (size_t j = 0; j < n; j++)
+      for (size_t p = 0; p < k; p++) panel[p * n + j] = b[j * k + p];
+    bk = panel.data();
+  }
+  size_t blocks = (m + 31) / 32;
+#pragma omp parallel for schedule(dynamic)
+  for (size_t q = 0; q < blocks; q++) gemm_rows_blocked<T>(m, k, n, a, ta, bk, out, q * 32, std::min(m, q * 32 + 32));
+}
+
 struct Program;
 
 struct Frame {
@@ -482,16 +520,10 @@ void matmul(const Instr& i, std::vector<Buf>& s, bool ta, bool tb) {
   if (bb.empty() && !ta) {
     // A 2-D right operand: the left operand's leading dims stack into rows of one matrix, so one gemm does it.
     size_t rows = prod(ba) * m;
-    if (g_row_parallel_gemm && rows * k * n >= PARALLEL_FLOPS && rows >= 128) {
+    if (g_row_parallel_gemm && rows * k * n >= PARALLEL_FLOPS && rows >= 64) {
       // Checker-only speed-up (off by default, so the CPU baseline stays the reference's serial
-      // loop): blocks of rows on separate threads. Every element keeps its p-ascending sum, so
-      // results are bit-identical to the serial call.
-      size_t blocks = (rows + 63) / 64;
-#pragma omp parallel for schedule(static)
-      for (size_t q = 0; q < blocks; q++) {
-        size_t r0 = q * 64, r1 = std::min(rows, r0 + 64);
-        gemm<T>(r1 - r0, k, n, a + r0 * k, false, b, tb, dst + r0 * n);
-      }
+      // loop): blocked rows on every thread, bit-identical to the serial call.
+      gemm_checker<T>(rows, k, n, a, false, b, tb, dst);
       return;
     }
     gemm<T>(rows, k, n, a, false, b, tb, dst);
@@ -512,6 +544,11 @@ void matmul(const Instr& i, std::vector<Buf>& s, bool ta, bool tb) {
   std::vector<std::array<size_t, 3>> offs;
   walk<3>(batch, st, [&](size_t* off) { offs.push_back({off[0], off[1], off[2]}); });
   bool par = m * k * n * offs.size() >= PARALLEL_FLOPS;
+  if (g_row_parallel_gemm && par && offs.size() < 8 && m >= 64) {
+    // Few large products (the weight gradients): each one spread over the threads instead.
+    for (auto& o : offs) gemm_checker<T>(m, k, n, a + o[1], ta, b + o[2], tb, dst + o[0]);
+    return;
+  }
 #pragma omp parallel for schedule(static) if (par)
   for (size_t q = 0; q < offs.size(); q++) gemm<T>(m, k, n, a + offs[q][1], ta, b + offs[q][2], tb, dst + offs[q][0]);
 }

@@ -601,6 +601,14 @@ Json Compiled::validate(const std::vector<Tensor>& examples) {
       dc["detail"] = info;
       checks.push(dc);
       diagnostics.insert(diagnostics.end(), ds.begin(), ds.end());
+      if (info.get("skipped") && *info.get("skipped") == "no_cpu_reference_backend") {
+        // The product ships no CPU interpreter: say so instead of passing the gate silently.
+        Json obs = Json::obj();
+        obs["device"] = device->name;
+        obs["available"] = Json(available_backends());
+        diagnostics.push_back(diag("DEVICE_CHECK_SKIPPED", "warning", Json(), obs,
+                                   "no_cpu_reference_backend_registered_device_results_unchecked", "verified"));
+      }
     }
   }
   if (level >= Level::Thorough) {

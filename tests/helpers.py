@@ -124,3 +124,79 @@ class G:
 
 def diag_code(excinfo):
     return excinfo.value.diagnostic["code"]
+
+
+# ---- the device C ABI through ctypes (include/rg_hip.h) ----
+
+import ctypes
+
+
+class RunDesc(ctypes.Structure):
+    """rg_run_desc of include/rg_hip.h."""
+    _fields_ = [("n_swaps", ctypes.c_int64), ("swaps", ctypes.POINTER(ctypes.c_int64)),
+                ("n_copies", ctypes.c_int64), ("copies", ctypes.POINTER(ctypes.c_int64)),
+                ("n_data", ctypes.c_int64), ("data_slots", ctypes.POINTER(ctypes.c_int64)),
+                ("data_bytes", ctypes.POINTER(ctypes.c_uint64)), ("n_batches", ctypes.c_int64),
+                ("batches", ctypes.POINTER(ctypes.c_void_p)), ("n_history", ctypes.c_int64),
+                ("history_slots", ctypes.POINTER(ctypes.c_int64)), ("steps", ctypes.c_int64),
+                ("history", ctypes.POINTER(ctypes.c_double))]
+
+
+class RunResult(ctypes.Structure):
+    """rg_run_result of include/rg_hip.h."""
+    _fields_ = [("done", ctypes.c_int64), ("nonfinite_step", ctypes.c_int64), ("seconds", ctypes.c_double)]
+
+
+def plan_io(words):
+    """Input slots and output slots of a flat plan (include/rg_plan.h: header, slots, consts,
+    inputs, outputs)."""
+    k = 2
+    k += 1 + 3 * words[k]
+    k += 1 + 3 * words[k]
+    n = words[k]
+    inputs = [words[k + 1 + 2 * j] for j in range(n)]
+    k += 1 + 2 * n
+    n = words[k]
+    k += 1
+    outputs = []
+    for _ in range(n):
+        outputs.append(words[k])
+        k += 3 + words[k + 2]
+    return inputs, outputs
+
+
+def hip_abi():
+    """librg_hip.so with argument and result types set for the entry points tests call."""
+    from rustautograd_amd import _native
+    lib = ctypes.CDLL(_native.HIP_LIBRARY)
+    vp, i64, u64, cp, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t
+    lib.rg_hip_program_new.restype = vp
+    lib.rg_hip_program_new.argtypes = [ctypes.POINTER(i64), sz, cp, sz, cp, sz]
+    lib.rg_hip_exec_new.restype = vp
+    lib.rg_hip_exec_new.argtypes = [vp, cp, sz]
+    for name in ("rg_hip_exec_free", "rg_hip_program_free", "rg_hip_program_inject_failure"):
+        getattr(lib, name).argtypes = [vp]
+    lib.rg_hip_program_inject_failure_after.argtypes = [vp, i64]
+    lib.rg_hip_exec_write.argtypes = [vp, i64, vp, u64]
+    lib.rg_hip_exec_read.argtypes = [vp, i64, vp, u64]
+    for name in ("rg_hip_exec_run", "rg_hip_exec_run_noalloc"):
+        getattr(lib, name).argtypes = [vp, ctypes.POINTER(RunDesc), ctypes.POINTER(RunResult)]
+    lib.rg_hip_exec_failure.argtypes = [vp, cp, sz]
+    return lib
+
+
+def hip_program(lib, graph, outputs, optimize="none"):
+    """A device program for `outputs` of `graph`, built through the C ABI: (handle, inputs, outputs)."""
+    from rustautograd_amd import _rg
+    words, blob = _rg.plan_words(graph, list(outputs), "hip", optimize)
+    ins, outs = plan_io(words)
+    arr = (ctypes.c_int64 * len(words))(*words)
+    err = ctypes.create_string_buffer(4096)
+    prog = lib.rg_hip_program_new(arr, len(words), blob, len(blob), err, len(err))
+    assert prog, err.value
+    return prog, ins, outs
+
+
+def exec_failure(lib, e):
+    msg = ctypes.create_string_buffer(1024)
+    return msg.value.decode() if lib.rg_hip_exec_failure(e, msg, len(msg)) else None

@@ -7,6 +7,7 @@ through hiprtc (which needs no device). The CPU oracle implements the same ABI u
 """
 
 import ctypes
+import json
 import os
 import re
 
@@ -128,3 +129,28 @@ def test_c3_program_compiles_for_gfx950():
     words, _ = _rg.plan_words(g, ids, "hip", "search-linear")
     n, err = _compile_check(words)
     assert n >= 10, err
+
+
+def test_standard_validation_without_a_cpu_reference_says_the_device_check_was_skipped():
+    """With no CPU interpreter registered (the product alone ships none), validate='standard'
+    cannot compare the device with the CPU: the report marks the check skipped and carries a
+    DEVICE_CHECK_SKIPPED warning rather than passing silently. Run in a child process whose only
+    backend is the oracle registered under another name, standing in for a device."""
+    import subprocess
+    import sys
+    from conftest import ORACLE
+    code = f"""
+import json, sys
+sys.path.insert(0, {ROOT!r})
+import numpy as np
+import rustautograd_amd as rg
+from rustautograd_amd import _native
+_native.register_backend("stand_in", {ORACLE!r}, "rg_cpu_")
+c = rg.compile(lambda x: (x * 2.0).sum(), (rg.tensor(np.ones(4, np.float32)),), validate="standard", device="stand_in")
+check = next(k for k in c.report["checks"] if k["name"] == "device_equivalence")
+print(json.dumps([check["status"], [d["code"] for d in c.report["diagnostics"]], c.report["status"]]))
+"""
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    status, codes, overall = json.loads(out.stdout.strip().splitlines()[-1])
+    assert status == "skipped" and codes == ["DEVICE_CHECK_SKIPPED"] and overall == "warning"

@@ -554,6 +554,37 @@ def test_row_parallel_checker_gemm_is_bit_identical_to_the_serial_loop():
     np.testing.assert_allclose(serial, a.astype(np.float64) @ b, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_blocked_checker_gemm_is_bit_identical_for_every_transpose_flag(ta, tb):
+    """The checker's blocked products (stacked rows, single large products such as the weight
+    gradients, transposed operands through a copied panel) add each output's terms in the
+    serial loop's order: every flag combination gives the serial loop's bits."""
+    import ctypes
+    from conftest import ORACLE
+    lib = ctypes.CDLL(ORACLE)
+    r = np.random.default_rng(2)
+    m, k, n = 150, 333, 290
+    a = r.normal(size=(k, m) if ta else (m, k)).astype(np.float32)
+    b = r.normal(size=(n, k) if tb else (k, n)).astype(np.float32)
+    g = G()
+    x, w = g.input(a.shape, "float32"), g.input(b.shape, "float32")
+    lhs = g.un("transpose", x, perm=[1, 0]) if ta else x
+    rhs = g.un("transpose", w, perm=[1, 0]) if tb else w
+    c = g.compile([g.bin("matmul", lhs, rhs)], [a, b], optimize="standard")
+    assert any(st.get("op") == "matmul_t" for st in c.plan_summary()) == (ta or tb)
+    args = [rg.tensor(a)._t, rg.tensor(b)._t]
+    try:
+        lib.rg_cpu_set_row_parallel_gemm(0)
+        serial = rg.Tensor(c.call(args)[0]).numpy()
+        lib.rg_cpu_set_row_parallel_gemm(1)
+        blocked = rg.Tensor(c.call(args)[0]).numpy()
+    finally:
+        lib.rg_cpu_set_row_parallel_gemm(1)
+    assert np.array_equal(serial.view(np.int32), blocked.view(np.int32))
+    want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b)
+    np.testing.assert_allclose(serial, want, rtol=1e-4, atol=1e-4)
+
+
 def test_where_with_broadcast_operand_differentiates_in_a_growing_graph():
     """Regression: the gradient of where() through a broadcast operand, built while the node table
     reallocates (unbroadcast once read its target shape through a reference into that table)."""

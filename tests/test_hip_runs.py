@@ -10,7 +10,7 @@ import pytest
 import rustautograd_amd as rg
 from rustautograd_amd import _rg, nn, optim, random, workloads
 
-from helpers import close, op, seq, t
+from helpers import RunDesc, RunResult, close, hip_abi, hip_program, op, seq, t
 
 pytestmark = pytest.mark.gpu
 
@@ -176,61 +176,16 @@ def test_a_failure_in_the_middle_of_a_run_reports_the_completed_steps():
         assert r.state.numpy().tolist() == [0.125, 0.25, 0.375, 0.5]
 
 
-def _plan_io(words):
-    """Input and output slots of a flat plan (include/rg_plan.h: header, slots, consts, inputs, outputs)."""
-    k = 2
-    n = words[k]; k += 1 + 3 * n
-    n = words[k]; k += 1 + 3 * n
-    n = words[k]; inputs = [words[k + 1 + 2 * j] for j in range(n)]; k += 1 + 2 * n
-    n = words[k]; k += 1
-    outputs = []
-    for _ in range(n):
-        outputs.append(words[k])
-        k += 3 + words[k + 2]
-    return inputs, outputs
-
-
-class _RunDesc(ctypes.Structure):
-    _fields_ = [("n_swaps", ctypes.c_int64), ("swaps", ctypes.POINTER(ctypes.c_int64)),
-                ("n_copies", ctypes.c_int64), ("copies", ctypes.POINTER(ctypes.c_int64)),
-                ("n_data", ctypes.c_int64), ("data_slots", ctypes.POINTER(ctypes.c_int64)),
-                ("data_bytes", ctypes.POINTER(ctypes.c_uint64)), ("n_batches", ctypes.c_int64),
-                ("batches", ctypes.POINTER(ctypes.c_void_p)), ("n_history", ctypes.c_int64),
-                ("history_slots", ctypes.POINTER(ctypes.c_int64)), ("steps", ctypes.c_int64),
-                ("history", ctypes.POINTER(ctypes.c_double))]
-
-
-class _RunResult(ctypes.Structure):
-    _fields_ = [("done", ctypes.c_int64), ("nonfinite_step", ctypes.c_int64), ("seconds", ctypes.c_double)]
-
-
 def test_run_failure_leaves_the_state_of_the_completed_steps_at_the_abi():
     """Through the C ABI: after a failure the state slot holds the state after `done` steps (as
     the reference's host loop leaves it, validate.rs:329-335), not a half-run chunk."""
-    from rustautograd_amd import _native
-    lib = ctypes.CDLL(_native.HIP_LIBRARY)
-    lib.rg_hip_program_new.restype = ctypes.c_void_p
-    lib.rg_hip_program_new.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t,
-                                       ctypes.c_char_p, ctypes.c_size_t]
-    lib.rg_hip_exec_new.restype = ctypes.c_void_p
-    lib.rg_hip_exec_new.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
-    for name in ("rg_hip_exec_free", "rg_hip_program_free", "rg_hip_program_inject_failure"):
-        getattr(lib, name).argtypes = [ctypes.c_void_p]
-    lib.rg_hip_program_inject_failure_after.argtypes = [ctypes.c_void_p, ctypes.c_int64]
-    lib.rg_hip_exec_write.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_uint64]
-    lib.rg_hip_exec_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_uint64]
-    lib.rg_hip_exec_run.argtypes = [ctypes.c_void_p, ctypes.POINTER(_RunDesc), ctypes.POINTER(_RunResult)]
-    lib.rg_hip_exec_failure.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    lib = hip_abi()
 
     g = _rg.Graph()
     w = g.input([4], "float32")
     nw = op(g, "mul", [w, g.constant(rg.tensor(np.float32(0.5))._t)])
-    words, blob = _rg.plan_words(g, [nw, op(g, "sum", [nw], axes=[0], keepdims=False)], "hip", "none")
-    (win,), (wout, lout) = _plan_io(words)
-    arr = (ctypes.c_int64 * len(words))(*words)
+    prog, (win,), (wout, lout) = hip_program(lib, g, [nw, op(g, "sum", [nw], axes=[0], keepdims=False)])
     err = ctypes.create_string_buffer(4096)
-    prog = lib.rg_hip_program_new(arr, len(words), blob, len(blob), err, len(err))
-    assert prog, err.value
     try:
         for history, fail_after in ((False, 5), (True, 70), (True, 0)):
             e = lib.rg_hip_exec_new(prog, err, len(err))
@@ -241,9 +196,9 @@ def test_run_failure_leaves_the_state_of_the_completed_steps_at_the_abi():
             hs = (ctypes.c_int64 * 1)(lout)
             steps = 100
             hist = (ctypes.c_double * steps)()
-            d = _RunDesc(n_swaps=1, swaps=swaps, n_history=1 if history else 0, history_slots=hs, steps=steps, history=hist)
+            d = RunDesc(n_swaps=1, swaps=swaps, n_history=1 if history else 0, history_slots=hs, steps=steps, history=hist)
             lib.rg_hip_program_inject_failure_after(prog, fail_after)
-            out = _RunResult()
+            out = RunResult()
             assert lib.rg_hip_exec_run(e, ctypes.byref(d), ctypes.byref(out)) == -1
             assert out.done == fail_after, (history, out.done)
             msg = ctypes.create_string_buffer(256)
