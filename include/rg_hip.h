@@ -119,6 +119,18 @@ int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, in
  * the same description. `out->seconds` is the step loop alone (validate.rs:264-265): batch
  * upload and graph capture are excluded. */
 int rg_hip_exec_run(void* exec, const rg_run_desc* desc, rg_run_result* out);
+/* The step loop of rg_hip_exec_run for callers that cannot allocate device memory (code that
+ * must not call hipMalloc: tight serving loops, harnesses that forbid it). It has no counterpart
+ * in the reference. It calls no hipMalloc, hipFree or other allocating routine and instantiates
+ * no graph: the run's step counter, history record, cycled batches and state-copy temporaries
+ * live in a static device array of RG_NOALLOC_SCRATCH_BYTES (32 MiB) that each GPU holds until
+ * the process ends, and the steps are launched directly. A run whose buffers would exceed it is
+ * refused (-1, message in rg_hip_exec_failure) before anything runs. Results equal
+ * rg_hip_exec_run's, bit for bit. With history it waits after every step to check the recorded
+ * values. Every call on one GPU shares that GPU's array and leaves its contents behind: calls
+ * that overlap on one GPU race. It keeps no snapshot: after a device failure the state slots
+ * are unspecified. */
+int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* desc, rg_run_result* out);
 
 #ifdef __cplusplus
 }

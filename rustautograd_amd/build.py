@@ -25,7 +25,7 @@ BUILD = os.path.join(ROOT, "_build")
 
 ENGINE_SOURCES = ["graph.cpp", "autodiff.cpp", "optimize.cpp", "egraph.cpp", "plan.cpp", "attention.cpp", "backend.cpp", "validate.cpp",
                   "module.cpp"]
-HIP_SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "runtime.cpp", "jit.cpp"]
+HIP_SOURCES = ["kernels.hip", "gemm.hip", "attention.hip", "noalloc.hip", "runtime.cpp", "jit.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result",

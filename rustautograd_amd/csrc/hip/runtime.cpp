@@ -21,6 +21,7 @@
 #include "../../../include/rg_hip.h"
 #include "jit.h"
 #include "kernels.h"
+#include "noalloc.h"
 
 using namespace rgplan;
 
@@ -51,16 +52,24 @@ using StepFn = std::function<void(hipStream_t, void* const*, void*)>;
 // that a later run with the same description only uploads its batches and resets the counter.
 // `key` is the description (slot lists, sizes, batch count, chunk); `table` the two slot tables
 // the state handoff alternates between, each with its graph.
+// Device buffers one run of the step loop works in: the step counter, the history ring
+// (`chunk` entries per recorded output), the cycled batches and the temporaries of the state
+// copies.
+struct RunBuffers {
+  uint64_t* counter = nullptr;
+  double* hist = nullptr;
+  uint64_t chunk = 1;
+  std::vector<void*> batch_bufs, temps;
+};
+
 struct RunCache {
   std::vector<int64_t> key;
   std::vector<void*> table[2];
   int n_graphs = 0;
-  uint64_t chunk = 0;
-  void* mem = nullptr;  // one allocation holding everything below
+  void* mem = nullptr;  // one allocation holding the run buffers and the snapshot
   uint64_t mem_bytes = 0;
-  uint64_t* counter = nullptr;
-  double* hist = nullptr;
-  std::vector<void*> batch_bufs, temps, snap;
+  RunBuffers buf;
+  std::vector<void*> snap;
   std::vector<int64_t> state_slots;
   std::vector<hipGraph_t> graphs;
   std::vector<hipGraphExec_t> execs;
@@ -76,8 +85,7 @@ struct RunCache {
     mem = nullptr;
     mem_bytes = 0;
     key.clear();
-    batch_bufs.clear();
-    temps.clear();
+    buf = RunBuffers{};
     snap.clear();
     state_slots.clear();
   }
@@ -864,6 +872,74 @@ void run_steps(Exec* e, size_t begin, size_t end) {
 
 double now() { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); }
 
+// Where a run's buffers lie in one block of device memory (offsets from its start).
+struct RunLayout {
+  uint64_t counter = 0, hist = 0, bytes = 0, chunk = 1;
+  std::vector<uint64_t> batches, temps;
+  RunBuffers place(void* base) const {
+    RunBuffers b;
+    b.counter = (uint64_t*)((char*)base + counter);
+    b.hist = (double*)((char*)base + hist);
+    b.chunk = chunk;
+    for (auto o : batches) b.batch_bufs.push_back((char*)base + o);
+    for (auto o : temps) b.temps.push_back((char*)base + o);
+    return b;
+  }
+};
+
+RunLayout run_layout(const Program& p, const rg_run_desc* d, uint64_t chunk) {
+  RunLayout lay;
+  lay.chunk = chunk;
+  auto take = [&](uint64_t bytes) {
+    uint64_t at = lay.bytes;
+    lay.bytes += (std::max<uint64_t>(bytes, 1) + ALIGN - 1) / ALIGN * ALIGN;
+    return at;
+  };
+  lay.counter = take(8);
+  lay.hist = take((uint64_t)std::max<int64_t>(d->n_history, 1) * chunk * 8);
+  for (int64_t j = 0; j < d->n_data && d->n_batches > 1; j++) lay.batches.push_back(take(d->data_bytes[j] * (uint64_t)d->n_batches));
+  for (int64_t c = 0; c < d->n_copies; c++) lay.temps.push_back(take(p.slot_bytes[(size_t)d->copies[3 * c + 1]]));
+  return lay;
+}
+
+// Copies the run's cycled batches into their device buffers (no wait).
+void upload_batches(const rg_run_desc* d, const RunBuffers& b, hipStream_t s) {
+  for (int64_t j = 0; j < (int64_t)b.batch_bufs.size(); j++)
+    for (int64_t k = 0; k < d->n_batches; k++)
+      HIP_OK(hipMemcpyAsync((char*)b.batch_bufs[(size_t)j] + d->data_bytes[j] * k, d->batches[k * d->n_data + j], d->data_bytes[j],
+                            hipMemcpyHostToDevice, s));
+}
+
+// Everything one step of the loop enqueues under slot table `t`: batch loads, the plan, history
+// records, the state copies into the next table `next` (every source read before any
+// destination is written, validate.rs:349-355) and the step counter.
+void enqueue_run_step(const Program& p, hipStream_t s, void* ws, const rg_run_desc* d, const RunBuffers& b, const std::vector<void*>& t,
+                      const std::vector<void*>& next) {
+  for (int64_t j = 0; j < (int64_t)b.batch_bufs.size(); j++)
+    rgk::load_batch(s, t[(size_t)d->data_slots[j]], b.batch_bufs[(size_t)j], d->data_bytes[j], d->n_batches, b.counter);
+  enqueue_range(p, s, t.data(), ws, 0, p.steps.size());
+  for (int64_t h = 0; h < d->n_history; h++) {
+    int64_t sl = d->history_slots[h];
+    rgk::record_history(s, p.plan.slots[(size_t)sl].dtype, t[(size_t)sl], b.hist + h * b.chunk, b.counter, b.chunk);
+  }
+  for (int64_t c = 0; c < d->n_copies; c++) {
+    int64_t os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
+    rgk::copy_bytes(s, b.temps[(size_t)c], t[(size_t)os], (uint64_t)n * esize(p.plan.slots[(size_t)os].dtype));
+  }
+  for (int64_t c = 0; c < d->n_copies; c++) {
+    int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
+    rgk::copy_bytes(s, next[(size_t)is], b.temps[(size_t)c], (uint64_t)n * esize(p.plan.slots[(size_t)os].dtype));
+  }
+  rgk::counter_inc(s, b.counter);
+}
+
+// The two slot tables a run alternates between: `start`, and `start` with every swap applied.
+void run_tables(const std::vector<void*>& start, const rg_run_desc* d, std::vector<void*> out[2]) {
+  out[0] = start;
+  out[1] = start;
+  for (int64_t k = 0; k < d->n_swaps; k++) std::swap(out[1][(size_t)d->swaps[2 * k]], out[1][(size_t)d->swaps[2 * k + 1]]);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1168,37 +1244,23 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     key.insert(key.end(), d->data_slots, d->data_slots + d->n_data);
     for (int64_t j = 0; j < d->n_data; j++) key.push_back((int64_t)d->data_bytes[j]);
     key.insert(key.end(), d->history_slots, d->history_slots + d->n_history);
-    auto tables_from = [&](const std::vector<void*>& start) {
-      rc.table[0] = start;
-      rc.table[1] = start;
-      for (int64_t k = 0; k < d->n_swaps; k++) std::swap(rc.table[1][(size_t)d->swaps[2 * k]], rc.table[1][(size_t)d->swaps[2 * k + 1]]);
-    };
+    auto tables_from = [&](const std::vector<void*>& start) { run_tables(start, d, rc.table); };
     if (rc.key != key) {
       rc.release();
-      // One allocation: counter, history ring, batch tables, copy temporaries, snapshot.
-      std::vector<uint64_t> sizes{8, (uint64_t)std::max<int64_t>(d->n_history, 1) * chunk * 8};
-      const bool cycled = d->n_batches > 1;
-      for (int64_t j = 0; j < d->n_data && cycled; j++) sizes.push_back(d->data_bytes[j] * (uint64_t)d->n_batches);
-      for (int64_t c = 0; c < d->n_copies; c++) sizes.push_back(p->slot_bytes[(size_t)d->copies[3 * c + 1]]);
+      // One allocation: the run buffers, then the snapshot of the changing state slots.
+      RunLayout lay = run_layout(*p, d, chunk);
       for (int64_t k = 0; k < d->n_swaps; k++) rc.state_slots.push_back(d->swaps[2 * k]);
       for (int64_t k = 0; k < d->n_copies; k++) rc.state_slots.push_back(d->copies[3 * k]);
-      for (auto sl : rc.state_slots) sizes.push_back(p->slot_bytes[(size_t)sl]);
-      uint64_t total = 0;
-      std::vector<uint64_t> off;
-      for (auto b : sizes) {
-        off.push_back(total);
-        total += (b + ALIGN - 1) / ALIGN * ALIGN;
+      uint64_t total = lay.bytes;
+      std::vector<uint64_t> snap_off;
+      for (auto sl : rc.state_slots) {
+        snap_off.push_back(total);
+        total += (p->slot_bytes[(size_t)sl] + ALIGN - 1) / ALIGN * ALIGN;
       }
-      HIP_OK(hipMalloc(&rc.mem, total));
+      HIP_OK(hipMalloc(&rc.mem, std::max<uint64_t>(total, ALIGN)));
       rc.mem_bytes = total;
-      char* base = (char*)rc.mem;
-      size_t q = 0;
-      rc.counter = (uint64_t*)(base + off[q++]);
-      rc.hist = (double*)(base + off[q++]);
-      for (int64_t j = 0; j < d->n_data && cycled; j++) rc.batch_bufs.push_back(base + off[q++]);
-      for (int64_t c = 0; c < d->n_copies; c++) rc.temps.push_back(base + off[q++]);
-      for (size_t k = 0; k < rc.state_slots.size(); k++) rc.snap.push_back(base + off[q++]);
-      rc.chunk = chunk;
+      rc.buf = lay.place(rc.mem);
+      for (auto o : snap_off) rc.snap.push_back((char*)rc.mem + o);
       rc.n_graphs = n_graphs;
       tables_from(f->slot);
       rc.key = key;
@@ -1209,29 +1271,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     }
     // Step k (counted from this run's start) runs under table (parity + k) % n_graphs.
     const int parity = f->slot == rc.table[0] ? 0 : 1;
-    // Everything one step enqueues under slot table g: batch loads, the plan, history records,
-    // the state copies (all sources read before any destination is written, validate.rs:349-355)
-    // and the step counter.
-    auto enqueue_step = [&](int g) {
-      const std::vector<void*>& t = rc.table[g];
-      for (int64_t j = 0; j < (int64_t)rc.batch_bufs.size(); j++)
-        rgk::load_batch(f->stream, t[(size_t)d->data_slots[j]], rc.batch_bufs[(size_t)j], d->data_bytes[j], d->n_batches, rc.counter);
-      enqueue_range(*p, f->stream, t.data(), f->workspace, 0, p->steps.size());
-      for (int64_t h = 0; h < d->n_history; h++) {
-        int64_t sl = d->history_slots[h];
-        rgk::record_history(f->stream, p->plan.slots[(size_t)sl].dtype, t[(size_t)sl], rc.hist + h * chunk, rc.counter, chunk);
-      }
-      for (int64_t c = 0; c < d->n_copies; c++) {
-        int64_t os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
-        rgk::copy_bytes(f->stream, rc.temps[(size_t)c], t[(size_t)os], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
-      }
-      const std::vector<void*>& next = rc.table[(g + 1) % n_graphs];
-      for (int64_t c = 0; c < d->n_copies; c++) {
-        int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
-        rgk::copy_bytes(f->stream, next[(size_t)is], rc.temps[(size_t)c], (uint64_t)n * esize(p->plan.slots[(size_t)os].dtype));
-      }
-      rgk::counter_inc(f->stream, rc.counter);
-    };
+    auto enqueue_step = [&](int g) { enqueue_run_step(*p, f->stream, f->workspace, d, rc.buf, rc.table[g], rc.table[(g + 1) % n_graphs]); };
     // Each slot table is captured once as a HIP graph and replayed; RG_HIP_GRAPHS=0 launches the
     // same kernels directly instead (for tools that do not follow graph launches).
     const char* env = getenv("RG_HIP_GRAPHS");
@@ -1249,11 +1289,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
         rc.execs.push_back(ge);
       }
     }
-    // Batches for this run, uploaded together with one wait.
-    for (int64_t j = 0; j < (int64_t)rc.batch_bufs.size(); j++)
-      for (int64_t k = 0; k < d->n_batches; k++)
-        HIP_OK(hipMemcpyAsync((char*)rc.batch_bufs[(size_t)j] + d->data_bytes[j] * k, d->batches[k * d->n_data + j], d->data_bytes[j],
-                              hipMemcpyHostToDevice, f->stream));
+    upload_batches(d, rc.buf, f->stream);
     auto table_of = [&](int64_t k) { return (int)((parity + k) % n_graphs); };
     auto launch = [&](int64_t k) -> hipError_t {
       if (use_graphs) return hipGraphLaunch(rc.execs[(size_t)table_of(k)], f->stream);
@@ -1268,7 +1304,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       }
     };
     HIP_OK(hipGetLastError());
-    rgk::set_counter(f->stream, rc.counter, 0);
+    rgk::set_counter(f->stream, rc.buf.counter, 0);
     HIP_OK(hipStreamSynchronize(f->stream));
     double t0 = now();
     int64_t done = 0;
@@ -1297,7 +1333,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       }
       int64_t bad = -1;
       if (d->n_history > 0) {
-        HIP_OK(hipMemcpy(hbuf.data(), rc.hist, (size_t)d->n_history * chunk * 8, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(hbuf.data(), rc.buf.hist, (size_t)d->n_history * chunk * 8, hipMemcpyDeviceToHost));
         for (int64_t k = c0; k < c1 && bad < 0; k++)
           for (int64_t h = 0; h < d->n_history; h++)
             if (!std::isfinite(hbuf[(size_t)(h * chunk + (k - c0))])) bad = k;
@@ -1307,7 +1343,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       if (bad >= 0) {
         // Back to the chunk start, then exactly through the bad step.
         snapshot(g0, true);
-        rgk::set_counter(f->stream, rc.counter, (uint64_t)c0);
+        rgk::set_counter(f->stream, rc.buf.counter, (uint64_t)c0);
         for (int64_t k = c0; k <= bad; k++) latch(e, launch(k), "step launch");
         if (latch(e, hipStreamSynchronize(f->stream), "device execution")) {
           result = -1;
@@ -1327,6 +1363,89 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     if (e->failure.empty()) e->failure = ex.what();
     result = -1;
   }
+  hipStreamSynchronize(f->stream);
+  return result;
+}
+
+// The step loop with no allocation (include/rg_hip.h): the run's counter, history record, cycled
+// batches and copy temporaries live in the static scratch array (noalloc.hip); the steps are
+// launched directly (no graph is instantiated) and no snapshot is kept. With history, the loop
+// waits after every step and reads the recorded values, so it stops exactly after the first
+// step (and its handoff) that recorded a non-finite value, as rg_hip_exec_run does.
+int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* d, rg_run_result* out) {
+  auto* e = (Exec*)exec;
+  Program* p = e->prog;
+  Frame* f = e->frame;
+  out->done = 0;
+  out->nonfinite_step = -1;
+  out->seconds = 0;
+  if (!e->failure.empty()) return -1;
+  const int64_t fail_at = p->fail_in.exchange(-1);
+  std::string why;
+  void* base = rgk::noalloc_scratch(&why);
+  if (!base) {
+    e->failure = "rg_hip_exec_run_noalloc: " + why;
+    return -1;
+  }
+  RunLayout lay = run_layout(*p, d, 1);
+  if (lay.bytes > RG_NOALLOC_SCRATCH_BYTES) {
+    e->failure = "rg_hip_exec_run_noalloc: this run needs " + std::to_string(lay.bytes) + " bytes of scratch (counter, history, " +
+                 std::to_string(d->n_batches > 1 ? d->n_batches : 0) + " cycled batches, " + std::to_string(d->n_copies) +
+                 " state copies); the static scratch holds " + std::to_string(RG_NOALLOC_SCRATCH_BYTES);
+    return -1;
+  }
+  const RunBuffers b = lay.place(base);
+  const int n_tables = d->n_swaps > 0 ? 2 : 1;
+  std::vector<void*> table[2];
+  run_tables(f->slot, d, table);
+  int result = 0;
+  int64_t done = 0;
+  try {
+    upload_batches(d, b, f->stream);
+    rgk::set_counter(f->stream, b.counter, 0);
+    HIP_OK(hipStreamSynchronize(f->stream));
+    double t0 = now();
+    std::vector<double> hbuf((size_t)std::max<int64_t>(d->n_history, 1));
+    for (int64_t k = 0; k < d->steps; k++) {
+      if (k == fail_at) {
+        e->failure = "injected failure";
+        result = -1;
+        break;
+      }
+      enqueue_run_step(*p, f->stream, f->workspace, d, b, table[k % n_tables], table[(k + 1) % n_tables]);
+      if (latch(e, hipGetLastError(), "step launch")) {
+        result = -1;
+        break;
+      }
+      if (d->n_history == 0) {
+        done = k + 1;
+        continue;
+      }
+      // On the frame's stream: it does not synchronize with the null stream a plain hipMemcpy uses.
+      if (latch(e, hipMemcpyAsync(hbuf.data(), b.hist, (size_t)d->n_history * 8, hipMemcpyDeviceToHost, f->stream), "history read") ||
+          latch(e, hipStreamSynchronize(f->stream), "device execution")) {
+        result = -1;
+        break;
+      }
+      done = k + 1;
+      bool bad = false;
+      for (int64_t h = 0; h < d->n_history; h++) {
+        d->history[h * d->steps + k] = hbuf[(size_t)h];
+        bad |= !std::isfinite(hbuf[(size_t)h]);
+      }
+      if (bad) {
+        out->nonfinite_step = k;
+        break;
+      }
+    }
+    if (latch(e, hipStreamSynchronize(f->stream), "device execution")) result = -1;
+    out->seconds = now() - t0;
+  } catch (std::exception& ex) {
+    if (e->failure.empty()) e->failure = ex.what();
+    result = -1;
+  }
+  out->done = done;
+  f->slot = table[(size_t)(done % n_tables)];
   hipStreamSynchronize(f->stream);
   return result;
 }

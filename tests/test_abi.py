@@ -46,9 +46,10 @@ def test_hip_library_loads_and_exports_every_declared_symbol():
 
 # Entry points the engine binds as optional (backend.cpp), with a host-side fallback each: the
 # per-step timer, the JSON breakdown, the class timer and the device-resident run loop (the oracle uses the
-# engine's host run loop, validate.rs:289-363), plus the HIP-only build check and memory query.
+# engine's host run loop, validate.rs:289-363), plus the HIP-only build check and memory query, and
+# the run loop for callers that cannot allocate (a device-only entry point the engine does not bind).
 OPTIONAL = {"rg_hip_exec_step_timed", "rg_hip_exec_breakdown", "rg_hip_exec_run", "rg_hip_exec_time_steps", "rg_hip_compile_check",
-            "rg_hip_device_memory_bytes"}
+            "rg_hip_device_memory_bytes", "rg_hip_exec_run_noalloc"}
 
 
 def test_oracle_implements_the_same_abi():
