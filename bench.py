@@ -31,6 +31,19 @@ def _numel(s):
     return n
 
 
+def skinny_product(m, n, k, ta, tb):
+    """Whether the backend streams an unbatched fp32 product through its skinny kernels (few rows
+    or one column with a long K, a K of at most 16, or few outputs): the HBM-bound class.
+    Mirrors skinny_plan in rustautograd_amd/csrc/hip/gemm.hip."""
+    if k <= 16 and n % 4 == 0 and m * n >= (1 << 14):
+        return True
+    if m <= 16 and k >= 512 and n >= 64 and ((not tb and n % 4 == 0) or (tb and not ta and k % 256 == 0 and n % 4 == 0)):
+        return True
+    if n == 1 and k >= 512 and m >= 64 and ((ta and m % 4 == 0) or (not ta and k % 256 == 0 and m % 4 == 0)):
+        return True
+    return m * n <= 16384 and k >= 512
+
+
 def classify(plan):
     """Groups plan steps into kernel classes with their algorithmic work (flops for products,
     bytes for everything else, as defined for the roofline) and the step indices of each."""
@@ -61,9 +74,16 @@ def classify(plan):
             a = args[0]
             kd = a[-1] if len(a) >= 1 and not st["ta"] else (a[-2] if len(a) >= 2 else a[0])
             flops = 2.0 * _numel(shape) * kd
-            m_rows = _numel(shape) // (shape[-1] if shape else 1)
-            mfma = st["dtype"] == "float32" and len(shape) >= 2 and shape[-1] >= 32 and m_rows >= 32
-            add("gemm_mfma" if mfma else "gemm_plain", k, flops=flops, nbytes=(sum(_numel(s) for s in args) + _numel(shape)) * ds)
+            n_cols = shape[-1] if shape else 1
+            m_rows = _numel(shape) // n_cols
+            nbytes = (sum(_numel(s) for s in args) + _numel(shape)) * ds
+            batched = len(args[1]) > 2
+            skinny = st["dtype"] == "float32" and not batched and skinny_product(m_rows, n_cols, kd, st["ta"], st["tb"])
+            mfma = st["dtype"] == "float32" and len(shape) >= 2 and n_cols >= 32 and m_rows >= 32 and kd >= 8
+            if skinny:
+                add("gemm_skinny", k, nbytes=nbytes)
+            else:
+                add("gemm_mfma" if mfma else "gemm_plain", k, flops=flops, nbytes=nbytes)
         elif op in ("sum", "max", "min"):
             add("reduce", k, nbytes=(_numel(args[0]) + st["n"]) * ds)
         elif op in ("take", "take_along"):
@@ -142,13 +162,72 @@ def cpu_baseline(cfg, sample_batch=4, steps=3):
                       f"steps/s scaled by {sample.batch}/{cfg.batch}; OpenMP threads where the reference uses rayon"}
 
 
+def roofline_of(compiled, inputs, reps):
+    """(roofline dict, per-class table, device seconds per pass) from each kernel class's plan
+    steps replayed back to back between two HIP events on the execution stream."""
+    classes = classify(compiled.plan_summary())
+    time_classes(compiled, inputs, classes, 1)
+    time_classes(compiled, inputs, classes, reps)
+    total_s = sum(c["seconds"] for c in classes.values())
+    dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])
+    per_launch = (dom["flops"] or dom["bytes"]) / dom["launches"]
+    avg_s = dom["seconds"] / dom["launches"]
+    if dom["unit"] == "TFLOP/s":
+        roof = {"bound": "mfma", "achieved": round(dom["achieved"], 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(dom["achieved"] / FP32_MFMA_PEAK_TFLOPS, 4)}
+    else:
+        roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4)}
+    roof["traffic"] = measured_traffic(dom_name)
+    roof.update({"kernel": dom_name, "launches_per_step": dom["launches"], "algorithmic_per_launch": round(per_launch),
+                 "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]), "avg_launch_us": round(avg_s * 1e6, 2)})
+    kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
+                   "unit": v["unit"], "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4)}
+               for k, v in sorted(classes.items(), key=lambda kv: -kv[1]["seconds"])}
+    return roof, kernels, total_s
+
+
+def bench_program(args, rg, workloads):
+    """C5: one evaluation of the matrix-chain program (value and the gradients for B and C) per
+    pass. Timed region: `repeats` back-to-back passes over the whole plan between two HIP events,
+    the inputs already in HBM (rg_hip_exec_time_steps)."""
+    program, inputs = workloads.matrix_chain()
+    compiled = rg.compile(program, inputs, validate="basic", device="hip")
+    natives = [x._t for x in inputs]
+    every = list(range(len(compiled.plan_summary())))
+    compiled._n.time_steps(natives, every, max(1, args.warmup))
+    passes = max(1, args.steps)
+    seconds = [compiled._n.time_steps(natives, every, passes) for _ in range(max(1, args.repeats))]
+    sec = sorted(seconds)[len(seconds) // 2]
+    value = passes / sec
+    print(f"# C5: {passes} passes in {sec * 1e3:.3f} ms (median of {len(seconds)})", file=sys.stderr, flush=True)
+    roof, kernels, total_s = roofline_of(compiled, natives, max(1, args.timing_reps))
+    n, k = 4096, 8
+    # The reordered plan reads B once and C twice (A@B, then (A@B)@C and the gradient through C)
+    # and writes dB and dC: five n x n fp32 matrices; the k-wide operands are noise beside them.
+    moved = 5 * n * n * 4
+    return {
+        "metric": "C5 matrix-chain passes/s (value + dB + dC) on 1 MI355X; % of HBM roofline",
+        "value": round(value, 2), "unit": "passes/s", "n_gpus": 1, "steps": passes, "warmup": args.warmup,
+        "ms_per_step": round(1e3 / value, 4),
+        "timed_region": "back-to-back replays of every plan step between two HIP events, inputs resident in HBM; median of repeats",
+        "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: A, B, C, D ~ N(0, 1/64) from numpy default_rng(0)",
+        "config": {"workload": "C5 matrix chain sum(((A@B)@C)@D), gradients w.r.t. B and C, e-graph reordered plan",
+                   "n": n, "k": k, "gflop_per_pass": 1.34, "min_hbm_mb_per_pass": round(moved / 1e6, 1)},
+        "roofline": roof, "kernels": kernels, "device_ms_per_step": round(total_s * 1e3, 4),
+        "pass_hbm_fraction": round(moved / (1e3 / value * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--repeats", type=int, default=3, help="timed runs of K steps; the median is reported")
-    ap.add_argument("--workload", default="C4", choices=["C3", "C4"])
+    ap.add_argument("--workload", default="C4", choices=["C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--timing-reps", type=int, default=5, help="per-step HIP-event timing passes after the timed run (0: skip)")
     ap.add_argument("--probe", choices=["copy"], help="run only a plain copy kernel of known size (for counter calibration)")
@@ -164,8 +243,15 @@ def main():
     if args.probe == "copy":
         copy_probe(rg)
         return
-    cfg = workloads.GPT_CONFIGS[args.workload]
-    step, state = workloads.gpt_train_step(cfg)
+    if args.workload == "C5":
+        print(json.dumps(bench_program(args, rg, workloads)), flush=True)
+        return
+    if args.workload == "C2":
+        cfg = workloads.MLPConfig()
+        step, state = workloads.mlp_train_step(cfg)
+    else:
+        cfg = workloads.GPT_CONFIGS[args.workload]
+        step, state = workloads.gpt_train_step(cfg)
     t0 = time.perf_counter()
     compiled = rg.compile(step, (state,), validate="basic", device="hip")
     compile_s = time.perf_counter() - t0
@@ -191,35 +277,28 @@ def main():
     print(f"# {args.steps} steps: step loop {loop_s:.4f}s (median of {len(loops)}: {', '.join(f'{x:.4f}' for x in loops)}), "
           f"whole rg.run {wall_s:.4f}s; loss {res.history['aux'][0]:.4f} -> {res.history['aux'][-1]:.4f}", file=sys.stderr, flush=True)
 
-    # Per-class device times: each class's plan steps replayed back to back between two HIP
-    # events on the execution stream, after one full step has filled every slot.
     roof, kernels, total_s = None, None, None
     if args.timing_reps > 0:
         inputs = [rg.tensor(x)._t for x in rg.tree.leaves((res.state,))]
-        classes = classify(compiled.plan_summary())
-        time_classes(compiled, inputs, classes, 1)
-        time_classes(compiled, inputs, classes, args.timing_reps)
-        total_s = sum(c["seconds"] for c in classes.values())
-        dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])
-        per_launch = (dom["flops"] or dom["bytes"]) / dom["launches"]
-        avg_s = dom["seconds"] / dom["launches"]
-        if dom["unit"] == "TFLOP/s":
-            roof = {"bound": "mfma", "achieved": round(dom["achieved"], 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(dom["achieved"] / FP32_MFMA_PEAK_TFLOPS, 4)}
-        else:
-            roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4)}
-        roof["traffic"] = measured_traffic(dom_name)
-        roof.update({"kernel": dom_name, "launches_per_step": dom["launches"], "algorithmic_per_launch": round(per_launch),
-                     "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]), "avg_launch_us": round(avg_s * 1e6, 2)})
-        kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
-                       "unit": v["unit"],
-                       "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4)}
-                   for k, v in sorted(classes.items(), key=lambda kv: -kv[1]["seconds"])}
+        roof, kernels, total_s = roofline_of(compiled, inputs, args.timing_reps)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
+    if args.workload == "C2":
+        metric = "train steps/s, MLP 512-2048-2048-1 batch 4096 (C2) on 1 MI355X; % of HBM / fp32-MFMA roofline"
+        data = "synthetic: x ~ N(0,1) drawn inside the step from a seeded key, target sum(sin(x[:, :16])); random-init weights"
+        config = {"workload": "C2 MLP regression training step", "batch": cfg.batch, "d_in": cfg.d_in, "hidden": cfg.hidden,
+                  "optimizer": "adamw", "lr": cfg.lr, "gemm_gflop_per_step": 120.3}
+        cpu = None
+    else:
+        metric = "train steps/s, char-GPT d=256 6L on 1 MI355X; % of HBM / fp32-MFMA roofline"
+        if args.workload != "C4":
+            metric = f"train steps/s, char-GPT {args.workload} on 1 MI355X; % of HBM / fp32-MFMA roofline"
+        data = "synthetic: token ids uniform in [0,96) drawn inside the step from a seeded key; random-init weights"
+        config = {"workload": f"{args.workload} char-GPT training step", "batch": cfg.batch, "seq_len": cfg.block, "d_model": cfg.d,
+                  "heads": cfg.heads, "layers": cfg.layers, "vocab": cfg.vocab, "optimizer": "adamw", "lr": cfg.lr,
+                  "gemm_gflop_per_step": round(workloads.gpt_gemm_flops(cfg) / 1e9, 2)}
+        cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
     out = {
-        "metric": "train steps/s, char-GPT d=256 6L on 1 MI355X; % of HBM / fp32-MFMA roofline",
+        "metric": metric,
         "value": round(value, 3),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -232,10 +311,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: token ids uniform in [0,96) drawn inside the step from a seeded key; random-init weights",
-        "config": {"workload": f"{args.workload} char-GPT training step", "batch": cfg.batch, "seq_len": cfg.block, "d_model": cfg.d,
-                   "heads": cfg.heads, "layers": cfg.layers, "vocab": cfg.vocab, "optimizer": "adamw", "lr": cfg.lr,
-                   "gemm_gflop_per_step": round(workloads.gpt_gemm_flops(cfg) / 1e9, 2)},
+        "data": data,
+        "config": config,
         "roofline": roof,
         "kernels": kernels,
         "device_ms_per_step": round(total_s * 1e3, 3) if total_s else None,

@@ -16,7 +16,9 @@
 // is chosen per product to fill 256 CUs with little padding (32-wide tiles for 32-wide attention
 // heads); products whose output still has too few tiles split K and combine the partial sums in a
 // fixed order (deterministic). Unaligned operands take the same kernel with scalar loads.
-// fp64 and tiny or skinny fp32 products use a plain kernel, one thread per output element.
+// fp32 products with at most 16 rows and a long K, or a K of at most 16, stream through the
+// skinny kernels below (HBM-bound shapes); fp64 and the remaining tiny products use a plain
+// kernel, one thread per output element.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -397,6 +399,273 @@ __global__ void __launch_bounds__(256) k_gemm_plain(const T* __restrict__ A, con
   C[(uint64_t)b * M * N + t] = acc;
 }
 
+// ---- skinny fp32 products: HBM-bound shapes streamed at full bandwidth -------------------------
+//
+// Products with at most 16 rows and a long K (a few vectors against a large matrix), or with a
+// K of at most 16 (outer products), do about 4 flops per byte they move: the matrix cores cannot
+// speed them up, the number of bytes in flight can. Each kernel reads its large operand exactly
+// once with 16-byte loads and fixes the order of every sum, so results are deterministic.
+
+// C (M <= MR rows) = op(A) B with B row-major K x N (N % 4 == 0, 16-byte aligned). A block of
+// four waves owns 256 columns (a float4 per lane) and one K split; its waves take consecutive
+// quarters of the split, sum their k in increasing order, and combine in wave order through
+// LDS. With several splits, split s writes partials [s][M N], summed in split order afterwards.
+// The loop has no branches: a wave's K range is made uniform (readfirstlane), so op(A) values are
+// scalar loads that never wait on the B rows in flight; rows m >= M read row M - 1 and columns
+// past N read the last column, and neither is stored.
+template <int MR, int UNROLL = 8>
+__global__ void __launch_bounds__(256) k_gemm_skinny_rows(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ out,
+                                                          int M, int N, int K, bool ta, int kps) {
+  __shared__ float4 red[3][MR][64];  // the sums of waves 1..3; wave 0 keeps its own
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int col = (blockIdx.x * 64 + lane) * 4;
+  const int colr = min(col, N - 4);
+  const int k0 = blockIdx.y * kps, k1 = min(K, k0 + kps);
+  const int quarter = (k1 - k0 + 3) / 4;
+  const int kw0 = min(k1, k0 + wave * quarter), kw1 = min(k1, kw0 + quarter);
+  const uint64_t sm = ta ? 1 : (uint64_t)K, sk = ta ? (uint64_t)M : 1;  // op(A)[m][k] = A[m * sm + k * sk]
+  float4 acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+  int k = kw0;
+  for (; k + UNROLL <= kw1; k += UNROLL) {
+    float4 b[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++) b[u] = *(const float4*)(B + (uint64_t)(k + u) * N + colr);
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++)
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        const float a = A[(uint64_t)min(m, M - 1) * sm + (uint64_t)(k + u) * sk];
+        acc[m] = make_float4(fmaf(a, b[u].x, acc[m].x), fmaf(a, b[u].y, acc[m].y), fmaf(a, b[u].z, acc[m].z), fmaf(a, b[u].w, acc[m].w));
+      }
+  }
+  for (; k < kw1; k++) {
+    const float4 b = *(const float4*)(B + (uint64_t)k * N + colr);
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const float a = A[(uint64_t)min(m, M - 1) * sm + (uint64_t)k * sk];
+      acc[m] = make_float4(fmaf(a, b.x, acc[m].x), fmaf(a, b.y, acc[m].y), fmaf(a, b.z, acc[m].z), fmaf(a, b.w, acc[m].w));
+    }
+  }
+  if (wave > 0)
+#pragma unroll
+    for (int m = 0; m < MR; m++) red[wave - 1][m][lane] = acc[m];
+  __syncthreads();
+  if (wave != 0 || col >= N) return;
+  float* dst = out + (uint64_t)blockIdx.y * M * N;
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+    if (m < M) {
+      float4 v = acc[m];
+#pragma unroll
+      for (int w = 0; w < 3; w++) {
+        const float4 x = red[w][m][lane];
+        v = make_float4(v.x + x.x, v.y + x.y, v.z + x.z, v.w + x.w);
+      }
+      *(float4*)(dst + (uint64_t)m * N + col) = v;
+    }
+}
+
+// C (M <= MR rows) = A B^T with A row-major M x K and B stored N x K (N % NC == 0, K % 256 == 0,
+// both 16-byte aligned): every output is the dot product of two contiguous rows. A block owns
+// 4 NC consecutive columns of C (NC per wave) and one K split of `kps` (a multiple of 256, at
+// most DOT_KPS); it copies its A panel to LDS while its first B rows load, so the loop's only
+// global loads are the B rows, four float4 steps deep. Lanes take k in float4 steps 256 apart, each lane summing its
+// share in increasing k; the 64 lane sums combine by a fixed xor butterfly, and with several
+// splits, split s writes partials [s][M N], summed in split order afterwards. Rows m >= M read
+// row M - 1 and are not stored. (For 16 rows the split is at most DOT_KPS / 2.)
+constexpr int DOT_KPS = 1024;
+template <int MR, int NC>
+__global__ void __launch_bounds__(256) k_gemm_skinny_dot(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ out,
+                                                         int M, int N, int K, int kps) {
+  constexpr int KPS_MAX = MR <= 8 ? DOT_KPS : DOT_KPS / 2;  // a 32 KiB panel either way
+  __shared__ float4 panel[MR][KPS_MAX / 4];
+  const int lane = threadIdx.x & 63;
+  // Blocks side by side take different K chunks (rotated by the column tile), so concurrent
+  // blocks read B at addresses spread over the rows rather than one column range of every row.
+  const int split = (blockIdx.y + blockIdx.x) % gridDim.y;
+  const int k0 = split * kps, len = min(K - k0, kps);
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * NC;
+  const bool active = n0 < N;
+  const int nr = active ? n0 : N - NC;  // an idle wave reads valid rows and stores nothing
+  // The first four steps of B rows are issued before the panel copy, so their latency overlaps it.
+  auto load = [&](float4 (&b)[4][NC], int kk) {
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+      for (int c = 0; c < NC; c++)
+        b[h][c] = kk + h * 256 < len ? *(const float4*)(B + (uint64_t)(nr + c) * K + k0 + kk + h * 256) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  float4 b[4][NC];
+  load(b, lane * 4);
+  for (int q = threadIdx.x; q < MR * (len / 4); q += 256) {
+    const int m = q / (len / 4), c = q % (len / 4);
+    panel[m][c] = *(const float4*)(A + (uint64_t)min(m, M - 1) * K + k0 + 4 * c);
+  }
+  __syncthreads();
+  if (!active) return;
+  float acc[MR][NC];
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int c = 0; c < NC; c++) acc[m][c] = 0.f;
+  for (int kk = lane * 4; kk < len; kk += 1024) {
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+      if (kk + h * 256 < len)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+          const float4 a = panel[m][(kk + h * 256) / 4];
+#pragma unroll
+          for (int c = 0; c < NC; c++)
+            acc[m][c] = fmaf(a.w, b[h][c].w, fmaf(a.z, b[h][c].z, fmaf(a.y, b[h][c].y, fmaf(a.x, b[h][c].x, acc[m][c]))));
+        }
+    if (kk + 1024 < len) load(b, kk + 1024);
+  }
+  float* dst = out + (uint64_t)split * M * N;
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      float v = acc[m][c];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      if (m < M && lane == 0) dst[(uint64_t)m * N + n0 + c] = v;
+    }
+}
+
+// C (M x N, N % 4 == 0) = op(A) op(B) with K <= KR (an outer product of a few vectors): write
+// bound. A block of four waves owns 256 columns; each lane keeps its float4 of every op(B) row in
+// registers and walks the wave's rows, reading op(A)'s row values as wave-uniform scalars.
+template <int KR, bool TA, bool TB>
+__global__ void __launch_bounds__(256) k_gemm_outer(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+                                                    int N, int K, int rows_per_wave) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = (blockIdx.x * 64 + lane) * 4;
+  if (col >= N) return;
+  // Rows k >= K are zeros: the extra terms add exact zeros, so the sums are unchanged.
+  float4 b[KR];
+#pragma unroll
+  for (int k = 0; k < KR; k++) {
+    if (k < K) {
+      if (TB) b[k] = make_float4(B[(uint64_t)col * K + k], B[(uint64_t)(col + 1) * K + k], B[(uint64_t)(col + 2) * K + k], B[(uint64_t)(col + 3) * K + k]);
+      else b[k] = *(const float4*)(B + (uint64_t)k * N + col);
+    } else {
+      b[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const int r0 = (blockIdx.y * 4 + wave) * rows_per_wave, r1 = min(M, r0 + rows_per_wave);
+  for (int i = r0; i < r1; i++) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+      const float a = k < K ? (TA ? A[(uint64_t)k * M + i] : A[(uint64_t)i * K + k]) : 0.f;
+      acc = make_float4(fmaf(a, b[k].x, acc.x), fmaf(a, b[k].y, acc.y), fmaf(a, b[k].z, acc.z), fmaf(a, b[k].w, acc.w));
+    }
+    *(float4*)(C + (uint64_t)i * N + col) = acc;
+  }
+}
+
+// A few outputs with a long K (at most 16384 outputs): one wave per output, its lanes taking k
+// 64 apart in increasing order, then a fixed xor butterfly. Any flags, any alignment.
+__global__ void __launch_bounds__(256) k_gemm_tiny_out(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+                                                       int N, int K, bool ta, bool tb) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= M * N) return;
+  const int i = e / N, j = e % N;
+  float acc = 0.f;
+  int k = lane;
+  for (; k + 7 * 64 < K; k += 8 * 64) {  // eight loads of each operand in flight
+    float a[8], b[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint64_t kk = (uint64_t)(k + u * 64);
+      a[u] = ta ? A[kk * M + i] : A[(uint64_t)i * K + kk];
+      b[u] = tb ? B[(uint64_t)j * K + kk] : B[kk * N + j];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) acc = fmaf(a[u], b[u], acc);
+  }
+  for (; k < K; k += 64) {
+    const float a = ta ? A[(uint64_t)k * M + i] : A[(uint64_t)i * K + k];
+    const float b = tb ? B[(uint64_t)j * K + k] : B[(uint64_t)k * N + j];
+    acc = fmaf(a, b, acc);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) C[e] = acc;
+}
+
+enum SkinnyKind { SKINNY_NONE = 0, SKINNY_ROWS, SKINNY_DOT, SKINNY_OUTER, SKINNY_TINY };
+
+// A skinny product as one of the kernels sees it. A matrix-vector product (n == 1) is run as its
+// transpose, C^T = op(B)^T op(A)^T: with one column, C and C^T are the same memory, and the
+// streamed matrix becomes the kernels' right operand.
+struct Skinny {
+  SkinnyKind kind = SKINNY_NONE;
+  bool swapped = false;  // roles of A and B exchanged (n == 1)
+  uint64_t m = 0, n = 0, k = 0;
+  bool ta = false;
+};
+
+// Which skinny kernel a product takes, from shapes and flags alone (alignment is checked at
+// launch; an unaligned operand falls back to the general kernels).
+Skinny skinny_plan(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
+  Skinny sk;
+  if (dtype != RG_F32 || batch != 1 || m == 0 || n == 0 || k == 0) return sk;
+  sk.m = m;
+  sk.n = n;
+  sk.k = k;
+  sk.ta = ta;
+  if (k <= 16 && n % 4 == 0 && m * n >= (1ull << 14)) {
+    sk.kind = SKINNY_OUTER;
+    return sk;
+  }
+  if (m <= 16 && k >= 512 && n >= 64) {
+    if (!tb && n % 4 == 0) sk.kind = SKINNY_ROWS;
+    else if (tb && !ta && k % 256 == 0 && n % 4 == 0) sk.kind = SKINNY_DOT;
+    if (sk.kind != SKINNY_NONE) return sk;
+  }
+  if (n == 1 && k >= 512 && m >= 64) {
+    // op(A) x with A stored K x M (ta): rows kernel over A; stored M x K: dot kernel over A's rows.
+    sk.swapped = true;
+    sk.m = 1;
+    sk.n = m;
+    sk.ta = false;
+    if (ta && m % 4 == 0) sk.kind = SKINNY_ROWS;
+    else if (!ta && k % 256 == 0 && m % 4 == 0) sk.kind = SKINNY_DOT;
+    if (sk.kind != SKINNY_NONE) return sk;
+    sk = Skinny{};
+  }
+  if (m * n <= 16384 && k >= 512) {
+    sk = Skinny{};
+    sk.kind = SKINNY_TINY;
+    sk.m = m;
+    sk.n = n;
+    sk.k = k;
+    sk.ta = ta;
+  }
+  return sk;
+}
+
+// K split length of SKINNY_DOT: the whole K in chunks of at most DOT_KPS (1024, or 512 for 16
+// rows, whose panel would not fit), each a multiple of 256.
+int skinny_dot_kps(uint64_t m, uint64_t k) {
+  const uint64_t cap = m <= 8 ? DOT_KPS : DOT_KPS / 2;
+  const uint64_t splits = (k + cap - 1) / cap;
+  return (int)(((k + splits - 1) / splits + 255) / 256 * 256);
+}
+
+// K splits of SKINNY_ROWS: about 1024 waves, each at least 64 rows of K deep, at most 16.
+int skinny_rows_splits(uint64_t n, uint64_t k) {
+  const uint64_t blocks = (n + 255) / 256;
+  uint64_t want = (256 + blocks - 1) / blocks;
+  const uint64_t most = std::max<uint64_t>(1, k / 256);
+  return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 16));
+}
+
 bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
   return dtype == RG_F32 && m >= 32 && n >= 32 && k >= 8 && m * n * k >= (1u << 18);
 }
@@ -484,21 +753,103 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
 
 }  // namespace
 
-int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
-  if (m == 0 || n == 0 || batch == 0 || !use_mfma(dtype, m, n, k)) return 1;
+int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
+  if (m == 0 || n == 0 || batch == 0) return 1;
+  const Skinny sk = skinny_plan(dtype, m, n, k, batch, ta, tb);
+  if (sk.kind == SKINNY_ROWS) {
+    const int splits = skinny_rows_splits(sk.n, sk.k);
+    const uint64_t kps = (sk.k + splits - 1) / splits;
+    return (int)((sk.k + kps - 1) / kps);
+  }
+  if (sk.kind == SKINNY_DOT) {
+    const uint64_t kps = (uint64_t)skinny_dot_kps(sk.m, sk.k);
+    return (int)((sk.k + kps - 1) / kps);
+  }
+  if (sk.kind != SKINNY_NONE || !use_mfma(dtype, m, n, k)) return 1;
   TileCfg t = pick_tile(m, n, k, batch, tb);
   int splits = split_count(t, m, n, k, batch);
   uint64_t kps = ((k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk;
   return (int)((k + kps - 1) / kps);
 }
 
-uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
-  int s = gemm_splits(dtype, m, n, k, batch, tb);
+uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
+  int s = gemm_splits(dtype, m, n, k, batch, ta, tb);
   return s > 1 ? (uint64_t)s * batch * m * n * sizeof(float) : 0;
 }
 
+// Launches the skinny kernel of `sk`; false when an operand is not aligned for it.
+bool gemm_skinny(hipStream_t s, const GemmArgs& g, const Skinny& sk) {
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (g.bias || g.a_off || g.b_off || !aligned(g.c)) return false;
+  // With the roles exchanged (n == 1) the vector is the left operand of one row.
+  const float* A = (const float*)(sk.swapped ? g.b : g.a);
+  const float* B = (const float*)(sk.swapped ? g.a : g.b);
+  float* C = (float*)g.c;
+  const int M = (int)sk.m, N = (int)sk.n, K = (int)sk.k;
+  const SkinnyKind kind = sk.kind;
+  if (kind == SKINNY_TINY) {
+    hipLaunchKernelGGL(k_gemm_tiny_out, dim3((uint32_t)((M * N + 3) / 4)), dim3(256), 0, s, A, B, C, M, N, K, g.ta, g.tb);
+    return true;
+  }
+  if (kind == SKINNY_OUTER) {
+    // 16 rows per wave for tall outputs; fewer for short ones, so more waves share the work.
+    const int rows = std::max(1, std::min(16, M / 256));
+    dim3 grid((uint32_t)((N + 255) / 256), (uint32_t)((M + 4 * rows - 1) / (4 * rows)));
+    if (!g.tb && !aligned(B)) return false;
+#define RG_OUTER_K(KR_, TA_, TB_) hipLaunchKernelGGL((k_gemm_outer<KR_, TA_, TB_>), grid, dim3(256), 0, s, A, B, C, M, N, K, rows)
+#define RG_OUTER(TA_, TB_)                   \
+  do {                                       \
+    if (K <= 1) RG_OUTER_K(1, TA_, TB_);     \
+    else if (K <= 4) RG_OUTER_K(4, TA_, TB_); \
+    else if (K <= 8) RG_OUTER_K(8, TA_, TB_); \
+    else RG_OUTER_K(16, TA_, TB_);           \
+  } while (0)
+    if (g.ta && g.tb) RG_OUTER(true, true);
+    else if (g.ta) RG_OUTER(true, false);
+    else if (g.tb) RG_OUTER(false, true);
+    else RG_OUTER(false, false);
+#undef RG_OUTER
+#undef RG_OUTER_K
+    return true;
+  }
+  // Both K-split kernels leave split s's partials at [s][M N] of the workspace; the split sum (or
+  // the deferred fold_wide) adds them in split order.
+  auto sum_splits = [&](const float* part, int splits) {
+    if (splits > 1 && !g.defer_split) {
+      const uint64_t mn = g.m * g.n;
+      hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 1023) / 1024), 1), dim3(256), 0, s, part, C, mn, splits, (const float*)nullptr, g.n);
+    }
+  };
+  if (kind == SKINNY_DOT) {
+    if (!aligned(A) || !aligned(B)) return false;
+    constexpr int NC = 4;
+    const int kps = skinny_dot_kps(sk.m, sk.k);
+    const int splits = (K + kps - 1) / kps;
+    float* out = splits > 1 ? (float*)g.workspace : C;
+    dim3 grid((uint32_t)((N + 4 * NC - 1) / (4 * NC)), (uint32_t)splits);
+    if (M <= 8) hipLaunchKernelGGL((k_gemm_skinny_dot<8, NC>), grid, dim3(256), 0, s, A, B, out, M, N, K, kps);
+    else hipLaunchKernelGGL((k_gemm_skinny_dot<16, NC>), grid, dim3(256), 0, s, A, B, out, M, N, K, kps);
+    sum_splits(out, splits);
+    return true;
+  }
+  if (!aligned(B)) return false;
+  const int splits0 = skinny_rows_splits(sk.n, sk.k);
+  const int kps = (K + splits0 - 1) / splits0;
+  const int splits = (K + kps - 1) / kps;
+  float* out = splits > 1 ? (float*)g.workspace : C;
+  dim3 grid((uint32_t)((N + 255) / 256), (uint32_t)splits);
+  if (M <= 8) hipLaunchKernelGGL((k_gemm_skinny_rows<8, 8>), grid, dim3(256), 0, s, A, B, out, M, N, K, sk.ta, kps);
+  else hipLaunchKernelGGL((k_gemm_skinny_rows<16, 8>), grid, dim3(256), 0, s, A, B, out, M, N, K, sk.ta, kps);
+  sum_splits(out, splits);
+  return true;
+}
+
+// Plan slots start 256-byte aligned, so a lowered product always meets the skinny kernels'
+// alignment; a K-split skinny product whose partials are deferred to the fold area relies on it.
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m == 0 || g.n == 0 || g.batch == 0) return;
+  const Skinny sk = skinny_plan(g.dtype, g.m, g.n, g.k, g.batch, g.ta, g.tb);
+  if (sk.kind != SKINNY_NONE && gemm_skinny(s, g, sk)) return;
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
     TileCfg t = pick_tile(g.m, g.n, g.k, g.batch, g.tb);
     int splits = split_count(t, g.m, g.n, g.k, g.batch);

@@ -166,8 +166,8 @@ void attention_backward(hipStream_t s, const AttnArgs& a);
 
 // The number of K splits the product runs with (1: none), and the workspace bytes its split-K
 // partials need.
-int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb);
-uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb);
+int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb);
+uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb);
 void gemm(hipStream_t s, const GemmArgs& g);
 
 }  // namespace rgk

@@ -241,7 +241,7 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
   const int64_t bias = i.args.size() == 3 ? i.args[2].slot : -1;
   if (bias >= 0 && (dtype != RG_F32 || i.args[2].shape.empty() || (uint64_t)i.args[2].shape.back() != n))
     throw std::runtime_error("product bias operand does not match the product's columns");
-  const int splits = rgk::gemm_splits(dtype, base.m, base.n, base.k, base.batch, tb);
+  const int splits = rgk::gemm_splits(dtype, base.m, base.n, base.k, base.batch, ta, tb);
   const uint64_t mn = base.m * base.n;
   if (splits > 1 && base.batch == 1 && mn % 4 == 0 && mn < (1ull << 32) && bias < 0) {
     // K-split partials go to the fold area; their sum joins the deferred folds (fold_wide).
@@ -261,7 +261,7 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
       rgk::gemm(s, g);
     };
   }
-  uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch, tb);
+  uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch, ta, tb);
   prog.workspace_bytes = std::max(prog.workspace_bytes, ws);
   base.workspace_bytes = ws;
   return [base, as, bs, dst, bias](hipStream_t s, void* const* sl, void* wsp) {

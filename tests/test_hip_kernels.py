@@ -360,3 +360,40 @@ def test_fp32_pow_over_wide_ranges_within_two_ulp():
     base = np.concatenate([rng.uniform(0.0, 4.0, 3000), rng.uniform(-3.0, 0.0, 500).round(), np.float32([2.0, 10.0, 0.5, 1.0001])])
     expo = np.concatenate([rng.uniform(-40.0, 40.0, 3000), rng.integers(-9, 10, 500).astype(np.float64), np.float32([127.0, 38.0, 149.0, 80000.0])])
     agree(lambda g, i: op(g, "pow", [i[0], i[1]]), [t(base.astype(np.float32)), t(expo.astype(np.float32))], what="wide pow", ulps=2)
+
+
+def _product_graph(sa, sb, ta, tb):
+    """op(A) @ op(B) with the transposes written as nodes, which the optimizer turns into flags."""
+    def build(g, i):
+        a = op(g, "transpose", [i[0]], perm=[1, 0]) if ta else i[0]
+        b = op(g, "transpose", [i[1]], perm=[1, 0]) if tb else i[1]
+        return op(g, "matmul", [a, b])
+    return build
+
+
+# (m, k, n, ta, tb): products with few rows and a long K (row-major or transposed right operand)
+# and outer products with a short K, which the HIP backend streams through its skinny kernels.
+SKINNY = [
+    (8, 4096, 4096, False, False), (1, 512, 256, False, False), (16, 2048, 1024, True, False), (9, 777, 68, False, False),
+    (8, 4096, 4096, False, True), (5, 1024, 100, False, True), (16, 512, 640, False, True),
+    (4096, 8, 1024, True, False), (2048, 1, 1024, False, False), (1024, 16, 1024, False, True), (1024, 3, 2048, True, True),
+    (8, 8, 4096, False, True),
+    # matrix-vector products (run as their transposes) and tiny outputs with a long K
+    (4096, 2048, 1, False, False), (2048, 4096, 1, True, False), (1000, 1000, 1, True, True), (1001, 512, 1, True, False),
+    (8, 4096, 8, False, False), (3, 2000, 5, True, True), (16, 600, 16, False, True),
+]
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", SKINNY)
+def test_skinny_products_match_numpy_and_the_oracle(m, k, n, ta, tb):
+    rng = np.random.default_rng(m * 7 + k + n)
+    a = rng.normal(size=(k, m) if ta else (m, k)).astype(np.float32)
+    b = rng.normal(size=(n, k) if tb else (k, n)).astype(np.float32)
+    build = _product_graph(a.shape, b.shape, ta, tb)
+    hip = run_graph("hip", build, [t(a), t(b)], optimize="standard")[0]
+    want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    scale = np.abs(want).max()
+    assert np.abs(hip - want).max() <= 1e-4 * scale, f"{np.abs(hip - want).max() / scale:.2e} relative to max|want|"
+    if m * k * n <= (1 << 27):
+        cpu = run_graph("cpu", build, [t(a), t(b)], optimize="standard")[0]
+        close(hip, cpu, 1e-4, "skinny vs oracle")
