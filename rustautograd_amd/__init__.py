@@ -21,6 +21,7 @@ from .ops import (
 from .transforms import custom_vjp, grad, hessian, jvp, value_and_grad
 from .control import cond, scan, while_loop
 from .program import Compiled, Report, RunResult, compile, devices, inspect, run
+from .checkpoint import load, save
 from . import nn, optim, random, tree
 
 __version__ = "0.2.0"
