@@ -171,3 +171,60 @@ def matrix_chain(n=4096, k=8, seed=0):
         return value, gb, gc
 
     return program, tuple(rg.tensor(x) for x in (a, b, c, d))
+
+
+# ---- generation: the inference-side caller of the same run loop --------------------------------
+
+def windows(tokens, key, batch, block):
+    """`batch` random windows of `block + 1` consecutive tokens: inputs and next-token targets
+    (the reference's examples/gpt.py:50-55), drawn on the device from `key`."""
+    n = tokens.shape[0]
+    start = random.randint(key, (batch,), 0, n - block - 1)
+    w = rg.take(tokens, start[:, None] + rg.arange(block + 1))
+    return w[:, :-1], w[:, 1:]
+
+
+def window_train_step(model, opt, batch):
+    """A training step over random windows of a token tensor passed as data: `step(state, tokens)`."""
+
+    def loss_fn(params, x, y):
+        return nn.cross_entropy(model(params, x), y)
+
+    def step(state, tokens):
+        k_next, k_win, _ = random.split(state["key"], 3)
+        x, y = windows(tokens, k_win, batch, model.block)
+        value, grads = rg.value_and_grad(loss_fn)(state["params"], x, y)
+        params, opt_state = opt.update(grads, state["opt"], state["params"])
+        return {"params": params, "opt": opt_state, "key": k_next}, value
+
+    return step
+
+
+def compile_sampler(model, params, temperature=1.0, top_k=None, top_p=None, device=None):
+    """A compiled step that appends one sampled token to a fixed-length context (the reference's
+    examples/gpt.py:71-86): the model's last-position logits, scaled by 1/temperature, optionally
+    filtered to the top k or the nucleus p, drawn by the Gumbel-max trick; the context shifts left
+    by one. `rg.run(sampler, state, steps=n)` then generates n tokens with no Python per token."""
+
+    def step(state):
+        k_next, k_draw = random.split(state["key"])
+        logits = model(params, state["ctx"])[:, -1, :] / temperature
+        if top_k:
+            logits = nn.top_k_logits(logits, top_k)
+        if top_p:
+            logits = nn.top_p_logits(logits, top_p)
+        token = random.categorical(k_draw, logits)
+        ctx = rg.concatenate([state["ctx"][:, 1:], token[:, None]], axis=1)
+        return {"ctx": ctx, "key": k_next}, token[0]
+
+    start = {"ctx": rg.zeros((1, model.block), "int32"), "key": random.key(0)}
+    return rg.compile(step, (start,), validate="basic", device=device)
+
+
+def generate(sampler, block, prompt_ids, n, seed=0):
+    """`n` token ids continuing `prompt_ids`. The context is fixed at `block` ids: the prompt is
+    left-padded with its first id (or cut to its last `block` ids)."""
+    ids = ([prompt_ids[0]] * block + list(prompt_ids))[-block:]
+    state = {"ctx": rg.tensor([ids], "int32"), "key": random.key(seed)}
+    out = rg.run(sampler, state, steps=n)
+    return [int(t) for t in out.history["aux"]]

@@ -313,3 +313,23 @@ def test_run_with_iterator_callback_and_early_stop():
     with pytest.raises(rg.DiagnosticError) as e:
         rg.run(c, w0, data=iter([rg.tensor([1.0, 2.0])]), steps=1)
     assert e.value.diagnostic["code"] == "INPUT_SIGNATURE_MISMATCH"
+
+
+def test_a_small_gpt_learns_a_pattern_and_its_sampler_continues_it():
+    """examples/gpt.py of the reference end to end on the oracle: train on windows of a repeating
+    text, then generate greedily (top_k=1) and with a nucleus filter (top_p=0.5)."""
+    from rustautograd_amd import optim, workloads
+    text = "abcd" * 100
+    chars = sorted(set(text))
+    tokens = rg.tensor(np.array([chars.index(c) for c in text], dtype=np.int32))
+    model = workloads.GPT(vocab=4, block=4, d=16, heads=2, layers=1)
+    params = model.init(random.key(0))
+    opt = optim.adamw(5e-3, weight_decay=0.0)
+    state = {"params": params, "opt": opt.init(params), "key": random.key(1)}
+    step = workloads.window_train_step(model, opt, 8)
+    r = rg.run(rg.compile(step, (state, tokens)), state, tokens, steps=200)
+    assert r.history["aux"][-1] < 0.1 * r.history["aux"][0]
+    for kw in ({"top_k": 1}, {"top_p": 0.5}):
+        sampler = workloads.compile_sampler(model, r.state["params"], **kw)
+        out = workloads.generate(sampler, 4, [0, 1, 2, 3], 8)
+        assert "".join(chars[t] for t in out) == "abcdabcd", kw
