@@ -31,67 +31,40 @@ def _numel(s):
     return n
 
 
-def skinny_product(m, n, k, ta, tb):
-    """Whether the backend streams an unbatched fp32 product through its skinny kernels (few rows
-    or one column with a long K, a K of at most 16, or few outputs): the HBM-bound class.
-    Mirrors skinny_plan in rustautograd_amd/csrc/hip/gemm.hip."""
-    if k <= 16 and n % 4 == 0 and m * n >= (1 << 14):
-        return True
-    if m <= 16 and k >= 512 and n >= 64 and ((not tb and n % 4 == 0) or (tb and not ta and k % 256 == 0 and n % 4 == 0)):
-        return True
-    if n == 1 and k >= 512 and m >= 64 and ((ta and m % 4 == 0) or (not ta and k % 256 == 0 and m % 4 == 0)):
-        return True
-    return m * n <= 16384 and k >= 512
-
-
 def classify(plan):
-    """Groups plan steps into kernel classes with their algorithmic work (flops for products,
-    bytes for everything else, as defined for the roofline) and the step indices of each."""
+    """Groups plan steps into kernel classes with their algorithmic work and the step indices of
+    each. The work of a step is the engine's (plan_summary's flops, bytes and bound): flops for
+    attention and for products on matrix cores, bytes (each distinct input read once, each
+    output written once) for everything else, including the products the backend streams."""
     classes = {}
 
-    def add(name, k, flops=0.0, nbytes=0.0):
+    def add(name, k, st):
         c = classes.setdefault(name, {"steps": [], "flops": 0.0, "bytes": 0.0, "launches": 0})
         c["steps"].append(k)
-        c["flops"] += flops
-        c["bytes"] += nbytes
+        if st["bound"] == "mfma":
+            c["flops"] += st["flops"]
+        c["bytes"] += st["bytes"]
         c["launches"] += 1
 
     for k, st in enumerate(plan):
-        ds = 8 if st["dtype"] == "float64" else 4
         if st["kind"] == "attention":
-            # The products of the nodes the step replaces: q k^T and P v forward; dO v^T, P^T dO,
-            # dS k and dS^T q backward (tiles the mask hides entirely are skipped, not subtracted).
-            per = 2.0 * st["bh"] * st["tq"] * st["tk"] * st["hd"]
-            add("attention", k, flops=(4 if st["backward"] else 2) * per,
-                nbytes=(len(st["input_slots"]) + len(st["output_slots"])) * st["n"] * ds)
-            continue
-        if st["kind"] == "fused":
-            n = st["n"]
-            add("fused_elementwise", k, nbytes=sum(_numel(s) for s in st["inputs"]) * ds + n * st["n_outputs"] * ds)
-            continue
-        op, shape, args = st["op"], st["shape"], st["arg_shapes"]
-        if op in ("matmul", "matmul_t"):
-            a = args[0]
-            kd = a[-1] if len(a) >= 1 and not st["ta"] else (a[-2] if len(a) >= 2 else a[0])
-            flops = 2.0 * _numel(shape) * kd
+            add("attention", k, st)
+        elif st["kind"] == "fused":
+            add("fused_elementwise", k, st)
+        elif st["op"] in ("matmul", "matmul_t"):
+            shape = st["shape"]
             n_cols = shape[-1] if shape else 1
-            m_rows = _numel(shape) // n_cols
-            nbytes = (sum(_numel(s) for s in args) + _numel(shape)) * ds
-            batched = len(args[1]) > 2
-            skinny = st["dtype"] == "float32" and not batched and skinny_product(m_rows, n_cols, kd, st["ta"], st["tb"])
-            mfma = st["dtype"] == "float32" and len(shape) >= 2 and n_cols >= 32 and m_rows >= 32 and kd >= 8
-            if skinny:
-                add("gemm_skinny", k, nbytes=nbytes)
+            m_rows = _numel(shape) // max(n_cols, 1)
+            if st["bound"] != "mfma":
+                add("gemm_skinny", k, st)
             else:
-                add("gemm_mfma" if mfma else "gemm_plain", k, flops=flops, nbytes=nbytes)
-        elif op in ("sum", "max", "min"):
-            add("reduce", k, nbytes=(_numel(args[0]) + st["n"]) * ds)
-        elif op in ("take", "take_along"):
-            add("gather_scatter", k, nbytes=_numel(args[1]) * 4 + 2 * st["n"] * ds)
-        elif op in ("take_grad", "take_along_grad"):
-            add("gather_scatter", k, nbytes=(_numel(args[0]) + st["n"]) * ds + _numel(args[1]) * 4)
+                add("gemm_mfma" if len(shape) >= 2 and n_cols >= 32 and m_rows >= 32 else "gemm_plain", k, st)
+        elif st["op"] in ("sum", "max", "min"):
+            add("reduce", k, st)
+        elif st["op"] in ("take", "take_along", "take_grad", "take_along_grad"):
+            add("gather_scatter", k, st)
         else:
-            add("structural_other", k, nbytes=(sum(_numel(s) for s in args) + st["n"]) * ds)
+            add("structural_other", k, st)
     return classes
 
 

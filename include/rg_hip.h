@@ -110,6 +110,16 @@ int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len);
  * execution stream, and stores the elapsed seconds. Gives a kernel class's average launch
  * duration without per-step event overhead. Slot contents afterwards are unspecified. */
 int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, int64_t repeats, double* seconds);
+/* Roofline support for `Compiled::profile` (validate.rs:875-919 times operations; this adds the
+ * ceiling they are measured against), with no reference counterpart. Whether the backend runs
+ * a product of op(A) m x k by op(B) k x n over `batch` problems through its bandwidth-bound
+ * streaming kernels (1) or its matrix-core kernels (0): a pure function of the arguments that
+ * touches no device. */
+int rg_hip_gemm_streamed(int32_t dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int32_t ta, int32_t tb);
+/* The current device's published peaks: peaks[0] HBM bandwidth in GB/s, peaks[1] dense fp32
+ * matrix-core TFLOP/s, peaks[2] dense fp64 matrix-core TFLOP/s, and its name in `name`.
+ * Returns 0, or 1 (message in `name`) when no device is visible or it has no published figures. */
+int rg_hip_device_peaks(double* peaks, char* name, size_t len);
 /* The device-resident `run_loop` (validate.rs:289-363): steps captured in HIP graphs and
  * replayed, batches and history kept on the device, state handed off by buffer swaps and
  * copies. Semantics equal the host loop: a non-finite history value stops the run after that

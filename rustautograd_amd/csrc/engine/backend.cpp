@@ -53,6 +53,8 @@ void register_backend(const std::string& name, const std::string& path, const st
   bind(*b, b->exec_breakdown, "exec_breakdown", false);
   bind(*b, b->exec_time_steps, "exec_time_steps", false);
   bind(*b, b->exec_run, "exec_run", false);
+  bind(*b, b->gemm_streamed, "gemm_streamed", false);
+  bind(*b, b->device_peaks, "device_peaks", false);
   g_backends.push_back(std::move(b));
 }
 

@@ -39,6 +39,8 @@ struct Backend {
   int (*exec_breakdown)(void*, int64_t, char*, size_t) = nullptr;  // optional
   int (*exec_time_steps)(void*, const int64_t*, int64_t, int64_t, double*) = nullptr;  // optional
   int (*exec_run)(void*, const rg_run_desc*, rg_run_result*) = nullptr;  // optional
+  int (*gemm_streamed)(int32_t, int64_t, int64_t, int64_t, int64_t, int32_t, int32_t) = nullptr;  // optional
+  int (*device_peaks)(double*, char*, size_t) = nullptr;  // optional
 };
 
 // Loads `path` and resolves `<prefix><entry point>` for every ABI function; throws a message.

@@ -242,8 +242,15 @@ PYBIND11_MODULE(_rg, m) {
            [](const PyCompiled& c) {
              // Per-step description for measurement tools: kind, op, dtype, n, shapes.
              py::list out;
+             const StreamedFn streamed = c.c->streamed_products();
              for (auto& s : c.c->plan.steps) {
                py::dict d;
+               // Algorithmic work: flops priced against the matrix-core peak ("mfma"), or bytes
+               // against HBM bandwidth ("hbm").
+               const StepWork w = step_work(s, streamed);
+               d["flops"] = w.flops;
+               d["bytes"] = w.bytes;
+               d["bound"] = w.compute ? "mfma" : "hbm";
                if (s.attn) {
                  const Attn& a = s.att;
                  d["kind"] = "attention";

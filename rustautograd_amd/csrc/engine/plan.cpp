@@ -1095,6 +1095,108 @@ size_t Plan::n_fused_ops() const {
   return k;
 }
 
+StepWork step_work(const Step& s, const StreamedFn& streamed) {
+  StepWork w;
+  if (s.attn) {
+    const AttnShape& a = s.att.shape;
+    const double ds = (double)dsize(s.att.dtype);
+    // The products the step replaces: q k^T and P v forward; dO v^T, P^T dO, dS k and dS^T q backward.
+    w.flops = (s.att.backward ? 4.0 : 2.0) * 2.0 * (double)a.bh * (double)a.tq * (double)a.tk * (double)a.hd;
+    // Operands in order q, k, v (, O, dO) and O (or dq, dk, dv): key-length ones are k, v, dk, dv.
+    auto rows = [&](size_t j, bool out) {
+      const bool key = out ? (s.att.backward && j >= 1) : (j == 1 || j == 2);
+      return (double)(key ? a.tk : a.tq);
+    };
+    for (size_t j = 0; j < s.att.in.size(); j++) w.bytes += rows(j, false) * (double)(a.bh * a.hd) * ds;
+    for (size_t j = 0; j < s.att.out.size(); j++) w.bytes += rows(j, true) * (double)(a.bh * a.hd) * ds;
+    w.compute = true;
+    return w;
+  }
+  if (s.fused) {
+    const Fused& f = s.group;
+    const double ds = (double)dsize(f.dtype);
+    std::vector<size_t> seen;
+    for (size_t j = 0; j < f.inputs.size(); j++) {
+      if (std::find(seen.begin(), seen.end(), f.inputs[j].slot) != seen.end()) continue;
+      seen.push_back(f.inputs[j].slot);
+      w.bytes += (double)numel(f.input_shapes[j]) * ds;
+    }
+    if (f.row_len == 0) {
+      w.bytes += (double)(f.n * f.outputs.size()) * ds;
+      return w;
+    }
+    // A row group: a register holds one value per row when it is read per row (a splat, or a
+    // broadcast of a [rows..., 1] value), is a last-axis reduction, or is computed from such
+    // registers alone; a reduction over the rows holds one value per column.
+    const size_t L = f.row_len, rows = f.n / std::max<size_t>(L, 1), last = f.shape.size() - 1;
+    std::vector<int> level(f.regs, 0);  // 0 full, 1 per row, 2 per column
+    for (size_t j = 0; j < f.inputs.size(); j++) {
+      const FusedIn& in = f.inputs[j];
+      if (in.reg == SIZE_MAX) continue;
+      const Shape& xs = f.input_shapes[j];
+      level[in.reg] = in.kind == RG_ARG_SPLAT || (in.kind == RG_ARG_BROADCAST && (xs.empty() || xs.back() == 1)) ? 1 : 0;
+    }
+    for (auto& m : f.ops) {
+      if (m.op.kind == RG_OP_REDUCE) {
+        const bool over_last = std::find(m.op.v.begin(), m.op.v.end(), (int64_t)last) != m.op.v.end();
+        level[m.reg] = over_last ? 1 : 2;
+        continue;
+      }
+      bool per_row = true;
+      for (auto& a : m.args) per_row = per_row && a.first && level[a.second] == 1;
+      level[m.reg] = per_row ? 1 : 0;
+    }
+    for (auto& o : f.outputs) w.bytes += (double)(level[o.first] == 1 ? rows : level[o.first] == 2 ? L : f.n) * ds;
+    return w;
+  }
+  const Instr& i = s.instr;
+  const double ds = (double)dsize(i.dtype);
+  double in_elems = 0;
+  for (auto& a : i.arg_shapes) in_elems += (double)numel(a);
+  switch (i.op.kind) {
+    case RG_OP_MATMUL:
+    case RG_OP_MATMUL_T: {
+      // Dimensions as the backend lowers the product: a 2-D right operand with an untransposed
+      // left one folds the left operand's batch dimensions into its rows.
+      const bool ta = i.op.kind == RG_OP_MATMUL_T && i.op.ta, tb = i.op.kind == RG_OP_MATMUL_T && i.op.tb;
+      const Shape &sa = i.arg_shapes[0], &sb = i.arg_shapes[1];
+      const size_t ar = sa.size(), br = sb.size();
+      uint64_t m = ar >= 2 ? (ta ? sa[ar - 1] : sa[ar - 2]) : 1;
+      const uint64_t k = ar >= 2 ? (ta ? sa[ar - 2] : sa[ar - 1]) : (ar ? sa[0] : 1);
+      const uint64_t n = br >= 2 ? (tb ? sb[br - 2] : sb[br - 1]) : 1;
+      uint64_t batch = 1;
+      Shape ba(sa.begin(), sa.begin() + (ar >= 2 ? ar - 2 : 0)), bb(sb.begin(), sb.begin() + (br >= 2 ? br - 2 : 0));
+      if (bb.empty() && !ta) {
+        m *= numel(ba);
+      } else {
+        const size_t r = std::max(ba.size(), bb.size());
+        for (size_t q = 0; q < r; q++) {
+          const size_t x = q < r - ba.size() ? 1 : ba[q - (r - ba.size())];
+          const size_t y = q < r - bb.size() ? 1 : bb[q - (r - bb.size())];
+          batch *= std::max(x, y);
+        }
+      }
+      w.flops = 2.0 * (double)m * (double)n * (double)k * (double)batch;
+      w.bytes = (in_elems + (double)i.n) * ds;
+      w.compute = i.dtype != DType::I32 && !(streamed && streamed(i.dtype, m, n, k, batch, ta, tb));
+      return w;
+    }
+    case RG_OP_TAKE:
+    case RG_OP_TAKE_ALONG:
+      // The indices, and each gathered element read once and written once.
+      w.bytes = (double)numel(i.arg_shapes[1]) * 4.0 + 2.0 * (double)i.n * ds;
+      return w;
+    case RG_OP_TAKE_GRAD:
+    case RG_OP_TAKE_ALONG_GRAD:
+      // The cotangent read, the indices, and the result written.
+      w.bytes = ((double)numel(i.arg_shapes[0]) + (double)i.n) * ds + (double)numel(i.arg_shapes[1]) * 4.0;
+      return w;
+    default:
+      w.bytes = (in_elems + (double)i.n) * ds;
+      return w;
+  }
+}
+
 Plan build_plan(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse) {
   return build_with(g, outputs, reuse, nullptr);
 }

@@ -184,6 +184,19 @@ struct Plan {
   void serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) const;
 };
 
+// Algorithmic work of one step, the figure a roofline divides by its time: the flops of products
+// (fused attention, and matrix products on matrix cores) priced against the matrix-core peak, and
+// for every other step the bytes it must move at least (each distinct input read once, each output
+// written once) priced against HBM bandwidth. `streamed` says whether the device runs a product
+// of these dimensions through bandwidth-bound kernels (then it is priced by its bytes); when it is
+// empty every floating-point product is priced by its flops.
+struct StepWork {
+  double flops = 0, bytes = 0;
+  bool compute = false;  // priced by flops
+};
+using StreamedFn = std::function<bool(DType, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb)>;
+StepWork step_work(const Step& s, const StreamedFn& streamed);
+
 // Buffer assignment by last use, scanning steps in order; with reuse=false no buffer is shared (plan.rs:462-465).
 Plan build_plan(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse);
 // Buffer reuse plus fused groups (plan.rs:466-479).

@@ -680,6 +680,13 @@ Json Compiled::validate(const std::vector<Tensor>& examples) {
   return r;
 }
 
+StreamedFn Compiled::streamed_products() const {
+  if (!device->gemm_streamed) return {};
+  return [d = device](DType dt, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
+    return d->gemm_streamed((int32_t)dt, (int64_t)m, (int64_t)n, (int64_t)k, (int64_t)batch, ta, tb) != 0;
+  };
+}
+
 Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const {
   repeats = std::max<size_t>(repeats, 1);
   std::vector<double> seconds(plan.steps.size(), 0.0);
@@ -708,7 +715,32 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
       }
     }
   }
-  std::map<std::string, std::pair<double, size_t>> rows;
+  // Each operation's algorithmic work (flops against the matrix-core peak, or bytes against HBM
+  // bandwidth), as the device runs it, and the device's published peaks when it reports them.
+  const StreamedFn streamed = streamed_products();
+  double peaks[3] = {0, 0, 0};
+  Json roofline = Json::obj();
+  bool have_peaks = false;
+  if (device->device_peaks) {
+    char name[256] = {0};
+    have_peaks = device->device_peaks(peaks, name, sizeof name) == 0;
+    if (have_peaks) {
+      roofline["device"] = std::string(name);
+      roofline["hbm_gb_per_s"] = peaks[0];
+      roofline["fp32_tflop_per_s"] = peaks[1];
+      roofline["fp64_tflop_per_s"] = peaks[2];
+    } else {
+      roofline["unavailable"] = std::string(name);
+    }
+  } else {
+    roofline["unavailable"] = "the backend reports no device peaks";
+  }
+  struct Row {
+    double seconds = 0, flops = 0, bytes = 0;
+    size_t count = 0;
+    bool compute = false, f64 = false;
+  };
+  std::map<std::string, Row> rows;
   auto shape_str = [](const Shape& s) {
     std::string o = "[";
     for (size_t i = 0; i < s.size(); i++) o += (i ? ", " : "") + std::to_string(s[i]);
@@ -717,38 +749,69 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
   for (size_t s = 0; s < plan.steps.size(); s++) {
     const Step& st = plan.steps[s];
     std::string key;
+    DType dt;
     if (st.attn) {
       key = std::string(st.att.backward ? "attention backward" : "attention") + " bh=" + std::to_string(st.att.shape.bh) +
             " t=" + std::to_string(st.att.shape.tq) + "x" + std::to_string(st.att.shape.tk) + " hd=" + std::to_string(st.att.shape.hd);
+      dt = st.att.dtype;
     } else if (st.fused) {
       key = "fused[";
       for (size_t m = 0; m < st.group.ops.size(); m++) key += std::string(m ? "," : "") + st.group.ops[m].op.name();
       key += "] n=" + std::to_string(st.group.n);
+      dt = st.group.dtype;
     } else {
       key = std::string(st.instr.op.name()) + " " + shape_str(st.instr.shape) + " <- [";
       for (size_t a = 0; a < st.instr.arg_shapes.size(); a++) key += (a ? ", " : "") + shape_str(st.instr.arg_shapes[a]);
       key += "]";
+      dt = st.instr.dtype;
     }
-    rows[key].first += seconds[s];
-    rows[key].second++;
+    if (dt == DType::F64) key += " f64";
+    const StepWork w = step_work(st, streamed);
+    Row& r = rows[key];
+    r.seconds += seconds[s];
+    r.count++;
+    r.flops += w.flops;
+    r.bytes += w.bytes;
+    r.compute = w.compute;
+    r.f64 = dt == DType::F64;
   }
   double total = 0;
   for (double t : seconds) total += t;
-  std::vector<std::pair<std::string, std::pair<double, size_t>>> list(rows.begin(), rows.end());
-  std::stable_sort(list.begin(), list.end(), [](auto& a, auto& b) { return a.second.first > b.second.first; });
+  std::vector<std::pair<std::string, Row>> list(rows.begin(), rows.end());
+  std::stable_sort(list.begin(), list.end(), [](auto& a, auto& b) { return a.second.seconds > b.second.seconds; });
   Json ops = Json::arr();
+  double ideal = 0;  // seconds per pass if every operation ran at its peak
   for (auto& [k, v] : list) {
     Json o = Json::obj();
     o["operation"] = k;
-    o["count"] = v.second;
-    o["microseconds_per_run"] = v.first / (double)repeats * 1e6;
-    o["share"] = total > 0 ? v.first / total : 0.0;
+    o["count"] = v.count;
+    o["microseconds_per_run"] = v.seconds / (double)repeats * 1e6;
+    o["share"] = total > 0 ? v.seconds / total : 0.0;
+    o["bound"] = v.compute ? "mfma" : "hbm";
+    o["flops_per_run"] = v.flops;
+    o["bytes_per_run"] = v.bytes;
+    const double per_run = v.seconds / (double)repeats;
+    const double work = v.compute ? v.flops / 1e12 : v.bytes / 1e9;
+    o["unit"] = v.compute ? "TFLOP/s" : "GB/s";
+    if (per_run > 0) o["achieved"] = work / per_run;
+    if (have_peaks) {
+      const double peak = v.compute ? (v.f64 ? peaks[2] : peaks[1]) : peaks[0];
+      o["peak"] = peak;
+      if (per_run > 0) o["fraction_of_peak"] = work / per_run / peak;
+      ideal += work / peak;
+    }
     ops.push(o);
+  }
+  if (have_peaks && total > 0) {
+    // The whole pass against the sum of its operations' roofline times.
+    roofline["seconds_at_peak_per_run"] = ideal;
+    roofline["fraction_of_peak"] = ideal / (total / (double)repeats);
   }
   Json j = Json::obj();
   j["repeats"] = repeats;
   j["microseconds_per_run"] = total / (double)repeats * 1e6;
   j["operations"] = ops;
+  j["roofline"] = roofline;
   j["breakdown"] = breakdown;
   return j;
 }

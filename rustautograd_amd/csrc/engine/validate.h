@@ -46,6 +46,8 @@ class Compiled {
   std::vector<Tensor> try_call(const std::vector<Tensor>& inputs) const;
   Json check(const std::vector<Tensor>& inputs);
   Json profile(const std::vector<Tensor>& inputs, size_t repeats) const;
+  // How the device prices matrix products for step_work: which run on its streaming kernels.
+  StreamedFn streamed_products() const;
   void validate_spec(const RunSpec& spec) const;
   RunOut run(const RunSpec& spec, const std::vector<Tensor>& state, const std::vector<std::vector<Tensor>>& batches,
              size_t steps) const;

@@ -753,6 +753,10 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
 
 }  // namespace
 
+bool gemm_streamed(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
+  return skinny_plan(dtype, m, n, k, batch, ta, tb).kind != SKINNY_NONE;
+}
+
 int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
   if (m == 0 || n == 0 || batch == 0) return 1;
   const Skinny sk = skinny_plan(dtype, m, n, k, batch, ta, tb);

@@ -164,6 +164,10 @@ uint64_t attention_mask_words(const AttnArgs& a);
 void attention_forward(hipStream_t s, const AttnArgs& a, bool build_mask_bits = true);
 void attention_backward(hipStream_t s, const AttnArgs& a);
 
+// Whether the product runs through the bandwidth-bound skinny kernels (alignment aside: an
+// unaligned operand falls back to the general kernels at launch).
+bool gemm_streamed(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb);
+
 // The number of K splits the product runs with (1: none), and the workspace bytes its split-K
 // partials need.
 int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb);

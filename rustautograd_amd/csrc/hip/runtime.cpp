@@ -955,6 +955,47 @@ int rg_hip_available(void) {
   return avail;
 }
 
+int rg_hip_gemm_streamed(int32_t dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int32_t ta, int32_t tb) {
+  if (m <= 0 || n <= 0 || k <= 0 || batch <= 0) return 0;
+  return rgk::gemm_streamed(dtype, (uint64_t)m, (uint64_t)n, (uint64_t)k, (uint64_t)batch, ta != 0, tb != 0) ? 1 : 0;
+}
+
+int rg_hip_device_peaks(double* peaks, char* name, size_t len) {
+  int dev = 0, n = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0 || hipGetDevice(&dev) != hipSuccess ||
+      hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    put(name, len, "no HIP device is visible");
+    return 1;
+  }
+  // AMD's published dense figures: HBM3E at 8 TB/s; fp32 and fp64 matrix-core peaks.
+  struct Part {
+    const char* name;
+    double hbm_gbs, fp32_tflops, fp64_tflops;
+  };
+  static const Part parts[] = {{"MI355X", 8000.0, 157.3, 78.6}, {"MI350X", 8000.0, 144.2, 72.1}};
+  for (const Part& p : parts)
+    if (strstr(prop.name, p.name)) {
+      peaks[0] = p.hbm_gbs;
+      peaks[1] = p.fp32_tflops;
+      peaks[2] = p.fp64_tflops;
+      put(name, len, std::string("AMD Instinct ") + p.name);
+      return 0;
+    }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) == 0 && prop.clockRate > 0) {
+    // Another CDNA4 part: 256 fp32 (128 fp64) matrix flops per clock per CU at its peak clock.
+    const double ghz = prop.clockRate / 1e6;
+    peaks[0] = 8000.0;
+    peaks[1] = 256.0 * prop.multiProcessorCount * ghz / 1000.0;
+    peaks[2] = peaks[1] / 2.0;
+    put(name, len, std::string(prop.name[0] ? prop.name : "gfx950") + ", " + std::to_string(prop.multiProcessorCount) + " CUs at " +
+                       std::to_string(prop.clockRate / 1000) + " MHz (compute peaks from CU count and clock)");
+    return 0;
+  }
+  put(name, len, std::string("no published peaks for ") + prop.name + " (" + prop.gcnArchName + ")");
+  return 1;
+}
+
 uint64_t rg_hip_device_memory_bytes(void) {
   size_t free_b = 0, total = 0;
   if (hipMemGetInfo(&free_b, &total) != hipSuccess) return 0;
