@@ -200,50 +200,82 @@ __global__ void __launch_bounds__(TPB) k_take_along(const E* __restrict__ src, c
 // the CPU's sequential order (src/plan.rs:1502-1531), so results are bit-identical. Index chunks
 // are staged in LDS and shared by the block.
 
-constexpr uint32_t TG_CHUNK = 4096;
+constexpr uint32_t TG_PER = 32;                // index entries each thread classifies per chunk
+constexpr uint32_t TG_CHUNK = TPB * TG_PER;     // 8192 entries: 32 KB of positions in LDS
 
-// Block (x, d, o) owns columns [x*256, x*256+256) of output row (o, d). The block first lists,
-// in increasing position, the index entries that hit row d (a stable compaction through LDS),
-// then every thread sums its column over that list: the CPU's order, coalesced reads.
+// Block (x, d, o) owns columns [x*256, x*256+256) of output row (o, d). Per chunk of 8192 index
+// entries, each thread classifies 32 consecutive entries (a bit mask of those that hit row d),
+// a block-wide exclusive scan of the mask counts places the matching positions in LDS in
+// increasing order, and every thread then sums its column over that list: the CPU's order, with
+// coalesced row reads. The adds are sequential but the loads are not: TG_INFLIGHT rows are loaded
+// before the first of them is added, so a row hit ~100 times costs a few memory latencies.
 template <class T>
 __global__ void __launch_bounds__(TPB) k_take_grad(const T* __restrict__ ct, const int* __restrict__ idx, T* __restrict__ dst,
                                                    uint32_t block, uint32_t dim, uint32_t n_idx) {
+  constexpr uint32_t TG_INFLIGHT = sizeof(T) == 4 ? 64 : 32;
   __shared__ uint32_t list[TG_CHUNK];
-  __shared__ uint32_t counts[TPB];
+  __shared__ uint32_t wave_total[TPB / 64];
   const uint32_t d = blockIdx.y, o = blockIdx.z;
   const uint32_t q = blockIdx.x * TPB + threadIdx.x;
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const bool vec = ((uintptr_t)idx & 15u) == 0;
+  const T* base = ct + (uint64_t)o * n_idx * block + (q < block ? q : 0);
   T acc = (T)0;
   for (uint32_t j0 = 0; j0 < n_idx; j0 += TG_CHUNK) {
     const uint32_t m = min(TG_CHUNK, n_idx - j0);
-    const uint32_t per = (m + TPB - 1) / TPB;
-    const uint32_t lo = min(m, threadIdx.x * per), hi = min(m, lo + per);
-    uint32_t c = 0;
-    for (uint32_t x = lo; x < hi; x++) c += clamp_index(idx[j0 + x], dim) == d;
-    counts[threadIdx.x] = c;
-    __syncthreads();
-    // Inclusive prefix sum of the counts (log2(TPB) steps), so each thread's matches land in
-    // increasing index order.
-    for (uint32_t off = 1; off < TPB; off <<= 1) {
-      const uint32_t v = threadIdx.x >= off ? counts[threadIdx.x - off] : 0u;
-      __syncthreads();
-      counts[threadIdx.x] += v;
-      __syncthreads();
+    const uint32_t lo = threadIdx.x * TG_PER;
+    uint32_t bits = 0;
+    if (vec && lo + TG_PER <= m) {
+      const int4* p = reinterpret_cast<const int4*>(idx + j0 + lo);
+#pragma unroll
+      for (uint32_t u = 0; u < TG_PER / 4; u++) {
+        const int4 w = p[u];
+        bits |= (uint32_t)(clamp_index(w.x, dim) == d) << (4 * u);
+        bits |= (uint32_t)(clamp_index(w.y, dim) == d) << (4 * u + 1);
+        bits |= (uint32_t)(clamp_index(w.z, dim) == d) << (4 * u + 2);
+        bits |= (uint32_t)(clamp_index(w.w, dim) == d) << (4 * u + 3);
+      }
+    } else {
+      for (uint32_t u = 0; u < TG_PER && lo + u < m; u++) bits |= (uint32_t)(clamp_index(idx[j0 + lo + u], dim) == d) << u;
     }
-    uint32_t at = counts[threadIdx.x] - c;
-    const uint32_t len = counts[TPB - 1];
-    for (uint32_t x = lo; x < hi; x++)
-      if (clamp_index(idx[j0 + x], dim) == d) list[at++] = j0 + x;
+    // Exclusive scan of the per-thread counts: within the wave by shuffles, across waves by LDS.
+    const uint32_t c = __popc(bits);
+    uint32_t incl = c;
+#pragma unroll
+    for (uint32_t off = 1; off < 64; off <<= 1) {
+      const uint32_t v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    if (lane == 63) wave_total[wave] = incl;
+    __syncthreads();
+    uint32_t at = incl - c, len = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < TPB / 64; w++) {
+      const uint32_t t = wave_total[w];
+      at += w < wave ? t : 0u;
+      len += t;
+    }
+    while (bits) {
+      const uint32_t u = __ffs(bits) - 1;
+      bits &= bits - 1;
+      list[at++] = j0 + lo + u;
+    }
     __syncthreads();
     if (q < block) {
-      // Eight rows' loads in flight, added in list order.
-      const T* base = ct + (uint64_t)o * n_idx * block + q;
       uint32_t e = 0;
+      for (; e + TG_INFLIGHT <= len; e += TG_INFLIGHT) {
+        T v[TG_INFLIGHT];
+#pragma unroll
+        for (uint32_t u = 0; u < TG_INFLIGHT; u++) v[u] = base[(uint64_t)list[e + u] * block];
+#pragma unroll
+        for (uint32_t u = 0; u < TG_INFLIGHT; u++) acc = acc + v[u];
+      }
       for (; e + 8 <= len; e += 8) {
         T v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = base[(uint64_t)list[e + u] * block];
+        for (uint32_t u = 0; u < 8; u++) v[u] = base[(uint64_t)list[e + u] * block];
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc = acc + v[u];
+        for (uint32_t u = 0; u < 8; u++) acc = acc + v[u];
       }
       for (; e < len; e++) acc = acc + base[(uint64_t)list[e] * block];
     }

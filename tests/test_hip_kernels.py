@@ -296,6 +296,11 @@ def test_scatter_add_at_embedding_shapes_is_bit_exact():
     ct2 = t(rng.normal(size=(3, 9000, 5)).astype(np.float32))
     idx2 = t(rng.integers(-3, 12, size=(9000,)), "int32")
     agree(lambda g, i: op(g, "take_grad", [i[0], i[1]], axis=1, shape=[3, 10, 5]), [ct2, idx2], ulps=0)
+    # One row hit by every entry (long in-order sums across two chunks), in float64 and float32.
+    for dtype in ("float64", "float32"):
+        ct3 = t(rng.normal(size=(10001, 3)), dtype)
+        idx3 = t(np.where(np.arange(10001) % 97 == 0, 2, 7), "int32")
+        agree(lambda g, i: op(g, "take_grad", [i[0], i[1]], axis=0, shape=[9, 3]), [ct3, idx3], ulps=0)
 
 
 I32_MIN, I32_MAX = -2 ** 31, 2 ** 31 - 1
