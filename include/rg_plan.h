@@ -71,6 +71,23 @@
  *   TAKE_ALONG_GRAD shape...           CONCAT     axis
  *   RAND_UNIFORM / RAND_NORMAL  dtype, shape...
  *   KEY_SPLIT      n                   ARG_TOP_K  k          CUMSUM reverse
+ *   SCAN           n_carry, n_x, length, reverse, RESULTS, BODIES
+ *   WHILE          n_carry, max_iterations, RESULTS, BODIES
+ *   COND           RESULTS, BODIES
+ *     RESULTS      n_results, per result the program reads: result index, slot
+ *     BODIES       n_bodies, per body: n_words, then a whole plan descriptor (header included)
+ *                  whose constants lie in the same blob (scan: body; while: condition, body;
+ *                  cond: then, else)
+ *   Control flow (plan.rs:737-831): the step's `dst` is -1 and its results go to the listed
+ *   slots. Scan runs its body `length` times (from the last position when `reverse`) over
+ *   inputs (carries, one slice of each x, captures); its results by index are the final
+ *   carries, the ys stacked along a new leading axis, then the carries as they were before each
+ *   step, stacked. While runs its condition and, while that is nonzero and fewer than
+ *   max_iterations steps ran, its body over (carries, captures); results are the final carries,
+ *   then the step count (int32). Cond runs `then` when its first argument is nonzero, else
+ *   `else`, over the remaining arguments; results are that body's outputs. A body's carry
+ *   results are written back to its carry inputs after every step, all read before any is
+ *   written.
  *
  * Slot buffers hold at least `capacity` elements (at least 4 bytes) and start zeroed; a value
  * is the row-major prefix of `n` elements of its slot.
@@ -352,6 +369,55 @@ inline Plan parse(const int64_t* w, size_t nw) {
   }
   if (p != nw) throw std::runtime_error("plan descriptor has trailing words");
   return pl;
+}
+
+/* The attributes of a control-flow step (SCAN, WHILE, COND). Bodies point into the step's
+ * attribute words; parse each with `parse`. */
+struct ControlAttr {
+  int64_t n_carry = 0, n_x = 0, length = 0, max_iterations = 0;
+  bool reverse = false;
+  std::vector<std::pair<int64_t, int64_t>> results; /* (result index, slot) */
+  std::vector<std::pair<const int64_t*, size_t>> bodies;
+};
+
+inline bool is_control(int32_t op) { return op == RG_OP_SCAN || op == RG_OP_WHILE || op == RG_OP_COND; }
+
+inline ControlAttr parse_control(const Instr& in) {
+  const std::vector<int64_t>& a = in.attr;
+  size_t q = 0;
+  auto next = [&]() -> int64_t {
+    if (q >= a.size()) throw std::runtime_error("control-flow attributes truncated");
+    return a[q++];
+  };
+  ControlAttr c;
+  if (in.op == RG_OP_SCAN) {
+    c.n_carry = next();
+    c.n_x = next();
+    c.length = next();
+    c.reverse = next() != 0;
+  } else if (in.op == RG_OP_WHILE) {
+    c.n_carry = next();
+    c.max_iterations = next();
+  }
+  int64_t n = next();
+  if (n < 0 || (size_t)n > a.size()) throw std::runtime_error("control-flow attributes have a bad length");
+  for (int64_t j = 0; j < n; j++) {
+    int64_t index = next();
+    c.results.push_back({index, next()});
+  }
+  n = next();
+  if (n < 0 || n > 2) throw std::runtime_error("control-flow step has a bad body count");
+  for (int64_t j = 0; j < n; j++) {
+    int64_t len = next();
+    if (len < 0 || q + (size_t)len > a.size()) throw std::runtime_error("control-flow body truncated");
+    c.bodies.push_back({a.data() + q, (size_t)len});
+    q += (size_t)len;
+  }
+  const size_t want = in.op == RG_OP_SCAN ? 1 : 2;
+  if (c.bodies.size() != want || c.n_carry < 0 || c.n_x < 0 || c.length < 0 || c.max_iterations < 0 ||
+      (size_t)(c.n_carry + c.n_x) > in.args.size())
+    throw std::runtime_error("control-flow step is malformed");
+  return c;
 }
 
 }  // namespace rgplan

@@ -19,7 +19,9 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
+#include <stdexcept>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -277,8 +279,52 @@ struct Exec {
   std::string failure;
 };
 
+// The control-flow attributes of a plan step (include/rg_plan.h): counts, result slots, and the
+// bodies' plans, each with its own control-flow steps parsed.
+struct Control;
+struct PlanX {
+  Plan plan;
+  std::vector<std::unique_ptr<Control>> control;  // per step; null for every other step
+};
+struct Control {
+  int op = 0;
+  int64_t n_carry = 0, n_x = 0, length = 0, max_iter = 0;
+  bool reverse = false;
+  std::vector<std::pair<int64_t, int64_t>> outs;  // (result index, slot)
+  std::vector<PlanX> bodies;                      // scan: body; while: condition, body; cond: then, else
+};
+
+void parse_control(PlanX& px);
+
+PlanX load_plan(const int64_t* w, size_t n) {
+  PlanX px;
+  px.plan = parse(w, n);
+  parse_control(px);
+  return px;
+}
+
+void parse_control(PlanX& px) {
+  px.control.resize(px.plan.steps.size());
+  for (size_t k = 0; k < px.plan.steps.size(); k++) {
+    const Step& st = px.plan.steps[k];
+    if (st.kind != RG_STEP_INSTR || !is_control(st.instr.op)) continue;
+    const ControlAttr a = parse_control(st.instr);
+    auto c = std::make_unique<Control>();
+    c->op = st.instr.op;
+    c->n_carry = a.n_carry;
+    c->n_x = a.n_x;
+    c->length = a.length;
+    c->max_iter = a.max_iterations;
+    c->reverse = a.reverse;
+    c->outs = a.results;
+    for (auto [w, n] : a.bodies) c->bodies.push_back(load_plan(w, n));
+    px.control[k] = std::move(c);
+  }
+}
+
 struct Program {
   Plan plan;
+  std::vector<std::unique_ptr<Control>> control;
   std::vector<uint8_t> blob;
   std::mutex mu;
   std::vector<Frame> pool;
@@ -1010,18 +1056,143 @@ void run_attention(const Attn& a, std::vector<Buf>& s) {
   }
 }
 
-void exec_step(Program* p, Frame& f, size_t k) {
-  const Step& st = p->plan.steps[k];
-  if (st.kind == RG_STEP_ATTN) {
-    run_attention(st.attn, f.slots);
-  } else if (st.kind == RG_STEP_ROWS) {
-    if (st.fused.dtype == RG_F32) run_rows<float>(st.fused, f.slots);
-    else run_rows<double>(st.fused, f.slots);
-  } else if (st.kind == RG_STEP_FUSED) {
-    if (st.fused.dtype == RG_F32) run_fused<float>(st.fused, f.slots);
-    else run_fused<double>(st.fused, f.slots);
+Frame frame_of(const Plan& plan, const std::vector<uint8_t>& blob) {
+  Frame f;
+  for (auto& s : plan.slots) f.slots.push_back(Buf{std::vector<uint8_t>(std::max<size_t>((size_t)s.cap * (size_t)dtype_size(s.dtype), 4), 0)});
+  for (auto& c : plan.consts)
+    memcpy(f.slots[(size_t)c.slot].bytes.data(), blob.data() + c.offset, (size_t)c.n * (size_t)dtype_size(plan.slots[(size_t)c.slot].dtype));
+  return f;
+}
+
+void exec_plan_step(const Plan& plan, const std::vector<std::unique_ptr<Control>>& control, const std::vector<uint8_t>& blob,
+                    std::vector<Buf>& slots, size_t k);
+
+void exec_plan(const PlanX& px, const std::vector<uint8_t>& blob, Frame& f) {
+  for (size_t k = 0; k < px.plan.steps.size(); k++) exec_plan_step(px.plan, px.control, blob, f.slots, k);
+}
+
+// Bytes of `n` elements of slot `slot` of `plan`.
+size_t slot_bytes(const Plan& plan, int64_t slot, int64_t n) { return (size_t)n * (size_t)dtype_size(plan.slots[(size_t)slot].dtype); }
+
+// Copies a body's carry results into its carry inputs, through a copy of all of them first, as
+// one result may be another carry's input (plan.rs:730-735).
+void feed_carry(const Plan& plan, Frame& f, size_t n_carry) {
+  std::vector<std::vector<uint8_t>> next;
+  for (size_t k = 0; k < n_carry; k++) {
+    const auto& o = plan.outputs[k];
+    const auto& b = f.slots[(size_t)o.slot].bytes;
+    next.emplace_back(b.begin(), b.begin() + (ptrdiff_t)slot_bytes(plan, o.slot, o.n));
+  }
+  for (size_t k = 0; k < n_carry; k++) memcpy(f.slots[(size_t)plan.inputs[k].first].bytes.data(), next[k].data(), next[k].size());
+}
+
+// Control flow (plan.rs:737-831): the bodies' plans run on frames of their own, fed by copies.
+void run_control(const Plan& plan, const Instr& in, const Control& c, const std::vector<uint8_t>& blob, std::vector<Buf>& s) {
+  auto arg_bytes = [&](size_t k) { return s[(size_t)in.args[k].slot].bytes.data(); };
+  auto load_inputs = [&](const PlanX& b, Frame& f, size_t first) {
+    for (size_t k = 0; k + first < in.args.size(); k++)
+      memcpy(f.slots[(size_t)b.plan.inputs[k].first].bytes.data(), arg_bytes(k + first),
+             slot_bytes(b.plan, b.plan.inputs[k].first, b.plan.inputs[k].second));
+  };
+  if (c.op == RG_OP_SCAN) {
+    const PlanX& b = c.bodies[0];
+    const size_t nc = (size_t)c.n_carry, nx = (size_t)c.n_x, len = (size_t)c.length;
+    const size_t n_y = b.plan.outputs.size() - nc;
+    Frame f = frame_of(b.plan, blob);
+    // Carries and captures once; the x slices every step.
+    for (size_t k = 0; k < in.args.size(); k++)
+      if (k < nc || k >= nc + nx)
+        memcpy(f.slots[(size_t)b.plan.inputs[k].first].bytes.data(), arg_bytes(k),
+               slot_bytes(b.plan, b.plan.inputs[k].first, b.plan.inputs[k].second));
+    for (size_t step = 0; step < len; step++) {
+      const size_t at = c.reverse ? len - 1 - step : step;
+      for (size_t k = nc; k < nc + nx; k++) {
+        const auto [slot, m] = b.plan.inputs[k];
+        const size_t bytes = slot_bytes(b.plan, slot, m);
+        memcpy(f.slots[(size_t)slot].bytes.data(), arg_bytes(k) + at * bytes, bytes);
+      }
+      for (auto& [index, dst] : c.outs)
+        if ((size_t)index >= nc + n_y) {
+          const auto [slot, m] = b.plan.inputs[(size_t)index - nc - n_y];
+          const size_t bytes = slot_bytes(b.plan, slot, m);
+          memcpy(s[(size_t)dst].bytes.data() + at * bytes, f.slots[(size_t)slot].bytes.data(), bytes);
+        }
+      exec_plan(b, blob, f);
+      for (auto& [index, dst] : c.outs)
+        if ((size_t)index >= nc && (size_t)index < nc + n_y) {
+          const auto& o = b.plan.outputs[(size_t)index];
+          const size_t bytes = slot_bytes(b.plan, o.slot, o.n);
+          memcpy(s[(size_t)dst].bytes.data() + at * bytes, f.slots[(size_t)o.slot].bytes.data(), bytes);
+        }
+      feed_carry(b.plan, f, nc);
+    }
+    for (auto& [index, dst] : c.outs)
+      if ((size_t)index < nc) {
+        const auto [slot, m] = b.plan.inputs[(size_t)index];
+        memcpy(s[(size_t)dst].bytes.data(), f.slots[(size_t)slot].bytes.data(), slot_bytes(b.plan, slot, m));
+      }
+  } else if (c.op == RG_OP_WHILE) {
+    const PlanX &cp = c.bodies[0], &bp = c.bodies[1];
+    const size_t nc = (size_t)c.n_carry;
+    Frame cf = frame_of(cp.plan, blob), bf = frame_of(bp.plan, blob);
+    load_inputs(cp, cf, 0);
+    load_inputs(bp, bf, 0);
+    int64_t count = 0;
+    for (;;) {
+      exec_plan(cp, blob, cf);
+      const auto& o = cp.plan.outputs[0];
+      const int d = cp.plan.slots[(size_t)o.slot].dtype;
+      Buf& v = cf.slots[(size_t)o.slot];
+      const double x = d == RG_F32 ? (double)v.as<float>()[0] : d == RG_F64 ? v.as<double>()[0] : (double)v.as<int32_t>()[0];
+      if (x == 0.0 || count == c.max_iter) break;
+      exec_plan(bp, blob, bf);
+      feed_carry(bp.plan, bf, nc);
+      for (size_t k = 0; k < nc; k++) {
+        const auto [slot, m] = bp.plan.inputs[k];
+        memcpy(cf.slots[(size_t)cp.plan.inputs[k].first].bytes.data(), bf.slots[(size_t)slot].bytes.data(), slot_bytes(bp.plan, slot, m));
+      }
+      count++;
+    }
+    for (auto& [index, dst] : c.outs) {
+      if ((size_t)index < nc) {
+        const auto [slot, m] = bp.plan.inputs[(size_t)index];
+        memcpy(s[(size_t)dst].bytes.data(), bf.slots[(size_t)slot].bytes.data(), slot_bytes(bp.plan, slot, m));
+      } else {
+        s[(size_t)dst].as<int32_t>()[0] = (int32_t)count;
+      }
+    }
   } else {
-    exec_instr(p->plan, st.instr, f.slots);
+    const int pd = plan.slots[(size_t)in.args[0].slot].dtype;
+    Buf& pv = s[(size_t)in.args[0].slot];
+    const double pred = pd == RG_F32 ? (double)pv.as<float>()[0] : pd == RG_F64 ? pv.as<double>()[0] : (double)pv.as<int32_t>()[0];
+    const PlanX& b = c.bodies[pred != 0.0 ? 0 : 1];
+    Frame f = frame_of(b.plan, blob);
+    load_inputs(b, f, 1);
+    exec_plan(b, blob, f);
+    for (auto& [index, dst] : c.outs) {
+      const auto& o = b.plan.outputs[(size_t)index];
+      memcpy(s[(size_t)dst].bytes.data(), f.slots[(size_t)o.slot].bytes.data(), slot_bytes(b.plan, o.slot, o.n));
+    }
+  }
+}
+
+void exec_step(Program* p, Frame& f, size_t k) { exec_plan_step(p->plan, p->control, p->blob, f.slots, k); }
+
+void exec_plan_step(const Plan& plan, const std::vector<std::unique_ptr<Control>>& control, const std::vector<uint8_t>& blob,
+                    std::vector<Buf>& slots, size_t k) {
+  const Step& st = plan.steps[k];
+  if (control[k]) {
+    run_control(plan, st.instr, *control[k], blob, slots);
+  } else if (st.kind == RG_STEP_ATTN) {
+    run_attention(st.attn, slots);
+  } else if (st.kind == RG_STEP_ROWS) {
+    if (st.fused.dtype == RG_F32) run_rows<float>(st.fused, slots);
+    else run_rows<double>(st.fused, slots);
+  } else if (st.kind == RG_STEP_FUSED) {
+    if (st.fused.dtype == RG_F32) run_fused<float>(st.fused, slots);
+    else run_fused<double>(st.fused, slots);
+  } else {
+    exec_instr(plan, st.instr, slots);
   }
 }
 
@@ -1046,16 +1217,11 @@ int rg_cpu_available(void) { return 1; }
 
 void* rg_cpu_program_new(const int64_t* words, size_t n_words, const void* blob, size_t blob_bytes, char* err, size_t err_len) {
   try {
+    PlanX px = load_plan(words, n_words);
     auto* p = new Program;
-    p->plan = parse(words, n_words);
+    p->plan = std::move(px.plan);
+    p->control = std::move(px.control);
     p->blob.assign((const uint8_t*)blob, (const uint8_t*)blob + blob_bytes);
-    for (auto& st : p->plan.steps) {
-      if (st.kind == RG_STEP_INSTR && (st.instr.op == RG_OP_SCAN || st.instr.op == RG_OP_WHILE || st.instr.op == RG_OP_COND)) {
-        delete p;
-        put_err(err, err_len, "control flow is not supported by this executor");
-        return nullptr;
-      }
-    }
     return p;
   } catch (std::exception& e) {
     put_err(err, err_len, e.what());

@@ -1,6 +1,6 @@
 // Reverse-mode differentiation: VJP rules emitted as ordinary IR nodes, so grad-of-grad needs
-// nothing extra. Follows the reference's src/autodiff.rs:6-16 (unbroadcast), 245-326 (grad) and
-// 328-558 (per-op rules). Control-flow VJPs (autodiff.rs:67-231) are not part of this build.
+// nothing extra. Follows the reference's src/autodiff.rs:6-16 (unbroadcast), 67-231 (control
+// flow), 245-326 (grad) and 328-558 (per-op rules).
 #include <algorithm>
 #include <map>
 
@@ -316,6 +316,197 @@ std::vector<std::pair<uint32_t, uint32_t>> vjp(Graph& g, size_t i, uint32_t ct, 
 
 }  // namespace
 
+namespace {
+
+// ---- control flow ---------------------------------------------------------------------------
+
+// A body's reverse pass as a graph of its own (autodiff.rs:22-59): the body's inputs, then one
+// cotangent input per floating-point result; its results are the gradients of
+// sum(result * cotangent) with respect to each floating-point input.
+struct BodyVjp {
+  Graph graph;
+  std::vector<uint32_t> grads;      // per entry of float_in
+  std::vector<size_t> float_in, float_out;
+};
+
+BodyVjp body_vjp(const Body& body) {
+  BodyVjp v;
+  v.graph = body.graph;
+  Graph& g = v.graph;
+  g.grads.clear();
+  g.notes.clear();
+  for (size_t k = 0; k < body.inputs.size(); k++)
+    if (body.input_dtype(k) != DType::I32) v.float_in.push_back(k);
+  for (size_t k = 0; k < body.outputs.size(); k++)
+    if (body.output_dtype(k) != DType::I32) v.float_out.push_back(k);
+  const DType d = v.float_in.empty() ? DType::F32 : body.input_dtype(v.float_in[0]);
+  uint32_t total = g.scalar(d, 0.0);
+  for (size_t k : v.float_out) {
+    const uint32_t ct = g.input(body.output_shape(k), body.output_dtype(k));
+    const uint32_t prod = bin(g, RG_OP_MUL, body.outputs[k], ct);
+    Op r = mk(RG_OP_REDUCE);
+    r.rk = RK::Sum;
+    for (size_t a = 0; a < g.shape(prod).size(); a++) r.v.push_back(a);
+    uint32_t sum = g.add(r, {prod});
+    if (g.dtype(sum) != d) {
+      Op c = mk(RG_OP_CAST);
+      c.dt = d;
+      sum = g.add(c, {sum});
+    }
+    total = bin(g, RG_OP_ADD, total, sum);
+  }
+  std::vector<uint32_t> wrts;
+  for (size_t k : v.float_in) wrts.push_back(body.inputs[k]);
+  v.grads = grad(g, total, wrts);
+  g.grads.clear();
+  g.notes.clear();
+  return v;
+}
+
+uint32_t zeros(Graph& g, const Shape& s, DType d) { return g.constant(Tensor::full(d, s, 0.0)); }
+
+Shape stacked(size_t len, const Shape& s) {
+  Shape r{len};
+  r.insert(r.end(), s.begin(), s.end());
+  return r;
+}
+
+// An input node with a chosen index, appended to a body graph being rewired.
+uint32_t numbered_input(Graph& g, size_t index, const Shape& s, DType d) {
+  Node n;
+  n.op = mk(RG_OP_INPUT);
+  n.op.a = index;
+  n.shape = s;
+  n.dtype = d;
+  g.nodes.push_back(std::move(n));
+  g.n_inputs++;
+  return (uint32_t)(g.nodes.size() - 1);
+}
+
+// Reverse rules of control flow (autodiff.rs:67-231). `cots` maps a result index of node `i` to
+// its cotangent.
+std::vector<std::pair<uint32_t, uint32_t>> vjp_control(Graph& g, size_t i, const std::map<size_t, uint32_t>& cots,
+                                                       const std::vector<bool>& rel) {
+  const Node node = g.nodes[i];
+  std::vector<std::pair<uint32_t, uint32_t>> out;
+  if (node.op.kind == RG_OP_WHILE) {
+    Json obs = Json::obj();
+    obs["alternative"] = "rg.scan with a fixed length";
+    throw DiagError{diag("GRAD_THROUGH_WHILE", "error", g.node_json((uint32_t)i), obs, "iteration_count_is_a_runtime_value", "verified")};
+  }
+  if (node.op.kind == RG_OP_COND) {
+    // The same cond over both branches' reverse passes, with the results' cotangents appended.
+    BodyVjp t = body_vjp(*node.op.body), e = body_vjp(*node.op.body2);
+    const Body& tb = *node.op.body;
+    std::vector<uint32_t> ins = node.inputs;
+    for (size_t k : t.float_out) {
+      auto c = cots.find(k);
+      ins.push_back(c != cots.end() ? c->second : zeros(g, tb.output_shape(k), tb.output_dtype(k)));
+    }
+    Op o = mk(RG_OP_COND);
+    o.body = Body::make(std::move(t.graph), t.grads);
+    o.body2 = Body::make(std::move(e.graph), e.grads);
+    const uint32_t cn = g.add(o, ins);
+    for (size_t j = 0; j < t.float_in.size(); j++) {
+      const uint32_t target = node.inputs[t.float_in[j] + 1];
+      if (rel[target]) out.push_back({target, g.output(cn, j, g.shape(target), g.dtype(target))});
+    }
+    return out;
+  }
+  // Scan: a scan in the opposite direction over the body's reverse pass.
+  const Body& body = *node.op.body;
+  const size_t c = node.op.n_carry, x = node.op.n_x, len = node.op.length;
+  const size_t m = body.inputs.size() - c - x;
+  const size_t n_y = body.outputs.size() - c;
+  BodyVjp v = body_vjp(body);
+  Graph& r = v.graph;
+  std::vector<size_t> fc, fy, g_x, g_cap;
+  for (size_t k : v.float_out) (k < c ? fc : fy).push_back(k);
+  for (size_t j = 0; j < v.float_in.size(); j++) {
+    if (v.float_in[j] >= c && v.float_in[j] < c + x) g_x.push_back(j);
+    if (v.float_in[j] >= c + x) g_cap.push_back(j);
+  }
+  const size_t n_ct = fc.size(), n_acc = g_cap.size();
+  // Cotangents of the stacked carries (second-order gradients) join each carry's gradient at its step.
+  std::vector<size_t> hist;
+  for (size_t k : fc)
+    if (cots.count(c + n_y + k)) hist = fc;
+  // The reverse scan's inputs: carries (carry cotangents, capture-gradient sums); xs (the carries
+  // before each forward step, the forward xs, the ys' cotangents, the stacked carries'
+  // cotangents); captures (the forward captures).
+  const size_t n_orig = c + x + m;
+  const size_t xs_at = n_ct + n_acc, caps_at = xs_at + c + x + fy.size() + hist.size();
+  for (auto& n : r.nodes) {
+    if (n.op.kind != RG_OP_INPUT) continue;
+    const size_t k = n.op.a;
+    if (k < c + x) n.op.a = xs_at + k;
+    else if (k < n_orig) n.op.a = caps_at + (k - c - x);
+    else if (k - n_orig < n_ct) n.op.a = k - n_orig;
+    else n.op.a = xs_at + c + x + (k - n_orig - n_ct);
+  }
+  std::vector<uint32_t> acc_in;
+  for (size_t a = 0; a < n_acc; a++) {
+    const uint32_t gid = v.grads[g_cap[a]];
+    acc_in.push_back(numbered_input(r, n_ct + a, r.shape(gid), r.dtype(gid)));
+  }
+  std::vector<uint32_t> outs;
+  for (size_t k : fc) {
+    const size_t j = (size_t)(std::find(v.float_in.begin(), v.float_in.end(), k) - v.float_in.begin());
+    uint32_t gradient = v.grads[j];
+    auto h = std::find(hist.begin(), hist.end(), k);
+    if (h != hist.end()) {
+      const uint32_t saved = numbered_input(r, xs_at + c + x + fy.size() + (size_t)(h - hist.begin()), r.shape(gradient), r.dtype(gradient));
+      gradient = bin(r, RG_OP_ADD, gradient, saved);
+    }
+    outs.push_back(gradient);
+  }
+  for (size_t a = 0; a < n_acc; a++) outs.push_back(bin(r, RG_OP_ADD, acc_in[a], v.grads[g_cap[a]]));
+  for (size_t j : g_x) outs.push_back(v.grads[j]);
+
+  std::vector<uint32_t> ins;
+  for (size_t k : fc) {
+    auto ct = cots.find(k);
+    ins.push_back(ct != cots.end() ? ct->second : zeros(g, body.output_shape(k), body.output_dtype(k)));
+  }
+  for (size_t j : g_cap) {
+    const uint32_t target = node.inputs[v.float_in[j]];
+    ins.push_back(zeros(g, g.shape(target), g.dtype(target)));
+  }
+  for (size_t k = 0; k < c; k++) ins.push_back(g.output((uint32_t)i, c + n_y + k, stacked(len, body.input_shape(k)), body.input_dtype(k)));
+  ins.insert(ins.end(), node.inputs.begin() + c, node.inputs.begin() + c + x);
+  for (size_t k : fy) {
+    auto ct = cots.find(k);
+    ins.push_back(ct != cots.end() ? ct->second : zeros(g, stacked(len, body.output_shape(k)), body.output_dtype(k)));
+  }
+  for (size_t k : hist) {
+    auto ct = cots.find(c + n_y + k);
+    ins.push_back(ct != cots.end() ? ct->second : zeros(g, stacked(len, body.input_shape(k)), body.input_dtype(k)));
+  }
+  ins.insert(ins.end(), node.inputs.begin() + c + x, node.inputs.end());
+  Op o = mk(RG_OP_SCAN);
+  o.body = Body::make(std::move(v.graph), outs);
+  o.n_carry = n_ct + n_acc;
+  o.n_x = c + x + fy.size() + hist.size();
+  o.length = len;
+  o.reverse = !node.op.reverse;
+  const uint32_t back = g.add(o, ins);
+  for (size_t a = 0; a < n_ct; a++) {
+    const uint32_t target = node.inputs[fc[a]];
+    if (rel[target]) out.push_back({target, g.output(back, a, g.shape(target), g.dtype(target))});
+  }
+  for (size_t a = 0; a < n_acc; a++) {
+    const uint32_t target = node.inputs[v.float_in[g_cap[a]]];
+    if (rel[target]) out.push_back({target, g.output(back, n_ct + a, g.shape(target), g.dtype(target))});
+  }
+  for (size_t a = 0; a < g_x.size(); a++) {
+    const uint32_t target = node.inputs[v.float_in[g_x[a]]];
+    if (rel[target]) out.push_back({target, g.output(back, n_ct + n_acc + a, g.shape(target), g.dtype(target))});
+  }
+  return out;
+}
+
+}  // namespace
+
 std::vector<uint32_t> grad(Graph& g, uint32_t y, const std::vector<uint32_t>& wrts) {
   if (g.nodes[y].n() != 1) {
     Json obs = Json::obj();
@@ -354,6 +545,21 @@ std::vector<uint32_t> grad(Graph& g, uint32_t y, const std::vector<uint32_t>& wr
   std::vector<int64_t> cot(end + 1, -1);
   if (rel[end]) cot[end] = g.constant(Tensor::full(g.dtype(y), g.shape(y), 1.0));
   for (size_t i = end + 1; i-- > 0;) {
+    if (g.nodes[i].op.is_control_flow()) {
+      if (!rel[i]) continue;
+      // The node's results are its later RG_OP_OUTPUT readers, whose cotangents are complete.
+      std::map<size_t, uint32_t> cots;
+      for (size_t o = i + 1; o <= end; o++) {
+        const Node& n = g.nodes[o];
+        if (n.op.kind == RG_OP_OUTPUT && n.inputs[0] == i && cot[o] >= 0) cots[n.op.a] = (uint32_t)cot[o];
+      }
+      if (cots.empty()) continue;
+      g.cur_source = g.nodes[i].source;
+      g.cur_origin = (int64_t)i;
+      for (auto& [input, c] : vjp_control(g, i, cots, rel))
+        cot[input] = cot[input] >= 0 ? (int64_t)bin(g, RG_OP_ADD, (uint32_t)cot[input], c) : (int64_t)c;
+      continue;
+    }
     if (cot[i] < 0) continue;
     uint32_t ct = (uint32_t)cot[i];
     g.cur_source = g.nodes[i].source;

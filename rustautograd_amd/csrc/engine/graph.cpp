@@ -138,6 +138,12 @@ std::string Op::key() const {
     k += ":C" + std::to_string(placeholder);
     for (auto& r : rules) k += "," + std::to_string(r.first) + "/" + std::to_string(r.second);
   }
+  if (is_control_flow()) {
+    char ids[64];
+    snprintf(ids, sizeof ids, ":B%p,%p", (const void*)body.get(), (const void*)body2.get());
+    k += ids;
+    k += ":" + std::to_string(n_carry) + "," + std::to_string(n_x) + "," + std::to_string(length) + "," + std::to_string(max_iter);
+  }
   return k;
 }
 
@@ -242,11 +248,17 @@ uint32_t Graph::add(const Op& op, const std::vector<uint32_t>& inputs) {
     static_err("ARITY_MISMATCH", op, obs, "wrong_input_count");
   }
   if (op.is_control_flow()) {
-    Json obs = Json::obj();
-    obs["operation"] = op.name();
-    static_err("UNSUPPORTED_OPERATION", op, obs, "control_flow_is_not_part_of_the_hip_backend_yet");
+    check_control_flow(op, inputs);
+    return push(op, inputs, {}, DType::F32);
   }
-  if (op.kind == RG_OP_OUTPUT) return push(op, inputs, op.v, op.dt);
+  if (op.kind == RG_OP_OUTPUT) {
+    if (inputs.size() != 1 || !nodes[inputs[0]].op.is_control_flow()) {
+      Json obs = Json::obj();
+      obs["input"] = inputs.empty() ? Json() : Json(nodes[inputs[0]].op.name());
+      static_err("INVALID_NODE_REF", op, obs, "output_reads_a_control_flow_node");
+    }
+    return push(op, inputs, op.v, op.dt);
+  }
 
   std::vector<DType> dtypes;
   for (uint32_t i : inputs) dtypes.push_back(dtype(i));
@@ -555,6 +567,90 @@ Shape Graph::infer(const Op& op, const std::vector<Shape>& s) const {
   }
 }
 
+// Inputs must match what the bodies were traced with (graph.rs:531-556). The frontend checks the
+// structure first, so a mismatch here comes from a direct IR user; the bodies' own results are
+// checked too, since the executors copy them into carries of the traced shapes.
+void Graph::check_control_flow(const Op& op, const std::vector<uint32_t>& inputs) const {
+  auto fail = [&](const Body* b, const std::vector<uint32_t>& args) {
+    Json want = Json::arr(), have = Json::arr();
+    if (b)
+      for (size_t k = 0; k < b->inputs.size(); k++) want.push(Json(b->input_shape(k)));
+    for (uint32_t a : args) have.push(Json(shape(a)));
+    Json obs = Json::obj();
+    obs["body_inputs"] = want;
+    obs["given_inputs"] = have;
+    static_err("CONTROL_FLOW_SHAPE_MISMATCH", op, obs, "inputs_differ_from_the_traced_body");
+  };
+  // Inputs [stacked_lo, stacked_hi) carry a leading axis of `length` over the body's input.
+  auto expect = [&](const Body* b, const std::vector<uint32_t>& args, size_t stacked_lo, size_t stacked_hi, size_t length) {
+    if (!b || b->inputs.size() != args.size()) fail(b, args);
+    for (size_t k = 0; k < args.size(); k++) {
+      const Shape& have = shape(args[k]);
+      const Shape& want = b->input_shape(k);
+      bool ok;
+      if (k >= stacked_lo && k < stacked_hi) ok = !have.empty() && have[0] == length && Shape(have.begin() + 1, have.end()) == want;
+      else ok = have == want;
+      if (!ok || dtype(args[k]) != b->input_dtype(k)) fail(b, args);
+    }
+  };
+  auto results_match = [&](const Body* b, size_t n, const Body* like, size_t offset) {
+    if (b->outputs.size() < n) return false;
+    for (size_t k = 0; k < n; k++)
+      if (b->output_shape(k) != like->input_shape(offset + k) || b->output_dtype(k) != like->input_dtype(offset + k)) return false;
+    return true;
+  };
+  switch (op.kind) {
+    case RG_OP_SCAN:
+      expect(op.body.get(), inputs, op.n_carry, op.n_carry + op.n_x, op.length);
+      if (!results_match(op.body.get(), op.n_carry, op.body.get(), 0)) fail(op.body.get(), inputs);
+      break;
+    case RG_OP_WHILE: {
+      expect(op.body2.get(), inputs, 0, 0, 0);
+      expect(op.body.get(), inputs, 0, 0, 0);
+      const Body* c = op.body2.get();
+      const bool scalar = c->outputs.size() == 1 && (c->output_shape(0).empty() || c->output_shape(0) == Shape{1});
+      if (!scalar || op.body->outputs.size() != op.n_carry || !results_match(op.body.get(), op.n_carry, op.body.get(), 0))
+        fail(op.body.get(), inputs);
+      break;
+    }
+    case RG_OP_COND: {
+      if (inputs.empty() || numel(shape(inputs[0])) != 1) fail(op.body.get(), inputs);
+      std::vector<uint32_t> args(inputs.begin() + 1, inputs.end());
+      expect(op.body.get(), args, 0, 0, 0);
+      expect(op.body2.get(), args, 0, 0, 0);
+      const Body *t = op.body.get(), *e = op.body2.get();
+      bool same = t->outputs.size() == e->outputs.size();
+      for (size_t k = 0; same && k < t->outputs.size(); k++)
+        same = t->output_shape(k) == e->output_shape(k) && t->output_dtype(k) == e->output_dtype(k);
+      if (!same) fail(t, args);
+      break;
+    }
+    default: break;
+  }
+}
+
+uint32_t Graph::output(uint32_t node, size_t index, const Shape& s, DType d) {
+  Op o = Op::make(RG_OP_OUTPUT);
+  o.a = index;
+  o.v = s;
+  o.dt = d;
+  return add(o, {node});
+}
+
+std::shared_ptr<const Body> Body::make(Graph g, std::vector<uint32_t> outputs) {
+  auto b = std::make_shared<Body>();
+  b->inputs.assign(g.n_inputs, UINT32_MAX);
+  for (size_t id = 0; id < g.nodes.size(); id++)
+    if (g.nodes[id].op.kind == RG_OP_INPUT && g.nodes[id].op.a < g.n_inputs) b->inputs[g.nodes[id].op.a] = (uint32_t)id;
+  for (uint32_t id : b->inputs)
+    if (id == UINT32_MAX) throw std::runtime_error("a control-flow body lacks one of its inputs");
+  for (uint32_t o : outputs)
+    if (o >= g.nodes.size()) throw std::runtime_error("a control-flow body returns an unknown node");
+  b->graph = std::move(g);
+  b->outputs = std::move(outputs);
+  return b;
+}
+
 std::vector<bool> Graph::reachable(const std::vector<uint32_t>& outputs) const {
   std::vector<bool> keep(nodes.size(), false);
   for (uint32_t o : outputs) keep[o] = true;
@@ -567,6 +663,8 @@ std::vector<bool> Graph::reachable(const std::vector<uint32_t>& outputs) const {
 Graph Graph::to_f64() const {
   Graph g = *this;
   for (auto& n : g.nodes) {
+    if (n.op.body) n.op.body = Body::make(n.op.body->graph.to_f64(), n.op.body->outputs);
+    if (n.op.body2) n.op.body2 = Body::make(n.op.body2->graph.to_f64(), n.op.body2->outputs);
     if (n.op.kind == RG_OP_OUTPUT && n.op.dt != DType::I32) n.op.dt = DType::F64;
     if (n.dtype == DType::I32) continue;
     n.dtype = DType::F64;

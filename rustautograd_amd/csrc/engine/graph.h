@@ -78,6 +78,8 @@ struct Tensor {
 
 enum class RK : int32_t { Sum = RG_REDUCE_SUM, Max = RG_REDUCE_MAX, Min = RG_REDUCE_MIN };
 
+struct Body;
+
 struct Op {
   rg_op kind = RG_OP_INPUT;
   size_t a = 0;  // Input index, Output index, Take/TakeGrad/Concat axis, KeySplit n, ArgTopK k
@@ -88,6 +90,15 @@ struct Op {
   std::shared_ptr<const Tensor> t;  // Const
   uint32_t placeholder = 0;
   std::vector<std::pair<uint32_t, uint32_t>> rules;  // Custom
+  // Control flow (graph.rs:101-107). Scan: `body` maps (carries, x slices, captures) to (carries,
+  // ys) over `length` steps, from the last when `reverse`; its node's outputs by index are the
+  // final carries, the stacked ys, then the stacked carries as they were before each step.
+  // While: `body2` is the condition over (carries, captures), `body` the step; outputs are the
+  // final carries, then the iteration count (int32), at most `max_iter`. Cond: input 0 is the
+  // predicate and `body` / `body2` the branches over the remaining inputs; outputs are the taken
+  // branch's. The node itself has shape [] and each result is an RG_OP_OUTPUT node reading it.
+  std::shared_ptr<const Body> body, body2;
+  size_t n_carry = 0, n_x = 0, length = 0, max_iter = 0;
 
   static Op make(rg_op k) {
     Op o;
@@ -140,6 +151,8 @@ class Graph {
   // Adds a node after arity, dtype and shape checks; throws DiagError with a structured diagnostic.
   uint32_t add(const Op& op, const std::vector<uint32_t>& inputs);
   std::vector<bool> reachable(const std::vector<uint32_t>& outputs) const;
+  // The RG_OP_OUTPUT node reading result `index` of control-flow node `node`.
+  uint32_t output(uint32_t node, size_t index, const Shape& shape, DType dtype);
   Graph to_f64() const;
   Json node_json(uint32_t id) const;
 
@@ -148,6 +161,21 @@ class Graph {
   Json pending_json(const Op& op) const;
   [[noreturn]] void static_err(const char* code, const Op& op, Json obs, const char* cause) const;
   Shape infer(const Op& op, const std::vector<Shape>& s) const;
+  void check_control_flow(const Op& op, const std::vector<uint32_t>& inputs) const;
+};
+
+// A traced control-flow body (graph.rs:11-31): its own graph, whose inputs are numbered as the
+// control-flow node feeds them, and the nodes it returns. Bodies are shared and immutable; a
+// node's identity for common-subexpression elimination includes the body's address.
+struct Body {
+  Graph graph;
+  std::vector<uint32_t> outputs;
+  std::vector<uint32_t> inputs;  // node of each graph input, by input index
+  static std::shared_ptr<const Body> make(Graph g, std::vector<uint32_t> outputs);
+  const Shape& output_shape(size_t k) const { return graph.shape(outputs[k]); }
+  DType output_dtype(size_t k) const { return graph.dtype(outputs[k]); }
+  const Shape& input_shape(size_t k) const { return graph.shape(inputs[k]); }
+  DType input_dtype(size_t k) const { return graph.dtype(inputs[k]); }
 };
 
 // Reverse-mode autodiff (src/autodiff.rs:245-326): adds the nodes computing the gradient of y with respect to each of `wrts`.

@@ -195,6 +195,54 @@ PYBIND11_MODULE(_rg, m) {
              return grad(g.g, y, wrts);
            },
            py::arg("y"), py::arg("wrts"), py::arg("source") = py::none())
+      // Control flow (python.rs:158-180): each body is a graph of its own, traced with inputs in
+      // the order the node feeds them; a body's graph is copied into the node.
+      .def("scan",
+           [](PyGraph& g, const PyGraph& body, const std::vector<uint32_t>& body_outputs, size_t n_carry, size_t n_x, size_t length,
+              const std::vector<uint32_t>& inputs, bool reverse, std::optional<std::string> source) {
+             Op op = Op::make(RG_OP_SCAN);
+             op.body = Body::make(body.g, body_outputs);
+             op.n_carry = n_carry;
+             op.n_x = n_x;
+             op.length = length;
+             op.reverse = reverse;
+             g.set_source(source);
+             return g.g.add(op, inputs);
+           },
+           py::arg("body"), py::arg("body_outputs"), py::arg("n_carry"), py::arg("n_x"), py::arg("length"), py::arg("inputs"),
+           py::arg("reverse") = false, py::arg("source") = py::none())
+      .def("while_loop",
+           [](PyGraph& g, const PyGraph& cond, uint32_t cond_output, const PyGraph& body, const std::vector<uint32_t>& body_outputs,
+              size_t n_carry, size_t max_iterations, const std::vector<uint32_t>& inputs, std::optional<std::string> source) {
+             Op op = Op::make(RG_OP_WHILE);
+             op.body2 = Body::make(cond.g, {cond_output});
+             op.body = Body::make(body.g, body_outputs);
+             op.n_carry = n_carry;
+             op.max_iter = max_iterations;
+             g.set_source(source);
+             return g.g.add(op, inputs);
+           },
+           py::arg("cond"), py::arg("cond_output"), py::arg("body"), py::arg("body_outputs"), py::arg("n_carry"),
+           py::arg("max_iterations"), py::arg("inputs"), py::arg("source") = py::none())
+      .def("cond",
+           [](PyGraph& g, const PyGraph& then_body, const std::vector<uint32_t>& then_outputs, const PyGraph& else_body,
+              const std::vector<uint32_t>& else_outputs, const std::vector<uint32_t>& inputs, std::optional<std::string> source) {
+             Op op = Op::make(RG_OP_COND);
+             op.body = Body::make(then_body.g, then_outputs);
+             op.body2 = Body::make(else_body.g, else_outputs);
+             g.set_source(source);
+             return g.g.add(op, inputs);
+           },
+           py::arg("then_body"), py::arg("then_outputs"), py::arg("else_body"), py::arg("else_outputs"), py::arg("inputs"),
+           py::arg("source") = py::none())
+      .def("output",
+           [](PyGraph& g, uint32_t node, size_t index, const std::vector<size_t>& shape, const std::string& dtype,
+              std::optional<std::string> source) {
+             g.set_source(source);
+             return g.g.output(node, index, shape, dtype_of(dtype));
+           },
+           py::arg("node"), py::arg("index"), py::arg("shape"), py::arg("dtype"), py::arg("source") = py::none())
+      .def_property_readonly("n_inputs", [](const PyGraph& g) { return g.g.n_inputs; })
       .def("placeholder",
            [](PyGraph& g, const std::vector<size_t>& shape, const std::string& dtype) {
              return g.g.placeholder(shape, dtype_of(dtype));

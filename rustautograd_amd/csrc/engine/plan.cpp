@@ -3,6 +3,7 @@
 // fusability, hoisting), 311-414 (greedy and level schedules), 416-457 (compile_group) and
 // 466-634 (build_fused / build_with).
 #include "plan.h"
+#include "optimize.h"
 
 #include <algorithm>
 #include <cstring>
@@ -625,8 +626,8 @@ std::vector<Item> schedule(const Graph& g, const std::vector<bool>& keep, const 
     if (!keep[i] || up[i] || leaf(n) || abs[i]) continue;
     if (fusable(g, i, cfg.device) && !(cfg.device && !cfg.fuse_f64 && n.dtype == DType::F64)) {
       bool same = open.empty() || (g.nodes[open[0]].shape == n.shape && g.nodes[open[0]].dtype == n.dtype);
-      size_t inputs = distinct_external(g, open, n);
-      if (!same || (cfg.device && inputs + open.size() + 1 > cfg.max_bindings)) close();
+      // Only device kernels bound their operand count; a CPU group's inputs need no count.
+      if (!same || (cfg.device && distinct_external(g, open, n) + open.size() + 1 > cfg.max_bindings)) close();
       open.push_back(i);
     } else {
       bool reads = false;
@@ -1026,6 +1027,44 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       in.arg_shapes.push_back(g.shape(x));
       in.args.push_back(value_slot[x]);
     }
+    if (node.op.is_control_flow()) {
+      // Results get slots before the inputs are released, so none lands on an input's buffer
+      // (plan.rs:611-620); the bodies are planned like the program itself.
+      for (uint32_t x : node.inputs) uses[x]--;
+      for (size_t o = i + 1; o < total; o++) {
+        const Node& on = g.nodes[o];
+        if (keep[o] && on.op.kind == RG_OP_OUTPUT && on.inputs[0] == i) {
+          const size_t sl = a.alloc(on.dtype, on.n(), exact[o]);
+          value_slot[o] = sl;
+          in.outs.push_back({on.op.a, sl});
+          p.naive_bytes += on.n() * dsize(on.dtype);
+        }
+      }
+      std::vector<uint32_t> dying;
+      for (uint32_t x : node.inputs)
+        if (uses[x] == 0 && std::find(dying.begin(), dying.end(), x) == dying.end()) dying.push_back(x);
+      for (uint32_t x : dying) a.release(value_slot[x]);
+      for (const Body* b : {node.op.body2.get(), node.op.body.get()}) {
+        if (!b) continue;
+        if (!fuse) {
+          in.bodies.push_back(std::make_shared<const Plan>(build_with(b->graph, b->outputs, reuse, nullptr)));
+        } else {
+          Optimized ob = optimize_mode(b->graph, b->outputs, fuse->device, OptMode::Standard);
+          in.bodies.push_back(std::make_shared<const Plan>(build_fused(ob.g, ob.outputs, *fuse)));
+        }
+      }
+      if (node.op.kind == RG_OP_COND) std::reverse(in.bodies.begin(), in.bodies.end());  // then, else
+      in.op = node.op;
+      in.node = (uint32_t)i;
+      in.dtype = node.dtype;
+      in.dst = SIZE_MAX;
+      in.shape = node.shape;
+      in.n = 0;
+      Step st;
+      st.instr = std::move(in);
+      p.steps.push_back(std::move(st));
+      continue;
+    }
     in.mode = binary_mode(node.op, node.shape, in.arg_shapes);
     for (uint32_t x : node.inputs) uses[x]--;
     std::vector<uint32_t> dying;
@@ -1321,10 +1360,50 @@ static void put_op_attr(std::vector<int64_t>& a, const Op& op) {
   }
 }
 
+static void write_plan(const Plan& plan, std::vector<int64_t>* words, std::vector<uint8_t>* blob);
+
+// Control flow: counts, the result slots, then each body's plan as a nested descriptor whose
+// constants share the blob.
+static void put_control_attr(std::vector<int64_t>& a, const Instr& in, std::vector<uint8_t>* blob) {
+  const Op& op = in.op;
+  if (op.kind == RG_OP_SCAN) {
+    a.push_back((int64_t)op.n_carry);
+    a.push_back((int64_t)op.n_x);
+    a.push_back((int64_t)op.length);
+    a.push_back(op.reverse ? 1 : 0);
+  } else if (op.kind == RG_OP_WHILE) {
+    a.push_back((int64_t)op.n_carry);
+    a.push_back((int64_t)op.max_iter);
+  }
+  a.push_back((int64_t)in.outs.size());
+  for (auto& [index, slot] : in.outs) {
+    a.push_back((int64_t)index);
+    a.push_back((int64_t)slot);
+  }
+  a.push_back((int64_t)in.bodies.size());
+  for (auto& b : in.bodies) {
+    std::vector<int64_t> sub;
+    write_plan(*b, &sub, blob);
+    a.push_back((int64_t)sub.size());
+    a.insert(a.end(), sub.begin(), sub.end());
+  }
+}
+
 void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) const {
-  auto& w = *words;
-  w.clear();
+  words->clear();
   blob->clear();
+  write_plan(*this, words, blob);
+}
+
+static void write_plan(const Plan& plan, std::vector<int64_t>* words, std::vector<uint8_t>* blob) {
+  const auto& slots = plan.slots;
+  const auto& pinned = plan.pinned;
+  const auto& consts = plan.consts;
+  const auto& input_slots = plan.input_slots;
+  const auto& input_ns = plan.input_ns;
+  const auto& outputs = plan.outputs;
+  const auto& steps = plan.steps;
+  auto& w = *words;
   auto shape = [&](const Shape& s) {
     w.push_back((int64_t)s.size());
     for (auto d : s) w.push_back((int64_t)d);
@@ -1410,7 +1489,8 @@ void Plan::serialize(std::vector<int64_t>* words, std::vector<uint8_t>* blob) co
         shape(in.arg_shapes[k]);
       }
       std::vector<int64_t> attr;
-      put_op_attr(attr, in.op);
+      if (in.op.is_control_flow()) put_control_attr(attr, in, blob);
+      else put_op_attr(attr, in.op);
       w.push_back((int64_t)attr.size());
       w.insert(w.end(), attr.begin(), attr.end());
     } else {

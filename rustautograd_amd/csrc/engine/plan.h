@@ -93,6 +93,8 @@ AttnShape attn_shape(const AttnRegion& r, const Graph& g);
 size_t attn_stats_words(const AttnRegion& r, const Graph& g);
 size_t attn_mask_words(const AttnRegion& r, const Graph& g);
 
+struct Plan;
+
 struct Instr {
   Op op;
   uint32_t node = 0;
@@ -103,6 +105,11 @@ struct Instr {
   std::vector<Shape> arg_shapes;
   size_t n = 0;
   rg_mode mode = RG_MODE_SAME;
+  // Control flow (plan.rs:127-140 `outs`): the slot of each result the plan reads, as (result
+  // index, slot), and the bodies' own plans (scan: body; while: condition, body; cond: then,
+  // else). `dst` is unused (SIZE_MAX).
+  std::vector<std::pair<size_t, size_t>> outs;
+  std::vector<std::shared_ptr<const Plan>> bodies;
 };
 
 struct FusedIn {

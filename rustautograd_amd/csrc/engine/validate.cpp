@@ -196,37 +196,134 @@ std::vector<uint32_t> Compiled::raw_outputs() const {
   return all;
 }
 
-// Observes every node of the plan built from the traced graph as written (no optimization), so
-// each finding carries the node id and source line the user traced (validate.rs:537-565,
-// observer at 132-230). Runs on the compiled device, one step at a time.
-Compiled::Observed Compiled::observed(const std::vector<Tensor>& inputs) {
-  Observed o;
-  std::vector<bool> keep = raw.reachable(raw_outputs());
-  for (size_t id = 0; id < raw.nodes.size(); id++) {
-    const Node& n = raw.nodes[id];
-    const Tensor* t = nullptr;
-    if (n.op.kind == RG_OP_INPUT) t = &inputs[n.op.a];
-    else if (n.op.kind == RG_OP_CONST) t = n.op.t.get();
-    if (!t || !keep[id] || t->is_finite()) continue;
-    Stats s = stats_of(*t, t->n());
-    Json obs = Json::obj();
-    obs["dtype"] = dname(n.dtype);
-    obs["shape"] = Json(n.shape);
-    obs["contains_inf"] = s.inf > 0;
-    obs["contains_nan"] = s.nan > 0;
-    obs["nonfinite_count"] = s.nan + s.inf;
-    obs["first_bad_index"] = s.first_bad >= 0 ? Json((long long)s.first_bad) : Json();
-    o.roots.push_back(diag("NONFINITE_INPUT", "error", raw.node_json((uint32_t)id), obs, "nonfinite_value_supplied", "verified"));
+namespace {
+
+// Runs a plan of the traced graph one step at a time on the device, observing each instruction
+// (validate.rs:132-230). Control-flow steps are interpreted here, each body iteration running as
+// a program of its own, so findings inside a body name the body's node, with the iteration and
+// nesting depth (validate.rs:143-153, 218-229), and a while loop stopped by its iteration limit is
+// reported (validate.rs:224-229).
+struct Observer {
+  Compiled::Observed& o;
+  Backend* device;
+  std::map<const Plan*, std::unique_ptr<DeviceProgram>>& programs;
+  std::vector<std::pair<const Body*, size_t>> scopes;
+
+  Json node_json(const Graph& g, uint32_t id) const {
+    Json v = g.node_json(id);
+    if (!scopes.empty()) {
+      Json cf = Json::obj();
+      cf["iteration"] = (unsigned long long)scopes.back().second;
+      cf["depth"] = (unsigned long long)scopes.size();
+      v["control_flow"] = cf;
+    }
+    return v;
   }
-  if (!raw_program) raw_program = std::make_unique<DeviceProgram>(device, raw_plan);
-  auto e = raw_program->exec();
-  for (size_t k = 0; k < inputs.size(); k++) e->load(k, inputs[k]);
-  for (size_t si = 0; si < raw_plan.steps.size(); si++) {
-    e->steps(si, si + 1);
-    const Instr& i = raw_plan.steps[si].instr;
-    auto read_arg = [&](size_t k) {
-      return e->prefix(i.args[k], numel(i.arg_shapes[k]), i.arg_shapes[k]);
-    };
+
+  // A body's plan run once on `inputs`, inside scope (body, iteration).
+  std::vector<Tensor> body(const Plan& plan, const Body& b, size_t iteration, const std::vector<Tensor>& inputs) {
+    auto& prog = programs[&plan];
+    if (!prog) prog = std::make_unique<DeviceProgram>(device, plan);
+    scopes.push_back({&b, iteration});
+    auto e = prog->exec();
+    std::vector<Tensor> out = run(plan, b.graph, *e, inputs);
+    scopes.pop_back();
+    return out;
+  }
+
+  std::vector<Tensor> run(const Plan& plan, const Graph& g, DeviceExec& e, const std::vector<Tensor>& inputs) {
+    std::vector<std::pair<size_t, const Tensor*>> loads;
+    for (size_t k = 0; k < inputs.size(); k++) loads.push_back({k, &inputs[k]});
+    e.load_all(loads);
+    for (size_t si = 0; si < plan.steps.size(); si++) {
+      const Instr& i = plan.steps[si].instr;
+      if (i.op.is_control_flow()) {
+        control(i, g, e);
+        continue;
+      }
+      e.steps(si, si + 1);
+      instr(i, g, e);
+    }
+    if (auto f = e.failure()) throw DiagError{device_failure(device->name, *f)};
+    std::vector<Tensor> out;
+    for (auto& po : plan.outputs) out.push_back(e.prefix(po.slot, po.n, po.shape));
+    return out;
+  }
+
+  // plan.rs:737-831, with every body iteration observed.
+  void control(const Instr& i, const Graph& g, DeviceExec& e) {
+    std::vector<Tensor> args;
+    for (size_t k = 0; k < i.args.size(); k++) args.push_back(e.prefix(i.args[k], numel(i.arg_shapes[k]), i.arg_shapes[k]));
+    std::map<size_t, Tensor> result;
+    const Op& op = i.op;
+    if (op.kind == RG_OP_SCAN) {
+      const Body& b = *op.body;
+      const size_t c = op.n_carry, x = op.n_x, len = op.length, n_y = b.outputs.size() - c;
+      std::vector<Tensor> carry(args.begin(), args.begin() + c);
+      std::vector<Tensor> ys(n_y), before(c);
+      for (size_t k = 0; k < n_y; k++) ys[k] = Tensor::full(b.output_dtype(k + c), stacked_shape(len, b.output_shape(k + c)), 0.0);
+      for (size_t k = 0; k < c; k++) before[k] = Tensor::full(b.input_dtype(k), stacked_shape(len, b.input_shape(k)), 0.0);
+      for (size_t step = 0; step < len; step++) {
+        const size_t at = op.reverse ? len - 1 - step : step;
+        std::vector<Tensor> in = carry;
+        for (size_t k = c; k < c + x; k++) in.push_back(row_of(args[k], at, b.input_shape(k)));
+        in.insert(in.end(), args.begin() + c + x, args.end());
+        for (size_t k = 0; k < c; k++) put_row(before[k], at, carry[k]);
+        std::vector<Tensor> out = body(*i.bodies[0], b, at, in);
+        for (size_t k = 0; k < n_y; k++) put_row(ys[k], at, out[c + k]);
+        carry.assign(out.begin(), out.begin() + c);
+      }
+      for (size_t k = 0; k < c; k++) result[k] = carry[k];
+      for (size_t k = 0; k < n_y; k++) result[c + k] = ys[k];
+      for (size_t k = 0; k < c; k++) result[c + n_y + k] = before[k];
+    } else if (op.kind == RG_OP_WHILE) {
+      const size_t c = op.n_carry;
+      std::vector<Tensor> state(args.begin(), args.begin() + c), caps(args.begin() + c, args.end());
+      size_t count = 0;
+      for (;;) {
+        std::vector<Tensor> in = state;
+        in.insert(in.end(), caps.begin(), caps.end());
+        if (body(*i.bodies[0], *op.body2, count, in)[0].at(0) == 0.0) break;
+        if (count == op.max_iter) {
+          Json obs = Json::obj();
+          obs["max_iterations"] = (unsigned long long)op.max_iter;
+          o.hard.push_back(diag("WHILE_LIMIT_REACHED", "error", node_json(g, i.node), obs, "condition_stayed_true_past_the_limit", "verified"));
+          break;
+        }
+        std::vector<Tensor> out = body(*i.bodies[1], *op.body, count, in);
+        state.assign(out.begin(), out.begin() + c);
+        count++;
+      }
+      for (size_t k = 0; k < c; k++) result[k] = state[k];
+      result[c] = Tensor::full(DType::I32, {}, (double)count);
+    } else {
+      const bool taken = args[0].at(0) != 0.0;
+      std::vector<Tensor> in(args.begin() + 1, args.end());
+      std::vector<Tensor> out = body(*i.bodies[taken ? 0 : 1], taken ? *op.body : *op.body2, 0, in);
+      for (size_t k = 0; k < out.size(); k++) result[k] = out[k];
+    }
+    for (auto& [index, slot] : i.outs) e.write_prefix(slot, result.at(index));
+  }
+
+  static Shape stacked_shape(size_t len, const Shape& s) {
+    Shape r{len};
+    r.insert(r.end(), s.begin(), s.end());
+    return r;
+  }
+  static Tensor row_of(const Tensor& t, size_t at, const Shape& shape) {
+    Tensor r;
+    r.shape = shape;
+    r.dtype = t.dtype;
+    const size_t bytes = numel(shape) * dsize(t.dtype);
+    r.data.assign(t.data.begin() + at * bytes, t.data.begin() + (at + 1) * bytes);
+    return r;
+  }
+  static void put_row(Tensor& t, size_t at, const Tensor& row) {
+    std::copy(row.data.begin(), row.data.end(), t.data.begin() + at * row.data.size());
+  }
+
+  void instr(const Instr& i, const Graph& g, DeviceExec& e) {
+    auto read_arg = [&](size_t k) { return e.prefix(i.args[k], numel(i.arg_shapes[k]), i.arg_shapes[k]); };
     // Index range check (validate.rs:148-161).
     if ((i.op.kind == RG_OP_TAKE || i.op.kind == RG_OP_TAKE_ALONG) && o.hard.size() < MAX_ROOTS) {
       size_t dim = i.op.kind == RG_OP_TAKE ? i.arg_shapes[0][i.op.a] : i.arg_shapes[0].back();
@@ -238,12 +335,12 @@ Compiled::Observed Compiled::observed(const std::vector<Tensor>& inputs) {
         obs["index_max"] = s.max;
         obs["axis_size"] = dim;
         obs["behavior_at_runtime"] = "clamped";
-        o.hard.push_back(diag("INDEX_OUT_OF_RANGE", "error", raw.node_json(i.node), obs, "index_outside_axis", "verified"));
+        o.hard.push_back(diag("INDEX_OUT_OF_RANGE", "error", node_json(g, i.node), obs, "index_outside_axis", "verified"));
       }
     }
-    if (i.dtype == DType::I32) continue;
-    Tensor dst = e->prefix(i.dst, i.n, i.shape);
-    if (!any_nonfinite(dst)) continue;
+    if (i.dtype == DType::I32) return;
+    Tensor dst = e.prefix(i.dst, i.n, i.shape);
+    if (!any_nonfinite(dst)) return;
     std::vector<Stats> args;
     std::vector<Tensor> argv;
     bool propagated = false;
@@ -254,9 +351,9 @@ Compiled::Observed Compiled::observed(const std::vector<Tensor>& inputs) {
     }
     if (propagated) {
       o.propagated++;
-      continue;
+      return;
     }
-    if (o.roots.size() == MAX_ROOTS) continue;
+    if (o.roots.size() == MAX_ROOTS) return;
     Stats out = stats_of(dst, i.n);
     Classified c = classify(i, args, out);
     int64_t bad = out.first_bad;
@@ -293,10 +390,38 @@ Compiled::Observed Compiled::observed(const std::vector<Tensor>& inputs) {
       obs["input_min"] = num(args[0].min);
       if (i.op.kind == RG_OP_EXP) obs["overflow_threshold"] = num(i.dtype == DType::F32 ? 88.722839 : 709.782712);
     }
-    o.roots.push_back(diag(c.code, "error", raw.node_json(i.node), obs, c.cause, c.certainty));
+    o.roots.push_back(diag(c.code, "error", node_json(g, i.node), obs, c.cause, c.certainty));
   }
-  if (auto f = e->failure()) throw DiagError{device_failure(device->name, *f)};
-  for (auto& po : raw_plan.outputs) o.vals.push_back(e->prefix(po.slot, po.n, po.shape));
+};
+
+}  // namespace
+
+// Observes every node of the plan built from the traced graph as written (no optimization), so
+// each finding carries the node id and source line the user traced (validate.rs:537-565,
+// observer at 132-230). Runs on the compiled device, one step at a time.
+Compiled::Observed Compiled::observed(const std::vector<Tensor>& inputs) {
+  Observed o;
+  std::vector<bool> keep = raw.reachable(raw_outputs());
+  for (size_t id = 0; id < raw.nodes.size(); id++) {
+    const Node& n = raw.nodes[id];
+    const Tensor* t = nullptr;
+    if (n.op.kind == RG_OP_INPUT) t = &inputs[n.op.a];
+    else if (n.op.kind == RG_OP_CONST) t = n.op.t.get();
+    if (!t || !keep[id] || t->is_finite()) continue;
+    Stats s = stats_of(*t, t->n());
+    Json obs = Json::obj();
+    obs["dtype"] = dname(n.dtype);
+    obs["shape"] = Json(n.shape);
+    obs["contains_inf"] = s.inf > 0;
+    obs["contains_nan"] = s.nan > 0;
+    obs["nonfinite_count"] = s.nan + s.inf;
+    obs["first_bad_index"] = s.first_bad >= 0 ? Json((long long)s.first_bad) : Json();
+    o.roots.push_back(diag("NONFINITE_INPUT", "error", raw.node_json((uint32_t)id), obs, "nonfinite_value_supplied", "verified"));
+  }
+  if (!raw_program) raw_program = std::make_unique<DeviceProgram>(device, raw_plan);
+  auto e = raw_program->exec();
+  Observer ob{o, device, body_programs, {}};
+  o.vals = ob.run(raw_plan, raw, *e, inputs);
   return o;
 }
 

@@ -1,5 +1,6 @@
 // Compile, validate and run (reference src/validate.rs).
 #pragma once
+#include <map>
 #include <memory>
 #include <optional>
 
@@ -41,6 +42,8 @@ class Compiled {
   Backend* device = nullptr;
   std::unique_ptr<DeviceProgram> program;
   std::unique_ptr<DeviceProgram> raw_program;  // built on first use by diagnostics
+  // Programs of the control-flow bodies of `raw_plan`, which diagnostics run one iteration at a time.
+  std::map<const Plan*, std::unique_ptr<DeviceProgram>> body_programs;
 
   void check_inputs(const std::vector<Tensor>& inputs) const;
   std::vector<Tensor> try_call(const std::vector<Tensor>& inputs) const;
@@ -58,12 +61,14 @@ class Compiled {
   Json validate(const std::vector<Tensor>& examples);
   std::vector<uint32_t> raw_outputs() const;
 
- private:
+  // What the instrumented run of the traced graph found.
   struct Observed {
     std::vector<Json> roots, hard;
     size_t propagated = 0;
     std::vector<Tensor> vals;
   };
+
+ private:
   Observed observed(const std::vector<Tensor>& inputs);
   std::pair<Json, std::vector<Json>> gradient_stats(const std::vector<Tensor>& vals) const;
   Json optimizer_check(const std::vector<Tensor>& examples) const;  // throws DiagError on mismatch

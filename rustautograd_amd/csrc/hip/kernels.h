@@ -113,6 +113,18 @@ void set_counter(hipStream_t s, uint64_t* counter, uint64_t value);
 // Keeps stream `s` busy for about `microseconds` (a bounded wait on the device wall clock).
 void hold_stream(hipStream_t s, double microseconds);
 void fill_zero(hipStream_t s, void* dst, uint64_t bytes);
+// Several copies in one launch: job j copies words[j] 32-bit words from src[j] to dst[j]. No
+// job's destination may overlap another job's source or destination.
+constexpr int COPY_JOBS = 16;
+struct CopyJobs {
+  uint32_t* dst[COPY_JOBS];
+  const uint32_t* src[COPY_JOBS];
+  uint64_t words[COPY_JOBS];
+  int n;
+};
+void copy_batch(hipStream_t s, const CopyJobs& jobs);
+// dst[0] = value, with a one-thread kernel.
+void set_i32(hipStream_t s, int32_t* dst, int32_t value);
 
 // Dense products. A is [M,K] (or [K,M] when ta), B is [K,N] (or [N,K] when tb), C is [M,N],
 // all row-major, over `batch` matrices at the given element offsets (nullptr = contiguous).

@@ -979,6 +979,27 @@ void reduce_general(hipStream_t s, int dtype, int kind, const void* a, void* d, 
   });
 }
 
+__global__ void __launch_bounds__(TPB) k_copy_batch(CopyJobs jobs) {
+  const int j = blockIdx.y;
+  const uint64_t words = jobs.words[j];
+  uint32_t* __restrict__ dst = jobs.dst[j];
+  const uint32_t* __restrict__ src = jobs.src[j];
+  for (uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x; i < words; i += (uint64_t)gridDim.x * TPB) dst[i] = src[i];
+}
+
+__global__ void k_set_i32(int32_t* dst, int32_t value) { dst[0] = value; }
+
+void copy_batch(hipStream_t s, const CopyJobs& jobs) {
+  if (jobs.n <= 0) return;
+  uint64_t most = 0;
+  for (int j = 0; j < jobs.n; j++) most = std::max(most, jobs.words[j]);
+  if (most == 0) return;
+  const uint32_t bx = (uint32_t)std::min<uint64_t>((most + TPB - 1) / TPB, 1024);
+  hipLaunchKernelGGL(k_copy_batch, dim3(bx, (uint32_t)jobs.n), dim3(TPB), 0, s, jobs);
+}
+
+void set_i32(hipStream_t s, int32_t* dst, int32_t value) { hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, s, dst, value); }
+
 void copy_bytes(hipStream_t s, void* dst, const void* src, uint64_t bytes) {
   uint64_t words = bytes / 4;
   RG_LAUNCH(k_copy_words, words, (uint32_t*)dst, (const uint32_t*)src, words);

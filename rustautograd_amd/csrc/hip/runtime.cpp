@@ -131,7 +131,29 @@ struct Program {
   uint64_t fold_base() const { return (workspace_bytes + 255) / 256 * 256; }
   std::vector<void*> device_tables;  // per-batch GEMM offset tables
   uint64_t workspace_bytes = 0;
+  // Slot sizes: this program's own slots, then those of its control-flow bodies (body_slots).
   std::vector<uint64_t> slot_bytes;
+  // Control-flow steps (include/rg_plan.h): each body is a program of its own whose slots follow
+  // this program's in the frame's slot table, from `slot_base`, and whose workspace follows this
+  // program's fold area, from `ws_offset`; `temp_offset` holds the step's staging copies of its
+  // carries. Null for every other step.
+  struct BodyProg {
+    std::unique_ptr<Program> prog;
+    size_t slot_base = 0;
+    uint64_t ws_offset = 0;
+  };
+  struct Control {
+    int op = 0;
+    ControlAttr attr;
+    std::vector<BodyProg> bodies;
+    uint64_t temp_offset = 0;
+    bool stage_carries = false;  // a carry result shares a buffer with another carry's input
+  };
+  std::vector<std::unique_ptr<Control>> control;
+  uint64_t body_ws_bytes = 0;  // workspace for the bodies, after the fold area
+  // A step waits for the device to decide what runs next (while, cond): never captured in a graph.
+  bool host_sync = false;
+  uint64_t ws_bytes() const { return fold_base() + (fold_bytes + 255) / 256 * 256 + body_ws_bytes; }
   std::mutex mu;
   std::vector<Frame*> pool;
   // Test hook: the plan step pass that fails next, counted from now (0: the next one), or -1.
@@ -624,6 +646,9 @@ std::vector<int64_t> step_reads(const Step& st) {
   return r;
 }
 
+StepFn lower_control(Program& prog, size_t k);
+void place_bodies(Program& prog);
+
 void build_program(Program& prog) {
   std::vector<size_t> fold_producer;  // per fold: the step of the row group that writes its partials
   std::ostringstream src;
@@ -707,6 +732,8 @@ void build_program(Program& prog) {
       });
     } else if (st.kind == RG_STEP_ATTN) {
       prog.steps.push_back(lower_attention(prog, st.attn));
+    } else if (is_control(st.instr.op)) {
+      prog.steps.push_back(lower_control(prog, k));
     } else {
       const Instr& in = st.instr;
       prog.steps.push_back(lower_instr(prog, in));
@@ -714,6 +741,7 @@ void build_program(Program& prog) {
     }
   }
   for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));
+  place_bodies(prog);
   // Each fold runs before the first later step reading its output, or right after its producer.
   const size_t n = prog.plan.steps.size();
   prog.folds_due.assign(n + 1, {});
@@ -730,6 +758,18 @@ void build_program(Program& prog) {
   }
 }
 
+// Constants of a program and of its bodies (whose constants share the root program's blob).
+void upload_consts(const Program& p, const std::vector<uint8_t>& blob, void* const* slots) {
+  for (auto& c : p.plan.consts) {
+    uint64_t bytes = (uint64_t)c.n * esize(p.plan.slots[(size_t)c.slot].dtype);
+    if (c.offset < 0 || (uint64_t)c.offset + bytes > blob.size()) throw std::runtime_error("a constant lies outside the plan's blob");
+    if (bytes) HIP_OK(hipMemcpy(slots[(size_t)c.slot], blob.data() + c.offset, bytes, hipMemcpyHostToDevice));
+  }
+  for (auto& ctl : p.control)
+    if (ctl)
+      for (auto& b : ctl->bodies) upload_consts(*b.prog, blob, slots + b.slot_base);
+}
+
 Frame* new_frame(Program& p) {
   auto* f = new Frame;
   uint64_t total = 0;
@@ -739,7 +779,7 @@ Frame* new_frame(Program& p) {
     total += (b + ALIGN - 1) / ALIGN * ALIGN;
   }
   uint64_t ws_off = total;
-  total += p.fold_base() + (p.fold_bytes + ALIGN - 1) / ALIGN * ALIGN;
+  total += p.ws_bytes();
   total = std::max<uint64_t>(total, ALIGN);
   hipError_t e = hipMalloc(&f->arena, total);
   if (e != hipSuccess) {
@@ -751,10 +791,7 @@ Frame* new_frame(Program& p) {
   for (auto o : off) f->slot.push_back((char*)f->arena + o);
   f->workspace = (char*)f->arena + ws_off;
   HIP_OK(hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking));
-  for (auto& c : p.plan.consts) {
-    uint64_t bytes = (uint64_t)c.n * esize(p.plan.slots[(size_t)c.slot].dtype);
-    if (bytes) HIP_OK(hipMemcpy(f->slot[(size_t)c.slot], p.blob.data() + c.offset, bytes, hipMemcpyHostToDevice));
-  }
+  upload_consts(p, p.blob, f->slot.data());
   return f;
 }
 
@@ -843,6 +880,250 @@ void enqueue_list(const Program& p, hipStream_t s, void* const* slots, void* ws,
     p.steps[k](s, slots, ws);
     q++;
   }
+}
+
+// ---- control flow (include/rg_plan.h SCAN / WHILE / COND; plan.rs:737-831) -------------------
+
+// Copies gathered into batches of one launch each (rgk::copy_batch).
+struct Copies {
+  hipStream_t s;
+  rgk::CopyJobs jobs{};
+  void add(void* dst, const void* src, uint64_t bytes) {
+    if (bytes == 0 || dst == src) return;
+    if (jobs.n == rgk::COPY_JOBS) flush();
+    jobs.dst[jobs.n] = (uint32_t*)dst;
+    jobs.src[jobs.n] = (const uint32_t*)src;
+    jobs.words[jobs.n] = bytes / 4;
+    jobs.n++;
+  }
+  void flush() {
+    rgk::copy_batch(s, jobs);
+    jobs.n = 0;
+  }
+};
+
+uint64_t input_bytes(const Program& p, size_t k) {
+  const auto [slot, n] = p.plan.inputs[k];
+  return (uint64_t)n * esize(p.plan.slots[(size_t)slot].dtype);
+}
+
+uint64_t output_bytes(const Program& p, size_t k) {
+  const auto& o = p.plan.outputs[k];
+  return (uint64_t)o.n * esize(p.plan.slots[(size_t)o.slot].dtype);
+}
+
+// Reads the first element of a slot as a double: a wait on the stream.
+double read_scalar(hipStream_t s, const void* src, int dtype) {
+  unsigned char raw[8] = {0};
+  if (hipMemcpyAsync(raw, src, (size_t)esize(dtype), hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+    return 0.0;  // the failure surfaces at the caller's next wait
+  if (dtype == RG_F32) {
+    float v;
+    memcpy(&v, raw, 4);
+    return v;
+  }
+  if (dtype == RG_F64) {
+    double v;
+    memcpy(&v, raw, 8);
+    return v;
+  }
+  int32_t v;
+  memcpy(&v, raw, 4);
+  return v;
+}
+
+// The body's carry results into its carry inputs, all read before any is written.
+void feed_carry(hipStream_t s, const Program::Control& c, const Program& b, void* const* bs, void* ws) {
+  Copies cp{s};
+  const size_t nc = (size_t)c.attr.n_carry;
+  if (!c.stage_carries) {
+    for (size_t k = 0; k < nc; k++) cp.add(bs[(size_t)b.plan.inputs[k].first], bs[(size_t)b.plan.outputs[k].slot], input_bytes(b, k));
+    cp.flush();
+    return;
+  }
+  char* temp = (char*)ws + c.temp_offset;
+  uint64_t at = 0;
+  for (size_t k = 0; k < nc; k++) {
+    cp.add(temp + at, bs[(size_t)b.plan.outputs[k].slot], input_bytes(b, k));
+    at += (input_bytes(b, k) + ALIGN - 1) / ALIGN * ALIGN;
+  }
+  cp.flush();
+  at = 0;
+  for (size_t k = 0; k < nc; k++) {
+    cp.add(bs[(size_t)b.plan.inputs[k].first], temp + at, input_bytes(b, k));
+    at += (input_bytes(b, k) + ALIGN - 1) / ALIGN * ALIGN;
+  }
+  cp.flush();
+}
+
+void run_scan(hipStream_t s, const Program::Control& c, const Instr& in, void* const* sl, void* ws) {
+  const Program::BodyProg& bp = c.bodies[0];
+  const Program& b = *bp.prog;
+  void* const* bs = sl + bp.slot_base;
+  void* bws = (char*)ws + bp.ws_offset;
+  const size_t nc = (size_t)c.attr.n_carry, nx = (size_t)c.attr.n_x, len = (size_t)c.attr.length;
+  const size_t n_y = b.plan.outputs.size() - nc;
+  Copies cp{s};
+  // Carries and captures once; the x slices every step.
+  for (size_t k = 0; k < in.args.size(); k++)
+    if (k < nc || k >= nc + nx) cp.add(bs[(size_t)b.plan.inputs[k].first], sl[(size_t)in.args[k].slot], input_bytes(b, k));
+  cp.flush();
+  for (size_t step = 0; step < len; step++) {
+    const size_t at = c.attr.reverse ? len - 1 - step : step;
+    for (size_t k = nc; k < nc + nx; k++) {
+      const uint64_t bytes = input_bytes(b, k);
+      cp.add(bs[(size_t)b.plan.inputs[k].first], (char*)sl[(size_t)in.args[k].slot] + at * bytes, bytes);
+    }
+    for (auto [index, dst] : c.attr.results)
+      if ((size_t)index >= nc + n_y) {
+        const size_t k = (size_t)index - nc - n_y;
+        const uint64_t bytes = input_bytes(b, k);
+        cp.add((char*)sl[(size_t)dst] + at * bytes, bs[(size_t)b.plan.inputs[k].first], bytes);
+      }
+    cp.flush();
+    enqueue_range(b, s, bs, bws, 0, b.steps.size());
+    for (auto [index, dst] : c.attr.results)
+      if ((size_t)index >= nc && (size_t)index < nc + n_y) {
+        const uint64_t bytes = output_bytes(b, (size_t)index);
+        cp.add((char*)sl[(size_t)dst] + at * bytes, bs[(size_t)b.plan.outputs[(size_t)index].slot], bytes);
+      }
+    cp.flush();
+    feed_carry(s, c, b, bs, ws);
+  }
+  for (auto [index, dst] : c.attr.results)
+    if ((size_t)index < nc) cp.add(sl[(size_t)dst], bs[(size_t)b.plan.inputs[(size_t)index].first], input_bytes(b, (size_t)index));
+  cp.flush();
+}
+
+void run_while(hipStream_t s, const Program::Control& c, const Instr& in, void* const* sl, void* ws) {
+  const Program &cb = *c.bodies[0].prog, &bb = *c.bodies[1].prog;
+  void* const* cs = sl + c.bodies[0].slot_base;
+  void* const* bs = sl + c.bodies[1].slot_base;
+  void* cws = (char*)ws + c.bodies[0].ws_offset;
+  void* bws = (char*)ws + c.bodies[1].ws_offset;
+  const size_t nc = (size_t)c.attr.n_carry;
+  Copies cp{s};
+  for (size_t k = 0; k < in.args.size(); k++) {
+    cp.add(cs[(size_t)cb.plan.inputs[k].first], sl[(size_t)in.args[k].slot], input_bytes(cb, k));
+    cp.add(bs[(size_t)bb.plan.inputs[k].first], sl[(size_t)in.args[k].slot], input_bytes(bb, k));
+  }
+  cp.flush();
+  const auto& co = cb.plan.outputs[0];
+  int64_t count = 0;
+  for (;;) {
+    enqueue_range(cb, s, cs, cws, 0, cb.steps.size());
+    if (read_scalar(s, cs[(size_t)co.slot], cb.plan.slots[(size_t)co.slot].dtype) == 0.0 || count == c.attr.max_iterations) break;
+    enqueue_range(bb, s, bs, bws, 0, bb.steps.size());
+    feed_carry(s, c, bb, bs, ws);
+    for (size_t k = 0; k < nc; k++) cp.add(cs[(size_t)cb.plan.inputs[k].first], bs[(size_t)bb.plan.inputs[k].first], input_bytes(bb, k));
+    cp.flush();
+    count++;
+  }
+  for (auto [index, dst] : c.attr.results) {
+    if ((size_t)index < nc) cp.add(sl[(size_t)dst], bs[(size_t)bb.plan.inputs[(size_t)index].first], input_bytes(bb, (size_t)index));
+    else rgk::set_i32(s, (int32_t*)sl[(size_t)dst], (int32_t)count);
+  }
+  cp.flush();
+}
+
+void run_cond(hipStream_t s, const Program::Control& c, const Program& owner, const Instr& in, void* const* sl, void* ws) {
+  const int pd = owner.plan.slots[(size_t)in.args[0].slot].dtype;
+  const size_t j = read_scalar(s, sl[(size_t)in.args[0].slot], pd) != 0.0 ? 0 : 1;
+  const Program& b = *c.bodies[j].prog;
+  void* const* bs = sl + c.bodies[j].slot_base;
+  Copies cp{s};
+  for (size_t k = 1; k < in.args.size(); k++) cp.add(bs[(size_t)b.plan.inputs[k - 1].first], sl[(size_t)in.args[k].slot], input_bytes(b, k - 1));
+  cp.flush();
+  enqueue_range(b, s, bs, (char*)ws + c.bodies[j].ws_offset, 0, b.steps.size());
+  for (auto [index, dst] : c.attr.results) cp.add(sl[(size_t)dst], bs[(size_t)b.plan.outputs[(size_t)index].slot], output_bytes(b, (size_t)index));
+  cp.flush();
+}
+
+// Every slot fits the device and the kernels' 32-bit element indexing.
+void check_slots(const Plan& plan) {
+  size_t free_b = 0, total = 0;
+  HIP_OK(hipMemGetInfo(&free_b, &total));
+  for (auto& s : plan.slots) {
+    uint64_t bytes = (uint64_t)s.cap * esize(s.dtype);
+    if (bytes > total)
+      throw std::runtime_error("a " + std::string(s.dtype == RG_F64 ? "float64" : s.dtype == RG_F32 ? "float32" : "int32") + " buffer of " +
+                               std::to_string(s.cap) + " elements exceeds this device's limit of " + std::to_string(total) + " bytes");
+    if (s.cap >= (1ll << 31)) throw std::runtime_error("a buffer of " + std::to_string(s.cap) + " elements exceeds the 2^31 element index range");
+  }
+}
+
+
+// A body's plan as a program of its own (kernels compiled, nested bodies placed).
+std::unique_ptr<Program> body_program(const int64_t* w, size_t n, int device) {
+  auto b = std::make_unique<Program>();
+  b->plan = parse(w, n);
+  b->device = device;
+  check_slots(b->plan);
+  build_program(*b);
+  return b;
+}
+
+StepFn lower_control(Program& prog, size_t k) {
+  const Instr& in = prog.plan.steps[k].instr;
+  auto c = std::make_unique<Program::Control>();
+  c->op = in.op;
+  c->attr = parse_control(in);
+  for (auto [w, n] : c->attr.bodies) {
+    Program::BodyProg bp;
+    bp.prog = body_program(w, n, prog.device);
+    c->bodies.push_back(std::move(bp));
+  }
+  c->attr.bodies.clear();  // they pointed into the plan words
+  // Check the body signatures against the step before anything runs.
+  const size_t nc = (size_t)c->attr.n_carry;
+  for (auto& bp : c->bodies) {
+    const Plan& bpl = bp.prog->plan;
+    const size_t want_in = c->op == RG_OP_COND ? in.args.size() - 1 : in.args.size();
+    if (bpl.inputs.size() != want_in) throw std::runtime_error("control-flow body has the wrong number of inputs");
+    prog.host_sync |= bp.prog->host_sync;
+  }
+  if (c->op != RG_OP_SCAN) prog.host_sync = true;
+  for (auto [index, slot] : c->attr.results)
+    if (index < 0 || slot < 0 || (size_t)slot >= prog.plan.slots.size()) throw std::runtime_error("control-flow result out of range");
+  const Program& body = *c->bodies[c->op == RG_OP_WHILE ? 1 : 0].prog;
+  if (c->op != RG_OP_COND) {
+    if (body.plan.outputs.size() < nc || body.plan.inputs.size() < nc) throw std::runtime_error("control-flow body lacks its carries");
+    // Staging when a carry result shares a buffer with the input of another carry.
+    for (size_t a = 0; a < nc; a++)
+      for (size_t q = 0; q < nc; q++)
+        if (a != q && body.plan.outputs[a].slot == body.plan.inputs[q].first) c->stage_carries = true;
+  }
+  Program::Control* ctl = c.get();
+  const Program* owner = &prog;
+  if (prog.control.size() < prog.plan.steps.size()) prog.control.resize(prog.plan.steps.size());
+  prog.control[k] = std::move(c);
+  return [ctl, owner, k](hipStream_t s, void* const* sl, void* ws) {
+    const Instr& ins = owner->plan.steps[k].instr;
+    if (ctl->op == RG_OP_SCAN) run_scan(s, *ctl, ins, sl, ws);
+    else if (ctl->op == RG_OP_WHILE) run_while(s, *ctl, ins, sl, ws);
+    else run_cond(s, *ctl, *owner, ins, sl, ws);
+  };
+}
+
+// Places the bodies' slots after this program's in the slot table, and their workspaces and the
+// carry staging areas after this program's fold area.
+void place_bodies(Program& prog) {
+  uint64_t ws = 0;
+  for (auto& c : prog.control) {
+    if (!c) continue;
+    if (c->stage_carries) {
+      c->temp_offset = prog.fold_base() + (prog.fold_bytes + 255) / 256 * 256 + ws;
+      const Program& body = *c->bodies[c->op == RG_OP_WHILE ? 1 : 0].prog;
+      for (size_t k = 0; k < (size_t)c->attr.n_carry; k++) ws += (input_bytes(body, k) + ALIGN - 1) / ALIGN * ALIGN;
+    }
+    for (auto& b : c->bodies) {
+      b.slot_base = prog.slot_bytes.size();
+      prog.slot_bytes.insert(prog.slot_bytes.end(), b.prog->slot_bytes.begin(), b.prog->slot_bytes.end());
+      b.ws_offset = prog.fold_base() + (prog.fold_bytes + 255) / 256 * 256 + ws;
+      ws += (b.prog->ws_bytes() + ALIGN - 1) / ALIGN * ALIGN;
+    }
+  }
+  prog.body_ws_bytes = ws;
 }
 
 // Consumes one pass of the failure countdown: true when this pass is the one that fails.
@@ -1008,18 +1289,7 @@ void* rg_hip_program_new(const int64_t* words, size_t n_words, const void* blob,
     if (!rg_hip_available()) throw std::runtime_error("no gfx950 device is visible to HIP");
     p->plan = parse(words, n_words);
     p->blob.assign((const uint8_t*)blob, (const uint8_t*)blob + blob_bytes);
-    size_t free_b = 0, total = 0;
-    HIP_OK(hipMemGetInfo(&free_b, &total));
-    for (auto& s : p->plan.slots) {
-      uint64_t bytes = (uint64_t)s.cap * esize(s.dtype);
-      if (bytes > total)
-        throw std::runtime_error("a " + std::string(s.dtype == RG_F64 ? "float64" : s.dtype == RG_F32 ? "float32" : "int32") + " buffer of " +
-                                 std::to_string(s.cap) + " elements exceeds this device's limit of " + std::to_string(total) + " bytes");
-      if (s.cap >= (1ll << 31)) throw std::runtime_error("a buffer of " + std::to_string(s.cap) + " elements exceeds the 2^31 element index range");
-    }
-    for (auto& st : p->plan.steps)
-      if (st.kind == RG_STEP_INSTR && (st.instr.op == RG_OP_SCAN || st.instr.op == RG_OP_WHILE || st.instr.op == RG_OP_COND))
-        throw std::runtime_error("control flow is not part of the HIP backend");
+    check_slots(p->plan);
     build_program(*p);
     return p;
   } catch (std::exception& e) {
@@ -1035,24 +1305,33 @@ void rg_hip_program_free(void* program) { delete (Program*)program; }
 // the build-time check of the code generator. Returns the number of kernels, or -1.
 int rg_hip_compile_check(const int64_t* words, size_t n_words, char* err, size_t err_len) {
   try {
-    Plan plan = parse(words, n_words);
     std::ostringstream src;
     int count = 0;
-    for (size_t k = 0; k < plan.steps.size(); k++) {
-      const auto& st = plan.steps[k];
-      if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
-      rgjit::FusedKernel fk;
-      if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), &fk);
-      else src << rgjit::generate(st.fused, "rgf" + std::to_string(k), &fk);
-      count++;
-    }
-    for (auto [first, last] : merge_sets(plan)) {
-      std::vector<const rgplan::Fused*> parts;
-      for (size_t j = first; j <= last; j++) parts.push_back(&plan.steps[j].fused);
-      rgjit::FusedKernel fk;
-      src << rgjit::generate_merged(parts, "rgm" + std::to_string(first), &fk);
-      count++;
-    }
+    // The plan's kernels and those of its control-flow bodies, each body's under its own prefix.
+    std::function<void(const Plan&, const std::string&)> add = [&](const Plan& plan, const std::string& prefix) {
+      for (size_t k = 0; k < plan.steps.size(); k++) {
+        const auto& st = plan.steps[k];
+        if (st.kind == RG_STEP_INSTR && is_control(st.instr.op)) {
+          const ControlAttr c = parse_control(st.instr);
+          for (size_t j = 0; j < c.bodies.size(); j++)
+            add(parse(c.bodies[j].first, c.bodies[j].second), prefix + "b" + std::to_string(k) + "_" + std::to_string(j) + "_");
+          continue;
+        }
+        if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
+        rgjit::FusedKernel fk;
+        if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, prefix + "rgr" + std::to_string(k), &fk);
+        else src << rgjit::generate(st.fused, prefix + "rgf" + std::to_string(k), &fk);
+        count++;
+      }
+      for (auto [first, last] : merge_sets(plan)) {
+        std::vector<const rgplan::Fused*> parts;
+        for (size_t j = first; j <= last; j++) parts.push_back(&plan.steps[j].fused);
+        rgjit::FusedKernel fk;
+        src << rgjit::generate_merged(parts, prefix + "rgm" + std::to_string(first), &fk);
+        count++;
+      }
+    };
+    add(parse(words, n_words), "");
     if (count) rgjit::compile_code(src.str());
     return count;
   } catch (std::exception& e) {
@@ -1316,7 +1595,7 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     // Each slot table is captured once as a HIP graph and replayed; RG_HIP_GRAPHS=0 launches the
     // same kernels directly instead (for tools that do not follow graph launches).
     const char* env = getenv("RG_HIP_GRAPHS");
-    const bool use_graphs = !(env && env[0] == '0');
+    const bool use_graphs = !(env && env[0] == '0') && !p->host_sync;
     if (use_graphs && rc.execs.empty()) {
       for (int g = 0; g < n_graphs; g++) {
         HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));

@@ -115,6 +115,21 @@ def test_fused_kernels_of_a_small_program_compile_for_gfx950():
     assert n >= 1, err
 
 
+def test_kernels_inside_control_flow_bodies_compile_for_gfx950():
+    """A scan's body is planned like a program: its fused groups are generated and compiled
+    too (the nested plan descriptors of include/rg_plan.h)."""
+    b = G()
+    c, x = b.input((64, 300), "float32"), b.input((64, 300), "float32")
+    nxt = b.un("tanh", b.bin("add", b.bin("mul", c, x), x))
+    g = G()
+    c0, xs = g.input((64, 300), "float32"), g.input((5, 64, 300), "float32")
+    node = g.g.scan(b.g, [nxt, b.un("exp", nxt)], 1, 1, 5, [c0, xs])
+    last = g.g.output(node, 0, [64, 300], "float32")
+    words_body, _ = _rg.plan_words(g.g, [last], "hip", "standard")
+    n_body, err = _compile_check(words_body)
+    assert n_body >= 1, err
+
+
 def test_c3_program_compiles_for_gfx950():
     """Every fused kernel of a whole GPT training step (C3 at reduced depth) compiles."""
     cfg = workloads.GPT_CONFIGS["C3"]._replace(batch=2, block=16, layers=1)
