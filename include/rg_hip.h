@@ -110,6 +110,10 @@ int rg_hip_exec_breakdown(void* exec, int64_t repeats, char* json, size_t len);
  * execution stream, and stores the elapsed seconds. Gives a kernel class's average launch
  * duration without per-step event overhead. Slot contents afterwards are unspecified. */
 int rg_hip_exec_time_steps(void* exec, const int64_t* steps, int64_t n_steps, int64_t repeats, double* seconds);
+/* The generated HIP source of every fused kernel of a plan (its control-flow bodies included),
+ * for inspection; touches no device. Returns the kernel count, -2 when `len` is too small (the
+ * source is cut), or -1 with the message in `buf`. No reference counterpart. */
+int rg_hip_kernel_source(const int64_t* words, size_t n_words, char* buf, size_t len);
 /* Roofline support for `Compiled::profile` (validate.rs:875-919 times operations; this adds the
  * ceiling they are measured against), with no reference counterpart. Whether the backend runs
  * a product of op(A) m x k by op(B) k x n over `batch` problems through its bandwidth-bound

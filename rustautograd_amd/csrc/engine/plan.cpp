@@ -502,6 +502,7 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
   for (size_t u = 0; u < n_units; u++) n_real += first[u] != SIZE_MAX;
   if (order.size() != n_real) throw std::logic_error("planner: scheduling units depend on each other in a cycle");
   std::vector<size_t> sunk;
+  std::vector<std::vector<size_t>> sunk_comps;
   std::vector<size_t> level(total, 0);
   // Members of each attention unit, in node order.
   std::vector<std::vector<size_t>> attn_members(n_attn_units);
@@ -549,11 +550,97 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     by_level[level[i]].push_back(i);
   }
   // Tails read earlier levels or same-shape tails only, so one last level can hold them all;
-  // node order keeps each producer ahead of its users within a group.
-  if (!sunk.empty()) by_level.push_back(sunk);
-  for (auto& nodes : by_level) {
+  // node order keeps each producer ahead of its users within a group. The tails connected
+  // through one another (an optimizer's moments and the parameter update they feed) are placed
+  // together, component after component, so that a group holding part of a chain holds all of it
+  // when the operand limit allows: no moment is written by one kernel and read back by the next.
+  if (!sunk.empty()) {
+    std::map<size_t, size_t> parent;
+    std::function<size_t(size_t)> root = [&](size_t x) { return parent[x] == x ? x : parent[x] = root(parent[x]); };
+    for (size_t i : sunk) parent[i] = i;
+    for (size_t i : sunk)
+      for (uint32_t x : g.nodes[i].inputs)
+        if (parent.count(x)) parent[root(i)] = root(x);
+    std::map<size_t, std::vector<size_t>> comps;  // keyed by each component's first node
+    std::map<size_t, size_t> first_of;
+    for (size_t i : sunk) {
+      size_t r = root(i);
+      if (!first_of.count(r)) first_of[r] = i;
+      comps[first_of[r]].push_back(i);
+    }
+    std::vector<size_t> ordered;
+    for (auto& [first_node, members] : comps) {
+      ordered.insert(ordered.end(), members.begin(), members.end());
+      sunk_comps.push_back(members);
+    }
+    by_level.push_back(ordered);
+  }
+  // Buffers a group of tails binds: its distinct external inputs and the members it writes out
+  // (plan outputs, or values read outside the group).
+  std::vector<bool> is_out(total, false);
+  for (uint32_t o : outputs) is_out[o] = true;
+  std::vector<std::vector<uint32_t>> users_of(total);
+  if (!sunk.empty())
+    for (size_t i = 0; i < total; i++)
+      if (keep[i])
+        for (uint32_t x : g.nodes[i].inputs) users_of[x].push_back((uint32_t)i);
+  auto bindings = [&](const std::vector<size_t>& members) {
+    std::set<size_t> in(members.begin(), members.end());
+    std::set<uint32_t> ext;
+    size_t written = 0;
+    for (size_t m : members) {
+      for (uint32_t x : g.nodes[m].inputs)
+        if (!in.count(x)) ext.insert(x);
+      bool out = is_out[m];
+      for (uint32_t u : users_of[m]) out |= !in.count(u);
+      written += out;
+    }
+    return ext.size() + written;
+  };
+  for (size_t lv = 0; lv < by_level.size(); lv++) {
+    const auto& nodes = by_level[lv];
     std::vector<std::vector<size_t>> groups;
     std::vector<size_t> aliases, rows, attns;
+    if (!sunk_comps.empty() && lv + 1 == by_level.size()) {
+      // The tails, a whole component at a time when it fits the most recent group of its shape.
+      std::vector<size_t> loose;
+      for (const auto& comp : sunk_comps) {
+        const Node& n = g.nodes[comp[0]];
+        int64_t found = -1;
+        for (size_t k = groups.size(); k-- > 0;) {
+          const Node& f = g.nodes[groups[k][0]];
+          if (f.shape == n.shape && f.dtype == n.dtype) {
+            found = (int64_t)k;
+            break;
+          }
+        }
+        std::vector<size_t> joined = found >= 0 ? groups[(size_t)found] : std::vector<size_t>{};
+        joined.insert(joined.end(), comp.begin(), comp.end());
+        if (found >= 0 && bindings(joined) <= cfg.max_bindings) groups[(size_t)found] = joined;
+        else if (bindings(comp) <= cfg.max_bindings) groups.push_back(comp);
+        else loose.insert(loose.end(), comp.begin(), comp.end());
+      }
+      for (size_t i : loose) {
+        const Node& n = g.nodes[i];
+        int64_t found = -1;
+        for (size_t k = groups.size(); k-- > 0;)
+          if (g.nodes[groups[k][0]].shape == n.shape && g.nodes[groups[k][0]].dtype == n.dtype) {
+            found = (int64_t)k;
+            break;
+          }
+        if (found >= 0 && distinct_external(g, groups[(size_t)found], n) + groups[(size_t)found].size() + 1 <= cfg.max_bindings)
+          groups[(size_t)found].push_back(i);
+        else
+          groups.push_back({i});
+      }
+      for (auto& m : groups) {
+        std::sort(m.begin(), m.end());
+        if (m.size() >= 2 || reads_absorbed(g, m, abs) || (cfg.device && indexed_inputs(g, m[0]))) items.push_back({true, 0, m});
+        else
+          for (size_t x : m) items.push_back({false, x, {}});
+      }
+      continue;
+    }
     for (size_t i : nodes) {
       if (i >= total + rgs.size()) {
         attns.push_back(i - total - rgs.size());

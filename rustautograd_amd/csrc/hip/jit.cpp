@@ -2,6 +2,8 @@
 
 #include <hip/hiprtc.h>
 
+#include <algorithm>
+#include <cstdlib>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -48,16 +50,24 @@ std::string expr(int op, const std::vector<std::string>& a) {
 
 }  // namespace
 
+// A kernel walks its elements grid-stride with at most EW_BLOCKS blocks (16 per CU), so waves are
+// long-lived; U vectors of V per thread per pass, all loaded before any is computed.
+constexpr int EW_UNROLL = 1;
+constexpr uint64_t EW_BLOCKS = 16 * 256;
+
 std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k, bool device_fn) {
   const bool dbl = f.dtype == RG_F64;
   const char* T = dbl ? "double" : "float";
   const int V = dbl ? 2 : 4;
+  const int U = EW_UNROLL;
   const uint64_t n = (uint64_t)f.n;
-  const bool wide = n * 2 >= (1ull << 31);
+  const uint64_t chunk = (uint64_t)TPB * V * U;  // elements a block handles per pass
+  const bool wide = n * 2 + chunk * 2 >= (1ull << 31);
   const char* I = wide ? "unsigned long long" : "unsigned int";
   k->name = name;
-  k->vec = V;
-  k->grid = (uint32_t)((n + (uint64_t)TPB * V - 1) / ((uint64_t)TPB * V));
+  k->vec = V * U;
+  const uint64_t blocks = (n + chunk - 1) / chunk;
+  k->grid = (uint32_t)(device_fn ? blocks : std::min<uint64_t>(blocks, EW_BLOCKS));
 
   std::ostringstream s;
   // Outputs that share a slot with an input are written in place, so no pointer is restrict.
@@ -72,9 +82,6 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
   s << ") {\n";
   s << "  typedef " << I << " I;\n";
   s << "  const I n = " << n << "ull;\n";
-  s << "  const I i0 = ((I)" << (device_fn ? "bid" : "blockIdx.x") << " * " << TPB << "u + (I)threadIdx.x) * " << V << "u;\n";
-  s << "  if (i0 >= n) return;\n";
-  s << "  const bool full = i0 + " << V << "u <= n;\n";
   const char* VT = dbl ? "double2" : "float4";
   const char* lanes[4] = {"x", "y", "z", "w"};
   // Operand expressions per register and per Full input.
@@ -83,27 +90,39 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
   auto ds = row_strides(f.shape);
   for (size_t j = 0; j < f.inputs.size(); j++) {
     const auto& in = f.inputs[j];
-    std::string x = "x" + std::to_string(j);
     if (in.kind == RG_ARG_SPLAT) {
-      s << "  const " << T << " " << x << "s = in" << j << "[0];\n";
-      reg_expr[(size_t)in.reg] = x + "s";
-      continue;
+      s << "  const " << T << " x" << j << "s = in" << j << "[0];\n";
+      reg_expr[(size_t)in.reg] = "x" + std::to_string(j) + "s";
+    } else if (in.reg >= 0) {
+      reg_expr[(size_t)in.reg] = "x" + std::to_string(j) + "[u][v]";
     }
-    s << "  " << T << " " << x << "[" << V << "];\n";
-    if (in.reg >= 0) reg_expr[(size_t)in.reg] = x + "[v]";
+  }
+  if (device_fn) s << "  {\n  const I blk = (I)bid * " << chunk << "u;\n";
+  else s << "  for (I blk = (I)blockIdx.x * " << chunk << "u; blk < n; blk += (I)gridDim.x * " << chunk << "u) {\n";
+  // Loads of every vector of the pass first.
+  for (size_t j = 0; j < f.inputs.size(); j++)
+    if (f.inputs[j].kind != RG_ARG_SPLAT) s << "  " << T << " x" << j << "[" << U << "][" << V << "];\n";
+  s << "#pragma unroll\n  for (int u = 0; u < " << U << "; u++) {\n";
+  s << "    const I i0 = blk + ((I)u * " << TPB << "u + (I)threadIdx.x) * " << V << "u;\n";
+  s << "    if (i0 >= n) break;\n";
+  s << "    const bool full = i0 + " << V << "u <= n;\n";
+  for (size_t j = 0; j < f.inputs.size(); j++) {
+    const auto& in = f.inputs[j];
+    std::string x = "x" + std::to_string(j) + "[u]";
+    if (in.kind == RG_ARG_SPLAT) continue;
     if (in.kind == RG_ARG_FULL) {
-      s << "  if (full) { " << VT << " t = *(const " << VT << "*)(in" << j << " + i0);";
+      s << "    if (full) { " << VT << " t = *(const " << VT << "*)(in" << j << " + i0);";
       for (int v = 0; v < V; v++) s << " " << x << "[" << v << "] = t." << lanes[v] << ";";
       s << " } else { for (int v = 0; v < " << V << "; v++) " << x << "[v] = i0 + v < n ? in" << j << "[i0 + v] : (" << T << ")0; }\n";
     } else if (in.kind == RG_ARG_ROW) {
       int64_t L = in.row_len;
       if (L % V == 0) {
-        s << "  if (full) { " << VT << " t = *(const " << VT << "*)(in" << j << " + i0 % " << L << "u);";
+        s << "    if (full) { " << VT << " t = *(const " << VT << "*)(in" << j << " + i0 % " << L << "u);";
         for (int v = 0; v < V; v++) s << " " << x << "[" << v << "] = t." << lanes[v] << ";";
         s << " } else { for (int v = 0; v < " << V << "; v++) " << x << "[v] = i0 + v < n ? in" << j << "[(i0 + v) % " << L
           << "u] : (" << T << ")0; }\n";
       } else {
-        s << "  for (int v = 0; v < " << V << "; v++) " << x << "[v] = i0 + v < n ? in" << j << "[(i0 + v) % " << L << "u] : ("
+        s << "    for (int v = 0; v < " << V << "; v++) " << x << "[v] = i0 + v < n ? in" << j << "[(i0 + v) % " << L << "u] : ("
           << T << ")0;\n";
       }
     } else {  // Broadcast: flat source index from the output coordinates
@@ -120,12 +139,18 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
         idx += c + " * " + std::to_string(bs) + "u";
       }
       if (idx.empty()) idx = "0u";
-      s << "  for (int v = 0; v < " << V << "; v++) { I i = i0 + v; " << x << "[v] = i < n ? in" << j << "[" << idx << "] : (" << T
+      s << "    for (int v = 0; v < " << V << "; v++) { I i = i0 + v; " << x << "[v] = i < n ? in" << j << "[" << idx << "] : (" << T
         << ")0; }\n";
     }
   }
-  for (size_t j = 0; j < f.outputs.size(); j++) s << "  " << T << " o" << j << "[" << V << "];\n";
-  s << "#pragma unroll\n  for (int v = 0; v < " << V << "; v++) {\n";
+  s << "  }\n";
+  // Then the arithmetic and the stores, vector by vector.
+  s << "#pragma unroll\n  for (int u = 0; u < " << U << "; u++) {\n";
+  s << "    const I i0 = blk + ((I)u * " << TPB << "u + (I)threadIdx.x) * " << V << "u;\n";
+  s << "    if (i0 >= n) break;\n";
+  s << "    const bool full = i0 + " << V << "u <= n;\n";
+  for (size_t j = 0; j < f.outputs.size(); j++) s << "    " << T << " o" << j << "[" << V << "];\n";
+  s << "#pragma unroll\n    for (int v = 0; v < " << V << "; v++) {\n";
   for (auto& m : f.ops) {
     std::vector<std::string> args;
     for (auto& [is_reg, idx] : m.args) {
@@ -133,25 +158,50 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
         const std::string& e = reg_expr[(size_t)idx];
         args.push_back(e.empty() ? "r" + std::to_string(idx) : e);
       } else {
-        args.push_back("x" + std::to_string(idx) + "[v]");
+        args.push_back("x" + std::to_string(idx) + "[u][v]");
       }
     }
-    s << "    const " << T << " r" << m.reg << " = " << expr(m.op, args) << ";\n";
+    s << "      const " << T << " r" << m.reg << " = " << expr(m.op, args) << ";\n";
   }
-  for (size_t j = 0; j < f.outputs.size(); j++) s << "    o" << j << "[v] = r" << f.outputs[j].first << ";\n";
-  s << "  }\n";
+  for (size_t j = 0; j < f.outputs.size(); j++) s << "      o" << j << "[v] = r" << f.outputs[j].first << ";\n";
+  s << "    }\n";
   for (size_t j = 0; j < f.outputs.size(); j++) {
-    s << "  if (full) { " << VT << " t;";
+    s << "    if (full) { " << VT << " t;";
     for (int v = 0; v < V; v++) s << " t." << lanes[v] << " = o" << j << "[" << v << "];";
     s << " *(" << VT << "*)(out" << j << " + i0) = t; } else { for (int v = 0; v < " << V << "; v++) if (i0 + v < n) out" << j
       << "[i0 + v] = o" << j << "[v]; }\n";
   }
+  s << "  }\n";
+  s << "  }\n";
   s << "}\n";
   return s.str();
 }
 
+std::vector<int64_t> merged_slots(const std::vector<const rgplan::Fused*>& parts) {
+  std::vector<int64_t> out;
+  auto add = [&](int64_t slot) {
+    if (std::find(out.begin(), out.end(), slot) == out.end()) out.push_back(slot);
+  };
+  for (const auto* f : parts) {
+    for (auto& in : f->inputs) add(in.slot);
+    for (auto& o : f->outputs) add(o.second);
+  }
+  return out;
+}
+
 std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, const std::string& name, FusedKernel* k) {
+  const std::vector<int64_t> slots = merged_slots(parts);
+  auto param = [&](int64_t slot) { return "q" + std::to_string(std::find(slots.begin(), slots.end(), slot) - slots.begin()); };
   std::ostringstream s, params, body;
+  for (size_t q = 0; q < slots.size(); q++) {
+    bool written = false, f64 = false;
+    for (const auto* f : parts) {
+      for (auto& o : f->outputs) written |= o.second == slots[q];
+      for (auto& in : f->inputs) f64 |= in.slot == slots[q] && f->dtype == RG_F64;
+      for (auto& o : f->outputs) f64 |= o.second == slots[q] && f->dtype == RG_F64;
+    }
+    params << (q ? ", " : "") << (written ? "" : "const ") << (f64 ? "double" : "float") << "* q" << q;
+  }
   uint32_t start = 0;
   body << "  const unsigned int b = blockIdx.x;\n";
   for (size_t j = 0; j < parts.size(); j++) {
@@ -159,13 +209,9 @@ std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, cons
     const std::string part = name + "_" + std::to_string(j);
     FusedKernel pk;
     s << generate(f, part, &pk, true);
-    const char* T = f.dtype == RG_F64 ? "double" : "float";
     std::string call = part + "(b - " + std::to_string(start) + "u";
-    for (size_t q = 0; q < f.inputs.size() + f.outputs.size(); q++) {
-      const std::string a = "p" + std::to_string(j) + "_" + std::to_string(q);
-      params << (params.tellp() > 0 ? ", " : "") << (q < f.inputs.size() ? "const " : "") << T << "* " << a;
-      call += ", " + a;
-    }
+    for (auto& in : f.inputs) call += ", " + param(in.slot);
+    for (auto& o : f.outputs) call += ", " + param(o.second);
     start += pk.grid;
     body << "  if (b < " << start << "u) { " << call << "); return; }\n";
   }

@@ -38,9 +38,12 @@ constexpr int COL_WAVES = 16;
 std::string generate(const rgplan::Fused& f, const std::string& name, FusedKernel* k, bool device_fn = false);
 
 // Source of one kernel computing several independent groups side by side (horizontal fusion):
-// blocks [start_j, start_j + grid_j) compute part j, and the parameters are each part's inputs
-// then outputs, part after part. For groups too small to fill the device on their own.
+// blocks [start_j, start_j + grid_j) compute part j. For groups too small to fill the device on
+// their own.
+// Its parameters are the distinct slots of the parts (merged_slots: inputs then outputs, part after
+// part, each slot once), so operands the parts share, such as an optimizer's scalars, pass once.
 std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, const std::string& name, FusedKernel* k);
+std::vector<int64_t> merged_slots(const std::vector<const rgplan::Fused*>& parts);
 
 // Source of one row-group kernel (RG_STEP_ROWS): `k->grid` blocks of four rows each, or, with
 // column reductions, COL_BLOCKS blocks of COL_WAVES waves walking the rows grid-stride and writing

@@ -587,7 +587,7 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
 // run reads or writes; a group's own in-place update is fine) become one kernel, up to
 // MERGE_MAX_ARGS pointer arguments.
 constexpr uint32_t MERGE_MAX_GRID = 256;
-constexpr size_t MERGE_MAX_ARGS = 120;
+constexpr size_t MERGE_MAX_ARGS = 240;
 
 uint32_t fused_grid(const rgplan::Fused& f) {
   const uint64_t per = (uint64_t)rgjit::TPB * (f.dtype == RG_F64 ? 2 : 4);
@@ -609,19 +609,23 @@ std::vector<std::pair<size_t, size_t>> merge_sets(const Plan& plan) {
       continue;
     }
     std::set<int64_t> reads, writes;
-    size_t args = 0, last = k;
+    size_t last = k;
     for (size_t j = k; j < plan.steps.size() && small(j); j++) {
       const auto& f = plan.steps[j].fused;
       std::set<int64_t> r, w;
       for (auto& in : f.inputs) r.insert(in.slot);
       for (auto& o : f.outputs) w.insert(o.second);
-      bool clash = args + f.inputs.size() + f.outputs.size() > MERGE_MAX_ARGS;
+      // The merged kernel takes each distinct slot once.
+      std::set<int64_t> all(reads);
+      all.insert(writes.begin(), writes.end());
+      all.insert(r.begin(), r.end());
+      all.insert(w.begin(), w.end());
+      bool clash = all.size() > MERGE_MAX_ARGS;
       for (int64_t x : w) clash |= reads.count(x) || writes.count(x);
       for (int64_t x : r) clash |= writes.count(x) > 0;
       if (clash) break;
       reads.insert(r.begin(), r.end());
       writes.insert(w.begin(), w.end());
-      args += f.inputs.size() + f.outputs.size();
       last = j;
     }
     if (last > k) sets.push_back({k, last});
@@ -678,12 +682,9 @@ void build_program(Program& prog) {
   prog.merged_at.assign(prog.plan.steps.size(), -1);
   for (size_t m = 0; m < sets.size(); m++) {
     auto [first, last] = sets[m];
-    std::vector<int64_t> slots;
-    for (size_t j = first; j <= last; j++) {
-      const auto& f = prog.plan.steps[j].fused;
-      for (auto& in : f.inputs) slots.push_back(in.slot);
-      for (auto& o : f.outputs) slots.push_back(o.second);
-    }
+    std::vector<const rgplan::Fused*> parts;
+    for (size_t j = first; j <= last; j++) parts.push_back(&prog.plan.steps[j].fused);
+    const std::vector<int64_t> slots = rgjit::merged_slots(parts);
     rgjit::FusedKernel* fk = merged_kernels[m];
     prog.merged_at[first] = (int64_t)m;
     prog.merged.push_back({first, last, [fk, slots](hipStream_t s, void* const* sl, void*) {
@@ -1040,6 +1041,37 @@ void run_cond(hipStream_t s, const Program::Control& c, const Program& owner, co
 }
 
 // Every slot fits the device and the kernels' 32-bit element indexing.
+// The HIP source of every fused kernel of a plan and of its control-flow bodies (each body's
+// kernels under their own prefix), as the runtime generates it; `count` kernels.
+std::string plan_source(const Plan& root, int* count) {
+  std::ostringstream src;
+  std::function<void(const Plan&, const std::string&)> add = [&](const Plan& plan, const std::string& prefix) {
+    for (size_t k = 0; k < plan.steps.size(); k++) {
+      const auto& st = plan.steps[k];
+      if (st.kind == RG_STEP_INSTR && is_control(st.instr.op)) {
+        const ControlAttr c = parse_control(st.instr);
+        for (size_t j = 0; j < c.bodies.size(); j++)
+          add(parse(c.bodies[j].first, c.bodies[j].second), prefix + "b" + std::to_string(k) + "_" + std::to_string(j) + "_");
+        continue;
+      }
+      if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
+      rgjit::FusedKernel fk;
+      if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, prefix + "rgr" + std::to_string(k), &fk);
+      else src << rgjit::generate(st.fused, prefix + "rgf" + std::to_string(k), &fk);
+      (*count)++;
+    }
+    for (auto [first, last] : merge_sets(plan)) {
+      std::vector<const rgplan::Fused*> parts;
+      for (size_t j = first; j <= last; j++) parts.push_back(&plan.steps[j].fused);
+      rgjit::FusedKernel fk;
+      src << rgjit::generate_merged(parts, prefix + "rgm" + std::to_string(first), &fk);
+      (*count)++;
+    }
+  };
+  add(root, "");
+  return src.str();
+}
+
 void check_slots(const Plan& plan) {
   size_t free_b = 0, total = 0;
   HIP_OK(hipMemGetInfo(&free_b, &total));
@@ -1203,13 +1235,24 @@ void enqueue_run_step(const Program& p, hipStream_t s, void* ws, const rg_run_de
     int64_t sl = d->history_slots[h];
     rgk::record_history(s, p.plan.slots[(size_t)sl].dtype, t[(size_t)sl], b.hist + h * b.chunk, b.counter, b.chunk);
   }
-  for (int64_t c = 0; c < d->n_copies; c++) {
-    int64_t os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
-    rgk::copy_bytes(s, b.temps[(size_t)c], t[(size_t)os], (uint64_t)n * esize(p.plan.slots[(size_t)os].dtype));
-  }
+  // The state copies, batched: straight from each output into the next table's input when no
+  // destination is also a source, else through the temporaries (all sources read first).
+  bool overlap = false;
+  for (int64_t c = 0; c < d->n_copies && !overlap; c++)
+    for (int64_t q = 0; q < d->n_copies && !overlap; q++)
+      overlap = next[(size_t)d->copies[3 * c]] == t[(size_t)d->copies[3 * q + 1]];
+  Copies cp{s};
   for (int64_t c = 0; c < d->n_copies; c++) {
     int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
-    rgk::copy_bytes(s, next[(size_t)is], b.temps[(size_t)c], (uint64_t)n * esize(p.plan.slots[(size_t)os].dtype));
+    cp.add(overlap ? b.temps[(size_t)c] : next[(size_t)is], t[(size_t)os], (uint64_t)n * esize(p.plan.slots[(size_t)os].dtype));
+  }
+  cp.flush();
+  if (overlap) {
+    for (int64_t c = 0; c < d->n_copies; c++) {
+      int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
+      cp.add(next[(size_t)is], b.temps[(size_t)c], (uint64_t)n * esize(p.plan.slots[(size_t)os].dtype));
+    }
+    cp.flush();
   }
   rgk::counter_inc(s, b.counter);
 }
@@ -1305,37 +1348,24 @@ void rg_hip_program_free(void* program) { delete (Program*)program; }
 // the build-time check of the code generator. Returns the number of kernels, or -1.
 int rg_hip_compile_check(const int64_t* words, size_t n_words, char* err, size_t err_len) {
   try {
-    std::ostringstream src;
     int count = 0;
-    // The plan's kernels and those of its control-flow bodies, each body's under its own prefix.
-    std::function<void(const Plan&, const std::string&)> add = [&](const Plan& plan, const std::string& prefix) {
-      for (size_t k = 0; k < plan.steps.size(); k++) {
-        const auto& st = plan.steps[k];
-        if (st.kind == RG_STEP_INSTR && is_control(st.instr.op)) {
-          const ControlAttr c = parse_control(st.instr);
-          for (size_t j = 0; j < c.bodies.size(); j++)
-            add(parse(c.bodies[j].first, c.bodies[j].second), prefix + "b" + std::to_string(k) + "_" + std::to_string(j) + "_");
-          continue;
-        }
-        if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
-        rgjit::FusedKernel fk;
-        if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, prefix + "rgr" + std::to_string(k), &fk);
-        else src << rgjit::generate(st.fused, prefix + "rgf" + std::to_string(k), &fk);
-        count++;
-      }
-      for (auto [first, last] : merge_sets(plan)) {
-        std::vector<const rgplan::Fused*> parts;
-        for (size_t j = first; j <= last; j++) parts.push_back(&plan.steps[j].fused);
-        rgjit::FusedKernel fk;
-        src << rgjit::generate_merged(parts, prefix + "rgm" + std::to_string(first), &fk);
-        count++;
-      }
-    };
-    add(parse(words, n_words), "");
-    if (count) rgjit::compile_code(src.str());
+    const std::string src = plan_source(parse(words, n_words), &count);
+    if (count) rgjit::compile_code(src);
     return count;
   } catch (std::exception& e) {
     put(err, err_len, e.what());
+    return -1;
+  }
+}
+
+int rg_hip_kernel_source(const int64_t* words, size_t n_words, char* buf, size_t len) {
+  try {
+    int count = 0;
+    const std::string src = plan_source(parse(words, n_words), &count);
+    put(buf, len, src);
+    return src.size() + 1 <= len ? count : -2;
+  } catch (std::exception& e) {
+    put(buf, len, e.what());
     return -1;
   }
 }
