@@ -40,6 +40,10 @@ struct Allocator {
     return s;
   }
   size_t pick(DType d, size_t n, bool exact) {
+    // A plan output sized exactly for its state handoff gets a buffer of its own: reusing one
+    // freed by an earlier step would order it after that step's readers, so the independent
+    // updates at the end of a training step could not run side by side.
+    if (exact) return new_slot(d, n, false);
     // Reusing a large buffer for a small value would keep the large one busy for as long as the small one lives.
     int64_t best = -1;
     for (size_t k = 0; k < free.size(); k++) {
@@ -602,22 +606,12 @@ std::vector<Item> schedule_levels(const Graph& g, const std::vector<bool>& keep,
     std::vector<std::vector<size_t>> groups;
     std::vector<size_t> aliases, rows, attns;
     if (!sunk_comps.empty() && lv + 1 == by_level.size()) {
-      // The tails, a whole component at a time when it fits the most recent group of its shape.
+      // The tails, one group per component (one parameter's update chain, say): independent
+      // chains stay separate kernels, which the runtime launches side by side, so each chain's
+      // elements spread over the whole device instead of one thread walking every chain.
       std::vector<size_t> loose;
       for (const auto& comp : sunk_comps) {
-        const Node& n = g.nodes[comp[0]];
-        int64_t found = -1;
-        for (size_t k = groups.size(); k-- > 0;) {
-          const Node& f = g.nodes[groups[k][0]];
-          if (f.shape == n.shape && f.dtype == n.dtype) {
-            found = (int64_t)k;
-            break;
-          }
-        }
-        std::vector<size_t> joined = found >= 0 ? groups[(size_t)found] : std::vector<size_t>{};
-        joined.insert(joined.end(), comp.begin(), comp.end());
-        if (found >= 0 && bindings(joined) <= cfg.max_bindings) groups[(size_t)found] = joined;
-        else if (bindings(comp) <= cfg.max_bindings) groups.push_back(comp);
+        if (bindings(comp) <= cfg.max_bindings) groups.push_back(comp);
         else loose.insert(loose.end(), comp.begin(), comp.end());
       }
       for (size_t i : loose) {
