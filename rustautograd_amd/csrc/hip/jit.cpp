@@ -253,11 +253,7 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   k->col_kind.assign(f.outputs.size(), -1);
   k->row_len = (uint32_t)L;
   if (has_col) {
-    static const int64_t col_blocks = [] {
-      const char* v = getenv("RG_COL_BLOCKS");
-      return v ? std::max<int64_t>(1, atoll(v)) : COL_BLOCKS;
-    }();
-    k->grid = (uint32_t)std::min<int64_t>((rows + COL_WAVES - 1) / COL_WAVES, col_blocks);
+    k->grid = (uint32_t)std::min<int64_t>((rows + COL_WAVES - 1) / COL_WAVES, COL_BLOCKS);
     k->block = 64 * COL_WAVES;
     for (size_t j = 0; j < f.outputs.size(); j++)
       for (auto& m : f.ops)

@@ -27,7 +27,8 @@ struct FusedKernel {
 };
 
 // A row group with column reductions: COL_BLOCKS blocks of COL_WAVES waves (one block per CU,
-// four waves per SIMD), each folding the rows it walks into one partial row.
+// four waves per SIMD), each folding the rows it walks into one partial row. (Two blocks per CU
+// at 64 registers, one row per wave, measured no faster on C4's layer norms.)
 constexpr int64_t COL_BLOCKS = 256;
 constexpr int COL_WAVES = 16;
 
