@@ -779,32 +779,56 @@ void rematerialize(const Graph& g, const std::vector<bool>& keep, const std::vec
         for (size_t u : C.members)
           for (uint32_t y : g.nodes[u].inputs)
             if (!in(C.members, y)) ext_c.insert(y);
-        // X's ancestors within G, up to the values C reads anyway.
-        std::vector<size_t> closure;
-        std::vector<uint32_t> stack(xs.begin(), xs.end());
-        bool ok = true;
-        while (!stack.empty()) {
-          uint32_t x = stack.back();
-          stack.pop_back();
-          if (std::find(closure.begin(), closure.end(), (size_t)x) != closure.end()) continue;
-          closure.push_back(x);
-          // Only reductions a row group folds per row may be recomputed.
-          if (g.nodes[x].op.kind == RG_OP_REDUCE && !(C.rows && last_axis_reduce(x))) ok = false;
-          for (uint32_t y : g.nodes[x].inputs)
-            if (in(G.members, y) && (!ext_c.count(y) || std::find(xs.begin(), xs.end(), y) != xs.end())) stack.push_back(y);
-        }
-        std::sort(closure.begin(), closure.end());
+        // G's members that G writes whatever C does (read outside G and C, or plan outputs).
+        auto written = [&](uint32_t y) {
+          if (is_out[y]) return true;
+          for (uint32_t w : users[y])
+            if (!in(G.members, w) && !in(C.members, w)) return true;
+          return false;
+        };
+        // X's ancestors within G, up to the values C reads anyway; with `stop`, also up to the
+        // values G writes anyway, which C then reads instead of recomputing them from their own
+        // inputs (a layer norm's backward reads the residual sum the forward stores rather than
+        // the two values it adds).
+        struct Option {
+          std::vector<size_t> closure;
+          std::set<uint32_t> fresh;
+          size_t full = 0;
+          bool ok = true;
+        };
+        auto option = [&](bool stop) {
+          Option o;
+          std::vector<uint32_t> stack(xs.begin(), xs.end());
+          while (!stack.empty()) {
+            uint32_t x = stack.back();
+            stack.pop_back();
+            if (std::find(o.closure.begin(), o.closure.end(), (size_t)x) != o.closure.end()) continue;
+            o.closure.push_back(x);
+            // Only reductions a row group folds per row may be recomputed.
+            if (g.nodes[x].op.kind == RG_OP_REDUCE && !(C.rows && last_axis_reduce(x))) o.ok = false;
+            for (uint32_t y : g.nodes[x].inputs) {
+              const bool is_x = std::find(xs.begin(), xs.end(), y) != xs.end();
+              if (in(G.members, y) && (!ext_c.count(y) || is_x) && (is_x || !stop || !written(y))) stack.push_back(y);
+            }
+          }
+          std::sort(o.closure.begin(), o.closure.end());
+          // Full-size values C would newly read.
+          for (size_t m : o.closure)
+            for (uint32_t y : g.nodes[m].inputs)
+              if (!in(o.closure, y) && !in(C.members, y) && !ext_c.count(y)) o.fresh.insert(y);
+          for (uint32_t y : o.fresh) o.full += numel(g.shape(y)) == cn;
+          return o;
+        };
+        Option a = option(false), b = option(true);
+        // The fewer full-size reads; on a tie the shorter recomputation.
+        Option& best = (b.ok && (!a.ok || b.full < a.full || (b.full == a.full && b.closure.size() < a.closure.size()))) ? b : a;
+        const std::vector<size_t>& closure = best.closure;
         // Full-size values C would newly read, against the full-size values it no longer reads
         // (and G no longer writes): a trade of equal reads still saves G's writes.
-        std::set<uint32_t> fresh;
-        for (size_t m : closure)
-          for (uint32_t y : g.nodes[m].inputs)
-            if (!in(closure, y) && !in(C.members, y) && !ext_c.count(y)) fresh.insert(y);
-        size_t full = 0, saved = 0;
-        for (uint32_t y : fresh) full += numel(g.shape(y)) == cn;
+        size_t saved = 0;
         for (uint32_t x : xs) saved += numel(g.shape(x)) == cn;
-        if (!ok || saved == 0 || full > saved || closure.size() > 64 ||
-            ext_c.size() + fresh.size() + C.members.size() + closure.size() > max_bindings)
+        if (!best.ok || saved == 0 || best.full > saved || closure.size() > 64 ||
+            ext_c.size() + best.fresh.size() + C.members.size() + closure.size() > max_bindings)
           continue;
         std::vector<size_t> merged;
         std::set_union(C.members.begin(), C.members.end(), closure.begin(), closure.end(), std::back_inserter(merged));

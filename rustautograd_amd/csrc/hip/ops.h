@@ -38,6 +38,56 @@ RG_DEFINE_OPS(
   template <class T> __device__ __forceinline__ T rg_gt(T a, T b) { return a > b ? (T)1 : (T)0; }
   template <class T> __device__ __forceinline__ T rg_ge(T a, T b) { return a >= b ? (T)1 : (T)0; }
   template <class T> __device__ __forceinline__ T rg_where(T c, T a, T b) { return c != (T)0 ? a : b; }
+  // Wave64 all-reductions without LDS: within each row of 16 lanes by DPP (quad exchanges, then
+  // the half-row and row mirrors), then across rows with the permlane swaps. Every lane combines
+  // the same two values at every step, so every lane ends with the same bits.
+  template <int C> __device__ __forceinline__ float rg_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), C, 0xf, 0xf, false));
+  }
+  template <int C> __device__ __forceinline__ double rg_dpp(double x) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, C, 0xf, 0xf, false);
+    const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), C, 0xf, 0xf, false);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+  }
+  __device__ __forceinline__ void rg_swap16(float x, float* a, float* b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    *a = __uint_as_float(p[0]);
+    *b = __uint_as_float(p[1]);
+  }
+  __device__ __forceinline__ void rg_swap32(float x, float* a, float* b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    *a = __uint_as_float(p[0]);
+    *b = __uint_as_float(p[1]);
+  }
+  __device__ __forceinline__ void rg_swap16(double x, double* a, double* b) {
+    const unsigned long long v = (unsigned long long)__double_as_longlong(x);
+    const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)(v >> 32), (unsigned)(v >> 32), false, false);
+    *a = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0]));
+    *b = __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+  }
+  __device__ __forceinline__ void rg_swap32(double x, double* a, double* b) {
+    const unsigned long long v = (unsigned long long)__double_as_longlong(x);
+    const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)(v >> 32), (unsigned)(v >> 32), false, false);
+    *a = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0]));
+    *b = __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+  }
+  template <class T, class F> __device__ __forceinline__ T rg_wave_all(T x, F f) {
+    x = f(x, rg_dpp<0xB1>(x));   /* quad_perm [1,0,3,2] */
+    x = f(x, rg_dpp<0x4E>(x));   /* quad_perm [2,3,0,1] */
+    x = f(x, rg_dpp<0x141>(x));  /* row_half_mirror */
+    x = f(x, rg_dpp<0x140>(x));  /* row_mirror */
+    T a, b;
+    rg_swap16(x, &a, &b);
+    x = f(a, b);
+    rg_swap32(x, &a, &b);
+    return f(a, b);
+  }
+  template <class T> __device__ __forceinline__ T rg_wave_sum(T x) { return rg_wave_all(x, [](T a, T b) { return a + b; }); }
+  template <class T> __device__ __forceinline__ T rg_wave_max(T x) { return rg_wave_all(x, [](T a, T b) { return rg_max(a, b); }); }
+  template <class T> __device__ __forceinline__ T rg_wave_min(T x) { return rg_wave_all(x, [](T a, T b) { return rg_min(a, b); }); }
 )
 
 // Opcode dispatch for the precompiled single-operation kernels (RG_OP_* of rg_plan.h).
