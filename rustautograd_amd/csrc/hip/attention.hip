@@ -54,14 +54,19 @@ __device__ __forceinline__ floatx4 mfma4(floatx4 acc, float4 a, float4 b) {
   return acc;
 }
 
-// Lanes l, l ^ 16, l ^ 32, l ^ 48 share a row.
+// Lanes l, l ^ 16, l ^ 32, l ^ 48 share a row: combined by the permlane swaps (no LDS), every
+// lane taking its two values in the same order.
 __device__ __forceinline__ float row_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+  float a, b;
+  rg_swap16(x, &a, &b);
+  rg_swap32(fmaxf(a, b), &a, &b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float row_sum(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
+  float a, b;
+  rg_swap16(x, &a, &b);
+  rg_swap32(a + b, &a, &b);
+  return a + b;
 }
 
 constexpr float LOG2E = 1.4426950408889634f;

@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "kernels.h"
+#include "ops.h"
 
 namespace rgk {
 
@@ -528,9 +529,7 @@ __global__ void __launch_bounds__(256) k_gemm_skinny_dot(const float* __restrict
   for (int m = 0; m < MR; m++)
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-      float v = acc[m][c];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      const float v = rg_wave_sum(acc[m][c]);
       if (m < M && lane == 0) dst[(uint64_t)m * N + n0 + c] = v;
     }
 }
@@ -593,8 +592,7 @@ __global__ void __launch_bounds__(256) k_gemm_tiny_out(const float* __restrict__
     const float b = tb ? B[(uint64_t)j * K + k] : B[(uint64_t)k * N + j];
     acc = fmaf(a, b, acc);
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  acc = rg_wave_sum(acc);
   if (lane == 0) C[e] = acc;
 }
 
