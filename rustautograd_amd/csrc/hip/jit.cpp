@@ -191,7 +191,6 @@ std::vector<int64_t> merged_slots(const std::vector<const rgplan::Fused*>& parts
 
 std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, const std::string& name, FusedKernel* k) {
   const std::vector<int64_t> slots = merged_slots(parts);
-  auto param = [&](int64_t slot) { return "q" + std::to_string(std::find(slots.begin(), slots.end(), slot) - slots.begin()); };
   std::ostringstream s, params, body;
   for (size_t q = 0; q < slots.size(); q++) {
     bool written = false, f64 = false;
@@ -203,15 +202,24 @@ std::string generate_merged(const std::vector<const rgplan::Fused*>& parts, cons
     params << (q ? ", " : "") << (written ? "" : "const ") << (f64 ? "double" : "float") << "* q" << q;
   }
   uint32_t start = 0;
+  // Each branch reads only its part's pointers from the kernel argument segment. Passing the
+  // named parameters instead has the compiler load all of them (up to MERGE_MAX_ARGS) at entry
+  // and spill most to VGPR lanes, a prologue of hundreds of instructions in every block.
   body << "  const unsigned int b = blockIdx.x;\n";
+  body << "  const __attribute__((address_space(4))) unsigned long long* ka = (const __attribute__((address_space(4))) unsigned long "
+          "long*)__builtin_amdgcn_kernarg_segment_ptr();\n";
+  auto arg = [&](int64_t slot, bool out, bool f64) {
+    const size_t q = std::find(slots.begin(), slots.end(), slot) - slots.begin();
+    return std::string("(") + (out ? "" : "const ") + (f64 ? "double" : "float") + "*)ka[" + std::to_string(q) + "]";
+  };
   for (size_t j = 0; j < parts.size(); j++) {
     const rgplan::Fused& f = *parts[j];
     const std::string part = name + "_" + std::to_string(j);
     FusedKernel pk;
     s << generate(f, part, &pk, true);
     std::string call = part + "(b - " + std::to_string(start) + "u";
-    for (auto& in : f.inputs) call += ", " + param(in.slot);
-    for (auto& o : f.outputs) call += ", " + param(o.second);
+    for (auto& in : f.inputs) call += ", " + arg(in.slot, false, f.dtype == RG_F64);
+    for (auto& o : f.outputs) call += ", " + arg(o.second, true, f.dtype == RG_F64);
     start += pk.grid;
     body << "  if (b < " << start << "u) { " << call << "); return; }\n";
   }
