@@ -1003,7 +1003,14 @@ __global__ void __launch_bounds__(TPB) k_copy_batch(CopyJobs jobs) {
   const uint64_t words = jobs.words[j];
   uint32_t* __restrict__ dst = jobs.dst[j];
   const uint32_t* __restrict__ src = jobs.src[j];
-  for (uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x; i < words; i += (uint64_t)gridDim.x * TPB) dst[i] = src[i];
+  const uint64_t first = (uint64_t)blockIdx.x * TPB + threadIdx.x, stride = (uint64_t)gridDim.x * TPB;
+  if ((words & 3) == 0 && ((uintptr_t)dst & 15) == 0 && ((uintptr_t)src & 15) == 0) {  // 16 bytes per thread
+    uint4* __restrict__ d4 = (uint4*)dst;
+    const uint4* __restrict__ s4 = (const uint4*)src;
+    for (uint64_t i = first; i < words / 4; i += stride) d4[i] = s4[i];
+    return;
+  }
+  for (uint64_t i = first; i < words; i += stride) dst[i] = src[i];
 }
 
 __global__ void k_set_i32(int32_t* dst, int32_t value) { dst[0] = value; }

@@ -1646,12 +1646,15 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
       enqueue_step(table_of(k));
       return hipGetLastError();
     };
+    // The changing state slots to or from the chunk's snapshot, COPY_JOBS slots per launch.
     auto snapshot = [&](int g, bool restore) {
+      Copies cp{f->stream};
       for (size_t q = 0; q < rc.state_slots.size(); q++) {
         void* live = rc.table[g][(size_t)rc.state_slots[q]];
         uint64_t bytes = p->slot_bytes[(size_t)rc.state_slots[q]];
-        rgk::copy_bytes(f->stream, restore ? live : rc.snap[q], restore ? rc.snap[q] : live, bytes);
+        cp.add(restore ? live : rc.snap[q], restore ? rc.snap[q] : live, bytes);
       }
+      cp.flush();
     };
     HIP_OK(hipGetLastError());
     rgk::set_counter(f->stream, rc.buf.counter, 0);
