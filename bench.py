@@ -72,22 +72,30 @@ def classify(plan):
 def time_classes(compiled, inputs, classes, repeats, trials=7):
     """Device seconds per pass of each kernel class, measured inside the pass: every plan step
     replayed back to back `repeats` times between two HIP events on the execution stream, minus
-    the same replay without the class's steps (rg_hip_exec_time_steps; the median of `trials`
-    each). The class's kernels so run with the caches and clocks they meet inside a training
-    step (the operands a product or attention step reads were just written by the step before
-    it), and no event separates them. The replay of the class's steps alone is kept as
-    `isolated_seconds`. Returns the seconds of the whole replayed pass."""
-    def timed(steps):
-        if not steps:
-            return 0.0
-        return sorted(compiled._n.time_steps(inputs, steps, repeats) / repeats for _ in range(trials))[trials // 2]
+    the same replay without the class's steps, timed right after it (rg_hip_exec_time_steps);
+    the median over `trials` such pairs, so that a slow drift of the clock cancels. The class's
+    kernels so run with the caches and clocks they meet inside a training step (the operands a
+    product or attention step reads were just written by the step before it), and no event
+    separates them. The replay of the class's steps alone is kept as `isolated_seconds`.
+    Returns the seconds of the whole replayed pass."""
+    def once(steps):
+        return compiled._n.time_steps(inputs, steps, repeats) / repeats if steps else 0.0
+
+    def median(xs):
+        return sorted(xs)[len(xs) // 2]
 
     every = sorted(s for c in classes.values() for s in c["steps"])
-    full = timed(every)
+    fulls = []
     for c in classes.values():
         own = set(c["steps"])
-        in_pass = full - timed([s for s in every if s not in own])
-        c["isolated_seconds"] = timed(c["steps"])
+        rest = [s for s in every if s not in own]
+        diffs = []
+        for _ in range(trials):
+            f = once(every)
+            fulls.append(f)
+            diffs.append(f - once(rest))
+        in_pass = median(diffs)
+        c["isolated_seconds"] = median([once(c["steps"]) for _ in range(trials)])
         # A class too small to stand out of the pass's run-to-run spread keeps its isolated time.
         c["timing"] = "in_pass" if in_pass >= 0.5 * c["isolated_seconds"] else "isolated"
         c["seconds"] = in_pass if c["timing"] == "in_pass" else c["isolated_seconds"]
@@ -95,7 +103,7 @@ def time_classes(compiled, inputs, classes, repeats, trials=7):
             c["achieved"], c["unit"] = c["flops"] / c["seconds"] / 1e12, "TFLOP/s"
         else:
             c["achieved"], c["unit"] = c["bytes"] / c["seconds"] / 1e9, "GB/s"
-    return full
+    return median(fulls)
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_hbm_traffic.txt")
