@@ -566,34 +566,49 @@ __global__ void __launch_bounds__(256) k_gemm_outer(const float* __restrict__ A,
   }
 }
 
-// A few outputs with a long K (at most 16384 outputs): one wave per output, its lanes taking k
-// 64 apart in increasing order, then a fixed xor butterfly. Any flags, any alignment.
-__global__ void __launch_bounds__(256) k_gemm_tiny_out(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
-                                                       int N, int K, bool ta, bool tb) {
-  const int lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (e >= M * N) return;
+// A few outputs with a long K (at most 16384 outputs): one block of W waves per output, its
+// threads taking k 64 W apart in increasing order (eight loads of each operand in flight), each
+// wave's sum by a fixed butterfly, and the W wave sums added in wave order. Any flags, any
+// alignment.
+template <int W>
+__global__ void __launch_bounds__(64 * W) k_gemm_tiny_out(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+                                                          int N, int K, bool ta, bool tb) {
+  constexpr int NT = 64 * W;
+  __shared__ float wsum[W];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int e = blockIdx.x;
   const int i = e / N, j = e % N;
   float acc = 0.f;
-  int k = lane;
-  for (; k + 7 * 64 < K; k += 8 * 64) {  // eight loads of each operand in flight
+  int k = threadIdx.x;
+  for (; k + 7 * NT < K; k += 8 * NT) {
     float a[8], b[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      const uint64_t kk = (uint64_t)(k + u * 64);
+      const uint64_t kk = (uint64_t)(k + u * NT);
       a[u] = ta ? A[kk * M + i] : A[(uint64_t)i * K + kk];
       b[u] = tb ? B[(uint64_t)j * K + kk] : B[kk * N + j];
     }
 #pragma unroll
     for (int u = 0; u < 8; u++) acc = fmaf(a[u], b[u], acc);
   }
-  for (; k < K; k += 64) {
+  for (; k < K; k += NT) {
     const float a = ta ? A[(uint64_t)k * M + i] : A[(uint64_t)i * K + k];
     const float b = tb ? B[(uint64_t)j * K + k] : B[(uint64_t)k * N + j];
     acc = fmaf(a, b, acc);
   }
   acc = rg_wave_sum(acc);
-  if (lane == 0) C[e] = acc;
+  if (W == 1) {
+    if (lane == 0) C[e] = acc;
+    return;
+  }
+  if (lane == 0) wsum[w] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = wsum[0];
+#pragma unroll
+    for (int q = 1; q < W; q++) t += wsum[q];
+    C[e] = t;
+  }
 }
 
 enum SkinnyKind { SKINNY_NONE = 0, SKINNY_ROWS, SKINNY_DOT, SKINNY_OUTER, SKINNY_TINY };
@@ -790,7 +805,14 @@ bool gemm_skinny(hipStream_t s, const GemmArgs& g, const Skinny& sk) {
   const int M = (int)sk.m, N = (int)sk.n, K = (int)sk.k;
   const SkinnyKind kind = sk.kind;
   if (kind == SKINNY_TINY) {
-    hipLaunchKernelGGL(k_gemm_tiny_out, dim3((uint32_t)((M * N + 3) / 4)), dim3(256), 0, s, A, B, C, M, N, K, g.ta, g.tb);
+    // Waves per output: enough that each thread's share of K is one batch of eight loads.
+    const dim3 grid((uint32_t)(M * N));
+    const int w = std::min(16, std::max(1, (K + 511) / 512));
+    if (w <= 1) hipLaunchKernelGGL(k_gemm_tiny_out<1>, grid, dim3(64), 0, s, A, B, C, M, N, K, g.ta, g.tb);
+    else if (w <= 2) hipLaunchKernelGGL(k_gemm_tiny_out<2>, grid, dim3(128), 0, s, A, B, C, M, N, K, g.ta, g.tb);
+    else if (w <= 4) hipLaunchKernelGGL(k_gemm_tiny_out<4>, grid, dim3(256), 0, s, A, B, C, M, N, K, g.ta, g.tb);
+    else if (w <= 8) hipLaunchKernelGGL(k_gemm_tiny_out<8>, grid, dim3(512), 0, s, A, B, C, M, N, K, g.ta, g.tb);
+    else hipLaunchKernelGGL(k_gemm_tiny_out<16>, grid, dim3(1024), 0, s, A, B, C, M, N, K, g.ta, g.tb);
     return true;
   }
   if (kind == SKINNY_OUTER) {
