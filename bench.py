@@ -109,10 +109,12 @@ def time_classes(compiled, inputs, classes, repeats, trials=7):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_hbm_traffic.txt")
 
 
-def measured_traffic(kernel_class):
+def measured_traffic(workload, kernel_class):
     """HBM bytes per launch of `kernel_class`, from the counter summary committed under profiles/
-    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script, scaled by the copy-kernel
-    calibration recorded in the same file), or None when no measurement exists."""
+    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script on C4, scaled by the copy-kernel
+    calibration recorded in the same file), or None when no measurement exists (any other workload)."""
+    if workload != "C4":
+        return None
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
@@ -162,7 +164,7 @@ def cpu_baseline(cfg, sample_batch=4, steps=3):
                       f"steps/s scaled by {sample.batch}/{cfg.batch}; OpenMP threads where the reference uses rayon"}
 
 
-def roofline_of(compiled, inputs, reps):
+def roofline_of(compiled, inputs, reps, workload):
     """(roofline dict, per-class table, device seconds per pass) from each kernel class's device
     time inside the replayed pass (time_classes)."""
     classes = classify(compiled.plan_summary())
@@ -177,7 +179,7 @@ def roofline_of(compiled, inputs, reps):
     else:
         roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4)}
-    roof["traffic"] = measured_traffic(dom_name)
+    roof["traffic"] = measured_traffic(workload, dom_name)
     roof.update({"kernel": dom_name, "launches_per_step": dom["launches"], "algorithmic_per_launch": round(per_launch),
                  "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]), "avg_launch_us": round(avg_s * 1e6, 2)})
     kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
@@ -201,7 +203,7 @@ def bench_program(args, rg, workloads):
     sec = sorted(seconds)[len(seconds) // 2]
     value = passes / sec
     print(f"# C5: {passes} passes in {sec * 1e3:.3f} ms (median of {len(seconds)})", file=sys.stderr, flush=True)
-    roof, kernels, total_s = roofline_of(compiled, natives, max(1, args.timing_reps))
+    roof, kernels, total_s = roofline_of(compiled, natives, max(1, args.timing_reps), "C5")
     n, k = 4096, 8
     # The reordered plan reads B once and C twice (A@B, then (A@B)@C and the gradient through C)
     # and writes dB and dC: five n x n fp32 matrices; the k-wide operands are noise beside them.
@@ -280,7 +282,7 @@ def main():
     roof, kernels, total_s = None, None, None
     if args.timing_reps > 0:
         inputs = [rg.tensor(x)._t for x in rg.tree.leaves((res.state,))]
-        roof, kernels, total_s = roofline_of(compiled, inputs, args.timing_reps)
+        roof, kernels, total_s = roofline_of(compiled, inputs, args.timing_reps, args.workload)
 
     if args.workload == "C2":
         metric = "train steps/s, MLP 512-2048-2048-1 batch 4096 (C2) on 1 MI355X; % of HBM / fp32-MFMA roofline"

@@ -623,6 +623,10 @@ struct Skinny {
   bool ta = false;
 };
 
+bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
+  return dtype == RG_F32 && m >= 32 && n >= 32 && k >= 8 && m * n * k >= (1u << 18);
+}
+
 // Which skinny kernel a product takes, from shapes and flags alone (alignment is checked at
 // launch; an unaligned operand falls back to the general kernels).
 Skinny skinny_plan(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb) {
@@ -652,7 +656,9 @@ Skinny skinny_plan(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch
     if (sk.kind != SKINNY_NONE) return sk;
     sk = Skinny{};
   }
-  if (m * n <= 16384 && k >= 512) {
+  // Outputs with both sides at least 32 (a tied embedding's gradient, 96 x 128 over 4096 rows)
+  // go to the MFMA tiles, which read both operands in coalesced tiles.
+  if (m * n <= 16384 && k >= 512 && !use_mfma(dtype, m, n, k)) {
     sk = Skinny{};
     sk.kind = SKINNY_TINY;
     sk.m = m;
@@ -677,10 +683,6 @@ int skinny_rows_splits(uint64_t n, uint64_t k) {
   uint64_t want = (256 + blocks - 1) / blocks;
   const uint64_t most = std::max<uint64_t>(1, k / 256);
   return (int)std::max<uint64_t>(1, std::min<uint64_t>(std::min(want, most), 16));
-}
-
-bool use_mfma(int dtype, uint64_t m, uint64_t n, uint64_t k) {
-  return dtype == RG_F32 && m >= 32 && n >= 32 && k >= 8 && m * n * k >= (1u << 18);
 }
 
 struct TileCfg {
