@@ -689,11 +689,14 @@ struct TileCfg {
   int bm, bn, bk, wm, wn, ms = 16;
 };
 
+int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t batch);
+
 // Block tile, from measurements of C4's products on MI355X: 32-wide tiles for outputs 32..96 wide
 // or 32 tall (attention heads, the vocabulary); 128x128 when that still yields two blocks per CU
 // (512), then 128x64 at two blocks per CU; 128x64 with eight waves (two per SIMD) at one block per
 // CU, and for long-K products with at least 32 such tiles (split over K to 256 blocks); 64x128 at
-// one block per CU; else 64x64 (split over K when that leaves the CUs idle).
+// one block per CU; 64x64 (split over K when that leaves the CUs idle); 32x32 when even split
+// 64x64 tiles come to fewer than 256 blocks (C3's products).
 TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
   auto blocks = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
   if (n <= 96 && n % 32 == 0) return {128, 32, 32, 4, 1};
@@ -704,7 +707,11 @@ TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
   if (tb && blocks(128, 64) >= 256) return {64, 64, 32, 2, 2, 32};
   if (blocks(128, 64) >= 256 || (blocks(128, 64) >= 32 && k >= 4096)) return {128, 64, 32, 2, 4};
   if (blocks(64, 128) >= 256) return {64, 128, 32, 2, 2};
-  return {64, 64, 32, 2, 2};
+  // Small outputs: 32x32 tiles when 64x64 ones, split over K where K allows, would leave most
+  // CUs idle (C3's products: 4096 x 128 over K <= 512, 128 x 128 weight gradients).
+  const TileCfg t64 = {64, 64, 32, 2, 2};
+  if (blocks(64, 64) * (uint64_t)split_count(t64, m, n, k, batch) < 256) return {32, 32, 32, 2, 2};
+  return t64;
 }
 
 // K splits for products with too few tiles: about 256 blocks of eight waves or 768 of four, each
@@ -762,6 +769,7 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
   RG_TILE(64, 64, 32, 2, 2);
   RG_TILE(128, 32, 32, 4, 1);
   RG_TILE(32, 128, 32, 1, 4);
+  RG_TILE(32, 32, 32, 2, 2);
 #undef RG_TILE
   if (t.bm == 64 && t.bn == 64 && t.bk == 32 && t.wm == 2 && t.wn == 2 && t.ms == 32) return launch_flags<64, 64, 32, 2, 2, 32>(s, ta, tb, mode, l);
 }

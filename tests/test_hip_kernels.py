@@ -164,7 +164,8 @@ def _swap(g, x, rank):
 
 
 @pytest.mark.parametrize("m,k,n", [(256, 256, 768), (300, 70, 130), (8192, 256, 96), (256, 8192, 768), (64, 64, 64), (33, 17, 65),
-                                   (8192, 1024, 256), (1024, 8192, 256), (8200, 260, 264), (33, 4096, 65)])
+                                   (8192, 1024, 256), (1024, 8192, 256), (8200, 260, 264), (33, 4096, 65),
+                                   (4096, 512, 128), (128, 4096, 384)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
 def test_mfma_products_with_transpose_flags(m, k, n, ta, tb):
     rng = np.random.default_rng(m * 7 + k * 3 + n)
