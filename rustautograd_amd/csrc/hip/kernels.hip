@@ -947,7 +947,9 @@ void fold_jobs(hipStream_t s, const FoldJobs& jobs, uint32_t tiles) {
   if (jobs.n) hipLaunchKernelGGL(k_fold_jobs, dim3(tiles), dim3(1024), 0, s, jobs);
 }
 
-// Eight rows' loads in flight per thread, added in row order (the order of k_split_sum).
+// Up to sixteen rows' loads in flight per thread (a K split has at most 16 partials, so one
+// batch), added in row order (the order of k_split_sum). The last batch's loads are guarded
+// rather than issued one by one, so a short fold waits for one memory latency, not one per row.
 __global__ void __launch_bounds__(256) k_fold_wide(WideFolds jobs) {
   uint32_t j = 0;
   while (j + 1 < jobs.n && blockIdx.x >= jobs.job[j + 1].first_block) j++;
@@ -956,17 +958,14 @@ __global__ void __launch_bounds__(256) k_fold_wide(WideFolds jobs) {
   if (i >= f.n) return;
   const float* p = f.part + i;
   float4 acc = *(const float4*)p;
-  uint32_t r = 1;
-  for (; r + 7 < f.rows; r += 8) {
-    float4 v[8];
+  for (uint32_t r = 1; r < f.rows; r += 15) {
+    float4 v[15];
 #pragma unroll
-    for (int q = 0; q < 8; q++) v[q] = *(const float4*)(p + (uint64_t)(r + q) * f.n);
+    for (uint32_t q = 0; q < 15; q++)
+      if (r + q < f.rows) v[q] = *(const float4*)(p + (uint64_t)(r + q) * f.n);
 #pragma unroll
-    for (int q = 0; q < 8; q++) acc = make_float4(acc.x + v[q].x, acc.y + v[q].y, acc.z + v[q].z, acc.w + v[q].w);
-  }
-  for (; r < f.rows; r++) {
-    const float4 v = *(const float4*)(p + (uint64_t)r * f.n);
-    acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+    for (uint32_t q = 0; q < 15; q++)
+      if (r + q < f.rows) acc = make_float4(acc.x + v[q].x, acc.y + v[q].y, acc.z + v[q].z, acc.w + v[q].w);
   }
   *(float4*)(f.out + i) = acc;
 }

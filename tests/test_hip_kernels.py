@@ -387,7 +387,7 @@ SKINNY = [
     # matrix-vector products (run as their transposes) and tiny outputs with a long K
     (4096, 2048, 1, False, False), (2048, 4096, 1, True, False), (1000, 1000, 1, True, True), (1001, 512, 1, True, False),
     (8, 4096, 8, False, False), (3, 2000, 5, True, True), (16, 600, 16, False, True),
-    (4, 3000, 4, True, False), (2, 9000, 3, False, False), (128, 512, 128, False, True),
+    (4, 3000, 4, True, False), (2, 9000, 3, False, False), (16, 512, 20, False, True), (128, 512, 128, False, True),
     # a tied embedding's gradient (C3's head): MFMA tiles, not the tiny-output kernel
     (96, 4096, 128, True, False),
 ]
