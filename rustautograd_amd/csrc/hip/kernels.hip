@@ -392,6 +392,35 @@ __device__ __forceinline__ bool before(const T* row, uint32_t x, uint32_t y) {
   return x < y;
 }
 
+// The same ranking by value: p at position x ahead of q at position y.
+template <class T>
+__device__ __forceinline__ bool before_v(T p, uint32_t x, T q, uint32_t y) {
+  bool pn = p != p, qn = q != q;
+  if (pn || qn) return pn != qn ? qn : x < y;
+  if (p != q) return p > q;
+  return x < y;
+}
+
+// Rows of at most TOPK_RANK_MAX values: one block per row, the row in LDS, and every position's
+// rank (the number of positions ranking ahead of it) counted in parallel; positions ranked below
+// k are written at their rank. The ranking is a strict total order, so this is the same output
+// as choosing each next position in turn (k_arg_top_k below, for longer rows).
+constexpr uint32_t TOPK_RANK_MAX = 4096;
+template <class T>
+__global__ void __launch_bounds__(256) k_arg_top_k_rank(const T* __restrict__ a, int* __restrict__ d, uint32_t v, uint32_t k) {
+  __shared__ T vals[TOPK_RANK_MAX];
+  const uint64_t r = blockIdx.x;
+  const T* row = a + r * v;
+  for (uint32_t j = threadIdx.x; j < v; j += 256) vals[j] = row[j];
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < v; j += 256) {
+    const T q = vals[j];
+    uint32_t rank = 0;
+    for (uint32_t i = 0; i < v; i++) rank += before_v(vals[i], i, q, j) ? 1u : 0u;
+    if (rank < k) d[r * k + rank] = (int)j;
+  }
+}
+
 template <class T>
 __global__ void __launch_bounds__(TPB) k_arg_top_k(const T* __restrict__ a, int* __restrict__ d, uint32_t rows, uint32_t v, uint32_t k) {
   uint32_t r = blockIdx.x * TPB + threadIdx.x;
@@ -825,6 +854,12 @@ void argmax(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, 
 }
 
 void arg_top_k(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, uint64_t v, uint64_t k) {
+  if (rows == 0 || k == 0) return;
+  if (v <= TOPK_RANK_MAX) {
+    if (dtype == RG_F32) hipLaunchKernelGGL(k_arg_top_k_rank<float>, dim3((uint32_t)rows), dim3(256), 0, s, (const float*)a, d, (uint32_t)v, (uint32_t)k);
+    else hipLaunchKernelGGL(k_arg_top_k_rank<double>, dim3((uint32_t)rows), dim3(256), 0, s, (const double*)a, d, (uint32_t)v, (uint32_t)k);
+    return;
+  }
   if (dtype == RG_F32) RG_LAUNCH(k_arg_top_k<float>, rows, (const float*)a, d, (uint32_t)rows, (uint32_t)v, (uint32_t)k);
   else RG_LAUNCH(k_arg_top_k<double>, rows, (const double*)a, d, (uint32_t)rows, (uint32_t)v, (uint32_t)k);
 }
@@ -931,7 +966,15 @@ __global__ void __launch_bounds__(1024) k_fold_jobs(FoldJobs jobs) {
 #pragma unroll
       for (int q = 0; q < 8; q++) acc = combine(f.kind, acc, v[q]);
     }
-    for (; r < f.rows; r += 16) acc = combine(f.kind, acc, f.part[(uint64_t)r * f.k + c]);
+    if (r < f.rows) {  // the last rows as one guarded batch
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        if (r + q * 16 < f.rows) v[q] = f.part[(uint64_t)(r + q * 16) * f.k + c];
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        if (r + q * 16 < f.rows) acc = combine(f.kind, acc, v[q]);
+    }
   }
   part[ty][tx] = acc;
   __syncthreads();

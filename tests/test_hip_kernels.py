@@ -267,6 +267,17 @@ def test_sort_and_scan_kernels():
     agree(lambda g, i: op(g, "cumsum", [i[0]], reverse=False), [t(np.arange(12).reshape(3, 4), "int32")])
 
 
+@pytest.mark.parametrize("rows,v,k,dtype", [(1, 96, 96, "float32"), (70, 96, 20, "float32"), (5, 300, 300, "float32"),
+                                            (3, 4096, 7, "float64"), (2, 5000, 5, "float32")])
+def test_top_k_and_argsort_rank_rows_like_the_oracle(rows, v, k, dtype):
+    """Rows up to 4096 long rank every position in one block; longer rows choose positions in
+    turn. Ties (a coarse grid of values), NaNs and both ends of k must give the oracle's order."""
+    rng = np.random.default_rng(rows * 31 + v + k)
+    x = np.round(rng.normal(size=(rows, v)) * 4) / 4
+    x[rng.random(size=(rows, v)) < 0.02] = np.nan
+    agree(lambda g, i: op(g, "arg_top_k", [i[0]], k=k), [t(x.astype(dtype), dtype)])
+
+
 def test_float64_programs_run_on_the_device():
     def build(g, i):
         e = op(g, "exp", [i[0]])
