@@ -96,8 +96,10 @@ def time_classes(compiled, inputs, classes, repeats, trials=7):
             diffs.append(f - once(rest))
         in_pass = median(diffs)
         c["isolated_seconds"] = median([once(c["steps"]) for _ in range(trials)])
-        # A class too small to stand out of the pass's run-to-run spread keeps its isolated time.
-        c["timing"] = "in_pass" if in_pass >= 0.5 * c["isolated_seconds"] else "isolated"
+        # A class too small to stand out of the pass's run-to-run spread (its difference of two
+        # passes under half or over twice its time replayed alone) keeps its isolated time.
+        iso = c["isolated_seconds"]
+        c["timing"] = "in_pass" if 0.5 * iso <= in_pass <= 2.0 * iso else "isolated"
         c["seconds"] = in_pass if c["timing"] == "in_pass" else c["isolated_seconds"]
         if c["flops"]:
             c["achieved"], c["unit"] = c["flops"] / c["seconds"] / 1e12, "TFLOP/s"

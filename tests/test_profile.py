@@ -139,7 +139,8 @@ def _hip():
     (4096, 1, 4096, 1, 0, 0, 1),      # a matrix-vector product
     (4096, 1, 4096, 1, 1, 0, 1),      # A^T x
     (4096, 4096, 8, 1, 0, 0, 1),      # a short-K outer product
-    (32, 64, 8192, 1, 0, 0, 1),       # few outputs, long K
+    (16, 20, 8192, 1, 0, 0, 1),       # few outputs, long K: the tiny-output kernel
+    (32, 64, 8192, 1, 0, 0, 0),       # both sides at least 32: matrix cores
     (1024, 1024, 1024, 1, 0, 0, 0),   # a square product: matrix cores
     (8, 4096, 4096, 2, 0, 0, 0),      # batched: matrix cores
     (16, 2048, 1000, 1, 0, 1, 0),     # B^T with K not a multiple of 256
