@@ -69,7 +69,7 @@ def classify(plan):
     return classes
 
 
-def time_classes(compiled, inputs, classes, repeats, trials=7):
+def time_classes(compiled, inputs, classes, repeats, trials=15):
     """Device seconds per pass of each kernel class, measured inside the pass: every plan step
     replayed back to back `repeats` times between two HIP events on the execution stream, minus
     the same replay without the class's steps, timed right after it (rg_hip_exec_time_steps);
