@@ -855,7 +855,12 @@ void argmax(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, 
 
 void arg_top_k(hipStream_t s, int dtype, const void* a, int32_t* d, uint64_t rows, uint64_t v, uint64_t k) {
   if (rows == 0 || k == 0) return;
-  if (v <= TOPK_RANK_MAX) {
+  // Rough latencies in dependent steps: choosing in turn walks k * v cached global reads per row,
+  // every row at once; ranking walks v * ceil(v / 256) LDS reads (about 20 times cheaper), about
+  // 2048 rows (blocks) at a time. Many long rows with a small k stay on the first.
+  const uint64_t turn = ((rows + 65535) / 65536) * k * v;
+  const uint64_t rank = ((rows + 2047) / 2048) * v * ((v + 255) / 256) / 20;
+  if (v <= TOPK_RANK_MAX && rank <= turn) {
     if (dtype == RG_F32) hipLaunchKernelGGL(k_arg_top_k_rank<float>, dim3((uint32_t)rows), dim3(256), 0, s, (const float*)a, d, (uint32_t)v, (uint32_t)k);
     else hipLaunchKernelGGL(k_arg_top_k_rank<double>, dim3((uint32_t)rows), dim3(256), 0, s, (const double*)a, d, (uint32_t)v, (uint32_t)k);
     return;

@@ -268,10 +268,11 @@ def test_sort_and_scan_kernels():
 
 
 @pytest.mark.parametrize("rows,v,k,dtype", [(1, 96, 96, "float32"), (70, 96, 20, "float32"), (5, 300, 300, "float32"),
-                                            (3, 4096, 7, "float64"), (2, 5000, 5, "float32")])
+                                            (3, 4096, 7, "float64"), (2, 5000, 5, "float32"), (4096, 4096, 1, "float32")])
 def test_top_k_and_argsort_rank_rows_like_the_oracle(rows, v, k, dtype):
-    """Rows up to 4096 long rank every position in one block; longer rows choose positions in
-    turn. Ties (a coarse grid of values), NaNs and both ends of k must give the oracle's order."""
+    """Rows up to 4096 long rank every position in one block; longer rows, and many long rows
+    with a small k, choose positions in turn. Ties (a coarse grid of values), NaNs and both ends
+    of k must give the oracle's order."""
     rng = np.random.default_rng(rows * 31 + v + k)
     x = np.round(rng.normal(size=(rows, v)) * 4) / 4
     x[rng.random(size=(rows, v)) < 0.02] = np.nan
