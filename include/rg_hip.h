@@ -131,7 +131,10 @@ int rg_hip_device_peaks(double* peaks, char* name, size_t len);
  * state slots then hold the state after `out->done` steps, as in the host loop. The captured
  * graphs and the loop's device buffers stay with the frame and are reused by the next run with
  * the same description. `out->seconds` is the step loop alone (validate.rs:264-265): batch
- * upload and graph capture are excluded. */
+ * upload and graph capture are excluded. A description whose slot indices, counts, sizes or
+ * pointers do not fit the program (swaps of unequal or shared slots, copies or data larger than
+ * their slots, a missing batch pointer or history buffer) is refused with -1 and a message
+ * before anything is copied or launched. */
 int rg_hip_exec_run(void* exec, const rg_run_desc* desc, rg_run_result* out);
 /* The step loop of rg_hip_exec_run for callers that cannot allocate device memory (code that
  * must not call hipMalloc: tight serving loops, harnesses that forbid it). It has no counterpart
@@ -140,10 +143,12 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* desc, rg_run_result* out);
  * live in a static device array of RG_NOALLOC_SCRATCH_BYTES (32 MiB) that each GPU holds until
  * the process ends, and the steps are launched directly. A run whose buffers would exceed it is
  * refused (-1, message in rg_hip_exec_failure) before anything runs. Results equal
- * rg_hip_exec_run's, bit for bit. With history it waits after every step to check the recorded
- * values. Every call on one GPU shares that GPU's array and leaves its contents behind: calls
- * that overlap on one GPU race. It keeps no snapshot: after a device failure the state slots
- * are unspecified. */
+ * rg_hip_exec_run's, bit for bit, and descriptions are checked as there. With history it waits
+ * after every step to check the recorded values. `out->done` counts the steps a successful
+ * synchronization confirmed: without history that is the final one, so a device failure it
+ * reports gives 0. Every call on one GPU shares that GPU's array and leaves its contents behind;
+ * a per-device lock held for the whole call makes calls that overlap on one GPU take turns. It
+ * keeps no snapshot: after a device failure the state slots are unspecified. */
 int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* desc, rg_run_result* out);
 
 #ifdef __cplusplus

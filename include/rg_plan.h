@@ -127,8 +127,10 @@ enum rg_step_kind { RG_STEP_INSTR = 0, RG_STEP_FUSED = 1, RG_STEP_ROWS = 2, RG_S
 #define RG_ATTN_MAX_T 256
 
 #ifdef __cplusplus
+#include <algorithm>
 #include <cstring>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 namespace rgplan {
@@ -218,6 +220,80 @@ struct Plan {
 };
 
 inline int64_t dtype_size(int32_t d) { return d == RG_F64 ? 8 : 4; }
+
+/* Refuses a plan whose steps name slots it does not have or reach beyond a slot's capacity:
+ * constants, inputs and outputs within their slots; every instruction argument's elements and
+ * its `n` outputs within their slots; fused inputs by their read extent (Full n, Row row_len,
+ * Splat 1, Broadcast the source size) and outputs by what they write; attention views by the
+ * largest offset they touch, the statistics and the mask tables by their sizes. Called by
+ * `parse`, so a backend never launches a kernel on a plan that would index past its buffers. */
+inline void check_refs(const Plan& pl) {
+  const int64_t ns = (int64_t)pl.slots.size();
+  auto fail = [](const std::string& what) { throw std::runtime_error("plan descriptor: " + what); };
+  auto prod_of = [](const std::vector<int64_t>& v) {
+    int64_t n = 1;
+    for (int64_t d : v) {
+      if (d < 0) return (int64_t)-1;
+      n *= d;
+    }
+    return n;
+  };
+  auto fits = [&](int64_t slot, int64_t n, const char* what) {
+    if (slot < 0 || slot >= ns) fail(std::string(what) + " names slot " + std::to_string(slot) + " of " + std::to_string(ns));
+    if (n < 0 || n > pl.slots[(size_t)slot].cap)
+      fail(std::string(what) + " needs " + std::to_string(n) + " values of slot " + std::to_string(slot) + ", which holds " +
+           std::to_string(pl.slots[(size_t)slot].cap));
+  };
+  for (const Slot& s : pl.slots)
+    if ((s.dtype != RG_F32 && s.dtype != RG_F64 && s.dtype != RG_I32) || s.cap < 0) fail("a slot has a bad dtype or capacity");
+  for (const Const& c : pl.consts) {
+    fits(c.slot, c.n, "a constant");
+    if (c.offset < 0) fail("a constant has a negative offset");
+  }
+  for (const auto& in : pl.inputs) fits(in.first, in.second, "an input");
+  for (const Output& o : pl.outputs) {
+    fits(o.slot, o.n, "an output");
+    if (prod_of(o.shape) != o.n) fail("an output's shape does not hold its n values");
+  }
+  for (size_t k = 0; k < pl.steps.size(); k++) {
+    const Step& st = pl.steps[k];
+    const std::string at = "step " + std::to_string(k);
+    if (st.kind == RG_STEP_INSTR) {
+      const Instr& in = st.instr;
+      if (in.dst != -1) fits(in.dst, in.n, (at + " output").c_str());
+      for (const Arg& a : in.args)
+        if (a.slot != -1) fits(a.slot, prod_of(a.shape), (at + " argument").c_str());
+    } else if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
+      const Fused& f = st.fused;
+      const int64_t rows = f.row_len > 0 ? f.n / f.row_len : 0;
+      for (const FusedInput& fi : f.inputs) {
+        int64_t extent = fi.kind == RG_ARG_FULL ? f.n : fi.kind == RG_ARG_ROW ? fi.row_len : fi.kind == RG_ARG_SPLAT ? 1 : prod_of(fi.shape);
+        if (fi.kind < RG_ARG_FULL || fi.kind > RG_ARG_BROADCAST) fail(at + " has an input of unknown kind");
+        fits(fi.slot, extent, (at + " input").c_str());
+      }
+      for (const auto& o : f.outputs)
+        fits(o.second, f.row_len > 0 ? std::min(rows, f.row_len) : f.n, (at + " output").c_str());
+    } else if (st.kind == RG_STEP_ATTN) {
+      const Attn& a = st.attn;
+      const int64_t batch = a.bh / a.heads;
+      auto view = [&](const AttnView& v, int64_t t, const char* what) {
+        if (v.offset < 0 || v.sb < 0 || v.sh < 0 || v.st < 0 || t <= 0 || a.hd <= 0) fail(at + " has a bad " + what + " view");
+        fits(v.slot, v.offset + (batch - 1) * v.sb + (a.heads - 1) * v.sh + (t - 1) * v.st + a.hd, (at + " " + what).c_str());
+      };
+      const int64_t in_t[5] = {a.tq, a.tk, a.tk, a.tq, a.tq}, out_t[3] = {a.tq, a.tk, a.tk};
+      for (size_t j = 0; j < a.in.size(); j++) view(a.in[j], in_t[j], "operand");
+      for (size_t j = 0; j < a.out.size(); j++) view(a.out[j], a.backward ? out_t[j] : a.tq, "result");
+      fits(a.stats_slot, 3 * a.bh * a.tq, (at + " statistics").c_str());
+      if (a.mask_slot != -1) {
+        const int64_t* m = a.mask_strides;
+        if (m[0] < 0 || m[1] < 0 || m[2] < 0 || m[3] < 0) fail(at + " has a negative mask stride");
+        fits(a.mask_slot, (batch - 1) * m[0] + (a.heads - 1) * m[1] + (a.tq - 1) * m[2] + (a.tk - 1) * m[3] + 1, (at + " mask").c_str());
+        const int64_t slices = (m[0] ? batch : 1) * (m[1] ? a.heads : 1);
+        fits(a.mask_bits_slot, slices * (2 * a.tq * a.tk / 32 + a.tq), (at + " mask bits").c_str());
+      }
+    }
+  }
+}
 
 /* Parses the word array; throws std::runtime_error on a malformed descriptor. */
 inline Plan parse(const int64_t* w, size_t nw) {
@@ -368,6 +444,7 @@ inline Plan parse(const int64_t* w, size_t nw) {
     pl.steps.push_back(std::move(st));
   }
   if (p != nw) throw std::runtime_error("plan descriptor has trailing words");
+  check_refs(pl);
   return pl;
 }
 

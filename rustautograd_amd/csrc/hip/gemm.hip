@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <stdexcept>
+#include <string>
 #include <type_traits>
 
 #include "kernels.h"
@@ -814,6 +816,8 @@ bool gemm_skinny(hipStream_t s, const GemmArgs& g, const Skinny& sk) {
   float* C = (float*)g.c;
   const int M = (int)sk.m, N = (int)sk.n, K = (int)sk.k;
   const SkinnyKind kind = sk.kind;
+  if (g.defer_split && (kind == SKINNY_TINY || kind == SKINNY_OUTER))
+    throw std::runtime_error("deferred K-split product on a kernel that does not split K");
   if (kind == SKINNY_TINY) {
     // Waves per output: enough that each thread's share of K is one batch of eight loads.
     const dim3 grid((uint32_t)(M * N));
@@ -849,6 +853,9 @@ bool gemm_skinny(hipStream_t s, const GemmArgs& g, const Skinny& sk) {
   // Both K-split kernels leave split s's partials at [s][M N] of the workspace; the split sum (or
   // the deferred fold_wide) adds them in split order.
   auto sum_splits = [&](const float* part, int splits) {
+    if (g.defer_split && splits != g.planned_splits)
+      throw std::runtime_error("deferred K-split product: " + std::to_string(splits) + " streamed partial products, the fold expects " +
+                               std::to_string(g.planned_splits));
     if (splits > 1 && !g.defer_split) {
       const uint64_t mn = g.m * g.n;
       hipLaunchKernelGGL(k_split_sum, dim3((uint32_t)((mn + 1023) / 1024), 1), dim3(256), 0, s, part, C, mn, splits, (const float*)nullptr, g.n);
@@ -879,16 +886,25 @@ bool gemm_skinny(hipStream_t s, const GemmArgs& g, const Skinny& sk) {
 }
 
 // Plan slots start 256-byte aligned, so a lowered product always meets the skinny kernels'
-// alignment; a K-split skinny product whose partials are deferred to the fold area relies on it.
+// alignment. A product whose K-split partials are deferred to the fold area must leave exactly
+// the planned number of partial products there: a launch that would take another path (the
+// streaming kernel refusing its operands, another split count) throws instead, and the error is
+// latched like any failed launch, rather than letting the fold overwrite C with stale partials.
 void gemm(hipStream_t s, const GemmArgs& g) {
   if (g.m == 0 || g.n == 0 || g.batch == 0) return;
   const Skinny sk = skinny_plan(g.dtype, g.m, g.n, g.k, g.batch, g.ta, g.tb);
-  if (sk.kind != SKINNY_NONE && gemm_skinny(s, g, sk)) return;
+  if (sk.kind != SKINNY_NONE) {
+    if (gemm_skinny(s, g, sk)) return;
+    if (g.defer_split) throw std::runtime_error("deferred K-split product: the streaming kernel refused its operands");
+  }
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
     TileCfg t = pick_tile(g.m, g.n, g.k, g.batch, g.tb);
     int splits = split_count(t, g.m, g.n, g.k, g.batch);
     int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
     splits = (int)((g.k + kps - 1) / kps);
+    if (g.defer_split && splits != g.planned_splits)
+      throw std::runtime_error("deferred K-split product: " + std::to_string(splits) + " partial products, the fold expects " +
+                               std::to_string(g.planned_splits));
     // 16-byte vector loads need 16-byte aligned operand rows: aligned bases, leading dimensions
     // (K, or M / N for the contiguous-column layouts) and batch offsets that are multiples of 4.
     auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -922,6 +938,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     }
     return;
   }
+  if (g.defer_split) throw std::runtime_error("deferred K-split product on the plain kernel, which does not split K");
   dim3 grid((uint32_t)((g.m * g.n + 255) / 256), (uint32_t)g.batch);
   if (g.dtype == RG_F32)
     hipLaunchKernelGGL(k_gemm_plain<float>, grid, dim3(256), 0, s, (const float*)g.a, (const float*)g.b, (float*)g.c, (uint32_t)g.m,

@@ -142,6 +142,7 @@ struct GemmArgs {
   void* workspace;              // split-K partial sums, [batch][splits][M N]
   uint64_t workspace_bytes;
   bool defer_split = false;  // leave the partials for fold_wide instead of summing them into C
+  int planned_splits = 0;    // with defer_split: the split count the fold was sized for
   const void* bias = nullptr;  // f32 only: bias[c] added to column c of the finished product
 };
 // Fused attention (attention.hip) over bh = batch * heads independent (tq x hd, tk x hd)

@@ -17,18 +17,22 @@ static __device__ __align__(256) unsigned char scratch[RG_NOALLOC_SCRATCH_BYTES]
 constexpr int MAX_DEVICES = 64;
 std::mutex g_mu;
 void* g_ptr[MAX_DEVICES] = {};
+// One lock per device, held by a run for its whole call: runs on one GPU share that GPU's array,
+// so they take turns instead of overwriting each other's counter, history and temporaries.
+std::mutex g_run_mu[MAX_DEVICES];
 
 }  // namespace
 
 namespace rgk {
 
-void* noalloc_scratch(std::string* err) {
+void* noalloc_scratch(std::string* err, std::unique_lock<std::mutex>* hold) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
     *err = std::string("no current HIP device for the static scratch: ") + hipGetErrorString(e);
     return nullptr;
   }
+  *hold = std::unique_lock<std::mutex>(g_run_mu[dev]);
   std::lock_guard<std::mutex> lock(g_mu);
   if (!g_ptr[dev]) {
     void* ptr = nullptr;

@@ -273,6 +273,7 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
     prog.folds.push_back(fd);
     prog.fold_bytes += ((uint64_t)splits * mn * sizeof(float) + 255) / 256 * 256;
     base.defer_split = true;
+    base.planned_splits = splits;
     const Program* pp = &prog;
     return [base, as, bs, dst, off, pp](hipStream_t s, void* const* sl, void* wsp) {
       rgk::GemmArgs g = base;
@@ -1258,6 +1259,73 @@ void enqueue_run_step(const Program& p, hipStream_t s, void* ws, const rg_run_de
 }
 
 // The two slot tables a run alternates between: `start`, and `start` with every swap applied.
+// Refuses a run description whose sizes or pointers do not fit this program before anything is
+// copied or launched: every slot index in range; swapped slots pairwise disjoint, of one dtype
+// and capacity; copies within both slots and of one dtype; data inputs within their slots, with
+// a host pointer for every cycled batch; history slots holding at least one value and a history
+// buffer to receive them. An empty string means the description is usable.
+std::string check_run_desc(const Program& p, const rg_run_desc* d) {
+  const int64_t n_slots = (int64_t)p.plan.slots.size();
+  auto slot_ok = [&](int64_t s) { return s >= 0 && s < n_slots; };
+  auto cap = [&](int64_t s) { return p.plan.slots[(size_t)s].cap; };
+  auto dtype = [&](int64_t s) { return p.plan.slots[(size_t)s].dtype; };
+  std::ostringstream why;
+  if (!d) return "no run description";
+  if (d->steps < 0 || d->n_swaps < 0 || d->n_copies < 0 || d->n_data < 0 || d->n_batches < 0 || d->n_history < 0)
+    return "negative count in the run description";
+  if ((d->n_swaps && !d->swaps) || (d->n_copies && !d->copies) || (d->n_data && (!d->data_slots || !d->data_bytes)) ||
+      (d->n_history && !d->history_slots))
+    return "a run description list is missing";
+  std::vector<char> swapped((size_t)n_slots, 0);
+  for (int64_t k = 0; k < d->n_swaps; k++) {
+    int64_t a = d->swaps[2 * k], b = d->swaps[2 * k + 1];
+    if (!slot_ok(a) || !slot_ok(b) || a == b) {
+      why << "swap " << k << " names slots " << a << " and " << b << " of " << n_slots;
+      return why.str();
+    }
+    if (swapped[(size_t)a] || swapped[(size_t)b]) {
+      why << "slot " << (swapped[(size_t)a] ? a : b) << " is in two swaps";
+      return why.str();
+    }
+    swapped[(size_t)a] = swapped[(size_t)b] = 1;
+    if (dtype(a) != dtype(b) || cap(a) != cap(b) || p.slot_bytes[(size_t)a] != p.slot_bytes[(size_t)b]) {
+      why << "swap " << k << ": slots " << a << " and " << b << " differ in dtype or capacity";
+      return why.str();
+    }
+  }
+  for (int64_t c = 0; c < d->n_copies; c++) {
+    int64_t is = d->copies[3 * c], os = d->copies[3 * c + 1], n = d->copies[3 * c + 2];
+    if (!slot_ok(is) || !slot_ok(os) || n < 0 || n > cap(is) || n > cap(os) || dtype(is) != dtype(os)) {
+      why << "copy " << c << " of " << n << " values from slot " << os << " to slot " << is << " does not fit them";
+      return why.str();
+    }
+  }
+  for (int64_t j = 0; j < d->n_data; j++) {
+    int64_t s = d->data_slots[j];
+    if (!slot_ok(s) || d->data_bytes[j] > (uint64_t)cap(s) * (uint64_t)esize(dtype(s))) {
+      why << "data input " << j << " (" << d->data_bytes[j] << " bytes) does not fit slot " << s;
+      return why.str();
+    }
+    if (d->n_batches > 1) {
+      if (!d->batches) return "cycled batches without batch pointers";
+      for (int64_t b = 0; b < d->n_batches; b++)
+        if (d->data_bytes[j] && !d->batches[b * d->n_data + j]) {
+          why << "batch " << b << " has no host pointer for data input " << j;
+          return why.str();
+        }
+    }
+  }
+  for (int64_t h = 0; h < d->n_history; h++) {
+    int64_t s = d->history_slots[h];
+    if (!slot_ok(s) || cap(s) < 1) {
+      why << "history slot " << s << " holds no value";
+      return why.str();
+    }
+  }
+  if (d->n_history && d->steps && !d->history) return "history slots without a history buffer";
+  return "";
+}
+
 void run_tables(const std::vector<void*>& start, const rg_run_desc* d, std::vector<void*> out[2]) {
   out[0] = start;
   out[1] = start;
@@ -1580,6 +1648,11 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
   out->nonfinite_step = -1;
   out->seconds = 0;
   if (!e->failure.empty()) return -1;
+  const std::string bad_desc = check_run_desc(*p, d);
+  if (!bad_desc.empty()) {
+    e->failure = "rg_hip_exec_run: " + bad_desc;
+    return -1;
+  }
   const int64_t fail_at = p->fail_in.exchange(-1);  // step index of an injected failure, or -1
   RunCache& rc = f->run;
   int result = 0;
@@ -1629,7 +1702,15 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
     if (use_graphs && rc.execs.empty()) {
       for (int g = 0; g < n_graphs; g++) {
         HIP_OK(hipStreamBeginCapture(f->stream, hipStreamCaptureModeThreadLocal));
-        enqueue_step(g);
+        try {
+          enqueue_step(g);
+        } catch (...) {
+          // End the capture before reporting, so the stream is usable again.
+          hipGraph_t partial = nullptr;
+          if (hipStreamEndCapture(f->stream, &partial) == hipSuccess && partial) hipGraphDestroy(partial);
+          hipGetLastError();
+          throw;
+        }
         hipGraph_t graph;
         hipError_t ce = hipStreamEndCapture(f->stream, &graph);
         if (ce != hipSuccess) throw std::runtime_error("graph capture failed: " + err_str(ce));
@@ -1724,7 +1805,10 @@ int rg_hip_exec_run(void* exec, const rg_run_desc* d, rg_run_result* out) {
 // batches and copy temporaries live in the static scratch array (noalloc.hip); the steps are
 // launched directly (no graph is instantiated) and no snapshot is kept. With history, the loop
 // waits after every step and reads the recorded values, so it stops exactly after the first
-// step (and its handoff) that recorded a non-finite value, as rg_hip_exec_run does.
+// step (and its handoff) that recorded a non-finite value, as rg_hip_exec_run does. A step
+// counts as done only once a synchronization after it succeeded: without history that is the
+// final one, so a device failure it reports leaves `done` at 0. The device's run lock is held for the
+// whole call: overlapping calls on one GPU take turns.
 int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* d, rg_run_result* out) {
   auto* e = (Exec*)exec;
   Program* p = e->prog;
@@ -1733,9 +1817,15 @@ int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* d, rg_run_result* out
   out->nonfinite_step = -1;
   out->seconds = 0;
   if (!e->failure.empty()) return -1;
+  const std::string bad_desc = check_run_desc(*p, d);
+  if (!bad_desc.empty()) {
+    e->failure = "rg_hip_exec_run_noalloc: " + bad_desc;
+    return -1;
+  }
   const int64_t fail_at = p->fail_in.exchange(-1);
   std::string why;
-  void* base = rgk::noalloc_scratch(&why);
+  std::unique_lock<std::mutex> hold;
+  void* base = rgk::noalloc_scratch(&why, &hold);
   if (!base) {
     e->failure = "rg_hip_exec_run_noalloc: " + why;
     return -1;
@@ -1752,7 +1842,7 @@ int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* d, rg_run_result* out
   std::vector<void*> table[2];
   run_tables(f->slot, d, table);
   int result = 0;
-  int64_t done = 0;
+  int64_t enqueued = 0, done = 0;
   try {
     upload_batches(d, b, f->stream);
     rgk::set_counter(f->stream, b.counter, 0);
@@ -1770,10 +1860,8 @@ int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* d, rg_run_result* out
         result = -1;
         break;
       }
-      if (d->n_history == 0) {
-        done = k + 1;
-        continue;
-      }
+      enqueued = k + 1;
+      if (d->n_history == 0) continue;
       // On the frame's stream: it does not synchronize with the null stream a plain hipMemcpy uses.
       if (latch(e, hipMemcpyAsync(hbuf.data(), b.hist, (size_t)d->n_history * 8, hipMemcpyDeviceToHost, f->stream), "history read") ||
           latch(e, hipStreamSynchronize(f->stream), "device execution")) {
@@ -1791,14 +1879,17 @@ int rg_hip_exec_run_noalloc(void* exec, const rg_run_desc* d, rg_run_result* out
         break;
       }
     }
+    // Without history, the steps launched are complete once this synchronization succeeds.
     if (latch(e, hipStreamSynchronize(f->stream), "device execution")) result = -1;
+    else if (d->n_history == 0) done = enqueued;
     out->seconds = now() - t0;
   } catch (std::exception& ex) {
     if (e->failure.empty()) e->failure = ex.what();
     result = -1;
   }
   out->done = done;
-  f->slot = table[(size_t)(done % n_tables)];
+  // The frame's table follows every handoff enqueued; after a failure the state is unspecified.
+  f->slot = table[(size_t)(enqueued % n_tables)];
   hipStreamSynchronize(f->stream);
   return result;
 }

@@ -54,15 +54,30 @@ def mlp_train_step(cfg=MLPConfig()):
     def loss_fn(p, x, t):
         return nn.mse_loss(model(p, x), t)
 
+    def batch(key):
+        x = random.normal(key, (cfg.batch, cfg.d_in))
+        return x, rg.sin(x[:, :16]).sum(axis=1, keepdims=True)
+
+    def loss_and_grads(state):
+        _, k_x = random.split(state["key"])
+        return rg.value_and_grad(loss_fn)(state["params"], *batch(k_x))
+
     def step(state):
         k_next, k_x = random.split(state["key"])
-        x = random.normal(k_x, (cfg.batch, cfg.d_in))
-        target = rg.sin(x[:, :16]).sum(axis=1, keepdims=True)
-        value, grads = rg.value_and_grad(loss_fn)(state["params"], x, target)
+        value, grads = rg.value_and_grad(loss_fn)(state["params"], *batch(k_x))
         p, o = opt.update(grads, state["opt"], state["params"])
         return {"params": p, "opt": o, "key": k_next}, value
 
+    _describe(step, loss_and_grads, cfg.lr, cfg.weight_decay)
     return step, dict(params=params, opt=opt.init(params), key=random.key(1))
+
+
+def _describe(step, loss_and_grads, lr, weight_decay):
+    """Attaches to a training step the program of its first half, `loss_and_grads(state) ->
+    (loss, gradient tree)` with the same draws, and its AdamW settings, for tests that compare
+    a step's gradients and updates on their own."""
+    step.loss_and_grads = loss_and_grads
+    step.adamw = {"lr": lr, "weight_decay": weight_decay, "b1": 0.9, "b2": 0.999, "eps": 1e-8}
 
 
 # ---- C3 / C4: character-level GPT -------------------------------------------------------------
@@ -132,14 +147,21 @@ def gpt_train_step(cfg):
     def loss_fn(p, x, y):
         return nn.cross_entropy(model(p, x), y)
 
+    def batch(key):
+        ids = random.randint(key, (cfg.batch, cfg.block + 1), 0, cfg.vocab)
+        return ids[:, :-1], ids[:, 1:]
+
+    def loss_and_grads(state):
+        _, k_ids = random.split(state["key"])
+        return rg.value_and_grad(loss_fn)(state["params"], *batch(k_ids))
+
     def step(state):
         k_next, k_ids = random.split(state["key"])
-        ids = random.randint(k_ids, (cfg.batch, cfg.block + 1), 0, cfg.vocab)
-        x, y = ids[:, :-1], ids[:, 1:]
-        value, grads = rg.value_and_grad(loss_fn)(state["params"], x, y)
+        value, grads = rg.value_and_grad(loss_fn)(state["params"], *batch(k_ids))
         p, o = opt.update(grads, state["opt"], state["params"])
         return {"params": p, "opt": o, "key": k_next}, value
 
+    _describe(step, loss_and_grads, cfg.lr, 0.01)
     return step, dict(params=params, opt=opt.init(params), key=random.key(1))
 
 
@@ -173,58 +195,101 @@ def matrix_chain(n=4096, k=8, seed=0):
     return program, tuple(rg.tensor(x) for x in (a, b, c, d))
 
 
-# ---- generation: the inference-side caller of the same run loop --------------------------------
+# ---- token streams and generation: callers of the same run loop -------------------------------
+
+class TokenWindows:
+    """Training windows cut from one long 1-D token tensor inside the compiled step.
+
+    A draw picks `batch` start offsets uniformly in [0, n - block - 1) (`random.randint`) and
+    gathers the `block + 1` consecutive ids at each: the first `block` are the inputs, the same
+    span shifted by one the next-token targets. The reference draws its windows this way
+    (examples/gpt.py:50-55); its published GPT losses (benches/results_gpt.json) depend on it."""
+
+    def __init__(self, batch, block):
+        self.batch, self.block = batch, block
+
+    def positions(self, starts):
+        """[batch, block + 1] token positions: every start plus 0, 1, ..., block."""
+        return starts.reshape(self.batch, 1) + rg.arange(self.block + 1)
+
+    def __call__(self, tokens, key):
+        last_start = tokens.shape[0] - self.block - 1
+        span = rg.take(tokens, self.positions(random.randint(key, (self.batch,), 0, last_start)))
+        return span[:, :self.block], span[:, 1:]
+
 
 def windows(tokens, key, batch, block):
-    """`batch` random windows of `block + 1` consecutive tokens: inputs and next-token targets
-    (the reference's examples/gpt.py:50-55), drawn on the device from `key`."""
-    n = tokens.shape[0]
-    start = random.randint(key, (batch,), 0, n - block - 1)
-    w = rg.take(tokens, start[:, None] + rg.arange(block + 1))
-    return w[:, :-1], w[:, 1:]
+    """(inputs, targets) of one `TokenWindows(batch, block)` draw."""
+    return TokenWindows(batch, block)(tokens, key)
 
 
 def window_train_step(model, opt, batch):
-    """A training step over random windows of a token tensor passed as data: `step(state, tokens)`."""
-
-    def loss_fn(params, x, y):
-        return nn.cross_entropy(model(params, x), y)
+    """`step(state, tokens)`: one optimizer step on a fresh draw of windows from `tokens`, the
+    token tensor `rg.run` passes as data. The state key is split three ways, as the reference's
+    training step does (examples/gpt.py:58-68): the key carried to the next step, the window
+    draw's key, and the model's dropout key, which this dropout-free GPT does not spend."""
+    draw = TokenWindows(batch, model.block)
+    loss_and_grads = rg.value_and_grad(lambda params, inputs, targets: nn.cross_entropy(model(params, inputs), targets))
 
     def step(state, tokens):
-        k_next, k_win, _ = random.split(state["key"], 3)
-        x, y = windows(tokens, k_win, batch, model.block)
-        value, grads = rg.value_and_grad(loss_fn)(state["params"], x, y)
-        params, opt_state = opt.update(grads, state["opt"], state["params"])
-        return {"params": params, "opt": opt_state, "key": k_next}, value
+        carried, for_windows, _for_dropout = random.split(state["key"], 3)
+        loss, grads = loss_and_grads(state["params"], *draw(tokens, for_windows))
+        new_params, new_opt = opt.update(grads, state["opt"], state["params"])
+        return {"params": new_params, "opt": new_opt, "key": carried}, loss
 
     return step
 
 
-def compile_sampler(model, params, temperature=1.0, top_k=None, top_p=None, device=None):
-    """A compiled step that appends one sampled token to a fixed-length context (the reference's
-    examples/gpt.py:71-86): the model's last-position logits, scaled by 1/temperature, optionally
-    filtered to the top k or the nucleus p, drawn by the Gumbel-max trick; the context shifts left
-    by one. `rg.run(sampler, state, steps=n)` then generates n tokens with no Python per token."""
+def prompt_state(prompt_ids, block, seed=0):
+    """A sampler state for a prompt: the context holds the prompt's last `block` ids, left-padded
+    with its first id when it is shorter, and the key is `random.key(seed)`."""
+    ids = list(prompt_ids)[-block:]
+    ids = [ids[0]] * (block - len(ids)) + ids
+    return {"ctx": rg.tensor([ids], "int32"), "key": random.key(seed)}
 
-    def step(state):
-        k_next, k_draw = random.split(state["key"])
-        logits = model(params, state["ctx"])[:, -1, :] / temperature
+
+class Sampler:
+    """Autoregressive generation as a compiled one-token step.
+
+    The state is a fixed-length context of ids and a key. A step scores the context, divides the
+    logits of its last position by `temperature`, applies the optional top-k and nucleus
+    filters, draws one id by the Gumbel-max trick (`random.categorical`) and slides the context
+    left by one position to append the id, which is also the step's aux output. `rg.run(...,
+    steps=n)` thus generates n ids with no Python between them. Behaviour of the reference's
+    examples/gpt.py:71-93."""
+
+    def __init__(self, model, params, temperature=1.0, top_k=None, top_p=None, device=None):
+        self.model, self.params, self.block, self.temperature = model, params, model.block, temperature
+        self.filters = []
         if top_k:
-            logits = nn.top_k_logits(logits, top_k)
+            self.filters.append(lambda z: nn.top_k_logits(z, top_k))
         if top_p:
-            logits = nn.top_p_logits(logits, top_p)
-        token = random.categorical(k_draw, logits)
-        ctx = rg.concatenate([state["ctx"][:, 1:], token[:, None]], axis=1)
-        return {"ctx": ctx, "key": k_next}, token[0]
+            self.filters.append(lambda z: nn.top_p_logits(z, top_p))
+        self.program = rg.compile(self.advance, (prompt_state([0], self.block),), validate="basic", device=device)
 
-    start = {"ctx": rg.zeros((1, model.block), "int32"), "key": random.key(0)}
-    return rg.compile(step, (start,), validate="basic", device=device)
+    def next_logits(self, context):
+        scores = self.model(self.params, context)[:, -1, :] / self.temperature
+        for keep in self.filters:
+            scores = keep(scores)
+        return scores
+
+    def advance(self, state):
+        carried, for_draw = random.split(state["key"])
+        picked = random.categorical(for_draw, self.next_logits(state["ctx"]))
+        shifted = rg.concatenate([state["ctx"][:, 1:], picked.reshape(1, 1)], axis=1)
+        return {"ctx": shifted, "key": carried}, picked[0]
+
+    def generate(self, prompt_ids, n, seed=0):
+        """`n` ids continuing `prompt_ids`, one device step each."""
+        return generate(self.program, self.block, prompt_ids, n, seed)
+
+
+def compile_sampler(model, params, temperature=1.0, top_k=None, top_p=None, device=None):
+    """The compiled one-token step of a `Sampler` (what `generate` runs)."""
+    return Sampler(model, params, temperature, top_k, top_p, device).program
 
 
 def generate(sampler, block, prompt_ids, n, seed=0):
-    """`n` token ids continuing `prompt_ids`. The context is fixed at `block` ids: the prompt is
-    left-padded with its first id (or cut to its last `block` ids)."""
-    ids = ([prompt_ids[0]] * block + list(prompt_ids))[-block:]
-    state = {"ctx": rg.tensor([ids], "int32"), "key": random.key(seed)}
-    out = rg.run(sampler, state, steps=n)
+    """`n` ids continuing `prompt_ids` from a compiled sampler step over a `block`-id context."""
+    out = rg.run(sampler, prompt_state(prompt_ids, block, seed), steps=n)
     return [int(t) for t in out.history["aux"]]

@@ -62,6 +62,64 @@ def close(got, want, tol, what=""):
         raise AssertionError(f"{what}[{j}]: hip {got.ravel()[j]!r} cpu {want.ravel()[j]!r} (tol {tol} x {scale})")
 
 
+def close_rel(got, want, tol, what=""):
+    """|got - want| <= tol * max|want| elementwise: relative to the array's own largest magnitude
+    (validate.rs:686-693 scales its device check the same way), so values well below 1 are not
+    compared absolutely. An all-zero `want` needs `got` equal to it. Returns the largest
+    difference in units of max|want|."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"{what}: NaN positions differ"
+    finite = np.isfinite(want)
+    scale = float(np.abs(want[finite]).max()) if finite.any() else 0.0
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    diff = np.where(same, 0.0, np.abs(got - want))
+    ok = diff <= tol * scale
+    if not ok.all():
+        j = int(np.argmax(~ok.ravel()))
+        raise AssertionError(f"{what}[{j}]: hip {got.ravel()[j]!r} cpu {want.ravel()[j]!r} "
+                             f"(tol {tol} x max|cpu| {scale:.3e}; worst {diff.max() / max(scale, 1e-300):.2e})")
+    return float(diff.max() / scale) if scale > 0 else 0.0
+
+
+def adamw_direction(mu, nu, count, b1, b2, eps):
+    """AdamW's update direction from first and second moments after `count` steps, in float64
+    (python/rg/optim.py:378-390 order): (mu / (1 - b1^t)) / (sqrt(nu / (1 - b2^t)) + eps)."""
+    mu, nu = np.asarray(mu, np.float64), np.asarray(nu, np.float64)
+    return (mu / (1.0 - b1 ** count)) / (np.sqrt(nu / (1.0 - b2 ** count)) + eps)
+
+
+def updates_agree(old, hip, cpu, tol, what, adamw):
+    """A parameter's update (new - old) on the device against the oracle's.
+
+    `hip` and `cpu` are (new parameter, mu, nu, count) of one AdamW step from the same `old`
+    parameter. AdamW divides each moment by the root of the second moment, so where a gradient
+    element is near zero, rounding-level moment differences (checked separately, relative to
+    each leaf's largest moment) become update differences up to the learning rate. The check
+    therefore takes out what the two sides' own moments explain, computed in float64:
+    |(dhip - dcpu) - lr (dir(cpu moments) - dir(hip moments))| <= tol * max|dcpu| + 2 ulp(new),
+    the 2 ulp because new - old is formed from f32 values on both sides. A wrong update rule,
+    bias correction or decay on either side fails it. Returns the worst residual beyond the 2 ulp
+    allowance, in units of max|dcpu|."""
+    p0 = np.asarray(old, np.float64)
+    (p1, m1, v1, t1), (p2, m2, v2, t2) = hip, cpu
+    assert float(t1) == float(t2), (what, t1, t2)
+    d1, d2 = np.asarray(p1, np.float64) - p0, np.asarray(p2, np.float64) - p0
+    lr = adamw["lr"]
+    explained = lr * (adamw_direction(m2, v2, float(t2), adamw["b1"], adamw["b2"], adamw["eps"])
+                      - adamw_direction(m1, v1, float(t1), adamw["b1"], adamw["b2"], adamw["eps"]))
+    residual = np.abs((d1 - d2) - explained)
+    scale = float(np.abs(d2).max())
+    ulp = np.spacing(np.abs(np.asarray(p2, np.float32))).astype(np.float64)
+    ok = residual <= tol * scale + 2.0 * ulp
+    if not ok.all():
+        j = int(np.argmax(~ok.ravel()))
+        raise AssertionError(f"{what} update[{j}]: hip {d1.ravel()[j]!r} cpu {d2.ravel()[j]!r} explained "
+                             f"{explained.ravel()[j]!r} (tol {tol} x max|dcpu| {scale:.3e})")
+    return float(np.maximum(residual - 2.0 * ulp, 0.0).max() / scale) if scale > 0 else 0.0
+
+
 def agree(build, inputs, tol=2e-6, what="", ulps=None):
     """Runs `build` on the HIP device and on the CPU oracle and compares every output."""
     hip = run_graph("hip", build, inputs)

@@ -171,3 +171,34 @@ print(json.dumps([check["status"], [d["code"] for d in c.report["diagnostics"]],
     assert out.returncode == 0, out.stderr
     status, codes, overall = json.loads(out.stdout.strip().splitlines()[-1])
     assert status == "skipped" and codes == ["DEVICE_CHECK_SKIPPED"] and overall == "warning"
+
+
+def test_plans_reaching_past_their_slots_are_refused_by_both_backends():
+    """The shared parser checks every slot reference and extent (rg_plan.h `check_refs`): a plan
+    whose slots are too small for its steps, or whose output names a slot it does not have, is
+    refused by the HIP library and by the oracle before any buffer is touched."""
+    g = G()
+    x = g.input((64, 300), "float32")
+    y = g.sum_all(g.un("exp", g.un("tanh", x)))
+    words, blob = _rg.plan_words(g.g, [y, g.grad(y, [x])[0]], "hip", "standard")
+    assert _compile_check(list(words))[0] >= 1
+    n_slots = words[2]
+    shrunk = list(words)
+    for s in range(n_slots):
+        shrunk[3 + 3 * s + 1] = 1  # every slot's capacity down to one value
+    misnamed = list(words)
+    k = 3 + 3 * n_slots
+    k += 1 + 3 * misnamed[k]  # constants
+    k += 1 + 2 * misnamed[k]  # inputs
+    misnamed[k + 1] = n_slots + 5  # the first output's slot
+    oracle = ctypes.CDLL(os.path.join(ROOT, "oracle", "_build", "librg_cpu.so"))
+    oracle.rg_cpu_program_new.restype = ctypes.c_void_p
+    oracle.rg_cpu_program_new.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t,
+                                          ctypes.c_char_p, ctypes.c_size_t]
+    for bad in (shrunk, misnamed):
+        n, err = _compile_check(bad)
+        assert n == -1 and "plan descriptor:" in err, (n, err)
+        arr = (ctypes.c_int64 * len(bad))(*bad)
+        msg = ctypes.create_string_buffer(4096)
+        assert not oracle.rg_cpu_program_new(arr, len(bad), blob, len(blob), msg, len(msg))
+        assert b"plan descriptor:" in msg.value, msg.value
