@@ -233,10 +233,13 @@ Simplified simplify(const Graph& g, const std::vector<uint32_t>& outputs, bool d
       Shape shape = ng.shape(ins[0]);
       if (device && shape.size() >= 2 && op.v.size() == shape.size() && node.n() == 1 &&
           ng.nodes[ins[0]].n() >= SPLIT_SUM_MIN && shape.back() > 1) {
+        // With keepdims the row sums keep their axis, so the result has the original rank. The
+        // reference drops it here (optimize.rs:372-375): a keepdims full sum then comes out one
+        // rank short, and a later full sum of it fails shape inference. The values are the same.
         Op rows = Op::make(RG_OP_REDUCE);
         rows.rk = RK::Sum;
         rows.v = {shape.size() - 1};
-        rows.keepdims = false;
+        rows.keepdims = op.keepdims;
         uint32_t rid = ng.add(rows, {ins[0]});
         backward.resize(ng.nodes.size(), false);
         backward[rid] = node.origin >= 0;

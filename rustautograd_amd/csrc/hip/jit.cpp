@@ -395,10 +395,10 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
     if (col_reg[(size_t)m.reg]) {  // fold this row into the lane's column accumulators
       std::string is_row;
       std::string a = operand(m.args[0], false, &is_row);
-      if (is_row == "1") throw std::runtime_error("column reduction of a row-level value");
       for (int64_t e = 0; e < E; e++) {
         std::string acc = "c" + std::to_string(m.reg) + "[" + std::to_string(e) + "]";
-        std::string v = a + "[" + std::to_string(e) + "]";
+        // A row-level operand (a per-row or broadcast value) stands at every position of the row.
+        std::string v = is_row == "1" ? a : a + "[" + std::to_string(e) + "]";
         if (exact) s << "  " << acc << " = " << col_comb(m.aux, acc, v) << ";\n";
         else s << "  if (" << valid(e) << ") " << acc << " = " << col_comb(m.aux, acc, v) << ";\n";
       }
@@ -415,7 +415,8 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
       };
       s << "  " << T << " " << rn << " = (" << T << ")" << init << ";\n";
       for (int64_t e = 0; e < E; e++) {
-        std::string v = a + "[" + std::to_string(e) + "]";
+        // A row-level operand (a per-row or broadcast value) stands at every position of the row.
+        std::string v = is_row == "1" ? a : a + "[" + std::to_string(e) + "]";
         if (exact) s << "  " << rn << " = " << comb(rn, v) << ";\n";
         else s << "  if (" << valid(e) << ") " << rn << " = " << comb(rn, v) << ";\n";
       }

@@ -1,6 +1,6 @@
 """Writes tests/golden/loss_curves.json: the CPU oracle's per-step training losses for the
-BASELINE configurations C2 (200 steps), C3 (300 steps) and C4 (the first 100 of its 300 steps),
-and summary statistics of every state leaf after the last of those steps.
+BASELINE configurations C2 (200 steps), C3 (300 steps) and C4 (300 steps), summary statistics
+of every state leaf after the last step, and of every parameter's movement over the run.
 
     python tests/golden/make_loss_curves.py [C2 C3 C4]
 
@@ -8,7 +8,13 @@ The oracle (oracle/cpu_exec.cpp, a restatement of the reference's CPU interprete
 same programs the device tests compile (rustautograd_amd/workloads.py), on the reference's CPU
 plan (Fuse::DEFAULT), with its checker-only row-parallel products, which are bit-identical to
 the reference's serial loop (tests/test_engine.py checks that). The device tests overlay their
-own full runs on these curves. CPU only; takes about half an hour on 8 cores.
+own full runs on these curves. CPU only; takes about an hour on 8 cores (C4 is 8 s a step).
+
+Movement summaries: for each parameter leaf, d = final - initial in float64, its L2 norm and
+its dot products with PROJECTIONS fixed random vectors (`projection(n, k)`, standard normal
+from seed 1000 + k). For a device run with movement d', (d' - d) . r has standard deviation
+|d' - d|, so the projections' differences measure the device's movement error in the L2 norm
+without storing the parameters.
 """
 
 import ctypes
@@ -23,7 +29,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
-STEPS = {"C2": 200, "C3": 300, "C4": 100}
+STEPS = {"C2": 200, "C3": 300, "C4": 300}
+PROJECTIONS = 4
 OUT = os.path.join(HERE, "loss_curves.json")
 
 
@@ -47,6 +54,30 @@ def leaf_stats(state):
     return stats
 
 
+def projection(n, k):
+    """The k-th fixed random vector of length n the movement summaries project onto."""
+    return np.random.default_rng(1000 + k).standard_normal(n)
+
+
+def _split_key_bias(name, v):
+    if name.endswith("attn.qkv.b"):
+        return [(f"{name}[{part}]", third) for part, third in zip("qkv", np.split(v, 3))]
+    return [(name, v)]
+
+
+def movement_stats(initial, final):
+    """Per parameter leaf (the attention projection bias per third): the L2 norm of final -
+    initial and its projections on the fixed random vectors."""
+    import rustautograd_amd as rg
+    stats = {}
+    for (name, a), (_, b) in zip(rg.tree.paths(initial), rg.tree.paths(final)):
+        d = b.numpy().astype(np.float64).ravel() - a.numpy().astype(np.float64).ravel()
+        for leaf, part in _split_key_bias(name, d):
+            stats[leaf] = {"norm": float(np.linalg.norm(part)),
+                           "proj": [float(part @ projection(part.size, k)) for k in range(PROJECTIONS)]}
+    return stats
+
+
 def main(which):
     import rustautograd_amd as rg
     from rustautograd_amd import _native, workloads
@@ -64,6 +95,7 @@ def main(which):
             "steps": r.steps,
             "loss": [float(x) for x in r.history["aux"]],
             "final_state": leaf_stats(r.state),
+            "movement": movement_stats(state["params"], r.state["params"]),
             "oracle_seconds": round(time.time() - t0, 1),
         }
         print(f"{name}: {r.steps} steps in {time.time() - t0:.0f}s, loss {r.history['aux'][0]:.6f} -> {r.history['aux'][-1]:.6f}",

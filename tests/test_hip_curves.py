@@ -6,9 +6,9 @@ summaries of the final state. Each test runs the whole device loop once (`rg.run
 between steps) and compares every step.
 
 Tolerances:
-- loss, every step: 1e-4 relative. The device sums in other orders (MFMA tiles, split-K, wave
-  reductions), so its losses are not the oracle's bits, but the per-step difference stays
-  orders of magnitude below this over the full runs (the largest seen is printed).
+- loss, every step: 1e-5 relative. The device sums in other orders (MFMA tiles, split-K, wave
+  reductions), so its losses are not the oracle's bits; the largest per-step difference seen
+  over the full runs on an MI355X is 5.2e-7 (C2, C3 and C4 alike; each run prints its own).
 - final state, per leaf: the L2 norm within 1e-3 relative of the oracle's, and the sum within
   1e-3 * sqrt(n) * norm (what a difference of relative norm 1e-3 could move it by). AdamW
   divides each update by the gradient's own running magnitude, so parameters whose gradients
@@ -30,7 +30,7 @@ from rustautograd_amd import workloads
 pytestmark = pytest.mark.gpu
 
 FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "loss_curves.json")
-LOSS_TOL = 1e-4
+LOSS_TOL = 1e-5
 STATE_TOL = 1e-3
 
 

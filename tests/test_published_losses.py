@@ -18,10 +18,11 @@ steps from the initial state; the figure is the loss of the last step.
   so equal bits are not guaranteed. Measured: tiny and small equal bit for bit (run here);
   medium, 12 steps at B32 T128 d256 L6, takes minutes on the oracle and was run once by hand:
   4.858211040496826 against the published 4.858211517333984, one ulp (9.8e-8) apart.
-- The HIP device sums in other orders (matrix-core tiles, split-K, wave reductions), so its
-  losses are within a tolerance, HIP_REL_TOL. For scale, the reference's own Metal backend is
-  2e-7 (tiny) and 8e-7 (small, medium) from its CPU on these figures (results_gpt.json:8-11,
-  45-48, 81-86).
+- The HIP device sums in other orders (matrix-core tiles, split-K, wave reductions), so equal
+  bits are not guaranteed either; it must be within HIP_ULPS f32 ulps (3e-7 relative). Measured
+  on an MI355X: all three equal the published values bit for bit. For scale, the reference's own
+  Metal backend is 2e-7 (tiny) and 8e-7 (small, medium) from its CPU on these figures
+  (results_gpt.json:8-11, 45-48, 81-86).
 - What the pin catches, planted on the oracle (tiny case): drawing the windows from the carried
   key moves the last loss by 3.2e-4 relative, swapping the init keys of the token and position
   tables by 1.6e-5. Both lie far outside the oracle's one-ulp bound (1e-7).
@@ -40,7 +41,7 @@ CASES = {
     "small": (32, 64, 128, 4, 4, 40, 4.858436584472656),   # results_gpt.json:40-44
     "medium": (32, 128, 256, 8, 6, 12, 4.858211517333984),  # results_gpt.json:76-80
 }
-HIP_REL_TOL = 1e-5
+HIP_ULPS = 3
 
 
 def published_run(name, device):
@@ -73,6 +74,6 @@ def test_oracle_reproduces_the_published_cpu_loss(name):
 def test_device_reproduces_the_published_cpu_loss(name):
     print(f"published case {name} on hip", flush=True)
     history, published = published_run(name, "hip")
-    rel = abs(history[-1] - published) / published
-    print(f"{name}: hip last loss {history[-1]!r}, published {published!r}, relative {rel:.2e}", flush=True)
-    assert rel <= HIP_REL_TOL, (history[-1], published)
+    ulps = f32_ulps(history[-1], published)
+    print(f"{name}: hip last loss {history[-1]!r}, published {published!r}, {ulps} ulp apart", flush=True)
+    assert ulps <= HIP_ULPS, (history[-1], published)
