@@ -9,15 +9,19 @@ Tolerances:
 - loss, every step: 1e-5 relative. The device sums in other orders (MFMA tiles, split-K, wave
   reductions), so its losses are not the oracle's bits; the largest per-step difference seen
   over the full runs on an MI355X is 5.2e-7 (C2, C3 and C4 alike; each run prints its own).
-- final state, per leaf: the L2 norm within 1e-3 relative of the oracle's, and the sum within
-  1e-3 * sqrt(n) * norm (what a difference of relative norm 1e-3 could move it by). AdamW
-  divides each update by the gradient's own running magnitude, so parameters whose gradients
-  are tiny drift more than the loss does.
-  The attention projection bias's key third is left out: its true gradient is exactly zero
-  (softmax ignores a per-row shift of the scores), so both sides hold rounding noise that AdamW
-  scales up to the learning rate; its q and v thirds are compared.
+- movement, per parameter leaf: d = final - initial against the fixture's summaries of the
+  oracle's d: its L2 norm within MOVE_TOL relative, and its dot products with PROJECTIONS fixed
+  random vectors within 4.5 * MOVE_TOL * |d_oracle|. For a device movement d', the projection
+  difference (d' - d) . r is normal with deviation |d' - d|, so the projections bound the
+  movement's L2 error without storing the parameters (4.5 deviations: over ~300 leaf and
+  projection pairs a chance failure has probability under 0.3 %). The final state itself is
+  not compared: it is dominated by the initial weights. The attention projection bias's key
+  third is left out: its true gradient is exactly zero (softmax ignores a per-row shift of the
+  scores), so both sides hold rounding noise that AdamW scales up to the learning rate; its q
+  and v thirds are compared.
 """
 
+import importlib.util
 import json
 import os
 
@@ -31,22 +35,20 @@ pytestmark = pytest.mark.gpu
 
 FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "loss_curves.json")
 LOSS_TOL = 1e-5
-STATE_TOL = 1e-3
+MOVE_TOL = 1e-2
+
+
+def _generator():
+    """tests/golden/make_loss_curves.py, for its projection vectors."""
+    spec = importlib.util.spec_from_file_location("make_loss_curves", os.path.join(os.path.dirname(FIXTURE), "make_loss_curves.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
 def _fixture(name):
     with open(FIXTURE) as f:
         return json.load(f)[name]
-
-
-def _summaries(state):
-    out = {}
-    for name, leaf in rg.tree.paths(state):
-        v = leaf.numpy().astype(np.float64)
-        parts = zip("qkv", np.split(v, 3)) if name.endswith("attn.qkv.b") else [(None, v)]
-        for part, x in parts:
-            out[name if part is None else f"{name}[{part}]"] = (x.size, float(x.sum()), float((x * x).sum()))
-    return out
 
 
 @pytest.mark.parametrize("name", ["C2", "C3", "C4"])
@@ -67,15 +69,18 @@ def test_full_length_loss_curve_overlays_the_oracle(name):
           f"(hip {got[worst]!r}, oracle {want[worst]!r}); mean {rel.mean():.3e}", flush=True)
     assert rel.max() <= LOSS_TOL, f"step {worst}: hip {got[worst]} oracle {want[worst]}"
 
-    mine = _summaries(r.state)
-    assert set(mine) == set(fx["final_state"]), set(mine) ^ set(fx["final_state"])
-    for leaf, ref in fx["final_state"].items():
-        if leaf.endswith("attn.qkv.b[k]") or ref["n"] == 0:
+    gen = _generator()
+    mine = gen.movement_stats(state["params"], r.state["params"])
+    assert set(mine) == set(fx["movement"]), set(mine) ^ set(fx["movement"])
+    errors = {}
+    for leaf, ref in fx["movement"].items():
+        if leaf.endswith("attn.qkv.b[k]") or ref["norm"] == 0.0:
             continue
-        n, total, sumsq = mine[leaf]
-        norm_ref = np.sqrt(ref["sumsq"])
-        if norm_ref == 0.0:
-            assert sumsq == 0.0, leaf
-            continue
-        assert abs(np.sqrt(sumsq) - norm_ref) <= STATE_TOL * norm_ref, (leaf, np.sqrt(sumsq), norm_ref)
-        assert abs(total - ref["sum"]) <= STATE_TOL * np.sqrt(n) * norm_ref, (leaf, total, ref["sum"])
+        got_leaf = mine[leaf]
+        norm_err = abs(got_leaf["norm"] - ref["norm"]) / ref["norm"]
+        proj_err = max(abs(a - b) for a, b in zip(got_leaf["proj"], ref["proj"])) / ref["norm"]
+        errors[leaf] = (norm_err, proj_err)
+        assert norm_err <= MOVE_TOL and proj_err <= 4.5 * MOVE_TOL, (leaf, norm_err, proj_err)
+    worst_norm = max(errors.items(), key=lambda kv: kv[1][0])
+    worst_proj = max(errors.items(), key=lambda kv: kv[1][1])
+    print(f"{name}: movement norm worst {worst_norm}, projection worst {worst_proj}", flush=True)
