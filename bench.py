@@ -1,6 +1,6 @@
 """Headline benchmark: train steps/s of the d=256, 6-layer char-GPT on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline | --cpu-full]
 
 One step is one full AdamW training step of the C4 program (B=32, T=256, d=256, 8 heads, 6 layers,
 vocab 96, fp32): ids drawn in the step from the state key, forward, backward, update. The timed
@@ -40,10 +40,11 @@ def classify(plan):
     classes = {}
 
     def add(name, k, st):
-        c = classes.setdefault(name, {"steps": [], "flops": 0.0, "bytes": 0.0, "launches": 0})
+        c = classes.setdefault(name, {"steps": [], "flops": 0.0, "executed_flops": 0.0, "bytes": 0.0, "launches": 0})
         c["steps"].append(k)
         if st["bound"] == "mfma":
             c["flops"] += st["flops"]
+            c["executed_flops"] += st.get("executed_flops", st["flops"])
         c["bytes"] += st["bytes"]
         c["launches"] += 1
 
@@ -142,12 +143,14 @@ def copy_probe(rg):
 
 
 def cpu_baseline(cfg, sample_batch=4, steps=3):
-    """The CPU oracle (a restatement of rg's CPU interpreter) on a bounded sample of the same
-    workload: the same model at `sample_batch` of its sequences, one warm-up step and `steps`
-    timed steps (BASELINE's 1 + 3-5), scaled to the full batch. A full C4 step takes about a
-    minute on the host; its cost is proportional to the tokens in the batch (the products' row
-    counts and attention are per sequence), except the optimizer update, whose fixed cost the
-    scaling counts `batch / sample_batch` times: the estimate errs towards a slower CPU."""
+    """The CPU oracle (a restatement of rg's CPU interpreter) on the same workload: one warm-up
+    step and `steps` timed steps (BASELINE's 1 + 3-5). A full C4 step takes about a minute on the
+    host, so by default the steps run the same model at `sample_batch` of its sequences and the
+    rate is extrapolated to the full batch (`extrapolated` true, the measured sample time beside
+    it): the cost is proportional to the tokens in the batch (the products' row counts and
+    attention are per sequence), except the optimizer update, whose fixed cost the scaling counts
+    `batch / sample_batch` times, so the estimate errs towards a slower CPU. `sample_batch` equal
+    to the batch (bench.py --cpu-full) times the full workload itself."""
     from rustautograd_amd import _native, workloads
     import rustautograd_amd as rg
     import ctypes
@@ -159,11 +162,16 @@ def cpu_baseline(cfg, sample_batch=4, steps=3):
     c = rg.compile(step, (state,), validate="none", device="cpu")
     warm = rg.run(c, state, steps=1)
     r = rg.run(c, warm.state, steps=steps)
+    per_step = r.elapsed / r.steps
     scale = sample.batch / cfg.batch
-    return {"value": r.steps / r.elapsed * scale, "unit": "steps/s", "cores": int(threads), "kind": "port",
-            "sample": f"1 warm-up + {r.steps} timed AdamW steps of the same model at batch {sample.batch} of {cfg.batch} "
-                      f"(T={cfg.block}) on the oracle (oracle/cpu_exec.cpp): {r.elapsed / r.steps:.2f} s per sample step, "
-                      f"steps/s scaled by {sample.batch}/{cfg.batch}; OpenMP threads where the reference uses rayon"}
+    full = sample.batch == cfg.batch
+    how = (f"1 warm-up + {r.steps} timed AdamW steps of the full workload (batch {cfg.batch}, T={cfg.block})" if full else
+           f"1 warm-up + {r.steps} timed AdamW steps of the same model at batch {sample.batch} of {cfg.batch} (T={cfg.block}), "
+           f"steps/s scaled by {sample.batch}/{cfg.batch}")
+    return {"value": 1.0 / per_step * scale, "unit": "steps/s", "cores": int(threads), "kind": "port",
+            "extrapolated": not full, "sample_batch": sample.batch, "sample_seconds_per_step": round(per_step, 3),
+            "sample": f"{how}, on the oracle (oracle/cpu_exec.cpp): {per_step:.2f} s per measured step; OpenMP threads where the "
+                      f"reference uses rayon"}
 
 
 def roofline_of(compiled, inputs, reps, workload):
@@ -188,6 +196,13 @@ def roofline_of(compiled, inputs, reps, workload):
                    "unit": v["unit"], "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4),
                    "isolated_ms_per_step": round(v["isolated_seconds"] * 1e3, 3), "timing": v["timing"]}
                for k, v in sorted(classes.items(), key=lambda kv: -kv[1]["seconds"])}
+    for k, v in classes.items():
+        # Attention skips the tiles a constant mask hides: its rate over the products it executes
+        # beside the rate over all the products of the unfused graph it replaces.
+        if v["flops"] and v["executed_flops"] != v["flops"]:
+            ex = v["executed_flops"] / v["seconds"] / 1e12
+            kernels[k].update({"executed_share": round(v["executed_flops"] / v["flops"], 5), "executed_achieved": round(ex, 2),
+                               "executed_frac": round(ex / FP32_MFMA_PEAK_TFLOPS, 4)})
     return roof, kernels, total_s
 
 
@@ -233,6 +248,8 @@ def main():
     ap.add_argument("--repeats", type=int, default=3, help="timed runs of K steps; the median is reported")
     ap.add_argument("--workload", default="C4", choices=["C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="time the CPU baseline on the full batch (1 warm-up + 3 steps, several minutes) instead of extrapolating")
     ap.add_argument("--timing-reps", type=int, default=5, help="per-step HIP-event timing passes after the timed run (0: skip)")
     ap.add_argument("--probe", choices=["copy"], help="run only a plain copy kernel of known size (for counter calibration)")
     args = ap.parse_args()
@@ -300,7 +317,7 @@ def main():
         config = {"workload": f"{args.workload} char-GPT training step", "batch": cfg.batch, "seq_len": cfg.block, "d_model": cfg.d,
                   "heads": cfg.heads, "layers": cfg.layers, "vocab": cfg.vocab, "optimizer": "adamw", "lr": cfg.lr,
                   "gemm_gflop_per_step": round(workloads.gpt_gemm_flops(cfg) / 1e9, 2)}
-        cpu = None if args.no_cpu_baseline else cpu_baseline(cfg)
+        cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, sample_batch=cfg.batch if args.cpu_full else 4)
     out = {
         "metric": metric,
         "value": round(value, 3),

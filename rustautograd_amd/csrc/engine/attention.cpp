@@ -358,6 +358,116 @@ size_t attn_mask_words(const AttnRegion& r, const Graph& g) {
   return a.mask_slices * (2 * a.tq * a.tk / 32 + a.tq);
 }
 
+// The device kernels work in 16 x 16 tiles of queries and keys. The forward skips a wave's key
+// tile when none of its 16 rows sees a key of it, unless some row sees no key at all; the query
+// pass walks the key tiles from the first to the last any of its rows sees, and the key pass the
+// query tiles from the first to the last any of its keys is seen by, both only when every query
+// row of the problem sees some key. Counted over the mask's distinct slices, as shares of all
+// tiles; the backward's two passes each do two of its four products.
+namespace {
+
+// The value of a node computed from constants by structural operations only (slices, reshapes,
+// broadcasts, transposes, casts), evaluated on the host; false for anything else.
+bool host_value(const Graph& g, uint32_t id, std::vector<double>* out, int depth = 0) {
+  const Node& n = g.nodes[id];
+  const Op& op = n.op;
+  if (depth > 16 || n.n() > (size_t)1 << 24) return false;
+  if (op.kind == RG_OP_CONST) {
+    out->resize(op.t->n());
+    for (size_t i = 0; i < op.t->n(); i++) (*out)[i] = op.t->at(i);
+    return true;
+  }
+  const bool structural = op.kind == RG_OP_RESHAPE || op.kind == RG_OP_STOP_GRADIENT || op.kind == RG_OP_CAST ||
+                          op.kind == RG_OP_SLICE || op.kind == RG_OP_BROADCAST_TO || op.kind == RG_OP_TRANSPOSE;
+  if (!structural || n.inputs.size() != 1) return false;
+  std::vector<double> x;
+  if (!host_value(g, n.inputs[0], &x, depth + 1)) return false;
+  if (op.kind == RG_OP_RESHAPE || op.kind == RG_OP_STOP_GRADIENT || op.kind == RG_OP_CAST) {
+    *out = std::move(x);
+    return true;
+  }
+  const Shape& is = g.shape(n.inputs[0]);
+  const Shape& os = g.shape(id);
+  std::vector<size_t> ist(is.size(), 1);
+  for (size_t d = is.size(); d-- > 1;) ist[d - 1] = ist[d] * is[d];
+  out->assign(n.n(), 0.0);
+  std::vector<size_t> idx(os.size(), 0);
+  for (size_t e = 0; e < n.n(); e++) {
+    size_t rem = e, src = 0;
+    for (size_t d = os.size(); d-- > 0;) {
+      idx[d] = rem % os[d];
+      rem /= os[d];
+    }
+    if (op.kind == RG_OP_SLICE) {
+      for (size_t d = 0; d < os.size(); d++) src += (idx[d] + (size_t)op.v[d]) * ist[d];
+    } else if (op.kind == RG_OP_TRANSPOSE) {
+      for (size_t d = 0; d < os.size(); d++) src += idx[d] * ist[(size_t)op.v[d]];
+    } else {  // broadcast, right-aligned
+      const size_t lead = os.size() - is.size();
+      for (size_t d = 0; d < is.size(); d++) src += (is[d] == 1 ? 0 : idx[lead + d]) * ist[d];
+    }
+    (*out)[e] = x[src];
+  }
+  return true;
+}
+
+}  // namespace
+
+std::pair<double, double> attn_executed_share(const AttnRegion& r, const Graph& g) {
+  std::vector<double> mv;
+  if (r.mask < 0 || !host_value(g, (uint32_t)r.mask, &mv)) return {1.0, 1.0};
+  struct Values {
+    const std::vector<double>& v;
+    double at(size_t i) const { return v[i]; }
+  } m{mv};
+  const AttnShape a = attn_shape(r, g);
+  const int64_t* st = a.mask_strides;
+  const size_t T = 16, nq = (a.tq + T - 1) / T, nk = (a.tk + T - 1) / T;
+  const size_t nb = st[0] ? a.bh / a.heads : 1, nh = st[1] ? a.heads : 1;
+  double fwd = 0, qpass = 0, kpass = 0;
+  for (size_t b = 0; b < nb; b++)
+    for (size_t h = 0; h < nh; h++) {
+      auto seen = [&](size_t q, size_t k) { return m.at((size_t)(b * st[0] + h * st[1] + q * st[2] + k * st[3])) != 0.0; };
+      std::vector<char> row_sees(a.tq, 0);
+      for (size_t q = 0; q < a.tq; q++)
+        for (size_t k = 0; k < a.tk && !row_sees[q]; k++) row_sees[q] = seen(q, k);
+      const bool all_rows = std::all_of(row_sees.begin(), row_sees.end(), [](char c) { return c != 0; });
+      for (size_t qt = 0; qt < nq; qt++) {
+        const size_t q0 = qt * T, q1 = std::min(a.tq, q0 + T);
+        bool wave_rows = true;
+        for (size_t q = q0; q < q1; q++) wave_rows = wave_rows && row_sees[q];
+        size_t lo = nk, hi = 0, live = 0;
+        for (size_t kt = 0; kt < nk; kt++) {
+          bool any = false;
+          for (size_t q = q0; q < q1 && !any; q++)
+            for (size_t k = kt * T; k < std::min(a.tk, kt * T + T) && !any; k++) any = seen(q, k);
+          if (any) {
+            live++;
+            lo = std::min(lo, kt);
+            hi = kt + 1;
+          }
+        }
+        fwd += wave_rows ? (double)live : (double)nk;
+        qpass += all_rows ? (double)(hi > lo ? hi - lo : 0) : (double)nk;
+      }
+      for (size_t kt = 0; kt < nk; kt++) {
+        size_t lo = nq, hi = 0;
+        for (size_t qt = 0; qt < nq; qt++) {
+          bool any = false;
+          for (size_t q = qt * T; q < std::min(a.tq, qt * T + T) && !any; q++)
+            for (size_t k = kt * T; k < std::min(a.tk, kt * T + T) && !any; k++) any = seen(q, k);
+          if (any) {
+            lo = std::min(lo, qt);
+            hi = qt + 1;
+          }
+        }
+        kpass += all_rows ? (double)(hi > lo ? hi - lo : 0) : (double)nq;
+      }
+    }
+  const double tiles = (double)(nb * nh * nq * nk);
+  return {fwd / tiles, (qpass + kpass) / (2.0 * tiles)};
+}
+
 AttnShape attn_shape(const AttnRegion& r, const Graph& g) {
   AttnShape a;
   const Shape& ss = g.shape(r.s);

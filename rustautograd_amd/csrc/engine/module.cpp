@@ -297,6 +297,7 @@ PYBIND11_MODULE(_rg, m) {
                // against HBM bandwidth ("hbm").
                const StepWork w = step_work(s, streamed);
                d["flops"] = w.flops;
+               d["executed_flops"] = w.executed_flops;
                d["bytes"] = w.bytes;
                d["bound"] = w.compute ? "mfma" : "hbm";
                if (s.attn) {

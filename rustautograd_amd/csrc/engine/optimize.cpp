@@ -15,6 +15,9 @@ namespace {
 
 constexpr size_t FOLD_LIMIT = 4096;
 constexpr size_t CSE_CONST_LIMIT = 16;
+// Device plans also merge equal constants up to this size (gradient seeds of ones, broadcast
+// fills), so products and groups reading them merge too; the key spells out the constant's bytes.
+constexpr size_t DEVICE_CSE_CONST_LIMIT = 4096;
 constexpr size_t REMAT_MIN = 1 << 14;
 constexpr size_t SPLIT_SUM_MIN = 4096;
 constexpr double SEARCH_MIN_GAIN = 0.9;
@@ -63,6 +66,23 @@ int64_t identity(const Graph& g, const Op& op, const std::vector<uint32_t>& ins,
       for (size_t i = 0; i < op.v.size(); i++)
         if (op.v[i] != i) return -1;
       return ins[0];
+    }
+    case RG_OP_SLICE: {
+      // A slice of the whole value (every start 0, every stop the dimension) is the value.
+      const Shape& in = g.shape(ins[0]);
+      for (size_t i = 0; i < in.size(); i++)
+        if (op.v[i] != 0 || op.w[i] != in[i]) return -1;
+      return ins[0];
+    }
+    case RG_OP_TAKE: {
+      // Constant indices 0, 1, ..., n - 1 along an axis of length n (a position table read at
+      // arange(n)): every row in order, so the result is the table itself.
+      const Node& idx = g.nodes[ins[1]];
+      const Shape& in = g.shape(ins[0]);
+      if (idx.op.kind != RG_OP_CONST || idx.shape.size() != 1 || op.a >= in.size() || idx.shape[0] != in[op.a]) return -1;
+      for (size_t i = 0; i < idx.shape[0]; i++)
+        if (idx.op.t->at(i) != (double)i) return -1;
+      return same(ins[0]) ? (int64_t)ins[0] : -1;
     }
     default: return -1;
   }
@@ -251,7 +271,7 @@ Simplified simplify(const Graph& g, const std::vector<uint32_t>& outputs, bool d
         ins = {rid};
       }
     }
-    bool big_const = op.kind == RG_OP_CONST && op.t->n() > CSE_CONST_LIMIT;
+    bool big_const = op.kind == RG_OP_CONST && op.t->n() > (device ? DEVICE_CSE_CONST_LIMIT : CSE_CONST_LIMIT);
     std::string key;
     if (!big_const) {
       key = op.key() + "|";

@@ -1071,6 +1071,8 @@ Plan build_with(const Graph& g, const std::vector<uint32_t>& outputs, bool reuse
       else
         at.out.push_back(view(r.out_o));
       at.node = bwd ? r.dq : r.o;
+      const auto share = attn_executed_share(r, g);
+      at.executed = bwd ? share.second : share.first;
       p.steps.push_back(std::move(st));
       for (uint32_t x : ins)
         if (--uses[x] == 0) a.release(value_slot[x]);
@@ -1253,6 +1255,7 @@ StepWork step_work(const Step& s, const StreamedFn& streamed) {
     };
     for (size_t j = 0; j < s.att.in.size(); j++) w.bytes += rows(j, false) * (double)(a.bh * a.hd) * ds;
     for (size_t j = 0; j < s.att.out.size(); j++) w.bytes += rows(j, true) * (double)(a.bh * a.hd) * ds;
+    w.executed_flops = w.flops * s.att.executed;
     w.compute = true;
     return w;
   }
@@ -1321,6 +1324,7 @@ StepWork step_work(const Step& s, const StreamedFn& streamed) {
         }
       }
       w.flops = 2.0 * (double)m * (double)n * (double)k * (double)batch;
+      w.executed_flops = w.flops;
       w.bytes = (in_elems + (double)i.n) * ds;
       w.compute = i.dtype != DType::I32 && !(streamed && streamed(i.dtype, m, n, k, batch, ta, tb));
       return w;

@@ -92,6 +92,10 @@ AttnShape attn_shape(const AttnRegion& r, const Graph& g);
 // (include/rg_plan.h RG_STEP_ATTN).
 size_t attn_stats_words(const AttnRegion& r, const Graph& g);
 size_t attn_mask_words(const AttnRegion& r, const Graph& g);
+// The share of the region's tile products the device kernels execute, forward and backward: they
+// skip 16 x 16 tiles a constant mask hides (the rules of csrc/hip/attention.hip). 1 when there is
+// no mask or the mask is not a constant (its hidden tiles are not known when planning).
+std::pair<double, double> attn_executed_share(const AttnRegion& r, const Graph& g);
 
 struct Plan;
 
@@ -156,6 +160,7 @@ struct Attn {
   size_t stats_slot = 0;
   std::vector<AttnView> in, out;  // forward: q, k, v -> O; backward: q, k, v, O, dO -> dq, dk, dv
   uint32_t node = 0;              // the O node (forward) or the dq node (backward)
+  double executed = 1.0;          // share of the tile products the kernels execute (attn_executed_share)
 };
 
 struct Step {
@@ -199,7 +204,8 @@ struct Plan {
 // empty every floating-point product is priced by its flops.
 struct StepWork {
   double flops = 0, bytes = 0;
-  bool compute = false;  // priced by flops
+  double executed_flops = 0;  // the flops the device executes: attention skips hidden tiles
+  bool compute = false;       // priced by flops
 };
 using StreamedFn = std::function<bool(DType, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb)>;
 StepWork step_work(const Step& s, const StreamedFn& streamed);

@@ -861,7 +861,7 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
     roofline["unavailable"] = "the backend reports no device peaks";
   }
   struct Row {
-    double seconds = 0, flops = 0, bytes = 0;
+    double seconds = 0, flops = 0, executed_flops = 0, bytes = 0;
     size_t count = 0;
     bool compute = false, f64 = false;
   };
@@ -896,6 +896,7 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
     r.seconds += seconds[s];
     r.count++;
     r.flops += w.flops;
+    r.executed_flops += w.executed_flops;
     r.bytes += w.bytes;
     r.compute = w.compute;
     r.f64 = dt == DType::F64;
@@ -914,6 +915,7 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
     o["share"] = total > 0 ? v.seconds / total : 0.0;
     o["bound"] = v.compute ? "mfma" : "hbm";
     o["flops_per_run"] = v.flops;
+    if (v.compute && v.executed_flops != v.flops) o["executed_flops_per_run"] = v.executed_flops;
     o["bytes_per_run"] = v.bytes;
     const double per_run = v.seconds / (double)repeats;
     const double work = v.compute ? v.flops / 1e12 : v.bytes / 1e9;
@@ -923,6 +925,11 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
       const double peak = v.compute ? (v.f64 ? peaks[2] : peaks[1]) : peaks[0];
       o["peak"] = peak;
       if (per_run > 0) o["fraction_of_peak"] = work / per_run / peak;
+      // Attention skips the tiles a mask hides: its rate over the products it executes.
+      if (per_run > 0 && v.compute && v.executed_flops != v.flops) {
+        o["executed_achieved"] = v.executed_flops / 1e12 / per_run;
+        o["executed_fraction_of_peak"] = v.executed_flops / 1e12 / per_run / peak;
+      }
       ideal += work / peak;
     }
     ops.push(o);

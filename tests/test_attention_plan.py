@@ -152,3 +152,18 @@ def test_cpu_plans_never_fuse_attention():
     fn = _program(mask=rg.tril(64))
     c = rg.compile(fn, _inputs((2, 2, 64, 32)), device="cpu", validate="none")
     assert _steps(c) == []
+
+
+@pytest.mark.parametrize("t", [32, 64, 128, 256])
+def test_executed_share_of_causal_attention(t):
+    """The engine's count of the 16 x 16 tiles the device kernels execute under a constant causal
+    mask (the forward skips fully hidden tiles, the backward walks each wave's visible range):
+    (n + 1) / 2n of them for n = t / 16 tiles per side, forward and backward; all without a mask."""
+    shape = (2, 2, t, 32)
+    n = t // 16
+    for mask, want in ((rg.tril(t), (n + 1) / (2 * n)), (None, 1.0)):
+        c = rg.compile(_program(mask=mask), _inputs(shape, 3), device=DEVPLAN, validate="none")
+        steps = _steps(c)
+        assert len(steps) == 2
+        for s in steps:
+            assert s["executed_flops"] == pytest.approx(want * s["flops"], rel=1e-12), (t, mask is None, s["backward"])

@@ -602,3 +602,52 @@ def test_where_with_broadcast_operand_differentiates_in_a_growing_graph():
     at = xt.sum(1, keepdim=True)
     torch.where(at > xt, at, xt).sum().backward()
     np.testing.assert_allclose(got, xt.grad.numpy(), rtol=1e-12)
+
+
+def _plan_ops(g, outs, inputs, device, optimize="standard"):
+    return [s["op"] if s["kind"] == "instr" else s["kind"] for s in g.compile(outs, inputs, device, optimize).plan_summary()]
+
+
+def test_whole_slices_and_in_order_gathers_are_their_input():
+    """A slice of the whole value and a gather at constant indices 0..n-1 along an axis of length
+    n (a position table read at arange(n)) are the value itself: no step, the same bits."""
+    g = G()
+    table = g.input((6, 5), "float32")
+    x = g.input((6, 5), "float32")
+    rows = g.op("take", [table, g.const(np.arange(6), dtype="int32")], axis=0)
+    whole = g.op("slice", [x], starts=[0, 0], stops=[6, 5])
+    part = g.op("slice", [x], starts=[1, 0], stops=[6, 5])
+    y = g.un("tanh", g.bin("add", rows, whole))
+    inputs = [np.linspace(-1, 1, 30, dtype=np.float32).reshape(6, 5), np.cos(np.arange(30, dtype=np.float32)).reshape(6, 5)]
+    for device in ("cpu", DEVPLAN):
+        ops = _plan_ops(g, [y, part], inputs, device)
+        assert "take" not in ops and ops.count("slice") == 1, (device, ops)
+        got = g.eval([y, part], inputs, device=device, optimize="standard")
+        want = g.eval([y, part], inputs, device="cpu", optimize="none")
+        for a, b in zip(got, want):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # A permuted or partial index set stays a gather.
+    h = G()
+    t2 = h.input((6, 5), "float32")
+    perm = h.op("take", [t2, h.const(np.array([1, 0, 2, 3, 4, 5]), dtype="int32")], axis=0)
+    assert "take" in _plan_ops(h, [perm], inputs[:1], "cpu")
+
+
+def test_device_plans_merge_equal_constants_beyond_the_reference_limit():
+    """Two equal 8 x 8 constants (64 values, above the 16 the reference merges) feeding the same
+    product: one product on device plans, the same values; CPU plans keep the reference's limit."""
+    g = G()
+    d = g.input((40, 8), "float32")
+    ones_a = g.const(np.ones((8, 8)), dtype="float32")
+    ones_b = g.const(np.ones((8, 8)), dtype="float32")
+    p1 = g.op("matmul", [ones_a, g.op("transpose", [d], perm=[1, 0])])
+    p2 = g.op("matmul", [ones_b, g.op("transpose", [d], perm=[1, 0])])
+    out = g.bin("add", p1, p2)
+    inputs = [np.sin(np.arange(320, dtype=np.float32)).reshape(40, 8)]
+    dev = _plan_ops(g, [out], inputs, DEVPLAN)
+    cpu = _plan_ops(g, [out], inputs, "cpu")
+    products = ("matmul", "matmul_t")
+    assert sum(o in products for o in dev) == 1 and sum(o in products for o in cpu) == 2, (dev, cpu)
+    a = g.eval([out], inputs, device=DEVPLAN, optimize="standard")[0]
+    b = g.eval([out], inputs, device="cpu", optimize="none")[0]
+    np.testing.assert_allclose(a, b, rtol=1e-6)
