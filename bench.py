@@ -182,16 +182,22 @@ def roofline_of(compiled, inputs, reps, workload):
     total_s = time_classes(compiled, inputs, classes, reps)
     dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])
     per_launch = (dom["flops"] or dom["bytes"]) / dom["launches"]
-    avg_s = dom["seconds"] / dom["launches"]
-    if dom["unit"] == "TFLOP/s":
-        roof = {"bound": "mfma", "achieved": round(dom["achieved"], 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(dom["achieved"] / FP32_MFMA_PEAK_TFLOPS, 4)}
+    # The dominant class's launches timed alone (its steps replayed back to back between two HIP
+    # events on the execution stream): the per-launch duration a kernel trace reports. The
+    # in-pass figure (the pass minus the pass without the class) also credits the overlap of
+    # each launch's start with the end of the kernel before it; it is kept beside.
+    avg_s = dom["isolated_seconds"] / dom["launches"]
+    achieved = per_launch / avg_s / (1e12 if dom["flops"] else 1e9)
+    if dom["flops"]:
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4)}
     else:
-        roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4)}
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4)}
     roof["traffic"] = measured_traffic(workload, dom_name)
     roof.update({"kernel": dom_name, "launches_per_step": dom["launches"], "algorithmic_per_launch": round(per_launch),
-                 "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]), "avg_launch_us": round(avg_s * 1e6, 2)})
+                 "algorithmic_bytes_per_launch": round(dom["bytes"] / dom["launches"]), "avg_launch_us": round(avg_s * 1e6, 2),
+                 "in_pass_avg_launch_us": round(dom["seconds"] / dom["launches"] * 1e6, 2)})
     kernels = {k: {"ms_per_step": round(v["seconds"] * 1e3, 3), "launches": v["launches"], "achieved": round(v["achieved"], 2),
                    "unit": v["unit"], "frac": round(v["achieved"] / (FP32_MFMA_PEAK_TFLOPS if v["unit"] == "TFLOP/s" else HBM_PEAK_GBS), 4),
                    "isolated_ms_per_step": round(v["isolated_seconds"] * 1e3, 3), "timing": v["timing"]}

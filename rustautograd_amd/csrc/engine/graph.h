@@ -1,10 +1,12 @@
 // rg's SSA IR: tensors, operations, nodes and the graph with shape/dtype inference.
 // Restates the reference's src/tensor.rs:3-138 (dtypes, tensors) and src/graph.rs:41-522 (IR).
 #pragma once
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../../include/rg_plan.h"
@@ -68,11 +70,36 @@ struct Tensor {
   static Tensor full(DType d, const Shape& s, double x) {
     return from_f64(d, s, std::vector<double>(numel(s), x));
   }
+  // Whether every element is finite: a scan of the exponent bits (all ones for inf and NaN), on
+  // several threads for large tensors.
   bool is_finite() const {
-    if (dtype == DType::I32) return true;
-    for (size_t i = 0; i < n(); i++)
-      if (!std::isfinite(at(i))) return false;
-    return true;
+    if (dtype != DType::F32 && dtype != DType::F64) return true;
+    const size_t w = dsize(dtype), count = n();
+    auto scan = [&](size_t lo, size_t hi) {
+      bool bad = false;
+      if (w == 4) {
+        for (size_t i = lo; i < hi; i++) {
+          uint32_t b;
+          memcpy(&b, &data[i * 4], 4);
+          bad |= (b & 0x7F800000u) == 0x7F800000u;
+        }
+      } else {
+        for (size_t i = lo; i < hi; i++) {
+          uint64_t b;
+          memcpy(&b, &data[i * 8], 8);
+          bad |= (b & 0x7FF0000000000000ull) == 0x7FF0000000000000ull;
+        }
+      }
+      return !bad;
+    };
+    const size_t threads = std::min<size_t>(8, std::max<size_t>(1, count >> 20));
+    if (threads <= 1) return scan(0, count);
+    std::vector<char> ok(threads, 1);
+    std::vector<std::thread> pool;
+    for (size_t t = 1; t < threads; t++) pool.emplace_back([&, t] { ok[t] = scan(count * t / threads, count * (t + 1) / threads); });
+    ok[0] = scan(0, count / threads);
+    for (auto& th : pool) th.join();
+    return std::all_of(ok.begin(), ok.end(), [](char c) { return c != 0; });
   }
 };
 

@@ -5,6 +5,7 @@
 #include <pybind11/stl.h>
 
 #include <chrono>
+#include <thread>
 
 #include "validate.h"
 
@@ -440,12 +441,18 @@ PYBIND11_MODULE(_rg, m) {
       .def("allocated_bytes", [](const PyCompiled& c) { return c.c->program->allocated_bytes(); })
       .def("inject_failure", [](const PyCompiled& c, int64_t after) { c.c->program->inject_failure(after); }, py::arg("after") = 0)
       .def("run",
+           // The state arrives as pointers to the Python objects' tensors: a list of PyTensor by
+           // value would be copied twice (tens of MB for a model's parameters and moments).
            [](const PyCompiled& c, const std::vector<std::pair<size_t, size_t>>& state_map, const std::vector<size_t>& data_inputs,
-              const std::vector<size_t>& history, const std::vector<PyTensor>& state,
+              const std::vector<size_t>& history, const std::vector<const PyTensor*>& state,
               const std::vector<std::vector<PyTensor>>& batches, size_t steps, bool skip_state_outputs) {
              RunSpec spec{state_map, data_inputs, history, skip_state_outputs};
              c.c->validate_spec(spec);
-             auto st = tensors(state);
+             std::vector<const Tensor*> st;
+             for (const PyTensor* p : state) {
+               if (!p) throw py::value_error("run: a state entry is None");
+               st.push_back(&p->t);
+             }
              std::vector<std::vector<Tensor>> bs;
              for (auto& b : batches) bs.push_back(tensors(b));
              RunOut out;
@@ -503,6 +510,24 @@ PYBIND11_MODULE(_rg, m) {
     return pc;
   });
   m.def("available_devices", []() { return available_backends(); });
+  // Whether every element of every tensor is finite, the tensors scanned on several threads (a
+  // run's returned state: one scan per run instead of one per tensor).
+  m.def("all_finite", [](const std::vector<const PyTensor*>& ts) {
+    std::vector<const Tensor*> v;
+    for (const PyTensor* p : ts)
+      if (p) v.push_back(&p->t);
+    py::gil_scoped_release nogil;
+    const size_t threads = std::min<size_t>(8, std::max<size_t>(1, v.size()));
+    std::vector<char> ok(threads, 1);
+    std::vector<std::thread> pool;
+    for (size_t t = 0; t < threads; t++)
+      pool.emplace_back([&, t] {
+        for (size_t k = t; k < v.size(); k += threads)
+          if (!v[k]->is_finite()) ok[t] = 0;
+      });
+    for (auto& th : pool) th.join();
+    return std::all_of(ok.begin(), ok.end(), [](char c) { return c != 0; });
+  });
   m.def("plan_words", [](const PyGraph& graph, const std::vector<uint32_t>& outputs, const std::string& flavor, const std::string& optimize) {
     // The serialized plan a device would receive (include/rg_plan.h), without needing the device.
     OptMode mode;

@@ -969,14 +969,14 @@ void Compiled::validate_spec(const RunSpec& spec) const {
 }
 
 // The hot loop (validate.rs:289-363).
-RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, const std::vector<std::vector<Tensor>>& batches,
+RunOut Compiled::run(const RunSpec& spec, const std::vector<const Tensor*>& state, const std::vector<std::vector<Tensor>>& batches,
                      size_t steps) const {
   RunOut r;
   std::unique_ptr<DeviceExec> e;
   try {
     e = program->exec();
   } catch (std::exception& ex) {
-    r.state = state;
+    for (const Tensor* t : state) r.state.push_back(*t);
     r.history.assign(spec.history.size(), {});
     r.device_error = ex.what();
     return r;
@@ -988,7 +988,7 @@ RunOut Compiled::run(const RunSpec& spec, const std::vector<Tensor>& state, cons
   {
     // The state (and a single batch) go over together, with one wait.
     std::vector<std::pair<size_t, const Tensor*>> first;
-    for (size_t k = 0; k < spec.state.size() && k < state.size(); k++) first.push_back({spec.state[k].first, &state[k]});
+    for (size_t k = 0; k < spec.state.size() && k < state.size(); k++) first.push_back({spec.state[k].first, state[k]});
     if (batches.size() == 1)
       for (size_t k = 0; k < spec.data.size() && k < batches[0].size(); k++) first.push_back({spec.data[k], &batches[0][k]});
     e->load_all(first);
@@ -1132,13 +1132,15 @@ std::optional<std::tuple<size_t, size_t, std::vector<Tensor>>> Compiled::replay(
     size_t b = batches.empty() ? 0 : k % batches.size();
     std::vector<std::vector<Tensor>> slice;
     if (!batches.empty()) slice.push_back(batches[b]);
-    RunOut out = run(spec, cur, slice, 1);
+    std::vector<const Tensor*> at;
+    for (auto& t : cur) at.push_back(&t);
+    RunOut out = run(spec, at, slice, 1);
     if (out.device_error) return std::nullopt;
     bool bad = false;
     for (auto& t : out.state) bad |= !t.is_finite();
     for (auto& t : out.outputs) bad |= !t.is_finite();
     if (bad) return std::make_tuple(k, b, cur);
-    cur = out.state;
+    cur = std::move(out.state);
   }
   return std::nullopt;
 }

@@ -52,7 +52,8 @@ class Compiled {
   // How the device prices matrix products for step_work: which run on its streaming kernels.
   StreamedFn streamed_products() const;
   void validate_spec(const RunSpec& spec) const;
-  RunOut run(const RunSpec& spec, const std::vector<Tensor>& state, const std::vector<std::vector<Tensor>>& batches,
+  // `state` is read in place (the run copies it to the device and returns the new state).
+  RunOut run(const RunSpec& spec, const std::vector<const Tensor*>& state, const std::vector<std::vector<Tensor>>& batches,
              size_t steps) const;
   // Replays one step at a time until the state or an output goes non-finite; returns that step, its batch index and the state it started from.
   std::optional<std::tuple<size_t, size_t, std::vector<Tensor>>> replay(const RunSpec& spec, const std::vector<Tensor>& state,

@@ -538,7 +538,10 @@ __global__ void __launch_bounds__(256) k_gemm_skinny_dot(const float* __restrict
 
 // C (M x N, N % 4 == 0) = op(A) op(B) with K <= KR (an outer product of a few vectors): write
 // bound. A block of four waves owns 256 columns; each lane keeps its float4 of every op(B) row in
-// registers and walks the wave's rows, reading op(A)'s row values as wave-uniform scalars.
+// registers and walks the wave's rows, reading op(A)'s row values as wave-uniform scalars. The
+// output is written with non-temporal stores: it is large (a full matrix from a few vectors) and
+// streaming it past the caches leaves them to the operands of the kernels that follow (4 % off a
+// C5 pass on MI355X).
 template <int KR, bool TA, bool TB>
 __global__ void __launch_bounds__(256) k_gemm_outer(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
                                                     int N, int K, int rows_per_wave) {
@@ -564,7 +567,7 @@ __global__ void __launch_bounds__(256) k_gemm_outer(const float* __restrict__ A,
       const float a = k < K ? (TA ? A[(uint64_t)k * M + i] : A[(uint64_t)i * K + k]) : 0.f;
       acc = make_float4(fmaf(a, b[k].x, acc.x), fmaf(a, b[k].y, acc.y), fmaf(a, b[k].z, acc.z), fmaf(a, b[k].w, acc.w));
     }
-    *(float4*)(C + (uint64_t)i * N + col) = acc;
+    __builtin_nontemporal_store(floatx4{acc.x, acc.y, acc.z, acc.w}, (floatx4*)(C + (uint64_t)i * N + col));
   }
 }
 

@@ -473,25 +473,53 @@ std::string generate_rows(const rgplan::Fused& f, const std::string& name, Fused
   if (has_col) {
     s << "  }\n";  // end of the row loop
     // The waves' accumulators, combined in wave order through LDS: one partial row per block.
-    s << "  __shared__ " << T << " cl[" << waves << " * " << L << "];\n";
-    for (size_t j = 0; j < f.outputs.size(); j++) {
-      int64_t r = f.outputs[j].first;
-      if (!col_reg[(size_t)r]) continue;
+    std::vector<size_t> cols;  // outputs that are column reductions
+    for (size_t j = 0; j < f.outputs.size(); j++)
+      if (col_reg[(size_t)f.outputs[j].first]) cols.push_back(j);
+    auto aux_of = [&](size_t j) {
       int64_t aux = 0;
       for (auto& m : f.ops)
-        if (m.reg == r) aux = m.aux;
-      const std::string c = "c" + std::to_string(r);
-      s << "  __syncthreads();\n";
+        if (m.reg == f.outputs[j].first) aux = m.aux;
+      return aux;
+    };
+    auto stage = [&](size_t j, const std::string& dst) {
+      const std::string c = "c" + std::to_string(f.outputs[j].first);
       for (int64_t e = 0; e < E; e++) {
-        std::string w = "  cl[(threadIdx.x >> 6) * " + std::to_string(L) + "u + " + col(e) + "] = " + c + "[" + std::to_string(e) + "];\n";
+        std::string w = "  " + dst + "[(threadIdx.x >> 6) * " + std::to_string(L) + "u + " + col(e) + "] = " + c + "[" + std::to_string(e) + "];\n";
         s << (exact ? w : "  if (" + valid(e) + ") " + w.substr(2));
       }
+    };
+    const uint64_t all_bytes = (uint64_t)cols.size() * waves * L * (dbl ? 8 : 4);
+    if (cols.size() > 1 && all_bytes <= COL_LDS_BYTES) {
+      // Every output's accumulators staged at once, then one thread per (output, column) adds
+      // its column's wave values in wave order: one barrier, and the outputs' sums in parallel.
+      s << "  __shared__ " << T << " cl[" << cols.size() << "][" << waves << " * " << L << "];\n";
+      for (size_t i = 0; i < cols.size(); i++) stage(cols[i], "cl[" + std::to_string(i) + "]");
       s << "  __syncthreads();\n";
-      s << "  for (unsigned q = threadIdx.x; q < " << L << "u; q += " << 64 * waves << "u) {\n";
-      s << "    " << T << " v = cl[q];\n";
-      s << "    for (int w = 1; w < " << waves << "; w++) v = " << col_comb(aux, "v", "cl[w * " + std::to_string(L) + "u + q]") << ";\n";
-      s << "    out" << j << "[(unsigned long long)blockIdx.x * " << L << "ull + q] = v;\n";
+      s << "  for (unsigned q = threadIdx.x; q < " << cols.size() * L << "u; q += " << 64 * waves << "u) {\n";
+      s << "    const unsigned o = q / " << L << "u, c = q % " << L << "u;\n";
+      for (size_t i = 0; i < cols.size(); i++) {
+        const int64_t aux = aux_of(cols[i]);
+        const std::string cl = "cl[" + std::to_string(i) + "]";
+        s << "    " << (i ? "else " : "") << "if (o == " << i << "u) {\n";
+        s << "      " << T << " v = " << cl << "[c];\n";
+        s << "      for (int w = 1; w < " << waves << "; w++) v = " << col_comb(aux, "v", cl + "[w * " + std::to_string(L) + "u + c]") << ";\n";
+        s << "      out" << cols[i] << "[(unsigned long long)blockIdx.x * " << L << "ull + c] = v;\n";
+        s << "    }\n";
+      }
       s << "  }\n";
+    } else {
+      s << "  __shared__ " << T << " cl[" << waves << " * " << L << "];\n";
+      for (size_t j : cols) {
+        s << "  __syncthreads();\n";
+        stage(j, "cl");
+        s << "  __syncthreads();\n";
+        s << "  for (unsigned q = threadIdx.x; q < " << L << "u; q += " << 64 * waves << "u) {\n";
+        s << "    " << T << " v = cl[q];\n";
+        s << "    for (int w = 1; w < " << waves << "; w++) v = " << col_comb(aux_of(j), "v", "cl[w * " + std::to_string(L) + "u + q]") << ";\n";
+        s << "    out" << j << "[(unsigned long long)blockIdx.x * " << L << "ull + q] = v;\n";
+        s << "  }\n";
+      }
     }
   }
   s << "}\n";

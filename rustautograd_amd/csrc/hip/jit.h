@@ -31,6 +31,8 @@ struct FusedKernel {
 // at 64 registers, one row per wave, measured no faster on C4's layer norms.)
 constexpr int64_t COL_BLOCKS = 256;
 constexpr int COL_WAVES = 16;
+// Column reductions of one group staged in LDS together when they take at most this many bytes.
+constexpr uint64_t COL_LDS_BYTES = 64 * 1024;
 
 // Source of one kernel named `name` computing group `f` (`k->grid` blocks). Outputs whose slot is
 // also an input slot are written in place (each element is read before it is written). With

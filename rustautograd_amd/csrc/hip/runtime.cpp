@@ -16,6 +16,8 @@
 #include <sstream>
 #include <stdexcept>
 #include <string>
+#include <thread>
+#include <tuple>
 #include <vector>
 
 #include "../../../include/rg_hip.h"
@@ -98,6 +100,11 @@ struct Frame {
   void* workspace = nullptr;
   hipStream_t stream = nullptr;
   RunCache run;
+  // Pinned host staging for the batched slot copies (rg_hip_exec_write_slots / read_slots), grown
+  // on demand: the DMA engines read and write it directly, where pageable memory goes through the
+  // runtime's own bounce buffer one slot at a time.
+  void* stage = nullptr;
+  uint64_t stage_bytes = 0;
 };
 
 struct Program {
@@ -164,6 +171,7 @@ struct Program {
       f->run.release();
       hipStreamDestroy(f->stream);
       hipFree(f->arena);
+      if (f->stage) hipHostFree(f->stage);
       delete f;
     }
     for (void* p : device_tables) hipFree(p);
@@ -1488,24 +1496,100 @@ int rg_hip_exec_write(void* exec, int64_t slot, const void* src, uint64_t bytes)
   return latch(e, hipStreamSynchronize(e->frame->stream), "write") ? -1 : 0;
 }
 
+// Batches of slot copies at least this large go through the frame's pinned staging.
+constexpr uint64_t STAGE_MIN_BYTES = 1ull << 20;
+
+// Host copies of `pieces` (destination, source, bytes), the total split evenly over up to eight
+// threads (at least 4 MiB each): one host thread copies well below the host's memory bandwidth.
+void parallel_copy(const std::vector<std::tuple<char*, const char*, uint64_t>>& pieces) {
+  uint64_t total = 0;
+  for (auto& pc : pieces) total += std::get<2>(pc);
+  const uint64_t hw = std::max(1u, std::thread::hardware_concurrency());
+  const uint64_t nt = std::max<uint64_t>(1, std::min<uint64_t>(std::min<uint64_t>(8, hw), total >> 22));
+  auto run = [&](uint64_t lo, uint64_t hi) {
+    uint64_t at = 0;
+    for (auto& [d, src, b] : pieces) {
+      const uint64_t a = std::max(lo, at), end = std::min(hi, at + b);
+      if (a < end) memcpy(d + (a - at), src + (a - at), end - a);
+      at += b;
+      if (at >= hi) break;
+    }
+  };
+  std::vector<std::thread> threads;
+  for (uint64_t t = 1; t < nt; t++) threads.emplace_back(run, total * t / nt, total * (t + 1) / nt);
+  run(0, total / nt);
+  for (auto& th : threads) th.join();
+}
+
+// Offsets of the copies' bytes in the staging (256-byte aligned each) and their total, or 0 when
+// the batch is small or the staging cannot grow to it.
+uint64_t stage_layout(Frame* f, int64_t n, const uint64_t* bytes, std::vector<uint64_t>* off) {
+  uint64_t total = 0, payload = 0;
+  for (int64_t k = 0; k < n; k++) {
+    off->push_back(total);
+    total += (bytes[k] + 255) / 256 * 256;
+    payload += bytes[k];
+  }
+  if (payload < STAGE_MIN_BYTES) return 0;
+  if (f->stage_bytes < total) {
+    if (f->stage) hipHostFree(f->stage);
+    f->stage = nullptr;
+    f->stage_bytes = 0;
+    if (hipHostMalloc(&f->stage, total, hipHostMallocDefault) != hipSuccess) {
+      f->stage = nullptr;
+      hipGetLastError();
+      return 0;
+    }
+    f->stage_bytes = total;
+  }
+  return total;
+}
+
 int rg_hip_exec_write_slots(void* exec, int64_t n, const int64_t* slots, const void* const* srcs, const uint64_t* bytes) {
   auto* e = (Exec*)exec;
+  Frame* f = e->frame;
   for (int64_t k = 0; k < n; k++)
-    if (slots[k] < 0 || (size_t)slots[k] >= e->frame->slot.size() || bytes[k] > e->prog->slot_bytes[(size_t)slots[k]]) return -1;
+    if (slots[k] < 0 || (size_t)slots[k] >= f->slot.size() || bytes[k] > e->prog->slot_bytes[(size_t)slots[k]]) return -1;
+  std::vector<uint64_t> off;
+  if (stage_layout(f, n, bytes, &off)) {
+    // Into the pinned staging on several host threads, then one DMA per slot.
+    std::vector<std::tuple<char*, const char*, uint64_t>> pieces;
+    for (int64_t k = 0; k < n; k++) pieces.push_back({(char*)f->stage + off[(size_t)k], (const char*)srcs[k], bytes[k]});
+    parallel_copy(pieces);
+    for (int64_t k = 0; k < n; k++)
+      if (bytes[k] && latch(e, hipMemcpyAsync(f->slot[(size_t)slots[k]], (char*)f->stage + off[(size_t)k], bytes[k], hipMemcpyHostToDevice, f->stream),
+                            "write"))
+        return -1;
+    return latch(e, hipStreamSynchronize(f->stream), "write") ? -1 : 0;
+  }
   for (int64_t k = 0; k < n; k++)
-    if (bytes[k] && latch(e, hipMemcpyAsync(e->frame->slot[(size_t)slots[k]], srcs[k], bytes[k], hipMemcpyHostToDevice, e->frame->stream), "write"))
+    if (bytes[k] && latch(e, hipMemcpyAsync(f->slot[(size_t)slots[k]], srcs[k], bytes[k], hipMemcpyHostToDevice, f->stream), "write"))
       return -1;
-  return latch(e, hipStreamSynchronize(e->frame->stream), "write") ? -1 : 0;
+  return latch(e, hipStreamSynchronize(f->stream), "write") ? -1 : 0;
 }
 
 int rg_hip_exec_read_slots(void* exec, int64_t n, const int64_t* slots, void* const* dsts, const uint64_t* bytes) {
   auto* e = (Exec*)exec;
+  Frame* f = e->frame;
   for (int64_t k = 0; k < n; k++)
-    if (slots[k] < 0 || (size_t)slots[k] >= e->frame->slot.size() || bytes[k] > e->prog->slot_bytes[(size_t)slots[k]]) return -1;
+    if (slots[k] < 0 || (size_t)slots[k] >= f->slot.size() || bytes[k] > e->prog->slot_bytes[(size_t)slots[k]]) return -1;
+  std::vector<uint64_t> off;
+  if (stage_layout(f, n, bytes, &off)) {
+    // One DMA per slot into the pinned staging, then out of it on several host threads.
+    for (int64_t k = 0; k < n; k++)
+      if (bytes[k] && latch(e, hipMemcpyAsync((char*)f->stage + off[(size_t)k], f->slot[(size_t)slots[k]], bytes[k], hipMemcpyDeviceToHost, f->stream),
+                            "read"))
+        return -1;
+    if (latch(e, hipStreamSynchronize(f->stream), "read")) return -1;
+    std::vector<std::tuple<char*, const char*, uint64_t>> pieces;
+    for (int64_t k = 0; k < n; k++) pieces.push_back({(char*)dsts[k], (const char*)f->stage + off[(size_t)k], bytes[k]});
+    parallel_copy(pieces);
+    return 0;
+  }
   for (int64_t k = 0; k < n; k++)
-    if (bytes[k] && latch(e, hipMemcpyAsync(dsts[k], e->frame->slot[(size_t)slots[k]], bytes[k], hipMemcpyDeviceToHost, e->frame->stream), "read"))
+    if (bytes[k] && latch(e, hipMemcpyAsync(dsts[k], f->slot[(size_t)slots[k]], bytes[k], hipMemcpyDeviceToHost, f->stream), "read"))
       return -1;
-  return latch(e, hipStreamSynchronize(e->frame->stream), "read") ? -1 : 0;
+  return latch(e, hipStreamSynchronize(f->stream), "read") ? -1 : 0;
 }
 
 int rg_hip_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes) {

@@ -340,7 +340,7 @@ def run(compiled, state, data=None, steps=1, callback=None, every=None):
         seconds += secs
         if bad_at is not None:
             nonfinite = done - ran + bad_at
-        elif not all(t.is_finite() for t in new_state):
+        elif not _rg.all_finite(new_state):
             nonfinite = done - 1
         current = new_state
         if contract.aux_def is not None and outputs:

@@ -1,8 +1,8 @@
 """Full-length training runs on the HIP device overlaid on the CPU oracle's committed curves.
 
 tests/golden/loss_curves.json holds the oracle's per-step losses for C2 (all 200 steps), C3
-(all 300) and C4 (the first 100 of 300), written by tests/golden/make_loss_curves.py, and
-summaries of the final state. Each test runs the whole device loop once (`rg.run`, no Python
+(all 300) and C4 (all 300), written by tests/golden/make_loss_curves.py, and summaries of each
+parameter's movement over the run. Each test runs the whole device loop once (`rg.run`, no Python
 between steps) and compares every step.
 
 Tolerances:
