@@ -10,8 +10,10 @@ Tolerances:
   reductions), so its losses are not the oracle's bits; the largest per-step difference seen
   over the full runs on an MI355X is 5.2e-7 (C2, C3 and C4 alike; each run prints its own).
 - movement, per parameter leaf: d = final - initial against the fixture's summaries of the
-  oracle's d: its L2 norm within MOVE_TOL relative, and its dot products with PROJECTIONS fixed
-  random vectors within 4.5 * MOVE_TOL * |d_oracle|. For a device movement d', the projection
+  oracle's d: its L2 norm within MOVE_TOL = 1e-4 relative, and its dot products with PROJECTIONS
+  fixed random vectors within 4.5 * MOVE_TOL * |d_oracle|. Largest seen on an MI355X over the
+  full runs: norm 5.1e-6 (C2), 2.5e-6 (C3), 2.1e-6 (C4); projection 6.1e-6 (C2), 1.2e-4 (C3, a
+  query-key-value weight), 4.1e-5 (C4), each relative to |d_oracle|. For a device movement d', the projection
   difference (d' - d) . r is normal with deviation |d' - d|, so the projections bound the
   movement's L2 error without storing the parameters (4.5 deviations: over ~300 leaf and
   projection pairs a chance failure has probability under 0.3 %). The final state itself is
@@ -35,7 +37,7 @@ pytestmark = pytest.mark.gpu
 
 FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "loss_curves.json")
 LOSS_TOL = 1e-5
-MOVE_TOL = 1e-2
+MOVE_TOL = 1e-4
 
 
 def _generator():
