@@ -85,10 +85,13 @@ int rg_hip_exec_write(void* exec, int64_t slot, const void* src, uint64_t bytes)
 /* `Exec::prefix` (plan.rs:35): the first bytes of a slot back to the host. */
 int rg_hip_exec_read(void* exec, int64_t slot, void* dst, uint64_t bytes);
 /* `Exec::load` for many slots at once (run_loop's state load, validate.rs:290-292): every copy is
- * enqueued, then one wait. Returns 0, or -1 for a bad slot or size (nothing copied) or a failure. */
+ * enqueued, then one wait; a batch of at least 1 MiB passes through the frame's pinned staging
+ * (filled on several host threads, then one DMA per slot), so `srcs` may be pageable memory.
+ * Returns 0, or -1 for a bad slot or size (nothing copied) or a failure. */
 int rg_hip_exec_write_slots(void* exec, int64_t n, const int64_t* slots, const void* const* srcs, const uint64_t* bytes);
 /* `Exec::prefix` for many slots at once (run_loop's final state read, validate.rs:361): every
- * copy is enqueued, then one wait. Returns as rg_hip_exec_write_slots. */
+ * copy is enqueued, then one wait (through the staging as above, drained after the wait).
+ * Returns as rg_hip_exec_write_slots. */
 int rg_hip_exec_read_slots(void* exec, int64_t n, const int64_t* slots, void* const* dsts, const uint64_t* bytes);
 /* `Exec::scalar` (plan.rs:37): element 0 of a slot as a double. */
 double rg_hip_exec_scalar(void* exec, int64_t slot);
