@@ -32,24 +32,39 @@ def _numel(s):
     return n
 
 
-def classify(plan):
+def classify(plan, runs_in=None):
     """Groups plan steps into kernel classes with their algorithmic work and the step indices of
     each. The work of a step is the engine's (plan_summary's flops, bytes and bound): flops for
     attention and for products on matrix cores, bytes (each distinct input read once, each
-    output written once) for everything else, including the products the backend streams."""
-    classes = {}
+    output written once) for everything else, including the products the backend streams.
 
-    def add(name, k, st):
+    `runs_in` (Compiled step_runs_in) names, per step, the step whose kernel computes it: a
+    product that computes an elementwise group in its epilogue, and that group, form their own
+    class (`gemm_mfma_epilogue`: the product's flops, the group's bytes beside the product's, one
+    launch), so the combined kernel's time is neither charged to the plain products nor counted
+    as elementwise work done in no time."""
+    classes = {}
+    runs_in = runs_in or list(range(len(plan)))
+    partner = {}
+    for k, r in enumerate(runs_in):
+        if r != k:
+            partner[k] = r
+            partner[r] = k
+
+    def add(name, k, st, launch=True):
         c = classes.setdefault(name, {"steps": [], "flops": 0.0, "executed_flops": 0.0, "bytes": 0.0, "launches": 0})
         c["steps"].append(k)
         if st["bound"] == "mfma":
             c["flops"] += st["flops"]
             c["executed_flops"] += st.get("executed_flops", st["flops"])
         c["bytes"] += st["bytes"]
-        c["launches"] += 1
+        c["launches"] += 1 if launch else 0
 
     for k, st in enumerate(plan):
-        if st["kind"] == "attention":
+        if k in partner:
+            product = st["kind"] != "fused"
+            add("gemm_mfma_epilogue", k, st if product else dict(st, bound="hbm"), launch=product)
+        elif st["kind"] == "attention":
             add("attention", k, st)
         elif st["kind"] == "fused":
             add("fused_elementwise", k, st)
@@ -177,7 +192,8 @@ def cpu_baseline(cfg, sample_batch=4, steps=3):
 def roofline_of(compiled, inputs, reps, workload):
     """(roofline dict, per-class table, device seconds per pass) from each kernel class's device
     time inside the replayed pass (time_classes)."""
-    classes = classify(compiled.plan_summary())
+    runs_in = compiled._n.step_runs_in() if hasattr(compiled._n, "step_runs_in") else None
+    classes = classify(compiled.plan_summary(), runs_in)
     time_classes(compiled, inputs, classes, 1, trials=1)
     total_s = time_classes(compiled, inputs, classes, reps)
     dom_name, dom = max(classes.items(), key=lambda kv: kv[1]["seconds"])

@@ -67,6 +67,11 @@ void* rg_hip_program_new(const int64_t* plan_words, size_t n_words, const void* 
 void rg_hip_program_free(void* program);
 /* metal.rs:385-388 `allocated_bytes()`: device bytes this process holds, to catch leaks. */
 uint64_t rg_hip_program_allocated_bytes(void* program);
+/* No counterpart in the reference (its Metal backend runs every plan step as its own dispatch):
+ * the plan step whose kernel computes `step`. A product that runs a following elementwise group
+ * in its epilogue computes both; the one of the two that does not launch anything returns the
+ * other, every other step itself; -1 for a step out of range. For per-step timing and rooflines. */
+int64_t rg_hip_program_step_runs_in(void* program, int64_t step);
 /* metal.rs:525-529 `inject_failure_for_test()`: the next step fails as a device error would. */
 void rg_hip_program_inject_failure(void* program);
 /* Test hook next to `inject_failure_for_test` (metal.rs:525-529), with no reference counterpart:

@@ -38,6 +38,7 @@ void register_backend(const std::string& name, const std::string& path, const st
   bind(*b, b->program_allocated_bytes, "program_allocated_bytes", true);
   bind(*b, b->program_inject_failure, "program_inject_failure", true);
   bind(*b, b->program_inject_failure_after, "program_inject_failure_after", false);
+  bind(*b, b->program_step_runs_in, "program_step_runs_in", false);
   bind(*b, b->exec_new, "exec_new", true);
   bind(*b, b->exec_free, "exec_free", true);
   bind(*b, b->exec_write, "exec_write", true);

@@ -24,6 +24,7 @@ struct Backend {
   uint64_t (*program_allocated_bytes)(void*) = nullptr;
   void (*program_inject_failure)(void*) = nullptr;
   void (*program_inject_failure_after)(void*, int64_t) = nullptr;  // optional
+  int64_t (*program_step_runs_in)(void*, int64_t) = nullptr;  // optional
   void* (*exec_new)(void*, char*, size_t) = nullptr;
   void (*exec_free)(void*) = nullptr;
   int (*exec_write)(void*, int64_t, const void*, uint64_t) = nullptr;
@@ -67,6 +68,8 @@ class DeviceProgram {
   // Test hooks (metal.rs:385-388, 525-529): device bytes held, and a failure after `after` passes.
   uint64_t allocated_bytes() const { return b_->program_allocated_bytes(p_); }
   void inject_failure(int64_t after) const;
+  // The step whose kernel computes step `k` (itself when none), where the backend says.
+  int64_t step_runs_in(int64_t k) const { return b_->program_step_runs_in ? b_->program_step_runs_in(p_, k) : k; }
  private:
   Backend* b_;
   void* p_ = nullptr;

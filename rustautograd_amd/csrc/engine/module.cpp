@@ -439,6 +439,14 @@ PYBIND11_MODULE(_rg, m) {
              return c.c->profile(in, repeats).dump();
            })
       .def("allocated_bytes", [](const PyCompiled& c) { return c.c->program->allocated_bytes(); })
+      // Per plan step, the step whose kernel computes it (a product running a fused group in its
+      // epilogue computes both; other steps compute themselves).
+      .def("step_runs_in",
+           [](const PyCompiled& c) {
+             std::vector<int64_t> at;
+             for (size_t k = 0; k < c.c->plan.steps.size(); k++) at.push_back(c.c->program->step_runs_in((int64_t)k));
+             return at;
+           })
       .def("inject_failure", [](const PyCompiled& c, int64_t after) { c.c->program->inject_failure(after); }, py::arg("after") = 0)
       .def("run",
            // The state arrives as pointers to the Python objects' tensors: a list of PyTensor by

@@ -871,7 +871,19 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
     for (size_t i = 0; i < s.size(); i++) o += (i ? ", " : "") + std::to_string(s[i]);
     return o + "]";
   };
+  // A fused group the device computes in a product's epilogue (step_runs_in pairs the two) is
+  // counted in the product's row: its time (the combined kernel runs at one of the two steps) and
+  // its bytes, with no launch or flops of its own.
+  std::vector<size_t> row_of(plan.steps.size());
+  for (size_t s = 0; s < plan.steps.size(); s++) row_of[s] = s;
   for (size_t s = 0; s < plan.steps.size(); s++) {
+    const int64_t r = program->step_runs_in((int64_t)s);
+    if (r < 0 || (size_t)r == s || (size_t)r >= plan.steps.size()) continue;
+    const size_t product = !plan.steps[s].fused && !plan.steps[s].attn ? s : (size_t)r;
+    row_of[s] = row_of[(size_t)r] = product;
+  }
+  for (size_t s0 = 0; s0 < plan.steps.size(); s0++) {
+    const size_t s = row_of[s0];
     const Step& st = plan.steps[s];
     std::string key;
     DType dt;
@@ -893,7 +905,11 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
     if (dt == DType::F64) key += " f64";
     const StepWork w = step_work(st, streamed);
     Row& r = rows[key];
-    r.seconds += seconds[s];
+    r.seconds += seconds[s0];
+    if (s0 != s) {  // the group in the product's epilogue
+      r.bytes += step_work(plan.steps[s0], streamed).bytes;
+      continue;
+    }
     r.count++;
     r.flops += w.flops;
     r.executed_flops += w.executed_flops;

@@ -14,6 +14,9 @@
 
 namespace rgjit {
 
+// The text of gemm_mfma.h (generated at build time), for products compiled with an epilogue.
+extern const char* const rg_gemm_mfma_source;
+
 namespace {
 
 std::vector<int64_t> row_strides(const std::vector<int64_t>& shape) {
@@ -174,6 +177,103 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
   s << "  }\n";
   s << "  }\n";
   s << "}\n";
+  return s.str();
+}
+
+std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, const ProductTile& t, const std::string& name,
+                          FusedKernel* k) {
+  if (f.dtype != RG_F32) throw std::runtime_error("product epilogue: fp32 groups only");
+  const std::string E = name + "_epi";
+  std::ostringstream s;
+  s << "struct " << E << " {\n  float* c;\n";
+  for (size_t j = 0; j < f.inputs.size(); j++) s << "  const float* in" << j << ";\n";
+  for (size_t j = 0; j < f.outputs.size(); j++) s << "  float* out" << j << ";\n";
+  s << "  __device__ __forceinline__ void begin(unsigned int, unsigned int) {}\n";
+  // The group's value of element e + v for v < W, from the product's outputs `a`.
+  auto body = [&](int W) {
+    std::ostringstream b;
+    std::vector<std::string> reg_expr((size_t)f.regs);
+    std::vector<std::string> in_expr(f.inputs.size());
+    for (size_t j = 0; j < f.inputs.size(); j++) {
+      const auto& in = f.inputs[j];
+      const std::string x = "x" + std::to_string(j);
+      if (in.kind == RG_ARG_SPLAT) {
+        b << "    const float " << x << "s = in" << j << "[0];\n";
+        in_expr[j] = x + "s";
+      } else if (in.kind == RG_ARG_FULL && in.slot == c_slot) {
+        in_expr[j] = "a[v]";
+      } else if (in.kind == RG_ARG_FULL || in.kind == RG_ARG_ROW) {
+        const std::string at = in.kind == RG_ARG_FULL ? "e" : "(e % " + std::to_string(in.row_len) + "ull)";
+        b << "    float " << x << "[" << W << "];\n";
+        if (W == 4) b << "    { const float4 t = *(const float4*)(in" << j << " + " << at << "); " << x << "[0] = t.x; " << x << "[1] = t.y; " << x
+                      << "[2] = t.z; " << x << "[3] = t.w; }\n";
+        else b << "    " << x << "[0] = in" << j << "[" << at << "];\n";
+        in_expr[j] = x + "[v]";
+      } else {
+        throw std::runtime_error("product epilogue: broadcast inputs are not supported");
+      }
+      if (in.reg >= 0) reg_expr[(size_t)in.reg] = in_expr[j];
+    }
+    for (size_t j = 0; j < f.outputs.size(); j++) b << "    float o" << j << "[" << W << "];\n";
+    b << "#pragma unroll\n    for (int v = 0; v < " << W << "; v++) {\n";
+    for (auto& m : f.ops) {
+      std::vector<std::string> args;
+      for (auto& [is_reg, idx] : m.args) {
+        if (is_reg) {
+          const std::string& e = reg_expr[(size_t)idx];
+          args.push_back(e.empty() ? "r" + std::to_string(idx) : e);
+        } else {
+          args.push_back(in_expr[(size_t)idx]);
+        }
+      }
+      b << "      const float r" << m.reg << " = " << expr(m.op, args) << ";\n";
+    }
+    for (size_t j = 0; j < f.outputs.size(); j++) b << "      o" << j << "[v] = r" << f.outputs[j].first << ";\n";
+    b << "    }\n";
+    for (size_t j = 0; j < f.outputs.size(); j++) {
+      if (W == 4) b << "    *(float4*)(out" << j << " + e) = make_float4(o" << j << "[0], o" << j << "[1], o" << j << "[2], o" << j << "[3]);\n";
+      else b << "    out" << j << "[e] = o" << j << "[0];\n";
+    }
+    return b.str();
+  };
+  s << "  __device__ __forceinline__ void put4(unsigned long long e, float4 acc) {\n";
+  if (store_c) s << "    *(float4*)(c + e) = acc;\n";
+  s << "    const float a[4] = {acc.x, acc.y, acc.z, acc.w};\n" << body(4) << "  }\n";
+  s << "  __device__ __forceinline__ void put1(unsigned long long e, float acc) {\n";
+  if (store_c) s << "    c[e] = acc;\n";
+  s << "    const float a[1] = {acc};\n" << body(1) << "  }\n";
+  s << "  __device__ __forceinline__ void put2(unsigned long long e, float2 acc) { put1(e, acc.x); put1(e + 1, acc.y); }\n";
+  s << "};\n";
+  const int nt = 64 * t.wm * t.wn;
+  // At least two waves per SIMD (at most 256 registers a wave, far above what the tile uses): with
+  // that bound the compiler keeps the MFMA accumulators in ordinary VGPRs, as the precompiled
+  // tiles are built (-amdgpu-mfma-vgpr-form), rather than copying them through AGPRs.
+  // The epilogue's pointers arrive as kernel parameters, restrict-qualified when no output shares
+  // a slot with an input or the product, so that the compiler may issue an output's loads before
+  // the stores of the outputs before it.
+  bool alias = false;
+  for (auto& o : f.outputs) {
+    alias |= o.second == c_slot;
+    for (auto& in : f.inputs) alias |= in.slot == o.second;
+  }
+  const char* R = alias ? "" : "__restrict__ ";
+  s << "extern \"C\" __global__ void __launch_bounds__(" << nt << ") __attribute__((amdgpu_waves_per_eu(2))) " << name
+    << "(const float* __restrict__ A, const float* __restrict__ B, int M, int N, int K, const rgg::int64_t* a_off, const rgg::int64_t* b_off, "
+       "rgg::uint64_t a_stride, rgg::uint64_t b_stride, int splits, int kps, const float* __restrict__ bias, rgg::uint32_t tiles_m, "
+       "rgg::uint32_t tiles_n, int swizzle, float* "
+    << R << "c";
+  for (size_t j = 0; j < f.inputs.size(); j++) s << ", const float* " << R << "in" << j;
+  for (size_t j = 0; j < f.outputs.size(); j++) s << ", float* " << R << "out" << j;
+  s << ") {\n  " << E << " epi{c";
+  for (size_t j = 0; j < f.inputs.size(); j++) s << ", in" << j;
+  for (size_t j = 0; j < f.outputs.size(); j++) s << ", out" << j;
+  s << "};\n";
+  s << "  rgg::gemm_mfma_block<" << t.bm << ", " << t.bn << ", " << t.bk << ", " << t.wm << ", " << t.wn << ", " << (t.ta ? "true" : "false") << ", "
+    << (t.tb ? "true" : "false") << ", " << t.mode << ", " << t.ms
+    << ">(A, B, M, N, K, a_off, b_off, a_stride, b_stride, splits, kps, bias, tiles_m, tiles_n, swizzle, epi);\n}\n";
+  k->name = name;
+  k->block = (uint32_t)nt;
+  k->vec = 1;
   return s.str();
 }
 
@@ -533,12 +633,18 @@ std::map<std::string, hipModule_t> g_modules;
 }  // namespace
 
 std::vector<char> compile_code(const std::string& body) {
-  std::string src = std::string(rg_ops_source) + "\n" + body;
+  std::string src = std::string(rg_ops_source) + "\n";
+  if (body.find("rgg::gemm_mfma_block") != std::string::npos) src += std::string(rg_gemm_mfma_source) + "\n";
+  src += body;
   hiprtcProgram prog;
   if (hiprtcCreateProgram(&prog, src.c_str(), "rg_fused.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
     throw std::runtime_error("hiprtcCreateProgram failed");
-  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-fno-fast-math",
-                        "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  // The package's own flags (rustautograd_amd/build.py): no contraction, no fast math, denormals
+  // kept, packed fp32 off. No -mllvm options: in a process that loaded another build of the code
+  // object manager first (torch's), hiprtc runs that build's LLVM, and an option it does not know
+  // ends the process.
+  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-fno-fast-math", "-fno-gpu-flush-denormals-to-zero",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
   hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
   if (r != HIPRTC_SUCCESS) {
     size_t len = 0;

@@ -53,6 +53,22 @@ std::vector<int64_t> merged_slots(const std::vector<const rgplan::Fused*>& parts
 // one partial row per block for each column output (see col_kind).
 std::string generate_rows(const rgplan::Fused& f, const std::string& name, FusedKernel* k);
 
+// A product's tile for generate_gemm (the template arguments of rgg::gemm_mfma_block).
+struct ProductTile {
+  int bm, bn, bk, wm, wn, ms, mode;
+  bool ta, tb;
+};
+
+// Source of one product kernel whose epilogue computes fused group `f` (a plain fused group over
+// the product's M x N outputs, reading the product through `c_slot`) from each finished output
+// before it is stored: the tile of gemm_mfma.h with an epilogue that loads the group's other
+// inputs at the output's position, applies its operations in its order (the values the plain
+// group kernel would compute) and stores its outputs, and the product itself when `store_c`.
+// The kernel's parameters are the tile kernel's, then the epilogue's pointers (product, the
+// group's inputs in order, its outputs in order).
+std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, const ProductTile& t, const std::string& name,
+                          FusedKernel* k);
+
 // Compiles all sources into one code object for gfx950 and resolves each kernel. Modules are
 // cached by source text for the life of the process. Throws std::runtime_error with the log.
 void compile(const std::string& source, std::vector<FusedKernel*>& kernels);

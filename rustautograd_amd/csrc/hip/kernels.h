@@ -185,6 +185,16 @@ bool gemm_streamed(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch
 // partials need.
 int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb);
 uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool ta, bool tb);
+
+// The MFMA tile of a single (unbatched) fp32 product whose operands are 16-byte aligned, as plan
+// slots are, when it runs unsplit on the tile kernel and each lane's finished outputs come in
+// runs of four adjacent columns (the form an elementwise epilogue takes): the shape arguments of
+// the tile kernel (gemm_mfma.h). False for any other product.
+struct GemmTile {
+  int bm, bn, bk, wm, wn, ms, mode, kps;
+  uint32_t tm, tn;
+};
+bool gemm_epilogue_tile(int dtype, uint64_t m, uint64_t n, uint64_t k, bool ta, bool tb, GemmTile* t);
 void gemm(hipStream_t s, const GemmArgs& g);
 
 }  // namespace rgk

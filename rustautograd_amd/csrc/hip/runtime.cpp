@@ -112,6 +112,9 @@ struct Program {
   std::vector<uint8_t> blob;
   std::vector<StepFn> steps;
   std::vector<std::unique_ptr<rgjit::FusedKernel>> fused;
+  // Per step: the product step whose kernel computes this fused group as its epilogue, or -1.
+  std::vector<int64_t> epilogue_of;
+  std::vector<bool> epilogue_sunk;  // per group step: the combined kernel runs at the group's step
   // Runs of consecutive small, independent fused groups launched as one kernel (merge_sets):
   // merged[m] replaces steps first..last when all of them run; merged_at[k] is the run starting
   // at step k, or -1. The single-step functions stay for partial ranges and per-step timing.
@@ -659,19 +662,223 @@ std::vector<int64_t> step_reads(const Step& st) {
   return r;
 }
 
+bool has_slot(const std::vector<int64_t>& v, int64_t x) { return std::find(v.begin(), v.end(), x) != v.end(); }
+
+bool flat_product(const Instr& i, uint64_t* m, uint64_t* n, uint64_t* k, bool* ta, bool* tb);
+
+// Product `i` launched through `fk`, its kernel with group `f` as the epilogue (generate_gemm):
+// the tile kernel's arguments, then the pointers of the epilogue (the product's output when
+// `store_c`, else null; the group's inputs; its outputs), one kernel argument each.
+StepFn lower_product_epilogue(const Instr& i, const rgplan::Fused& f, const rgjit::FusedKernel* fk, bool store_c) {
+  uint64_t m, n, k;
+  bool ta, tb;
+  rgk::GemmTile t;
+  if (!flat_product(i, &m, &n, &k, &ta, &tb) || !rgk::gemm_epilogue_tile(RG_F32, m, n, k, ta, tb, &t))
+    throw std::runtime_error("product epilogue: the product no longer fits a single tile kernel");
+  std::vector<int64_t> ptr_slots;
+  ptr_slots.push_back(store_c ? i.dst : -1);
+  for (auto& in : f.inputs) ptr_slots.push_back(in.slot);
+  for (auto& o : f.outputs) ptr_slots.push_back(o.second);
+  if (ptr_slots.size() > 128) throw std::runtime_error("product epilogue with more than 127 operands");
+  const int64_t as = i.args[0].slot, bs = i.args[1].slot, bias = i.args.size() == 3 ? i.args[2].slot : -1;
+  const int M = (int)m, N = (int)n, K = (int)k;
+  return [fk, ptr_slots, as, bs, bias, t, M, N, K](hipStream_t s, void* const* sl, void*) {
+    const void* A = sl[as];
+    const void* B = sl[bs];
+    const void* bias_p = bias >= 0 ? sl[bias] : nullptr;
+    int mm = M, nn = N, kk = K, splits = 1, kps = t.kps, swizzle = 1;
+    const void* a_off = nullptr;
+    const void* b_off = nullptr;
+    uint64_t a_stride = 0, b_stride = 0;
+    uint32_t tm = t.tm, tn = t.tn;
+    void* ptrs[128];
+    void* args[15 + 128] = {&A, &B, &mm, &nn, &kk, &a_off, &b_off, &a_stride, &b_stride, &splits, &kps, &bias_p, &tm, &tn, &swizzle};
+    for (size_t q = 0; q < ptr_slots.size(); q++) {
+      ptrs[q] = ptr_slots[q] >= 0 ? sl[ptr_slots[q]] : nullptr;
+      args[15 + q] = &ptrs[q];
+    }
+    hipModuleLaunchKernel(fk->fn, tm * tn, 1, 1, fk->block, 1, 1, 0, s, args, nullptr);
+  };
+}
+
+// Slots a plan step writes (control-flow steps are treated apart by their callers).
+std::vector<int64_t> step_writes(const Step& st) {
+  std::vector<int64_t> w;
+  if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
+    for (auto& o : st.fused.outputs) w.push_back(o.second);
+  } else if (st.kind == RG_STEP_ATTN) {
+    for (auto& v : st.attn.out) w.push_back(v.slot);
+    w.push_back(st.attn.stats_slot);
+    if (st.attn.build_bits) w.push_back(st.attn.mask_bits_slot);
+  } else if (st.instr.dst >= 0) {
+    w.push_back(st.instr.dst);
+  }
+  return w;
+}
+
+// A product instruction as one unbatched M x N x K product (the left operand's batch dims folded
+// into its rows where the right operand is 2-D, as lower_gemm does), or false.
+bool flat_product(const Instr& i, uint64_t* m, uint64_t* n, uint64_t* k, bool* ta, bool* tb) {
+  if (i.op == RG_OP_MATMUL) *ta = *tb = false;
+  else if (i.op == RG_OP_MATMUL_T) *ta = i.attr[0] != 0, *tb = i.attr[1] != 0;
+  else return false;
+  if (i.args.size() < 2) return false;
+  const auto &sa = i.args[0].shape, &sb = i.args[1].shape;
+  if (sa.size() < 2 || sb.size() != 2) return false;
+  const size_t ar = sa.size();
+  if (*ta && ar != 2) return false;
+  uint64_t lead = 1;
+  for (size_t d = 0; d + 2 < ar; d++) lead *= (uint64_t)sa[d];
+  *m = lead * (uint64_t)(*ta ? sa[ar - 1] : sa[ar - 2]);
+  *k = (uint64_t)(*ta ? sa[ar - 2] : sa[ar - 1]);
+  *n = (uint64_t)(*tb ? sb[0] : sb[1]);
+  return true;
+}
+
+// Elementwise groups computed in the epilogue of the product they read (at[j] = k: plain fused
+// group j reads product k's output and runs inside product k's kernel). Taken when product k is
+// one unsplit fp32 MFMA tile product (gemm_epilogue_tile), group j walks its M x N outputs with
+// Full, Row (length a multiple of 4) and Splat inputs and writes none of the product's operands
+// (other blocks of the product still read them while the epilogue stores), and the combined
+// kernel can run at one of the two steps without changing any value, with no control flow
+// between them:
+//  - at step k (`sunk` false) when nothing between them writes what the group reads, or reads or
+//    writes what it writes;
+//  - at step j (`sunk` true) when nothing between them writes the product's operands, or reads or
+//    writes its output (a weight-gradient product between an input-gradient product and the
+//    activation gradient that reads it, whose output reuses the slot the weight gradient reads).
+// Groups small enough to be merged are left to the merged launches. RG_HIP_EPILOGUE=0 turns this
+// off; RG_HIP_EPILOGUE=all also takes products whose output is read elsewhere.
+// Whether product k's output is read by a step other than j (or by the host) before it is next
+// written.
+bool product_output_needed(const Plan& plan, size_t k, size_t j) {
+  const int64_t c = plan.steps[k].instr.dst;
+  for (size_t q = k + 1; q < plan.steps.size(); q++) {
+    if (q != j && has_slot(step_reads(plan.steps[q]), c)) return true;
+    if (has_slot(step_writes(plan.steps[q]), c)) return false;
+  }
+  for (auto& o : plan.outputs)
+    if (o.slot == c) return true;
+  return false;
+}
+
+struct Epilogues {
+  std::vector<int64_t> at;  // per step: the product whose kernel computes this group, or -1
+  std::vector<bool> sunk;   // per group step: the combined kernel runs at the group's step
+};
+
+Epilogues find_epilogues(const Plan& plan) {
+  const auto& steps = plan.steps;
+  const size_t n = steps.size();
+  Epilogues ep{std::vector<int64_t>(n, -1), std::vector<bool>(n, false)};
+  const char* env = getenv("RG_HIP_EPILOGUE");
+  if (env && env[0] == '0') return ep;
+  std::vector<std::vector<int64_t>> reads(n), writes(n);
+  for (size_t q = 0; q < n; q++) {
+    reads[q] = step_reads(steps[q]);
+    writes[q] = step_writes(steps[q]);
+  }
+  std::vector<bool> taken(n, false);
+  for (size_t j = 0; j < n; j++) {
+    const Step& sj = steps[j];
+    if (sj.kind != RG_STEP_FUSED || sj.fused.row_len != 0 || sj.fused.dtype != RG_F32) continue;
+    const rgplan::Fused& f = sj.fused;
+    if (fused_grid(f) <= MERGE_MAX_GRID) continue;
+    bool kinds_ok = true;
+    for (auto& in : f.inputs)
+      kinds_ok = kinds_ok && (in.kind == RG_ARG_FULL || in.kind == RG_ARG_SPLAT || (in.kind == RG_ARG_ROW && in.row_len % 4 == 0));
+    if (!kinds_ok) continue;
+    // The product: the latest earlier writer of one of the group's Full inputs.
+    for (auto& in : f.inputs) {
+      if (in.kind != RG_ARG_FULL) continue;
+      int64_t k = -1;
+      for (size_t q = j; q-- > 0;)
+        if (has_slot(writes[q], in.slot)) {
+          k = (int64_t)q;
+          break;
+        }
+      if (k < 0 || taken[(size_t)k]) continue;
+      const Step& sk = steps[(size_t)k];
+      if (sk.kind != RG_STEP_INSTR || sk.instr.dtype != RG_F32 || sk.instr.dst != in.slot) continue;
+      uint64_t m, nn, kk;
+      bool ta, tb;
+      rgk::GemmTile tile;
+      if (!flat_product(sk.instr, &m, &nn, &kk, &ta, &tb) || (uint64_t)f.n != m * nn) continue;
+      if (!rgk::gemm_epilogue_tile(RG_F32, m, nn, kk, ta, tb, &tile)) continue;
+      bool ok = true;
+      for (auto& o : f.outputs)
+        for (auto& a : sk.instr.args) ok = ok && o.second != a.slot;
+      bool hoist = ok, sink = ok;
+      for (size_t q = (size_t)k + 1; q < j && (hoist || sink); q++) {
+        const Step& sq = steps[q];
+        if (sq.kind == RG_STEP_INSTR && is_control(sq.instr.op)) hoist = sink = false;
+        for (auto& x : f.inputs) hoist = hoist && !has_slot(writes[q], x.slot);
+        for (auto& o : f.outputs) hoist = hoist && !has_slot(writes[q], o.second) && !has_slot(reads[q], o.second);
+        for (auto& a : sk.instr.args) sink = sink && !has_slot(writes[q], a.slot);
+        sink = sink && !has_slot(writes[q], sk.instr.dst) && !has_slot(reads[q], sk.instr.dst);
+      }
+      if (!hoist && !sink) continue;
+      // A product whose output is read elsewhere too would write it beside the group's outputs, in
+      // a burst after its last tiles, where the plain kernels overlap better (measured on C4's
+      // gelu forward): only products whose output the group alone consumes, unless asked for all.
+      if (product_output_needed(plan, (size_t)k, j) && !(env && std::string(env) == "all")) continue;
+      ep.at[j] = k;
+      ep.sunk[j] = !hoist;
+      taken[(size_t)k] = true;
+      break;
+    }
+  }
+  return ep;
+}
+
 StepFn lower_control(Program& prog, size_t k);
 void place_bodies(Program& prog);
+
+// Source of product `pk`'s kernel with fused step `j` as its epilogue (kernel `prefix`rge`pk`).
+// The product's own output is still stored (`*store_c`) when a later step or the host reads it
+// before it is next written.
+std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::string& prefix, bool* store_c, rgjit::FusedKernel* fk) {
+  const Instr& pi = plan.steps[(size_t)pk].instr;
+  const int64_t c = pi.dst;
+  const bool keep = product_output_needed(plan, (size_t)pk, j);
+  *store_c = keep;
+  uint64_t m, nn, kk;
+  bool ta, tb;
+  rgk::GemmTile t;
+  if (!flat_product(pi, &m, &nn, &kk, &ta, &tb) || !rgk::gemm_epilogue_tile(RG_F32, m, nn, kk, ta, tb, &t))
+    throw std::runtime_error("product epilogue: the product does not fit a single tile kernel");
+  return rgjit::generate_gemm(plan.steps[j].fused, c, keep, rgjit::ProductTile{t.bm, t.bn, t.bk, t.wm, t.wn, t.ms, t.mode, ta, tb},
+                              prefix + "rge" + std::to_string(pk), fk);
+}
 
 void build_program(Program& prog) {
   std::vector<size_t> fold_producer;  // per fold: the step of the row group that writes its partials
   std::ostringstream src;
   std::vector<rgjit::FusedKernel*> kernels;
-  for (size_t k = 0; k < prog.plan.steps.size(); k++) {
+  const size_t n_steps = prog.plan.steps.size();
+  const Epilogues ep = find_epilogues(prog.plan);
+  prog.epilogue_of = ep.at;
+  prog.epilogue_sunk = ep.sunk;
+  std::vector<int64_t> epilogue_at(n_steps, -1);  // product step -> the group it computes
+  for (size_t j = 0; j < n_steps; j++)
+    if (ep.at[j] >= 0) epilogue_at[(size_t)ep.at[j]] = (int64_t)j;
+  std::vector<rgjit::FusedKernel*> kernel_of(n_steps, nullptr);
+  std::vector<bool> store_c(n_steps, false);
+  for (size_t k = 0; k < n_steps; k++) {
     const Step& st = prog.plan.steps[k];
     if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
       auto fk = std::make_unique<rgjit::FusedKernel>();
-      if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), fk.get());
-      else src << rgjit::generate(st.fused, "rgf" + std::to_string(k), fk.get());
+      const int64_t pk = prog.epilogue_of[k];
+      if (pk >= 0) {
+        bool keep = false;
+        src << epilogue_source(prog.plan, k, pk, "", &keep, fk.get());
+        store_c[(size_t)pk] = keep;
+      } else if (st.kind == RG_STEP_ROWS) {
+        src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), fk.get());
+      } else {
+        src << rgjit::generate(st.fused, "rgf" + std::to_string(k), fk.get());
+      }
+      kernel_of[k] = fk.get();
       kernels.push_back(fk.get());
       prog.fused.push_back(std::move(fk));
     }
@@ -709,6 +916,20 @@ void build_program(Program& prog) {
   size_t fi = 0;
   for (size_t k = 0; k < prog.plan.steps.size(); k++) {
     const Step& st = prog.plan.steps[k];
+    if ((st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) && ep.at[k] >= 0) {
+      // Computed by its product's kernel, run here when the product waits for this step.
+      fi++;
+      const size_t pk = (size_t)ep.at[k];
+      if (ep.sunk[k]) prog.steps.push_back(lower_product_epilogue(prog.plan.steps[pk].instr, st.fused, kernel_of[k], store_c[pk]));
+      else prog.steps.push_back([](hipStream_t, void* const*, void*) {});
+      continue;
+    }
+    if (st.kind == RG_STEP_INSTR && epilogue_at[k] >= 0) {
+      const size_t j = (size_t)epilogue_at[k];
+      if (ep.sunk[j]) prog.steps.push_back([](hipStream_t, void* const*, void*) {});
+      else prog.steps.push_back(lower_product_epilogue(st.instr, prog.plan.steps[j].fused, kernel_of[j], store_c[k]));
+      continue;
+    }
     if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
       rgjit::FusedKernel* fk = prog.fused[fi++].get();
       std::vector<int64_t> ins, outs;
@@ -755,10 +976,25 @@ void build_program(Program& prog) {
   // Each fold runs before the first later step reading its output, or right after its producer.
   const size_t n = prog.plan.steps.size();
   prog.folds_due.assign(n + 1, {});
+  // A product and the group in its epilogue read their inputs at the step the combined kernel
+  // runs at.
+  auto reads_at = [&](size_t j) {
+    std::vector<int64_t> r;
+    const bool combined_here = (ep.at[j] >= 0 && ep.sunk[j]) || (epilogue_at[j] >= 0 && !ep.sunk[(size_t)epilogue_at[j]]);
+    const bool moved_away = (ep.at[j] >= 0 && !ep.sunk[j]) || (epilogue_at[j] >= 0 && ep.sunk[(size_t)epilogue_at[j]]);
+    if (!moved_away && !combined_here) return step_reads(prog.plan.steps[j]);
+    if (combined_here) {
+      const size_t g = ep.at[j] >= 0 ? j : (size_t)epilogue_at[j];
+      const size_t pk = (size_t)ep.at[g];
+      for (auto& a : prog.plan.steps[pk].instr.args) r.push_back(a.slot);
+      for (auto& in : prog.plan.steps[g].fused.inputs) r.push_back(in.slot);
+    }
+    return r;
+  };
   for (size_t f = 0; f < prog.folds.size(); f++) {
     size_t due = fold_producer[f] + 1;
     for (size_t j = fold_producer[f] + 1; j < n; j++) {
-      auto r = step_reads(prog.plan.steps[j]);
+      auto r = reads_at(j);
       if (std::find(r.begin(), r.end(), prog.folds[f].out_slot) != r.end()) {
         due = j;
         break;
@@ -1055,6 +1291,7 @@ void run_cond(hipStream_t s, const Program::Control& c, const Program& owner, co
 std::string plan_source(const Plan& root, int* count) {
   std::ostringstream src;
   std::function<void(const Plan&, const std::string&)> add = [&](const Plan& plan, const std::string& prefix) {
+    const std::vector<int64_t> epi = find_epilogues(plan).at;
     for (size_t k = 0; k < plan.steps.size(); k++) {
       const auto& st = plan.steps[k];
       if (st.kind == RG_STEP_INSTR && is_control(st.instr.op)) {
@@ -1065,7 +1302,9 @@ std::string plan_source(const Plan& root, int* count) {
       }
       if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
       rgjit::FusedKernel fk;
-      if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, prefix + "rgr" + std::to_string(k), &fk);
+      bool keep;
+      if (epi[k] >= 0) src << epilogue_source(plan, k, epi[k], prefix, &keep, &fk);
+      else if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, prefix + "rgr" + std::to_string(k), &fk);
       else src << rgjit::generate(st.fused, prefix + "rgf" + std::to_string(k), &fk);
       (*count)++;
     }
@@ -1451,6 +1690,16 @@ uint64_t rg_hip_program_allocated_bytes(void* program) {
   size_t free_b = 0, total = 0;
   if (hipMemGetInfo(&free_b, &total) != hipSuccess) return 0;
   return total - free_b;
+}
+
+int64_t rg_hip_program_step_runs_in(void* program, int64_t step) {
+  const auto* p = (const Program*)program;
+  if (step < 0 || (size_t)step >= p->plan.steps.size()) return -1;
+  const size_t k = (size_t)step;
+  if (p->epilogue_of[k] >= 0) return p->epilogue_sunk[k] ? step : p->epilogue_of[k];
+  for (size_t j = 0; j < p->epilogue_of.size(); j++)
+    if (p->epilogue_of[j] == step && p->epilogue_sunk[j]) return (int64_t)j;
+  return step;
 }
 
 void rg_hip_program_inject_failure(void* program) { ((Program*)program)->fail_in = 0; }

@@ -50,7 +50,7 @@ def test_hip_library_loads_and_exports_every_declared_symbol():
 # the run loop for callers that cannot allocate (a device-only entry point the engine does not bind).
 OPTIONAL = {"rg_hip_exec_step_timed", "rg_hip_exec_breakdown", "rg_hip_exec_run", "rg_hip_exec_time_steps", "rg_hip_compile_check",
             "rg_hip_device_memory_bytes", "rg_hip_exec_run_noalloc", "rg_hip_gemm_streamed", "rg_hip_device_peaks",
-            "rg_hip_kernel_source"}
+            "rg_hip_kernel_source", "rg_hip_program_step_runs_in"}
 
 
 def test_oracle_implements_the_same_abi():
@@ -129,6 +129,42 @@ def test_kernels_inside_control_flow_bodies_compile_for_gfx950():
     words_body, _ = _rg.plan_words(g.g, [last], "hip", "standard")
     n_body, err = _compile_check(words_body)
     assert n_body >= 1, err
+
+
+def _step_words(step, state):
+    from rustautograd_amd import _pytree
+    from rustautograd_amd.tensor import Tracer, lift, tracing
+    leaves, in_def = _pytree.flatten((state,))
+    g = _rg.Graph()
+    tracers = [Tracer(g, g.input(list(t.shape), t.dtype, None)) for t in leaves]
+    with tracing(g):
+        out = step(*_pytree.unflatten(in_def, tracers))
+        ids = [lift(g, leaf, "float32") for leaf in _pytree.leaves(out)]
+    words, _ = _rg.plan_words(g, ids, "hip", "search-linear")
+    return words
+
+
+def _kernel_source(words):
+    lib = ctypes.CDLL(_native.HIP_LIBRARY)
+    buf = ctypes.create_string_buffer(8 << 20)
+    arr = (ctypes.c_int64 * len(words))(*words)
+    n = lib.rg_hip_kernel_source(arr, len(words), buf, len(buf))
+    assert n >= 0, buf.value[:500]
+    return buf.value.decode()
+
+
+def test_product_epilogue_kernels_compile_for_gfx950(monkeypatch):
+    """C2's hidden-layer activation gradient reads only an input-gradient product: it is generated
+    as that product's epilogue (the tile of gemm_mfma.h compiled with hiprtc), and the program's
+    kernels compile. With RG_HIP_EPILOGUE=0 every group keeps its own kernel."""
+    step, state = workloads.mlp_train_step()
+    words = _step_words(step, state)
+    src = _kernel_source(words)
+    assert src.count("rgg::gemm_mfma_block<") == 1 and "amdgpu_waves_per_eu(2)" in src
+    n, err = _compile_check(words)
+    assert n >= 5, err
+    monkeypatch.setenv("RG_HIP_EPILOGUE", "0")
+    assert "rgg::gemm_mfma_block<" not in _kernel_source(words)
 
 
 def test_c3_program_compiles_for_gfx950():

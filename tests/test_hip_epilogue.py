@@ -1,0 +1,45 @@
+"""Elementwise groups computed in the epilogue of the product they read, against the same program
+with every group in its own kernel (RG_HIP_EPILOGUE=0).
+
+The combined kernel applies the group's operations, in the group's order, to the product's
+finished outputs (the values the product's own kernel would have stored), so the two programs
+must agree bit for bit: the state after a device loop of C2 and after one C4 step, every loss on
+the way. `step_runs_in` names the pairs: C2's hidden-layer activation gradient reads only its
+input-gradient product; C4's six gelu backward groups read only theirs (five run at the
+product's step, the last layer's at its own, since the weight-gradient product between them
+reads the slot the group writes).
+"""
+
+import numpy as np
+import pytest
+
+import rustautograd_amd as rg
+from rustautograd_amd import _pytree, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _pairs(compiled):
+    runs_in = compiled._n.step_runs_in()
+    return [(k, r) for k, r in enumerate(runs_in) if r != k]
+
+
+def _bits(tree):
+    return [np.atleast_1d(np.asarray(x.numpy())).view(np.uint8) for x in _pytree.leaves(tree)]
+
+
+@pytest.mark.parametrize("name,steps,pairs", [("C2", 5, 1), ("C4", 1, 6)])
+def test_products_with_epilogues_match_separate_kernels_bit_for_bit(monkeypatch, name, steps, pairs):
+    step, state = workloads.mlp_train_step() if name == "C2" else workloads.gpt_train_step(workloads.GPT_CONFIGS[name])
+    print(f"{name}: compile with and without product epilogues, {steps} device steps", flush=True)
+    monkeypatch.setenv("RG_HIP_EPILOGUE", "0")
+    plain = rg.compile(step, (state,), validate="none", device="hip")
+    monkeypatch.delenv("RG_HIP_EPILOGUE")
+    fused = rg.compile(step, (state,), validate="none", device="hip")
+    assert _pairs(plain) == [] and len(_pairs(fused)) == pairs, _pairs(fused)
+    r0 = rg.run(plain, state, steps=steps)
+    r1 = rg.run(fused, state, steps=steps)
+    assert r0.status == r1.status == "completed"
+    assert np.array_equal(np.array(r0.history["aux"]).view(np.uint64), np.array(r1.history["aux"]).view(np.uint64))
+    for a, b in zip(_bits(r0.state), _bits(r1.state)):
+        assert np.array_equal(a, b)
