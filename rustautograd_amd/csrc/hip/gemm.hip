@@ -401,15 +401,15 @@ int split_count(const TileCfg& t, uint64_t m, uint64_t n, uint64_t k, uint64_t b
 // (512), then 128x64 at two blocks per CU; 128x64 with eight waves (two per SIMD) at one block per
 // CU, and for long-K products with at least 32 such tiles (split over K to 256 blocks); 64x128 at
 // one block per CU; 64x64 (split over K when that leaves the CUs idle); 32x32 when even split
-// 64x64 tiles come to fewer than 256 blocks (C3's products).
-TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch, bool tb) {
+// 64x64 tiles come to fewer than 256 blocks (C3's products). The same shapes whichever operand is
+// K-contiguous: with the non-temporal output stores, 64x64 tiles of 32x32 MFMAs, once faster for a
+// K-contiguous B, are 1-9 % slower than 128x64 ones on C4's input-gradient products.
+TileCfg pick_tile(uint64_t m, uint64_t n, uint64_t k, uint64_t batch) {
   auto blocks = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch; };
   if (n <= 96 && n % 32 == 0) return {128, 32, 32, 4, 1};
   if (m <= 32) return {32, 128, 32, 1, 4};
   if (blocks(128, 128) >= 512) return {128, 128, 16, 2, 2};
   if (blocks(128, 64) >= 512) return {128, 64, 16, 2, 2};
-  // With a K-contiguous B, 32x32 MFMAs on 64x64 tiles (two blocks per CU) do slightly better.
-  if (tb && blocks(128, 64) >= 256) return {64, 64, 32, 2, 2, 32};
   if (blocks(128, 64) >= 256 || (blocks(128, 64) >= 32 && k >= 4096)) return {128, 64, 32, 2, 4};
   if (blocks(64, 128) >= 256) return {64, 128, 32, 2, 2};
   // Small outputs: 32x32 tiles when 64x64 ones, split over K where K allows, would leave most
@@ -476,7 +476,6 @@ void launch_mfma(hipStream_t s, const TileCfg& t, bool ta, bool tb, int mode, co
   RG_TILE(32, 128, 32, 1, 4);
   RG_TILE(32, 32, 32, 2, 2);
 #undef RG_TILE
-  if (t.bm == 64 && t.bn == 64 && t.bk == 32 && t.wm == 2 && t.wn == 2 && t.ms == 32) return launch_flags<64, 64, 32, 2, 2, 32>(s, ta, tb, mode, l);
 }
 
 }  // namespace
@@ -498,7 +497,7 @@ int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, b
     return (int)((sk.k + kps - 1) / kps);
   }
   if (sk.kind != SKINNY_NONE || !use_mfma(dtype, m, n, k)) return 1;
-  TileCfg t = pick_tile(m, n, k, batch, tb);
+  TileCfg t = pick_tile(m, n, k, batch);
   int splits = split_count(t, m, n, k, batch);
   uint64_t kps = ((k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk;
   return (int)((k + kps - 1) / kps);
@@ -507,7 +506,7 @@ int gemm_splits(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t batch, b
 bool gemm_epilogue_tile(int dtype, uint64_t m, uint64_t n, uint64_t k, bool ta, bool tb, GemmTile* out) {
   if (m == 0 || n == 0 || m >= (1ull << 31) || n >= (1ull << 31) || k >= (1ull << 31)) return false;
   if (skinny_plan(dtype, m, n, k, 1, ta, tb).kind != SKINNY_NONE || !use_mfma(dtype, m, n, k)) return false;
-  const TileCfg t = pick_tile(m, n, k, 1, tb);
+  const TileCfg t = pick_tile(m, n, k, 1);
   if (split_count(t, m, n, k, 1) != 1) return false;
   // Runs of four adjacent output columns per lane: always with a K-contiguous B (the transposed
   // product form), with an N-contiguous B when each wave holds four tiles across N.
@@ -617,7 +616,7 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     if (g.defer_split) throw std::runtime_error("deferred K-split product: the streaming kernel refused its operands");
   }
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
-    TileCfg t = pick_tile(g.m, g.n, g.k, g.batch, g.tb);
+    TileCfg t = pick_tile(g.m, g.n, g.k, g.batch);
     int splits = split_count(t, g.m, g.n, g.k, g.batch);
     int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
     splits = (int)((g.k + kps - 1) / kps);

@@ -20,6 +20,7 @@ struct IC {
   static constexpr int value = V;
 };
 
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int64_t batch_offset(const int64_t* offs, uint64_t stride, uint32_t b) {
@@ -130,7 +131,10 @@ __device__ __forceinline__ void lds_read(const float* p, float* v) {
 // blocks (tile_of); split `sp` covers K range [sp * k_per_split, (sp + 1) * k_per_split).
 
 // The plain epilogue: each finished output (flat index `e` within the block's output matrix) is
-// stored into C, or into the block's split of the K-split partials.
+// stored into C, or into the block's split of the K-split partials. Non-temporal stores: every
+// block writes its whole tile at the end, all at once; written past the L2 they leave less for the
+// end of the kernel to write back (4-10 % off C4's products with 1024- and 768-wide outputs on
+// MI355X, results unchanged).
 struct StoreC {
   float* C;
   float* partial;
@@ -140,9 +144,9 @@ struct StoreC {
   __device__ __forceinline__ void begin(uint32_t b, uint32_t sp) {
     out = splits > 1 ? partial + ((uint64_t)b * splits + sp) * mn : C + (uint64_t)b * mn;
   }
-  __device__ __forceinline__ void put4(uint64_t e, float4 v) { *(float4*)(out + e) = v; }
-  __device__ __forceinline__ void put2(uint64_t e, float2 v) { *(float2*)(out + e) = v; }
-  __device__ __forceinline__ void put1(uint64_t e, float v) { out[e] = v; }
+  __device__ __forceinline__ void put4(uint64_t e, float4 v) { __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, (floatx4*)(out + e)); }
+  __device__ __forceinline__ void put2(uint64_t e, float2 v) { __builtin_nontemporal_store(floatx2{v.x, v.y}, (floatx2*)(out + e)); }
+  __device__ __forceinline__ void put1(uint64_t e, float v) { __builtin_nontemporal_store(v, out + e); }
 };
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE, int MS, class Epi>
