@@ -512,9 +512,9 @@ bool gemm_epilogue_tile(int dtype, uint64_t m, uint64_t n, uint64_t k, bool ta, 
   // the combined kernels on MI355X, results unchanged).
   if (t.bm == 128 && t.bn == 128 && k <= 1024) t = TileCfg{128, 64, 16, 2, 2};
   if (split_count(t, m, n, k, 1) != 1) return false;
-  // Runs of four adjacent output columns per lane: always with a K-contiguous B (the transposed
-  // product form), with an N-contiguous B when each wave holds four tiles across N.
-  if (!tb && (t.bn / t.wn) / t.ms != 4) return false;
+  // Runs of adjacent output columns per lane: four with a K-contiguous B (the transposed product
+  // form); with an N-contiguous B one per tile the wave holds across N, which must be two or four.
+  if (!tb && (t.bn / t.wn) / t.ms != 4 && (t.bn / t.wn) / t.ms != 2) return false;
   const bool vec = k % 4 == 0 && (!ta || m % 4 == 0) && (tb || n % 4 == 0) && n % 4 == 0;
   if (!vec) return false;
   const bool even = m % t.bm == 0 && n % t.bn == 0 && k % t.bk == 0;

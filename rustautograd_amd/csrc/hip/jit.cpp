@@ -207,6 +207,7 @@ std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, 
         b << "    float " << x << "[" << W << "];\n";
         if (W == 4) b << "    { const float4 t = *(const float4*)(in" << j << " + " << at << "); " << x << "[0] = t.x; " << x << "[1] = t.y; " << x
                       << "[2] = t.z; " << x << "[3] = t.w; }\n";
+        else if (W == 2) b << "    { const float2 t = *(const float2*)(in" << j << " + " << at << "); " << x << "[0] = t.x; " << x << "[1] = t.y; }\n";
         else b << "    " << x << "[0] = in" << j << "[" << at << "];\n";
         in_expr[j] = x + "[v]";
       } else {
@@ -232,6 +233,7 @@ std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, 
     b << "    }\n";
     for (size_t j = 0; j < f.outputs.size(); j++) {
       if (W == 4) b << "    *(float4*)(out" << j << " + e) = make_float4(o" << j << "[0], o" << j << "[1], o" << j << "[2], o" << j << "[3]);\n";
+      else if (W == 2) b << "    *(float2*)(out" << j << " + e) = make_float2(o" << j << "[0], o" << j << "[1]);\n";
       else b << "    out" << j << "[e] = o" << j << "[0];\n";
     }
     return b.str();
@@ -242,7 +244,9 @@ std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, 
   s << "  __device__ __forceinline__ void put1(unsigned long long e, float acc) {\n";
   if (store_c) s << "    c[e] = acc;\n";
   s << "    const float a[1] = {acc};\n" << body(1) << "  }\n";
-  s << "  __device__ __forceinline__ void put2(unsigned long long e, float2 acc) { put1(e, acc.x); put1(e + 1, acc.y); }\n";
+  s << "  __device__ __forceinline__ void put2(unsigned long long e, float2 acc) {\n";
+  if (store_c) s << "    *(float2*)(c + e) = acc;\n";
+  s << "    const float a[2] = {acc.x, acc.y};\n" << body(2) << "  }\n";
   s << "};\n";
   const int nt = 64 * t.wm * t.wn;
   // At least two waves per SIMD (at most 256 registers a wave, far above what the tile uses): with

@@ -747,8 +747,16 @@ bool flat_product(const Instr& i, uint64_t* m, uint64_t* n, uint64_t* k, bool* t
 //  - at step j (`sunk` true) when nothing between them writes the product's operands, or reads or
 //    writes its output (a weight-gradient product between an input-gradient product and the
 //    activation gradient that reads it, whose output reuses the slot the weight gradient reads).
-// Groups small enough to be merged are left to the merged launches. RG_HIP_EPILOGUE=0 turns this
-// off; RG_HIP_EPILOGUE=all also takes products whose output is read elsewhere.
+// Groups small enough to be merged are left to the merged launches. The product's kernel also
+// stores its own output when another step reads it. Only products of at least
+// EPILOGUE_MIN_TILES tiles are taken: every block of a product ends its K loop at about the
+// same time, and the epilogue's loads and stores then run with no products beside them unless a
+// second round of blocks is still multiplying (measured on MI355X: C4's GELU forward and
+// backward, 8192 x 1024 outputs in 1024 tiles, 1.7 % off the step; C2's activation gradient and
+// its 2048 x 2048 AdamW update, 512 tiles each, 1.1 % slower fused). RG_HIP_EPILOGUE=0 turns
+// this off; RG_HIP_EPILOGUE=all takes every product that qualifies otherwise.
+constexpr uint64_t EPILOGUE_MIN_TILES = 1024;  // two rounds of two blocks on each of 256 CUs
+
 // Whether product k's output is read by a step other than j (or by the host) before it is next
 // written.
 bool product_output_needed(const Plan& plan, size_t k, size_t j) {
@@ -773,6 +781,7 @@ Epilogues find_epilogues(const Plan& plan) {
   Epilogues ep{std::vector<int64_t>(n, -1), std::vector<bool>(n, false)};
   const char* env = getenv("RG_HIP_EPILOGUE");
   if (env && env[0] == '0') return ep;
+  const bool every = env && std::string(env) == "all";
   std::vector<std::vector<int64_t>> reads(n), writes(n);
   for (size_t q = 0; q < n; q++) {
     reads[q] = step_reads(steps[q]);
@@ -805,6 +814,7 @@ Epilogues find_epilogues(const Plan& plan) {
       rgk::GemmTile tile;
       if (!flat_product(sk.instr, &m, &nn, &kk, &ta, &tb) || (uint64_t)f.n != m * nn) continue;
       if (!rgk::gemm_epilogue_tile(RG_F32, m, nn, kk, ta, tb, &tile)) continue;
+      if (!every && (uint64_t)tile.tm * tile.tn < EPILOGUE_MIN_TILES) continue;
       bool ok = true;
       for (auto& o : f.outputs)
         for (auto& a : sk.instr.args) ok = ok && o.second != a.slot;
@@ -818,10 +828,6 @@ Epilogues find_epilogues(const Plan& plan) {
         sink = sink && !has_slot(writes[q], sk.instr.dst) && !has_slot(reads[q], sk.instr.dst);
       }
       if (!hoist && !sink) continue;
-      // A product whose output is read elsewhere too would write it beside the group's outputs, in
-      // a burst after its last tiles, where the plain kernels overlap better (measured on C4's
-      // gelu forward): only products whose output the group alone consumes, unless asked for all.
-      if (product_output_needed(plan, (size_t)k, j) && !(env && std::string(env) == "all")) continue;
       ep.at[j] = k;
       ep.sunk[j] = !hoist;
       taken[(size_t)k] = true;

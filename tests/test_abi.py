@@ -154,17 +154,33 @@ def _kernel_source(words):
 
 
 def test_product_epilogue_kernels_compile_for_gfx950(monkeypatch):
-    """C2's hidden-layer activation gradient reads only an input-gradient product: it is generated
-    as that product's epilogue (the tile of gemm_mfma.h compiled with hiprtc), and the program's
-    kernels compile. With RG_HIP_EPILOGUE=0 every group keeps its own kernel."""
-    step, state = workloads.mlp_train_step()
-    words = _step_words(step, state)
+    """An elementwise group that reads a product of at least 1024 tiles (8192 x 1024 outputs) is
+    generated as that product's epilogue (the tile of gemm_mfma.h compiled with hiprtc), and the
+    program's kernels compile; with RG_HIP_EPILOGUE=0 every group keeps its own kernel. In C2 only
+    the first layer's product has 1024 tiles (its activation, two adjacent columns per lane on an
+    N-contiguous weight); RG_HIP_EPILOGUE=all takes the 512-tile ones too: the second layer's
+    activation, the activation gradient (four adjacent columns per lane) and an AdamW update in
+    a weight gradient's epilogue."""
+    g = G()
+    x, w = g.input((8192, 256), "float32"), g.input((256, 1024), "float32")
+    y = g.op("matmul", [x, w])
+    z = g.un("tanh", g.bin("mul", y, y))
+    words, _ = _rg.plan_words(g.g, [z], "hip", "standard")
     src = _kernel_source(words)
     assert src.count("rgg::gemm_mfma_block<") == 1 and "amdgpu_waves_per_eu(2)" in src
     n, err = _compile_check(words)
-    assert n >= 5, err
+    assert n >= 1, err
     monkeypatch.setenv("RG_HIP_EPILOGUE", "0")
     assert "rgg::gemm_mfma_block<" not in _kernel_source(words)
+    step, state = workloads.mlp_train_step()
+    monkeypatch.delenv("RG_HIP_EPILOGUE")
+    words = _step_words(step, state)
+    assert _kernel_source(words).count("rgg::gemm_mfma_block<") == 1
+    monkeypatch.setenv("RG_HIP_EPILOGUE", "all")
+    src = _kernel_source(words)
+    assert src.count("rgg::gemm_mfma_block<") == 4, src.count("rgg::gemm_mfma_block<")
+    n, err = _compile_check(words)
+    assert n >= 5, err
 
 
 def test_c3_program_compiles_for_gfx950():

@@ -3,11 +3,14 @@ with every group in its own kernel (RG_HIP_EPILOGUE=0).
 
 The combined kernel applies the group's operations, in the group's order, to the product's
 finished outputs (the values the product's own kernel would have stored), so the two programs
-must agree bit for bit: the state after a device loop of C2 and after one C4 step, every loss on
-the way. `step_runs_in` names the pairs: C2's hidden-layer activation gradient reads only its
-input-gradient product; C4's six gelu backward groups read only theirs (five run at the
+must agree bit for bit: the state after one C4 step and after a device loop of C2, every loss on
+the way. `step_runs_in` names the pairs. C4 has twelve: each layer's GELU forward, computed by
+the first MLP product, which also stores its own output for the backward pass, and each layer's
+GELU backward, computed by the product that forms the activation gradient (five at the
 product's step, the last layer's at its own, since the weight-gradient product between them
-reads the slot the group writes).
+reads the slot the group writes). C2 has one by default (its first layer's activation: the only
+product of at least 1024 tiles) and four with RG_HIP_EPILOGUE=all, among them a weight gradient
+that runs its parameter's whole AdamW update in its epilogue.
 """
 
 import numpy as np
@@ -28,13 +31,16 @@ def _bits(tree):
     return [np.atleast_1d(np.asarray(x.numpy())).view(np.uint8) for x in _pytree.leaves(tree)]
 
 
-@pytest.mark.parametrize("name,steps,pairs", [("C2", 5, 1), ("C4", 1, 6)])
-def test_products_with_epilogues_match_separate_kernels_bit_for_bit(monkeypatch, name, steps, pairs):
+@pytest.mark.parametrize("name,mode,steps,pairs", [("C4", None, 1, 12), ("C2", None, 5, 1), ("C2", "all", 5, 4)])
+def test_products_with_epilogues_match_separate_kernels_bit_for_bit(monkeypatch, name, mode, steps, pairs):
     step, state = workloads.mlp_train_step() if name == "C2" else workloads.gpt_train_step(workloads.GPT_CONFIGS[name])
-    print(f"{name}: compile with and without product epilogues, {steps} device steps", flush=True)
+    print(f"{name}: compile with and without product epilogues ({mode or 'default'}), {steps} device steps", flush=True)
     monkeypatch.setenv("RG_HIP_EPILOGUE", "0")
     plain = rg.compile(step, (state,), validate="none", device="hip")
-    monkeypatch.delenv("RG_HIP_EPILOGUE")
+    if mode:
+        monkeypatch.setenv("RG_HIP_EPILOGUE", mode)
+    else:
+        monkeypatch.delenv("RG_HIP_EPILOGUE")
     fused = rg.compile(step, (state,), validate="none", device="hip")
     assert _pairs(plain) == [] and len(_pairs(fused)) == pairs, _pairs(fused)
     r0 = rg.run(plain, state, steps=steps)
