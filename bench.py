@@ -42,7 +42,8 @@ def classify(plan, runs_in=None):
     product that computes an elementwise group in its epilogue, and that group, form their own
     class (`gemm_mfma_epilogue`: the product's flops, the group's bytes beside the product's, one
     launch), so the combined kernel's time is neither charged to the plain products nor counted
-    as elementwise work done in no time."""
+    as elementwise work done in no time. Two products launched as one kernel stay in their class
+    with their flops, counted as one launch."""
     classes = {}
     runs_in = runs_in or list(range(len(plan)))
     partner = {}
@@ -60,8 +61,12 @@ def classify(plan, runs_in=None):
         c["bytes"] += st["bytes"]
         c["launches"] += 1 if launch else 0
 
+    def is_product(q):
+        return plan[q]["kind"] == "instr" and plan[q].get("op") in ("matmul", "matmul_t")
+
     for k, st in enumerate(plan):
-        if k in partner:
+        paired = k in partner and is_product(k) and is_product(partner[k])
+        if k in partner and not paired:
             product = st["kind"] != "fused"
             add("gemm_mfma_epilogue", k, st if product else dict(st, bound="hbm"), launch=product)
         elif st["kind"] == "attention":
@@ -72,10 +77,11 @@ def classify(plan, runs_in=None):
             shape = st["shape"]
             n_cols = shape[-1] if shape else 1
             m_rows = _numel(shape) // max(n_cols, 1)
+            launch = not paired or runs_in[k] == k
             if st["bound"] != "mfma":
-                add("gemm_skinny", k, st)
+                add("gemm_skinny", k, st, launch=launch)
             else:
-                add("gemm_mfma" if len(shape) >= 2 and n_cols >= 32 and m_rows >= 32 else "gemm_plain", k, st)
+                add("gemm_mfma" if len(shape) >= 2 and n_cols >= 32 and m_rows >= 32 else "gemm_plain", k, st, launch=launch)
         elif st["op"] in ("sum", "max", "min"):
             add("reduce", k, st)
         elif st["op"] in ("take", "take_along", "take_grad", "take_along_grad"):

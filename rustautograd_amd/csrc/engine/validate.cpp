@@ -874,12 +874,23 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
   // A fused group the device computes in a product's epilogue (step_runs_in pairs the two) is
   // counted in the product's row: its time (the combined kernel runs at one of the two steps) and
   // its bytes, with no launch or flops of its own.
+  // Two products the device launches together (one kernel at the first one's step) keep their
+  // own rows; the kernel's time is shared between them in proportion to their flops.
   std::vector<size_t> row_of(plan.steps.size());
+  std::vector<double> sec = seconds;
+  auto plain = [&](size_t q) { return !plan.steps[q].fused && !plan.steps[q].attn; };
   for (size_t s = 0; s < plan.steps.size(); s++) row_of[s] = s;
   for (size_t s = 0; s < plan.steps.size(); s++) {
     const int64_t r = program->step_runs_in((int64_t)s);
     if (r < 0 || (size_t)r == s || (size_t)r >= plan.steps.size()) continue;
-    const size_t product = !plan.steps[s].fused && !plan.steps[s].attn ? s : (size_t)r;
+    if (plain(s) && plain((size_t)r)) {
+      const double fa = step_work(plan.steps[(size_t)r], streamed).flops, fb = step_work(plan.steps[s], streamed).flops;
+      const double both = sec[(size_t)r] + sec[s];
+      sec[(size_t)r] = fa + fb > 0 ? both * fa / (fa + fb) : both;
+      sec[s] = both - sec[(size_t)r];
+      continue;
+    }
+    const size_t product = plain(s) ? s : (size_t)r;
     row_of[s] = row_of[(size_t)r] = product;
   }
   for (size_t s0 = 0; s0 < plan.steps.size(); s0++) {
@@ -905,7 +916,7 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
     if (dt == DType::F64) key += " f64";
     const StepWork w = step_work(st, streamed);
     Row& r = rows[key];
-    r.seconds += seconds[s0];
+    r.seconds += sec[s0];
     if (s0 != s) {  // the group in the product's epilogue
       r.bytes += step_work(plan.steps[s0], streamed).bytes;
       continue;

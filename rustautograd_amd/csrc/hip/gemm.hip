@@ -46,6 +46,34 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
                                                               tiles_m, tiles_n, swizzle, epi);
 }
 
+// One unbatched product's share of a paired launch (k_gemm_mfma_pair).
+struct PairPart {
+  const float *a, *b;
+  float *c, *part;
+  const float* bias;
+  int m, n, k, splits, kps;
+  uint32_t tm, tn, blocks;
+};
+
+// Two independent unbatched products on one tile shape in one launch: blocks [0, p0.blocks)
+// compute product 0, the rest product 1, both staging through the same LDS. Each block runs the
+// code of a single-product launch, so every output gets the same bits; the launch's fixed cost
+// is paid once, and the two grids (each about one block per CU) run side by side.
+template <int BM, int BN, int BK, int WM, int WN, bool TA0, bool TB0, bool TA1, bool TB1>
+__global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma_pair(PairPart p0, PairPart p1) {
+  constexpr int F0 = TileLds<BM, BN, BK, TA0, TB0>::FLOATS, F1 = TileLds<BM, BN, BK, TA1, TB1>::FLOATS;
+  __shared__ float smem[F0 > F1 ? F0 : F1];
+  if (blockIdx.x < p0.blocks) {
+    StoreC epi{p0.c, p0.part, p0.splits, (uint64_t)p0.m * p0.n};
+    gemm_mfma_tile<BM, BN, BK, WM, WN, TA0, TB0, LOAD_EVEN, 16>(p0.a, p0.b, p0.m, p0.n, p0.k, nullptr, nullptr, 0, 0, p0.splits, p0.kps,
+                                                                 p0.bias, p0.tm, p0.tn, 1, epi, blockIdx.x, p0.blocks, smem);
+  } else {
+    StoreC epi{p1.c, p1.part, p1.splits, (uint64_t)p1.m * p1.n};
+    gemm_mfma_tile<BM, BN, BK, WM, WN, TA1, TB1, LOAD_EVEN, 16>(p1.a, p1.b, p1.m, p1.n, p1.k, nullptr, nullptr, 0, 0, p1.splits, p1.kps,
+                                                                 p1.bias, p1.tm, p1.tn, 1, epi, blockIdx.x - p0.blocks, p1.blocks, smem);
+  }
+}
+
 // Sums the K-split partial products in split order. Four outputs per thread (16-byte loads when
 // M N is a multiple of 4), all splits' loads issued before the adds.
 __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ partial, float* __restrict__ C, uint64_t mn, int splits,
@@ -607,6 +635,55 @@ bool gemm_skinny(hipStream_t s, const GemmArgs& g, const Skinny& sk) {
   return true;
 }
 
+namespace {
+
+// The MFMA tile launch of product `g`: its tile, load mode and launch arguments.
+void mfma_launch(const GemmArgs& g, TileCfg* tile, int* load_mode, Launch* launch) {
+  TileCfg t = pick_tile(g.m, g.n, g.k, g.batch);
+  int splits = split_count(t, g.m, g.n, g.k, g.batch);
+  int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
+  splits = (int)((g.k + kps - 1) / kps);
+  if (g.defer_split && splits != g.planned_splits)
+    throw std::runtime_error("deferred K-split product: " + std::to_string(splits) + " partial products, the fold expects " +
+                             std::to_string(g.planned_splits));
+  // 16-byte vector loads need 16-byte aligned operand rows: aligned bases, leading dimensions
+  // (K, or M / N for the contiguous-column layouts) and batch offsets that are multiples of 4.
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  bool vec = aligned(g.a) && aligned(g.b) && g.k % 4 == 0 && (!g.ta || g.m % 4 == 0) && (g.tb || g.n % 4 == 0) &&
+             (g.a_off ? g.a_off4 : g.a_stride % 4 == 0) && (g.b_off ? g.b_off4 : g.b_stride % 4 == 0);
+  bool even = g.m % t.bm == 0 && g.n % t.bn == 0 && g.k % t.bk == 0 && kps % t.bk == 0;
+  int mode = !vec ? LOAD_SCALAR : even ? LOAD_EVEN : LOAD_VEC;
+  Launch l;
+  l.tm = (uint32_t)((g.m + t.bm - 1) / t.bm);
+  l.tn = (uint32_t)((g.n + t.bn - 1) / t.bn);
+  l.grid = dim3((uint32_t)(l.tm * l.tn * g.batch * splits));
+  l.a = (const float*)g.a;
+  l.b = (const float*)g.b;
+  l.c = (float*)g.c;
+  l.m = (int)g.m;
+  l.n = (int)g.n;
+  l.k = (int)g.k;
+  l.a_off = g.a_off;
+  l.b_off = g.b_off;
+  l.as = g.a_stride;
+  l.bs = g.b_stride;
+  l.splits = splits;
+  l.kps = kps;
+  l.part = splits > 1 ? (float*)g.workspace : nullptr;
+  l.bias = splits > 1 ? nullptr : (const float*)g.bias;
+  *tile = t;
+  *load_mode = mode;
+  *launch = l;
+}
+
+// Whether product `g` goes to the MFMA tiles (not a streaming kernel, not the plain kernel).
+bool on_mfma_tiles(const GemmArgs& g) {
+  return g.m && g.n && g.batch && skinny_plan(g.dtype, g.m, g.n, g.k, g.batch, g.ta, g.tb).kind == SKINNY_NONE &&
+         use_mfma(g.dtype, g.m, g.n, g.k);
+}
+
+}  // namespace
+
 // Plan slots start 256-byte aligned, so a lowered product always meets the skinny kernels'
 // alignment. A product whose K-split partials are deferred to the fold area must leave exactly
 // the planned number of partial products there: a launch that would take another path (the
@@ -620,38 +697,11 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     if (g.defer_split) throw std::runtime_error("deferred K-split product: the streaming kernel refused its operands");
   }
   if (use_mfma(g.dtype, g.m, g.n, g.k)) {
-    TileCfg t = pick_tile(g.m, g.n, g.k, g.batch);
-    int splits = split_count(t, g.m, g.n, g.k, g.batch);
-    int kps = (int)(((g.k + splits - 1) / splits + t.bk - 1) / t.bk * t.bk);
-    splits = (int)((g.k + kps - 1) / kps);
-    if (g.defer_split && splits != g.planned_splits)
-      throw std::runtime_error("deferred K-split product: " + std::to_string(splits) + " partial products, the fold expects " +
-                               std::to_string(g.planned_splits));
-    // 16-byte vector loads need 16-byte aligned operand rows: aligned bases, leading dimensions
-    // (K, or M / N for the contiguous-column layouts) and batch offsets that are multiples of 4.
-    auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-    bool vec = aligned(g.a) && aligned(g.b) && g.k % 4 == 0 && (!g.ta || g.m % 4 == 0) && (g.tb || g.n % 4 == 0) &&
-               (g.a_off ? g.a_off4 : g.a_stride % 4 == 0) && (g.b_off ? g.b_off4 : g.b_stride % 4 == 0);
-    bool even = g.m % t.bm == 0 && g.n % t.bn == 0 && g.k % t.bk == 0 && kps % t.bk == 0;
-    int mode = !vec ? LOAD_SCALAR : even ? LOAD_EVEN : LOAD_VEC;
+    TileCfg t;
+    int mode;
     Launch l;
-    l.tm = (uint32_t)((g.m + t.bm - 1) / t.bm);
-    l.tn = (uint32_t)((g.n + t.bn - 1) / t.bn);
-    l.grid = dim3((uint32_t)(l.tm * l.tn * g.batch * splits));
-    l.a = (const float*)g.a;
-    l.b = (const float*)g.b;
-    l.c = (float*)g.c;
-    l.m = (int)g.m;
-    l.n = (int)g.n;
-    l.k = (int)g.k;
-    l.a_off = g.a_off;
-    l.b_off = g.b_off;
-    l.as = g.a_stride;
-    l.bs = g.b_stride;
-    l.splits = splits;
-    l.kps = kps;
-    l.part = splits > 1 ? (float*)g.workspace : nullptr;
-    l.bias = splits > 1 ? nullptr : (const float*)g.bias;
+    mfma_launch(g, &t, &mode, &l);
+    const int splits = l.splits;
     launch_mfma(s, t, g.ta, g.tb, mode, l);
     if (splits > 1 && !g.defer_split) {
       uint64_t mn = g.m * g.n;
@@ -672,6 +722,42 @@ void gemm(hipStream_t s, const GemmArgs& g) {
     const uint64_t total = g.m * g.n * g.batch;
     hipLaunchKernelGGL(k_add_bias, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, (float*)g.c, (const float*)g.bias, total, g.n);
   }
+}
+
+bool gemm_pair(hipStream_t s, const GemmArgs& g0, const GemmArgs& g1, bool launch) {
+  if (!on_mfma_tiles(g0) || !on_mfma_tiles(g1) || g0.batch != 1 || g1.batch != 1) return false;
+  TileCfg t0, t1;
+  int m0, m1;
+  Launch l0, l1;
+  mfma_launch(g0, &t0, &m0, &l0);
+  mfma_launch(g1, &t1, &m1, &l1);
+  // Each product's K-split partials, if any, must be the deferred kind: a split sum after the
+  // paired launch would be a second launch anyway.
+  if ((l0.splits > 1 && !g0.defer_split) || (l1.splits > 1 && !g1.defer_split)) return false;
+  if (m0 != LOAD_EVEN || m1 != LOAD_EVEN || t0.bm != t1.bm || t0.bn != t1.bn || t0.bk != t1.bk || t0.wm != t1.wm || t0.wn != t1.wn ||
+      t0.ms != 16 || t1.ms != 16 || l0.grid.x % 8 != 0)
+    return false;
+  const bool shape = t0.bm == 128 && t0.bn == 64 && t0.bk == 32 && t0.wm == 2 && t0.wn == 4;
+  const bool flags = (!g0.ta && g0.tb && g1.ta && !g1.tb) || (g0.ta && !g0.tb && !g1.ta && g1.tb);
+  if (!launch) return shape && flags;
+  auto part = [](const Launch& l) {
+    return PairPart{l.a, l.b, l.c, l.part, l.bias, l.m, l.n, l.k, l.splits, l.kps, l.tm, l.tn, l.grid.x};
+  };
+  const PairPart p0 = part(l0), p1 = part(l1);
+  const dim3 grid(l0.grid.x + l1.grid.x);
+  // The shapes instantiated: C4's input- and weight-gradient products of a layer's first MLP
+  // product, on 128x64 tiles of eight waves.
+  if (t0.bm == 128 && t0.bn == 64 && t0.bk == 32 && t0.wm == 2 && t0.wn == 4) {
+    if (!g0.ta && g0.tb && g1.ta && !g1.tb) {
+      hipLaunchKernelGGL((k_gemm_mfma_pair<128, 64, 32, 2, 4, false, true, true, false>), grid, dim3(512), 0, s, p0, p1);
+      return true;
+    }
+    if (g0.ta && !g0.tb && !g1.ta && g1.tb) {
+      hipLaunchKernelGGL((k_gemm_mfma_pair<128, 64, 32, 2, 4, true, false, false, true>), grid, dim3(512), 0, s, p0, p1);
+      return true;
+    }
+  }
+  return false;
 }
 
 }  // namespace rgk

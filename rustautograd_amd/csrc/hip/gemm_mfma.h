@@ -35,8 +35,8 @@ struct TileIndex {
   uint32_t tm, tn, z;
 };
 
-__device__ __forceinline__ TileIndex tile_of(uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
-  uint32_t nb = gridDim.x, bid = blockIdx.x;
+// Block `bid` of a product launched as `nb` blocks (its share of the grid).
+__device__ __forceinline__ TileIndex tile_of(uint32_t bid, uint32_t nb, uint32_t tiles_m, uint32_t tiles_n, int swizzle) {
   uint32_t per_batch = tiles_m * tiles_n;
   if (!swizzle) return {(bid % per_batch) / tiles_n, bid % tiles_n, bid / per_batch};
   uint32_t lid = (nb % 8 == 0) ? (bid % 8) * (nb / 8) + bid / 8 : bid;
@@ -149,11 +149,23 @@ struct StoreC {
   __device__ __forceinline__ void put1(uint64_t e, float v) { __builtin_nontemporal_store(v, out + e); }
 };
 
+// LDS of one tile: two buffers of each operand's K step, in the operand's own layout (rows padded
+// by 4 floats where K is contiguous).
+template <int BM, int BN, int BK, bool TA, bool TB>
+struct TileLds {
+  static constexpr int LDA = !TA ? BK + 4 : BM, LDB = TB ? BK + 4 : BN;
+  static constexpr int SA = !TA ? BM * LDA : BK * LDA, SB = TB ? BN * LDB : BK * LDB;
+  static constexpr int FLOATS = 2 * (SA + SB);
+};
+
+// The tile of block `bid` of a product launched as `nb` blocks, staging through `smem` (at least
+// TileLds<...>::FLOATS floats of LDS): a kernel that runs two products side by side gives each
+// its share of the grid and the same LDS.
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE, int MS, class Epi>
-__device__ __forceinline__ void gemm_mfma_block(const float* __restrict__ A, const float* __restrict__ B, int M, int N, int K,
-                                                const int64_t* a_off, const int64_t* b_off, uint64_t a_stride, uint64_t b_stride, int splits,
-                                                int k_per_split, const float* __restrict__ bias, uint32_t tiles_m, uint32_t tiles_n,
-                                                int swizzle, Epi& epi) {
+__device__ __forceinline__ void gemm_mfma_tile(const float* __restrict__ A, const float* __restrict__ B, int M, int N, int K,
+                                               const int64_t* a_off, const int64_t* b_off, uint64_t a_stride, uint64_t b_stride, int splits,
+                                               int k_per_split, const float* __restrict__ bias, uint32_t tiles_m, uint32_t tiles_n,
+                                               int swizzle, Epi& epi, uint32_t bid, uint32_t nb, float* smem) {
   constexpr int NT = 64 * WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / MS, TN = WTN / MS;
   static_assert(TM >= 1 && TN >= 1 && TM <= 4 && TN <= 4 && (TM & (TM - 1)) == 0 && (TN & (TN - 1)) == 0, "wave tiles");
@@ -162,13 +174,13 @@ __device__ __forceinline__ void gemm_mfma_block(const float* __restrict__ A, con
   static_assert(BK % KG == 0, "K step");
   typedef Mfma<MS> MF;
   constexpr bool AK = !TA, BKC = TB;  // K-contiguous operands
-  constexpr int LDA = AK ? BK + 4 : BM, LDB = BKC ? BK + 4 : BN;
-  constexpr int SA = AK ? BM * LDA : BK * LDA, SB = BKC ? BN * LDB : BK * LDB;
-  __shared__ float As[2][SA];
-  __shared__ float Bs[2][SB];
+  typedef TileLds<BM, BN, BK, TA, TB> L;
+  constexpr int LDA = L::LDA, LDB = L::LDB, SA = L::SA, SB = L::SB;
+  float(*As)[SA] = (float(*)[SA])smem;
+  float(*Bs)[SB] = (float(*)[SB])(smem + 2 * SA);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const TileIndex ti = tile_of(tiles_m, tiles_n, swizzle);
+  const TileIndex ti = tile_of(bid, nb, tiles_m, tiles_n, swizzle);
   const uint32_t b = ti.z / splits, sp = ti.z % splits;
   const int m0 = ti.tm * BM, n0 = ti.tn * BN;
   const float* Ab = A + batch_offset(a_off, a_stride, b);
@@ -351,6 +363,17 @@ __device__ __forceinline__ void gemm_mfma_block(const float* __restrict__ A, con
         }
       }
   }
+}
+
+// One product over the whole grid, with its own LDS.
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MODE, int MS, class Epi>
+__device__ __forceinline__ void gemm_mfma_block(const float* __restrict__ A, const float* __restrict__ B, int M, int N, int K,
+                                                const int64_t* a_off, const int64_t* b_off, uint64_t a_stride, uint64_t b_stride, int splits,
+                                                int k_per_split, const float* __restrict__ bias, uint32_t tiles_m, uint32_t tiles_n,
+                                                int swizzle, Epi& epi) {
+  __shared__ float smem[TileLds<BM, BN, BK, TA, TB>::FLOATS];
+  gemm_mfma_tile<BM, BN, BK, WM, WN, TA, TB, MODE, MS>(A, B, M, N, K, a_off, b_off, a_stride, b_stride, splits, k_per_split, bias, tiles_m,
+                                                      tiles_n, swizzle, epi, blockIdx.x, gridDim.x, smem);
 }
 
 }  // namespace rgg

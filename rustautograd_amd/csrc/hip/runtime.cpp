@@ -49,6 +49,8 @@ uint64_t prod(const std::vector<int64_t>& s) {
 
 // One launch of a plan step: (stream, slot pointer table, workspace).
 using StepFn = std::function<void(hipStream_t, void* const*, void*)>;
+// A product's launch arguments from the frame's slot table and workspace.
+using GemmFill = std::function<rgk::GemmArgs(void* const*, void*)>;
 
 // Device buffers and captured graphs of the step loop (rg_hip_exec_run), kept on the frame so
 // that a later run with the same description only uploads its batches and resets the counter.
@@ -115,6 +117,8 @@ struct Program {
   // Per step: the product step whose kernel computes this fused group as its epilogue, or -1.
   std::vector<int64_t> epilogue_of;
   std::vector<bool> epilogue_sunk;  // per group step: the combined kernel runs at the group's step
+  // Per step: for the second of two products launched together (pair_products), the first; -1.
+  std::vector<int64_t> pair_of;
   // Runs of consecutive small, independent fused groups launched as one kernel (merge_sets):
   // merged[m] replaces steps first..last when all of them run; merged_at[k] is the run starting
   // at step k, or -1. The single-step functions stay for partial ranges and per-step timing.
@@ -195,7 +199,9 @@ void put(char* buf, size_t len, const std::string& s) {
 
 void* P(void* const* slots, int64_t s) { return slots[s]; }
 
-StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
+// The launch arguments of product `i` (empty for an empty product); `*base_out` gets them with
+// null operand pointers, for decisions made at program build.
+GemmFill gemm_fill(Program& prog, const Instr& i, bool ta, bool tb, rgk::GemmArgs* base_out) {
   const auto &sa = i.args[0].shape, &sb = i.args[1].shape;
   size_t ar = sa.size(), br = sb.size();
   uint64_t m, k;
@@ -269,7 +275,8 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
       base.b_off4 = all4(bo);
     }
   }
-  if (i.n == 0) return [](hipStream_t, void* const*, void*) {};
+  *base_out = base;
+  if (i.n == 0) return GemmFill();
   // A third operand is a bias added to every row of the product (f32 plans only).
   const int64_t bias = i.args.size() == 3 ? i.args[2].slot : -1;
   if (bias >= 0 && (dtype != RG_F32 || i.args[2].shape.empty() || (uint64_t)i.args[2].shape.back() != n))
@@ -285,28 +292,40 @@ StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
     prog.fold_bytes += ((uint64_t)splits * mn * sizeof(float) + 255) / 256 * 256;
     base.defer_split = true;
     base.planned_splits = splits;
+    *base_out = base;
     const Program* pp = &prog;
-    return [base, as, bs, dst, off, pp](hipStream_t s, void* const* sl, void* wsp) {
+    return [base, as, bs, dst, off, pp](void* const* sl, void* wsp) {
       rgk::GemmArgs g = base;
       g.a = sl[as];
       g.b = sl[bs];
       g.c = sl[dst];
       g.workspace = (char*)wsp + pp->fold_base() + off;
-      rgk::gemm(s, g);
+      return g;
     };
   }
   uint64_t ws = rgk::gemm_workspace(dtype, base.m, base.n, base.k, base.batch, ta, tb);
   prog.workspace_bytes = std::max(prog.workspace_bytes, ws);
   base.workspace_bytes = ws;
-  return [base, as, bs, dst, bias](hipStream_t s, void* const* sl, void* wsp) {
+  *base_out = base;
+  return [base, as, bs, dst, bias](void* const* sl, void* wsp) {
     rgk::GemmArgs g = base;
     g.a = sl[as];
     g.b = sl[bs];
     g.c = sl[dst];
     g.bias = bias >= 0 ? sl[bias] : nullptr;
     g.workspace = wsp;
-    rgk::gemm(s, g);
+    return g;
   };
+}
+
+StepFn gemm_step(const GemmFill& fill) {
+  if (!fill) return [](hipStream_t, void* const*, void*) {};
+  return [fill](hipStream_t s, void* const* sl, void* wsp) { rgk::gemm(s, fill(sl, wsp)); };
+}
+
+StepFn lower_gemm(Program& prog, const Instr& i, bool ta, bool tb) {
+  rgk::GemmArgs base{};
+  return gemm_step(gemm_fill(prog, i, ta, tb, &base));
 }
 
 StepFn lower_reduce(Program& prog, const Instr& i) {
@@ -857,6 +876,37 @@ std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::s
                               prefix + "rge" + std::to_string(pk), fk);
 }
 
+// Adjacent independent products launched as one kernel (rgk::gemm_pair): step k and step k + 1,
+// both plain products (no epilogue), neither reading or writing what the other writes, whose
+// launches pair at program build (same MFMA tile shape, one of those instantiated for pairs).
+// Step k then launches both, step k + 1 nothing; at run time a pair whose operands turn out not
+// to fit (alignment) is launched as two kernels, at step k. The pairs' results are those of the
+// single launches. RG_HIP_PAIR=0 turns this off.
+void pair_products(Program& prog, const std::vector<GemmFill>& fills, const std::vector<rgk::GemmArgs>& base) {
+  const size_t n = prog.plan.steps.size();
+  prog.pair_of.assign(n, -1);
+  const char* env = getenv("RG_HIP_PAIR");
+  if (env && env[0] == '0') return;
+  for (size_t k = 0; k + 1 < n; k++) {
+    if (!fills[k] || !fills[k + 1] || prog.pair_of[k] >= 0) continue;
+    const Instr &a = prog.plan.steps[k].instr, &b = prog.plan.steps[k + 1].instr;
+    bool independent = a.dst != b.dst;
+    for (auto& x : b.args) independent = independent && x.slot != a.dst;
+    for (auto& x : a.args) independent = independent && x.slot != b.dst;
+    if (!independent || !rgk::gemm_pair(nullptr, base[k], base[k + 1], false)) continue;
+    prog.pair_of[k + 1] = (int64_t)k;
+    const GemmFill f0 = fills[k], f1 = fills[k + 1];
+    prog.steps[k] = [f0, f1](hipStream_t s, void* const* sl, void* wsp) {
+      const rgk::GemmArgs g0 = f0(sl, wsp), g1 = f1(sl, wsp);
+      if (!rgk::gemm_pair(s, g0, g1)) {
+        rgk::gemm(s, g0);
+        rgk::gemm(s, g1);
+      }
+    };
+    prog.steps[k + 1] = [](hipStream_t, void* const*, void*) {};
+  }
+}
+
 void build_program(Program& prog) {
   std::vector<size_t> fold_producer;  // per fold: the step of the row group that writes its partials
   std::ostringstream src;
@@ -870,6 +920,8 @@ void build_program(Program& prog) {
     if (ep.at[j] >= 0) epilogue_at[(size_t)ep.at[j]] = (int64_t)j;
   std::vector<rgjit::FusedKernel*> kernel_of(n_steps, nullptr);
   std::vector<bool> store_c(n_steps, false);
+  std::vector<GemmFill> gemm_fills(n_steps);
+  std::vector<rgk::GemmArgs> gemm_base(n_steps);
   for (size_t k = 0; k < n_steps; k++) {
     const Step& st = prog.plan.steps[k];
     if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
@@ -973,10 +1025,17 @@ void build_program(Program& prog) {
       prog.steps.push_back(lower_control(prog, k));
     } else {
       const Instr& in = st.instr;
-      prog.steps.push_back(lower_instr(prog, in));
+      if (in.op == RG_OP_MATMUL || in.op == RG_OP_MATMUL_T) {
+        const bool ta = in.op == RG_OP_MATMUL_T && in.attr[0] != 0, tb = in.op == RG_OP_MATMUL_T && in.attr[1] != 0;
+        gemm_fills[k] = gemm_fill(prog, in, ta, tb, &gemm_base[k]);
+        prog.steps.push_back(gemm_step(gemm_fills[k]));
+      } else {
+        prog.steps.push_back(lower_instr(prog, in));
+      }
       while (fold_producer.size() < prog.folds.size()) fold_producer.push_back(k);
     }
   }
+  pair_products(prog, gemm_fills, gemm_base);
   for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));
   place_bodies(prog);
   // Each fold runs before the first later step reading its output, or right after its producer.
@@ -986,6 +1045,13 @@ void build_program(Program& prog) {
   // runs at.
   auto reads_at = [&](size_t j) {
     std::vector<int64_t> r;
+    // Two products launched together read their operands at the first one's step.
+    if (prog.pair_of[j] >= 0) return r;
+    if (j + 1 < n && prog.pair_of[j + 1] == (int64_t)j) {
+      for (size_t q : {j, j + 1})
+        for (auto& a : prog.plan.steps[q].instr.args) r.push_back(a.slot);
+      return r;
+    }
     const bool combined_here = (ep.at[j] >= 0 && ep.sunk[j]) || (epilogue_at[j] >= 0 && !ep.sunk[(size_t)epilogue_at[j]]);
     const bool moved_away = (ep.at[j] >= 0 && !ep.sunk[j]) || (epilogue_at[j] >= 0 && ep.sunk[(size_t)epilogue_at[j]]);
     if (!moved_away && !combined_here) return step_reads(prog.plan.steps[j]);
@@ -1702,6 +1768,7 @@ int64_t rg_hip_program_step_runs_in(void* program, int64_t step) {
   const auto* p = (const Program*)program;
   if (step < 0 || (size_t)step >= p->plan.steps.size()) return -1;
   const size_t k = (size_t)step;
+  if (p->pair_of[k] >= 0) return p->pair_of[k];
   if (p->epilogue_of[k] >= 0) return p->epilogue_sunk[k] ? step : p->epilogue_of[k];
   for (size_t j = 0; j < p->epilogue_of.size(); j++)
     if (p->epilogue_of[j] == step && p->epilogue_sunk[j]) return (int64_t)j;

@@ -1,5 +1,6 @@
-"""Elementwise groups computed in the epilogue of the product they read, against the same program
-with every group in its own kernel (RG_HIP_EPILOGUE=0).
+"""Kernels that compute two plan steps: elementwise groups computed in the epilogue of the product
+they read, against the same program with every group in its own kernel (RG_HIP_EPILOGUE=0), and
+pairs of independent products launched as one kernel, against single launches (RG_HIP_PAIR=0).
 
 The combined kernel applies the group's operations, in the group's order, to the product's
 finished outputs (the values the product's own kernel would have stored), so the two programs
@@ -35,6 +36,7 @@ def _bits(tree):
 def test_products_with_epilogues_match_separate_kernels_bit_for_bit(monkeypatch, name, mode, steps, pairs):
     step, state = workloads.mlp_train_step() if name == "C2" else workloads.gpt_train_step(workloads.GPT_CONFIGS[name])
     print(f"{name}: compile with and without product epilogues ({mode or 'default'}), {steps} device steps", flush=True)
+    monkeypatch.setenv("RG_HIP_PAIR", "0")  # pairs of products: the test below
     monkeypatch.setenv("RG_HIP_EPILOGUE", "0")
     plain = rg.compile(step, (state,), validate="none", device="hip")
     if mode:
@@ -45,6 +47,30 @@ def test_products_with_epilogues_match_separate_kernels_bit_for_bit(monkeypatch,
     assert _pairs(plain) == [] and len(_pairs(fused)) == pairs, _pairs(fused)
     r0 = rg.run(plain, state, steps=steps)
     r1 = rg.run(fused, state, steps=steps)
+    assert r0.status == r1.status == "completed"
+    assert np.array_equal(np.array(r0.history["aux"]).view(np.uint64), np.array(r1.history["aux"]).view(np.uint64))
+    for a, b in zip(_bits(r0.state), _bits(r1.state)):
+        assert np.array_equal(a, b)
+
+
+def test_products_launched_together_match_single_launches_bit_for_bit(monkeypatch):
+    """Each C4 layer's fc1 input-gradient and weight-gradient products are independent, adjacent
+    and on the same tile shape: they run as one kernel (its blocks split between the two, each
+    running the single product's tile code), at the first one's step. The state after a step and
+    the loss equal the single launches' bit for bit (RG_HIP_PAIR=0)."""
+    step, state = workloads.gpt_train_step(workloads.GPT_CONFIGS["C4"])
+    print("C4: compile with and without paired product launches, 1 device step", flush=True)
+    monkeypatch.setenv("RG_HIP_PAIR", "0")
+    single = rg.compile(step, (state,), validate="none", device="hip")
+    monkeypatch.delenv("RG_HIP_PAIR")
+    paired = rg.compile(step, (state,), validate="none", device="hip")
+    plan = paired.plan_summary()
+
+    def product_pairs(compiled):
+        return [(k, r) for k, r in _pairs(compiled) if plan[k].get("op", "").startswith("matmul") and plan[r].get("op", "").startswith("matmul")]
+    assert product_pairs(single) == [] and len(product_pairs(paired)) == 6, product_pairs(paired)
+    r0 = rg.run(single, state, steps=1)
+    r1 = rg.run(paired, state, steps=1)
     assert r0.status == r1.status == "completed"
     assert np.array_equal(np.array(r0.history["aux"]).view(np.uint64), np.array(r1.history["aux"]).view(np.uint64))
     for a, b in zip(_bits(r0.state), _bits(r1.state)):
