@@ -325,12 +325,18 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_fwd(AttnArgs a) {
 // Backward, query side: one block per 16 * WAVES queries; dq = dS k, and rowsum(dO * O) per
 // query. The next key tile's scores and dP are in flight while the current tile's dS is formed
 // and multiplied into dq.
+template <int HD>
+struct BwdQLds {
+  static constexpr int KP = HD + 4;
+  static constexpr int FLOATS = 2 * ATTN_MAX_KEYS * KP;  // K and V rows
+};
+
+// Block `bx` of problem `bh`, its K and V staged in `smem` (BwdQLds<HD>::FLOATS floats of LDS).
 template <int HD, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
+__device__ __forceinline__ void bwd_q_block(const AttnArgs& a, uint32_t bx, uint32_t bh, float* smem) {
   constexpr int KP = HD + 4, ND = HD / 16, NT = 64 * WAVES;
-  __shared__ float Ks[ATTN_MAX_KEYS * KP];
-  __shared__ float Vs[ATTN_MAX_KEYS * KP];
-  const uint32_t bh = blockIdx.y;
+  float* Ks = smem;
+  float* Vs = smem + ATTN_MAX_KEYS * KP;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int tq = a.tq, tk = a.tk, nkt = tk / 16;
   const float* Kb = row_of(a.k, a, bh, 0);
@@ -341,7 +347,7 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
     *(float4*)&Vs[key * KP + d] = *(const float4*)(Vb + key * a.v.st + d);
   }
   __syncthreads();
-  const int q0 = blockIdx.x * 16 * WAVES + wave_tile<WAVES>(w) * 16;
+  const int q0 = bx * 16 * WAVES + wave_tile<WAVES>(w) * 16;
   if (q0 >= tq) return;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
   const int q = q0 + l16;
@@ -420,19 +426,30 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
 // in flight while the current tile is consumed. (Measured on C4's shapes: 7 % faster than a loop
 // with a conditional next-tile block and the mask word picked from registers by a select chain.)
 template <int HD, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
+struct BwdKvLds {
+  static constexpr int KP = HD + 4, NW = ATTN_MAX_KEYS / 32;
+  static constexpr bool MW_LDS = HD <= 32;  // mask words in LDS where they fit beside the operand tiles
+  static constexpr int ROWS = 2 * ATTN_MAX_KEYS * KP;  // q and dO rows
+  // Then per query a float4 (row max, 1 / row sum, rowsum(dO * O)) and the mask words.
+  static constexpr int FLOATS = ROWS + 4 * ATTN_MAX_KEYS + (MW_LDS ? WAVES * NW * 64 : 1);
+};
+
+// Block `bx` of problem `bh`, its q, dO, statistics and mask words staged in `smem`
+// (BwdKvLds<HD, WAVES>::FLOATS floats of LDS, 16-byte aligned).
+template <int HD, int WAVES>
+__device__ __forceinline__ void bwd_kv_block(const AttnArgs& a, uint32_t bx, uint32_t bh, float* smem) {
   constexpr int KP = HD + 4, ND = HD / 16, NT = 64 * WAVES, NW = ATTN_MAX_KEYS / 32;
-  __shared__ float Qs[ATTN_MAX_KEYS * KP];
-  __shared__ float Gs[ATTN_MAX_KEYS * KP];
+  typedef BwdKvLds<HD, WAVES> L;
+  float* Qs = smem;
+  float* Gs = smem + ATTN_MAX_KEYS * KP;
   // Per query: row max, 1 / row sum, rowsum(dO * O). (Folding log2 of the sum into the max would
   // lose it next to the fill value's max of a fully masked row.)
-  __shared__ float4 St[ATTN_MAX_KEYS];
-  constexpr bool MW_LDS = HD <= 32;  // mask words in LDS where they fit beside the operand tiles
-  __shared__ uint32_t Mw[MW_LDS ? WAVES * NW * 64 : 1];
-  const uint32_t bh = blockIdx.y;
+  float4* St = (float4*)(smem + L::ROWS);
+  constexpr bool MW_LDS = L::MW_LDS;
+  uint32_t* Mw = (uint32_t*)(smem + L::ROWS + 4 * ATTN_MAX_KEYS);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int tq = a.tq, tk = a.tk, nqt = tq / 16;
-  const int k0 = blockIdx.x * 16 * WAVES + wave_tile<WAVES>(w) * 16;
+  const int k0 = bx * 16 * WAVES + wave_tile<WAVES>(w) * 16;
   const bool active = k0 < tk;
   const int l16 = lane & 15, g4 = (lane >> 4) * 4;
   const int key = k0 + l16;  // the lane's key in score tiles
@@ -559,6 +576,30 @@ __global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
   }
 }
 
+template <int HD, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_q(AttnArgs a) {
+  __shared__ float4 smem[BwdQLds<HD>::FLOATS / 4];
+  bwd_q_block<HD, WAVES>(a, blockIdx.x, blockIdx.y, (float*)smem);
+}
+
+template <int HD, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) k_attn_bwd_kv(AttnArgs a) {
+  __shared__ float4 smem[(BwdKvLds<HD, WAVES>::FLOATS + 3) / 4];
+  bwd_kv_block<HD, WAVES>(a, blockIdx.x, blockIdx.y, (float*)smem);
+}
+
+// Both backward passes in one launch: the problems' query-pass blocks at y < bh, their key-pass
+// blocks after them, over one LDS buffer sized for the larger. Each block runs the code of its
+// pass's own kernel: one launch instead of two, and the key pass's blocks start on the CUs the
+// query pass's blocks leave.
+template <int HD, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) k_attn_bwd(AttnArgs a) {
+  constexpr int F = BwdKvLds<HD, WAVES>::FLOATS > BwdQLds<HD>::FLOATS ? BwdKvLds<HD, WAVES>::FLOATS : BwdQLds<HD>::FLOATS;
+  __shared__ float4 smem[(F + 3) / 4];
+  if (blockIdx.y < a.bh) bwd_q_block<HD, WAVES>(a, blockIdx.x, blockIdx.y, (float*)smem);
+  else bwd_kv_block<HD, WAVES>(a, blockIdx.x, blockIdx.y - a.bh, (float*)smem);
+}
+
 // Sixteen waves (a whole 256-row problem per block: its K and V, or q and dO, are staged once)
 // when there are problems for every CU; else four waves per block unless the launch would still
 // give every CU two blocks with eight.
@@ -578,6 +619,12 @@ void forward_hd(hipStream_t s, const AttnArgs& a) {
 
 template <int HD>
 void backward_hd(hipStream_t s, const AttnArgs& a) {
+  // Equal grids (as many queries as keys, a whole problem per block): both passes in one launch.
+  if (a.tq == a.tk && waves_for(a, a.tq) == 16) {
+    const dim3 grid((uint32_t)((a.tq + 255) / 256), 2 * a.bh);
+    hipLaunchKernelGGL((k_attn_bwd<HD, 16>), grid, dim3(1024), 0, s, a);
+    return;
+  }
   {
     const int wv = waves_for(a, a.tq);
     const dim3 grid((uint32_t)((a.tq + 16 * wv - 1) / (16 * wv)), a.bh);
