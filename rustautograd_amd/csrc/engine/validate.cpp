@@ -874,24 +874,32 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
   // A fused group the device computes in a product's epilogue (step_runs_in pairs the two) is
   // counted in the product's row: its time (the combined kernel runs at one of the two steps) and
   // its bytes, with no launch or flops of its own.
-  // Two products the device launches together (one kernel at the first one's step) keep their
-  // own rows; the kernel's time is shared between them in proportion to their flops.
+  // Products the device launches together (one kernel at one of their steps) keep their own
+  // rows; the kernel's time is shared between them in proportion to their flops.
   std::vector<size_t> row_of(plan.steps.size());
   std::vector<double> sec = seconds;
   auto plain = [&](size_t q) { return !plan.steps[q].fused && !plan.steps[q].attn; };
+  std::map<size_t, std::vector<size_t>> launched_with;  // launch step -> the products it computes
   for (size_t s = 0; s < plan.steps.size(); s++) row_of[s] = s;
   for (size_t s = 0; s < plan.steps.size(); s++) {
     const int64_t r = program->step_runs_in((int64_t)s);
     if (r < 0 || (size_t)r == s || (size_t)r >= plan.steps.size()) continue;
     if (plain(s) && plain((size_t)r)) {
-      const double fa = step_work(plan.steps[(size_t)r], streamed).flops, fb = step_work(plan.steps[s], streamed).flops;
-      const double both = sec[(size_t)r] + sec[s];
-      sec[(size_t)r] = fa + fb > 0 ? both * fa / (fa + fb) : both;
-      sec[s] = both - sec[(size_t)r];
+      auto& g = launched_with[(size_t)r];
+      if (g.empty()) g.push_back((size_t)r);
+      g.push_back(s);
       continue;
     }
     const size_t product = plain(s) ? s : (size_t)r;
     row_of[s] = row_of[(size_t)r] = product;
+  }
+  for (auto& [r, g] : launched_with) {
+    double all = 0, flops = 0;
+    for (size_t q : g) {
+      all += sec[q];
+      flops += step_work(plan.steps[q], streamed).flops;
+    }
+    for (size_t q : g) sec[q] = flops > 0 ? all * step_work(plan.steps[q], streamed).flops / flops : all / (double)g.size();
   }
   for (size_t s0 = 0; s0 < plan.steps.size(); s0++) {
     const size_t s = row_of[s0];

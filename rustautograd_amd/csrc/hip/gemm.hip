@@ -46,32 +46,48 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma(const float* __restr
                                                               tiles_m, tiles_n, swizzle, epi);
 }
 
-// One unbatched product's share of a paired launch (k_gemm_mfma_pair).
-struct PairPart {
+// One unbatched product's share of a grouped launch (k_gemm_mfma_group).
+struct GroupPart {
   const float *a, *b;
   float *c, *part;
   const float* bias;
   int m, n, k, splits, kps;
   uint32_t tm, tn, blocks;
 };
+constexpr int GROUP_MAX = 3;
+struct GroupParts {
+  GroupPart p[GROUP_MAX];
+};
 
-// Two independent unbatched products on one tile shape in one launch: blocks [0, p0.blocks)
-// compute product 0, the rest product 1, both staging through the same LDS. Each block runs the
-// code of a single-product launch, so every output gets the same bits; the launch's fixed cost
-// is paid once, and the two grids (each about one block per CU) run side by side.
-template <int BM, int BN, int BK, int WM, int WN, bool TA0, bool TB0, bool TA1, bool TB1>
-__global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma_pair(PairPart p0, PairPart p1) {
-  constexpr int F0 = TileLds<BM, BN, BK, TA0, TB0>::FLOATS, F1 = TileLds<BM, BN, BK, TA1, TB1>::FLOATS;
-  __shared__ float smem[F0 > F1 ? F0 : F1];
-  if (blockIdx.x < p0.blocks) {
-    StoreC epi{p0.c, p0.part, p0.splits, (uint64_t)p0.m * p0.n};
-    gemm_mfma_tile<BM, BN, BK, WM, WN, TA0, TB0, LOAD_EVEN, 16>(p0.a, p0.b, p0.m, p0.n, p0.k, nullptr, nullptr, 0, 0, p0.splits, p0.kps,
-                                                                 p0.bias, p0.tm, p0.tn, 1, epi, blockIdx.x, p0.blocks, smem);
-  } else {
-    StoreC epi{p1.c, p1.part, p1.splits, (uint64_t)p1.m * p1.n};
-    gemm_mfma_tile<BM, BN, BK, WM, WN, TA1, TB1, LOAD_EVEN, 16>(p1.a, p1.b, p1.m, p1.n, p1.k, nullptr, nullptr, 0, 0, p1.splits, p1.kps,
-                                                                 p1.bias, p1.tm, p1.tn, 1, epi, blockIdx.x - p0.blocks, p1.blocks, smem);
-  }
+// Part I of a grouped launch: flags bits 2I (TB) and 2I + 1 (TA).
+template <int BM, int BN, int BK, int WM, int WN, int FLAGS, int I>
+__device__ __forceinline__ void group_part(const GroupPart& p, uint32_t bid, float* smem) {
+  constexpr bool TA = (FLAGS >> (2 * I + 1)) & 1, TB = (FLAGS >> (2 * I)) & 1;
+  StoreC epi{p.c, p.part, p.splits, (uint64_t)p.m * p.n};
+  gemm_mfma_tile<BM, BN, BK, WM, WN, TA, TB, LOAD_EVEN, 16>(p.a, p.b, p.m, p.n, p.k, nullptr, nullptr, 0, 0, p.splits, p.kps, p.bias, p.tm,
+                                                             p.tn, 1, epi, bid, p.blocks, smem);
+}
+
+template <int BM, int BN, int BK, int FLAGS, int I>
+constexpr int part_lds() {
+  return TileLds<BM, BN, BK, ((FLAGS >> (2 * I + 1)) & 1) != 0, ((FLAGS >> (2 * I)) & 1) != 0>::FLOATS;
+}
+
+// N independent unbatched products on one tile shape in one launch: part i takes the next
+// p[i].blocks blocks, all staging through the same LDS. Each block runs the code of a single
+// product's launch, so every output gets the same bits; the launch's fixed cost is paid once,
+// and the parts' grids (each about one block per CU) run side by side.
+template <int BM, int BN, int BK, int WM, int WN, int N, int FLAGS>
+__global__ void __launch_bounds__(64 * WM * WN) k_gemm_mfma_group(GroupParts g) {
+  constexpr int F0 = part_lds<BM, BN, BK, FLAGS, 0>(), F1 = part_lds<BM, BN, BK, FLAGS, 1>();
+  constexpr int F2 = N > 2 ? part_lds<BM, BN, BK, FLAGS, 2>() : 0;
+  constexpr int F01 = F0 > F1 ? F0 : F1;
+  __shared__ float smem[F01 > F2 ? F01 : F2];
+  uint32_t bid = blockIdx.x;
+  if (bid < g.p[0].blocks) return group_part<BM, BN, BK, WM, WN, FLAGS, 0>(g.p[0], bid, smem);
+  bid -= g.p[0].blocks;
+  if (N == 2 || bid < g.p[1].blocks) return group_part<BM, BN, BK, WM, WN, FLAGS, 1>(g.p[1], bid, smem);
+  if constexpr (N > 2) group_part<BM, BN, BK, WM, WN, FLAGS, 2>(g.p[2], bid - g.p[1].blocks, smem);
 }
 
 // Sums the K-split partial products in split order. Four outputs per thread (16-byte loads when
@@ -724,40 +740,46 @@ void gemm(hipStream_t s, const GemmArgs& g) {
   }
 }
 
-bool gemm_pair(hipStream_t s, const GemmArgs& g0, const GemmArgs& g1, bool launch) {
-  if (!on_mfma_tiles(g0) || !on_mfma_tiles(g1) || g0.batch != 1 || g1.batch != 1) return false;
-  TileCfg t0, t1;
-  int m0, m1;
-  Launch l0, l1;
-  mfma_launch(g0, &t0, &m0, &l0);
-  mfma_launch(g1, &t1, &m1, &l1);
-  // Each product's K-split partials, if any, must be the deferred kind: a split sum after the
-  // paired launch would be a second launch anyway.
-  if ((l0.splits > 1 && !g0.defer_split) || (l1.splits > 1 && !g1.defer_split)) return false;
-  if (m0 != LOAD_EVEN || m1 != LOAD_EVEN || t0.bm != t1.bm || t0.bn != t1.bn || t0.bk != t1.bk || t0.wm != t1.wm || t0.wn != t1.wn ||
-      t0.ms != 16 || t1.ms != 16 || l0.grid.x % 8 != 0)
-    return false;
-  const bool shape = t0.bm == 128 && t0.bn == 64 && t0.bk == 32 && t0.wm == 2 && t0.wn == 4;
-  const bool flags = (!g0.ta && g0.tb && g1.ta && !g1.tb) || (g0.ta && !g0.tb && !g1.ta && g1.tb);
-  if (!launch) return shape && flags;
-  auto part = [](const Launch& l) {
-    return PairPart{l.a, l.b, l.c, l.part, l.bias, l.m, l.n, l.k, l.splits, l.kps, l.tm, l.tn, l.grid.x};
-  };
-  const PairPart p0 = part(l0), p1 = part(l1);
-  const dim3 grid(l0.grid.x + l1.grid.x);
-  // The shapes instantiated: C4's input- and weight-gradient products of a layer's first MLP
-  // product, on 128x64 tiles of eight waves.
-  if (t0.bm == 128 && t0.bn == 64 && t0.bk == 32 && t0.wm == 2 && t0.wn == 4) {
-    if (!g0.ta && g0.tb && g1.ta && !g1.tb) {
-      hipLaunchKernelGGL((k_gemm_mfma_pair<128, 64, 32, 2, 4, false, true, true, false>), grid, dim3(512), 0, s, p0, p1);
-      return true;
-    }
-    if (g0.ta && !g0.tb && !g1.ta && g1.tb) {
-      hipLaunchKernelGGL((k_gemm_mfma_pair<128, 64, 32, 2, 4, true, false, false, true>), grid, dim3(512), 0, s, p0, p1);
-      return true;
-    }
+bool gemm_group(hipStream_t s, const GemmArgs* g, int count, bool launch) {
+  if (count < 2 || count > GROUP_MAX) return false;
+  TileCfg t[GROUP_MAX];
+  int mode[GROUP_MAX];
+  Launch l[GROUP_MAX];
+  int flags = 0;
+  for (int i = 0; i < count; i++) {
+    if (!on_mfma_tiles(g[i]) || g[i].batch != 1) return false;
+    mfma_launch(g[i], &t[i], &mode[i], &l[i]);
+    // K-split partials, if any, must be the deferred kind: a split sum after the grouped launch
+    // would be a second launch anyway.
+    if (l[i].splits > 1 && !g[i].defer_split) return false;
+    if (mode[i] != LOAD_EVEN || t[i].bm != t[0].bm || t[i].bn != t[0].bn || t[i].bk != t[0].bk || t[i].wm != t[0].wm ||
+        t[i].wn != t[0].wn || t[i].ms != 16 || (i + 1 < count && l[i].grid.x % 8 != 0))
+      return false;
+    flags |= ((g[i].ta ? 2 : 0) | (g[i].tb ? 1 : 0)) << (2 * i);
   }
-  return false;
+  // The shapes and flag sequences instantiated: C4's weight and input gradients around a layer's
+  // first MLP product (128x64 tiles of eight waves): fc1's input and weight gradient as a pair,
+  // with fc2's weight gradient ahead of them as a triple.
+  constexpr int T = 2, N = 1;  // (ta, tb) = (true, false) and (false, true)
+  const bool shape = t[0].bm == 128 && t[0].bn == 64 && t[0].bk == 32 && t[0].wm == 2 && t[0].wn == 4;
+  const bool known = shape && ((count == 2 && (flags == (N | T << 2) || flags == (T | N << 2))) ||
+                               (count == 3 && flags == (T | N << 2 | T << 4)));
+  if (!launch || !known) return known;
+  GroupParts parts{};
+  uint32_t blocks = 0;
+  for (int i = 0; i < count; i++) {
+    parts.p[i] = GroupPart{l[i].a, l[i].b, l[i].c, l[i].part, l[i].bias, l[i].m, l[i].n, l[i].k, l[i].splits, l[i].kps, l[i].tm, l[i].tn,
+                           l[i].grid.x};
+    blocks += l[i].grid.x;
+  }
+  const dim3 grid(blocks);
+  if (count == 2 && flags == (N | T << 2))
+    hipLaunchKernelGGL((k_gemm_mfma_group<128, 64, 32, 2, 4, 2, N | T << 2>), grid, dim3(512), 0, s, parts);
+  else if (count == 2)
+    hipLaunchKernelGGL((k_gemm_mfma_group<128, 64, 32, 2, 4, 2, T | N << 2>), grid, dim3(512), 0, s, parts);
+  else
+    hipLaunchKernelGGL((k_gemm_mfma_group<128, 64, 32, 2, 4, 3, T | N << 2 | T << 4>), grid, dim3(512), 0, s, parts);
+  return true;
 }
 
 }  // namespace rgk

@@ -196,10 +196,11 @@ struct GemmTile {
 };
 bool gemm_epilogue_tile(int dtype, uint64_t m, uint64_t n, uint64_t k, bool ta, bool tb, GemmTile* t);
 void gemm(hipStream_t s, const GemmArgs& g);
-// Two independent products in one launch, when both are unbatched MFMA tile products on the
-// same tile shape (one of those instantiated for it) with every operand's vectors inside its
-// tile grid, and any K split deferred to the fold area; false, launching nothing, otherwise.
-// With `launch` false it only answers (operand pointers may be null).
-bool gemm_pair(hipStream_t s, const GemmArgs& g0, const GemmArgs& g1, bool launch = true);
+// Two or three independent products in one launch, when all are unbatched MFMA tile products
+// on the same tile shape (with a sequence of operand layouts instantiated for it), every
+// operand's vectors inside its tile grid and any K split deferred to the fold area; false,
+// launching nothing, otherwise. With `launch` false it only answers (operand pointers may be
+// null).
+bool gemm_group(hipStream_t s, const GemmArgs* g, int count, bool launch = true);
 
 }  // namespace rgk

@@ -117,7 +117,8 @@ struct Program {
   // Per step: the product step whose kernel computes this fused group as its epilogue, or -1.
   std::vector<int64_t> epilogue_of;
   std::vector<bool> epilogue_sunk;  // per group step: the combined kernel runs at the group's step
-  // Per step: for the second of two products launched together (pair_products), the first; -1.
+  // Per step: for a product launched with others at another step (group_products), that step;
+  // -1 otherwise.
   std::vector<int64_t> pair_of;
   // Runs of consecutive small, independent fused groups launched as one kernel (merge_sets):
   // merged[m] replaces steps first..last when all of them run; merged_at[k] is the run starting
@@ -876,34 +877,74 @@ std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::s
                               prefix + "rge" + std::to_string(pk), fk);
 }
 
-// Adjacent independent products launched as one kernel (rgk::gemm_pair): step k and step k + 1,
-// both plain products (no epilogue), neither reading or writing what the other writes, whose
-// launches pair at program build (same MFMA tile shape, one of those instantiated for pairs).
-// Step k then launches both, step k + 1 nothing; at run time a pair whose operands turn out not
-// to fit (alignment) is launched as two kernels, at step k. The pairs' results are those of the
-// single launches. RG_HIP_PAIR=0 turns this off.
-void pair_products(Program& prog, const std::vector<GemmFill>& fills, const std::vector<rgk::GemmArgs>& base) {
+// Independent products launched as one kernel (rgk::gemm_group): two adjacent plain products
+// (no epilogue) k and k + 1, and with them, when it fits, the nearest earlier plain product j
+// moved down to step k (nothing between j and k writes j's operands or reads or writes its
+// output). No member reads or writes what another writes, and the launches group at program
+// build (same MFMA tile shape, a sequence of operand layouts instantiated for groups). Step k
+// launches them all, the others nothing; at run time a group whose operands turn out not to fit
+// (alignment) is launched as single kernels, at step k. The results are the single launches'.
+// RG_HIP_PAIR=0 turns this off.
+void group_products(Program& prog, const std::vector<GemmFill>& fills, const std::vector<rgk::GemmArgs>& base) {
   const size_t n = prog.plan.steps.size();
   prog.pair_of.assign(n, -1);
   const char* env = getenv("RG_HIP_PAIR");
   if (env && env[0] == '0') return;
-  for (size_t k = 0; k + 1 < n; k++) {
-    if (!fills[k] || !fills[k + 1] || prog.pair_of[k] >= 0) continue;
-    const Instr &a = prog.plan.steps[k].instr, &b = prog.plan.steps[k + 1].instr;
-    bool independent = a.dst != b.dst;
-    for (auto& x : b.args) independent = independent && x.slot != a.dst;
-    for (auto& x : a.args) independent = independent && x.slot != b.dst;
-    if (!independent || !rgk::gemm_pair(nullptr, base[k], base[k + 1], false)) continue;
-    prog.pair_of[k + 1] = (int64_t)k;
-    const GemmFill f0 = fills[k], f1 = fills[k + 1];
-    prog.steps[k] = [f0, f1](hipStream_t s, void* const* sl, void* wsp) {
-      const rgk::GemmArgs g0 = f0(sl, wsp), g1 = f1(sl, wsp);
-      if (!rgk::gemm_pair(s, g0, g1)) {
-        rgk::gemm(s, g0);
-        rgk::gemm(s, g1);
+  std::vector<bool> used(n, false);
+  auto independent = [&](const std::vector<size_t>& ks) {
+    for (size_t x : ks)
+      for (size_t y : ks) {
+        if (x == y) continue;
+        const Instr &a = prog.plan.steps[x].instr, &b = prog.plan.steps[y].instr;
+        if (a.dst == b.dst) return false;
+        for (auto& arg : b.args)
+          if (arg.slot == a.dst) return false;
       }
+    return true;
+  };
+  auto compatible = [&](const std::vector<size_t>& ks) {
+    std::vector<rgk::GemmArgs> g;
+    for (size_t x : ks) g.push_back(base[x]);
+    return rgk::gemm_group(nullptr, g.data(), (int)g.size(), false);
+  };
+  for (size_t k = 0; k + 1 < n; k++) {
+    if (!fills[k] || !fills[k + 1] || used[k] || used[k + 1]) continue;
+    std::vector<size_t> members = {k, k + 1};
+    if (!independent(members) || !compatible(members)) continue;
+    for (size_t j = k; j-- > 0 && j + 4 >= k;) {
+      if (used[j] || prog.plan.steps[j].kind != RG_STEP_INSTR) continue;
+      if (!fills[j]) {
+        if (is_control(prog.plan.steps[j].instr.op)) break;
+        continue;
+      }
+      const Instr& pj = prog.plan.steps[j].instr;
+      bool movable = true;
+      for (size_t q = j + 1; q < k && movable; q++) {
+        const Step& sq = prog.plan.steps[q];
+        if (sq.kind == RG_STEP_INSTR && is_control(sq.instr.op)) movable = false;
+        const auto w = step_writes(sq), r = step_reads(sq);
+        for (auto& arg : pj.args) movable = movable && !has_slot(w, arg.slot);
+        movable = movable && !has_slot(w, pj.dst) && !has_slot(r, pj.dst);
+      }
+      const std::vector<size_t> three = {j, k, k + 1};
+      if (movable && independent(three) && compatible(three)) members = three;
+      break;
+    }
+    std::vector<GemmFill> f;
+    for (size_t x : members) {
+      f.push_back(fills[x]);
+      used[x] = true;
+      if (x != k) {
+        prog.pair_of[x] = (int64_t)k;
+        prog.steps[x] = [](hipStream_t, void* const*, void*) {};
+      }
+    }
+    prog.steps[k] = [f](hipStream_t s, void* const* sl, void* wsp) {
+      rgk::GemmArgs g[3];
+      for (size_t i = 0; i < f.size(); i++) g[i] = f[i](sl, wsp);
+      if (!rgk::gemm_group(s, g, (int)f.size()))
+        for (size_t i = 0; i < f.size(); i++) rgk::gemm(s, g[i]);
     };
-    prog.steps[k + 1] = [](hipStream_t, void* const*, void*) {};
   }
 }
 
@@ -1035,7 +1076,7 @@ void build_program(Program& prog) {
       while (fold_producer.size() < prog.folds.size()) fold_producer.push_back(k);
     }
   }
-  pair_products(prog, gemm_fills, gemm_base);
+  group_products(prog, gemm_fills, gemm_base);
   for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));
   place_bodies(prog);
   // Each fold runs before the first later step reading its output, or right after its producer.
@@ -1045,11 +1086,16 @@ void build_program(Program& prog) {
   // runs at.
   auto reads_at = [&](size_t j) {
     std::vector<int64_t> r;
-    // Two products launched together read their operands at the first one's step.
+    // Products launched together read their operands at the step of the launch.
     if (prog.pair_of[j] >= 0) return r;
-    if (j + 1 < n && prog.pair_of[j + 1] == (int64_t)j) {
-      for (size_t q : {j, j + 1})
+    bool grouped = false;
+    for (size_t q = 0; q < n; q++)
+      if (prog.pair_of[q] == (int64_t)j) {
+        grouped = true;
         for (auto& a : prog.plan.steps[q].instr.args) r.push_back(a.slot);
+      }
+    if (grouped) {
+      for (auto& a : prog.plan.steps[j].instr.args) r.push_back(a.slot);
       return r;
     }
     const bool combined_here = (ep.at[j] >= 0 && ep.sunk[j]) || (epilogue_at[j] >= 0 && !ep.sunk[(size_t)epilogue_at[j]]);
