@@ -757,13 +757,16 @@ bool gemm_group(hipStream_t s, const GemmArgs* g, int count, bool launch) {
       return false;
     flags |= ((g[i].ta ? 2 : 0) | (g[i].tb ? 1 : 0)) << (2 * i);
   }
-  // The shapes and flag sequences instantiated: C4's weight and input gradients around a layer's
-  // first MLP product (128x64 tiles of eight waves): fc1's input and weight gradient as a pair,
-  // with fc2's weight gradient ahead of them as a triple.
+  // The shapes and flag sequences instantiated, from C4's backward pass: on 128x64 tiles of
+  // eight waves, fc1's input and weight gradients as a pair, with fc2's weight gradient ahead of
+  // them as a triple; on 64x64 tiles of four waves, the attention projection's weight gradient
+  // with the q, k, v projection's.
   constexpr int T = 2, N = 1;  // (ta, tb) = (true, false) and (false, true)
-  const bool shape = t[0].bm == 128 && t[0].bn == 64 && t[0].bk == 32 && t[0].wm == 2 && t[0].wn == 4;
-  const bool known = shape && ((count == 2 && (flags == (N | T << 2) || flags == (T | N << 2))) ||
-                               (count == 3 && flags == (T | N << 2 | T << 4)));
+  const bool wide = t[0].bm == 128 && t[0].bn == 64 && t[0].bk == 32 && t[0].wm == 2 && t[0].wn == 4;
+  const bool small = t[0].bm == 64 && t[0].bn == 64 && t[0].bk == 32 && t[0].wm == 2 && t[0].wn == 2;
+  const bool known = (wide && ((count == 2 && (flags == (N | T << 2) || flags == (T | N << 2))) ||
+                               (count == 3 && flags == (T | N << 2 | T << 4)))) ||
+                     (small && count == 2 && flags == (T | T << 2));
   if (!launch || !known) return known;
   GroupParts parts{};
   uint32_t blocks = 0;
@@ -773,7 +776,9 @@ bool gemm_group(hipStream_t s, const GemmArgs* g, int count, bool launch) {
     blocks += l[i].grid.x;
   }
   const dim3 grid(blocks);
-  if (count == 2 && flags == (N | T << 2))
+  if (small)
+    hipLaunchKernelGGL((k_gemm_mfma_group<64, 64, 32, 2, 2, 2, T | T << 2>), grid, dim3(256), 0, s, parts);
+  else if (count == 2 && flags == (N | T << 2))
     hipLaunchKernelGGL((k_gemm_mfma_group<128, 64, 32, 2, 4, 2, N | T << 2>), grid, dim3(512), 0, s, parts);
   else if (count == 2)
     hipLaunchKernelGGL((k_gemm_mfma_group<128, 64, 32, 2, 4, 2, T | N << 2>), grid, dim3(512), 0, s, parts);

@@ -880,11 +880,12 @@ std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::s
 // Independent products launched as one kernel (rgk::gemm_group): two adjacent plain products
 // (no epilogue) k and k + 1, and with them, when it fits, the nearest earlier plain product j
 // moved down to step k (nothing between j and k writes j's operands or reads or writes its
-// output). No member reads or writes what another writes, and the launches group at program
-// build (same MFMA tile shape, a sequence of operand layouts instantiated for groups). Step k
-// launches them all, the others nothing; at run time a group whose operands turn out not to fit
-// (alignment) is launched as single kernels, at step k. The results are the single launches'.
-// RG_HIP_PAIR=0 turns this off.
+// output); then, for a plain product k left alone, the nearest earlier one left alone moved down
+// to it the same way. No member reads or writes what another writes, and the launches group at
+// program build (same MFMA tile shape, a sequence of operand layouts instantiated for groups).
+// Step k launches them all, the others nothing; at run time a group whose operands turn out not
+// to fit (alignment) is launched as single kernels, at step k. The results are the single
+// launches'. RG_HIP_PAIR=0 turns this off.
 void group_products(Program& prog, const std::vector<GemmFill>& fills, const std::vector<rgk::GemmArgs>& base) {
   const size_t n = prog.plan.steps.size();
   prog.pair_of.assign(n, -1);
@@ -907,29 +908,33 @@ void group_products(Program& prog, const std::vector<GemmFill>& fills, const std
     for (size_t x : ks) g.push_back(base[x]);
     return rgk::gemm_group(nullptr, g.data(), (int)g.size(), false);
   };
-  for (size_t k = 0; k + 1 < n; k++) {
-    if (!fills[k] || !fills[k + 1] || used[k] || used[k + 1]) continue;
-    std::vector<size_t> members = {k, k + 1};
-    if (!independent(members) || !compatible(members)) continue;
-    for (size_t j = k; j-- > 0 && j + 4 >= k;) {
-      if (used[j] || prog.plan.steps[j].kind != RG_STEP_INSTR) continue;
-      if (!fills[j]) {
-        if (is_control(prog.plan.steps[j].instr.op)) break;
-        continue;
-      }
-      const Instr& pj = prog.plan.steps[j].instr;
-      bool movable = true;
-      for (size_t q = j + 1; q < k && movable; q++) {
-        const Step& sq = prog.plan.steps[q];
-        if (sq.kind == RG_STEP_INSTR && is_control(sq.instr.op)) movable = false;
-        const auto w = step_writes(sq), r = step_reads(sq);
-        for (auto& arg : pj.args) movable = movable && !has_slot(w, arg.slot);
-        movable = movable && !has_slot(w, pj.dst) && !has_slot(r, pj.dst);
-      }
-      const std::vector<size_t> three = {j, k, k + 1};
-      if (movable && independent(three) && compatible(three)) members = three;
-      break;
+  // Whether product j can run at step k > j instead: nothing between them writes its operands or
+  // reads or writes its output, and no control flow intervenes.
+  auto movable = [&](size_t j, size_t k) {
+    const Instr& pj = prog.plan.steps[j].instr;
+    for (size_t q = j + 1; q < k; q++) {
+      const Step& sq = prog.plan.steps[q];
+      if (sq.kind == RG_STEP_INSTR && is_control(sq.instr.op)) return false;
+      const auto w = step_writes(sq), r = step_reads(sq);
+      for (auto& arg : pj.args)
+        if (has_slot(w, arg.slot)) return false;
+      if (has_slot(w, pj.dst) || has_slot(r, pj.dst)) return false;
     }
+    return true;
+  };
+  // The nearest earlier plain product not yet grouped, within four steps of k, that can run at
+  // step k with `with` (the group it would join, k included).
+  auto earlier = [&](size_t k, const std::vector<size_t>& with) -> int64_t {
+    for (size_t j = k; j-- > 0 && j + 4 >= k;) {
+      if (prog.plan.steps[j].kind == RG_STEP_INSTR && is_control(prog.plan.steps[j].instr.op)) return -1;
+      if (used[j] || !fills[j]) continue;
+      std::vector<size_t> g = {j};
+      g.insert(g.end(), with.begin(), with.end());
+      if (movable(j, k) && independent(g) && compatible(g)) return (int64_t)j;
+    }
+    return -1;
+  };
+  auto launch_together = [&](const std::vector<size_t>& members, size_t k) {
     std::vector<GemmFill> f;
     for (size_t x : members) {
       f.push_back(fills[x]);
@@ -945,6 +950,19 @@ void group_products(Program& prog, const std::vector<GemmFill>& fills, const std
       if (!rgk::gemm_group(s, g, (int)f.size()))
         for (size_t i = 0; i < f.size(); i++) rgk::gemm(s, g[i]);
     };
+  };
+  for (size_t k = 0; k + 1 < n; k++) {
+    if (!fills[k] || !fills[k + 1] || used[k] || used[k + 1]) continue;
+    std::vector<size_t> members = {k, k + 1};
+    if (!independent(members) || !compatible(members)) continue;
+    const int64_t j = earlier(k, members);
+    if (j >= 0) members.insert(members.begin(), (size_t)j);
+    launch_together(members, k);
+  }
+  for (size_t k = 0; k < n; k++) {
+    if (!fills[k] || used[k]) continue;
+    const int64_t j = earlier(k, {k});
+    if (j >= 0) launch_together({(size_t)j, k}, k);
   }
 }
 
