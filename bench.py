@@ -38,19 +38,17 @@ def classify(plan, runs_in=None):
     attention and for products on matrix cores, bytes (each distinct input read once, each
     output written once) for everything else, including the products the backend streams.
 
-    `runs_in` (Compiled step_runs_in) names, per step, the step whose kernel computes it: a
-    product that computes an elementwise group in its epilogue, and that group, form their own
-    class (`gemm_mfma_epilogue`: the product's flops, the group's bytes beside the product's, one
-    launch), so the combined kernel's time is neither charged to the plain products nor counted
-    as elementwise work done in no time. Two products launched as one kernel stay in their class
-    with their flops, counted as one launch."""
+    `runs_in` (Compiled step_runs_in) names, per step, the step whose kernel computes it. The
+    steps one kernel computes form one unit: products only (a grouped launch) stay in their class
+    with their flops, counted as one launch; a product with the elementwise group of its epilogue
+    (and a column sum of that group's output) forms the class `gemm_mfma_epilogue`: the product's
+    flops, the other steps' bytes beside the product's, one launch, so the combined kernel's time
+    is neither charged to the plain products nor counted as elementwise work done in no time."""
     classes = {}
     runs_in = runs_in or list(range(len(plan)))
-    partner = {}
+    members = {}
     for k, r in enumerate(runs_in):
-        if r != k:
-            partner[k] = r
-            partner[r] = k
+        members.setdefault(r, []).append(k)
 
     def add(name, k, st, launch=True):
         c = classes.setdefault(name, {"steps": [], "flops": 0.0, "executed_flops": 0.0, "bytes": 0.0, "launches": 0})
@@ -65,10 +63,12 @@ def classify(plan, runs_in=None):
         return plan[q]["kind"] == "instr" and plan[q].get("op") in ("matmul", "matmul_t")
 
     for k, st in enumerate(plan):
-        paired = k in partner and is_product(k) and is_product(partner[k])
-        if k in partner and not paired:
-            product = st["kind"] != "fused"
-            add("gemm_mfma_epilogue", k, st if product else dict(st, bound="hbm"), launch=product)
+        unit = members[runs_in[k]]
+        combined = len(unit) > 1
+        products_only = combined and all(is_product(q) for q in unit)
+        launch = runs_in[k] == k
+        if combined and not products_only:
+            add("gemm_mfma_epilogue", k, st if is_product(k) else dict(st, bound="hbm"), launch=launch)
         elif st["kind"] == "attention":
             add("attention", k, st)
         elif st["kind"] == "fused":
@@ -77,7 +77,6 @@ def classify(plan, runs_in=None):
             shape = st["shape"]
             n_cols = shape[-1] if shape else 1
             m_rows = _numel(shape) // max(n_cols, 1)
-            launch = not paired or runs_in[k] == k
             if st["bound"] != "mfma":
                 add("gemm_skinny", k, st, launch=launch)
             else:

@@ -879,19 +879,28 @@ Json Compiled::profile(const std::vector<Tensor>& inputs, size_t repeats) const 
   std::vector<size_t> row_of(plan.steps.size());
   std::vector<double> sec = seconds;
   auto plain = [&](size_t q) { return !plan.steps[q].fused && !plan.steps[q].attn; };
+  auto product = [&](size_t q) {
+    if (!plain(q)) return false;
+    const std::string op = plan.steps[q].instr.op.name();
+    return op == "matmul" || op == "matmul_t";
+  };
   std::map<size_t, std::vector<size_t>> launched_with;  // launch step -> the products it computes
   for (size_t s = 0; s < plan.steps.size(); s++) row_of[s] = s;
   for (size_t s = 0; s < plan.steps.size(); s++) {
     const int64_t r = program->step_runs_in((int64_t)s);
     if (r < 0 || (size_t)r == s || (size_t)r >= plan.steps.size()) continue;
-    if (plain(s) && plain((size_t)r)) {
+    if (product(s) && product((size_t)r)) {
       auto& g = launched_with[(size_t)r];
       if (g.empty()) g.push_back((size_t)r);
       g.push_back(s);
       continue;
     }
-    const size_t product = plain(s) ? s : (size_t)r;
-    row_of[s] = row_of[(size_t)r] = product;
+    // A group in a product's epilogue, or a column sum of its output: the product's row.
+    size_t p = product(s) ? s : (size_t)r;
+    if (!product(p))
+      for (size_t q = 0; q < plan.steps.size(); q++)
+        if (program->step_runs_in((int64_t)q) == r && product(q)) p = q;
+    row_of[s] = row_of[(size_t)r] = p;
   }
   for (auto& [r, g] : launched_with) {
     double all = 0, flops = 0;

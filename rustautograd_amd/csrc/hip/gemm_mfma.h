@@ -144,7 +144,7 @@ struct StoreC {
   __device__ __forceinline__ void begin(uint32_t b, uint32_t sp) {
     out = splits > 1 ? partial + ((uint64_t)b * splits + sp) * mn : C + (uint64_t)b * mn;
   }
-  __device__ __forceinline__ void put4(uint64_t e, float4 v) { __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, (floatx4*)(out + e)); }
+  __device__ __forceinline__ void put4(uint64_t e, float4 v, int) { __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, (floatx4*)(out + e)); }
   __device__ __forceinline__ void put2(uint64_t e, float2 v) { __builtin_nontemporal_store(floatx2{v.x, v.y}, (floatx2*)(out + e)); }
   __device__ __forceinline__ void put1(uint64_t e, float v) { __builtin_nontemporal_store(v, out + e); }
 };
@@ -295,6 +295,9 @@ __device__ __forceinline__ void gemm_mfma_tile(const float* __restrict__ A, cons
   // block column MS n + gamma (K-contiguous B) or TN gamma + n (N-contiguous B). Either way a lane
   // holds adjacent output columns: four per group of four registers in one tile (K-contiguous B)
   // or one in each of its TN tiles.
+  // put4's third argument names which of the lane's runs of four columns it stores (with a
+  // K-contiguous B: tile n, register group g; the same for every row the lane stores), so that an
+  // epilogue can keep per-column sums in registers.
   epi.begin(b, sp);
   const bool vec_out = MODE != LOAD_SCALAR && N % 4 == 0;
   // A per-column bias (unsplit products only) added to the finished sums, as one fp32 addition.
@@ -335,7 +338,7 @@ __device__ __forceinline__ void gemm_mfma_tile(const float* __restrict__ A, cons
           const int col = n0 + wn * WTN + n * MS + 8 * g + q4;
           const auto& c = acc[i][n];
           if (vec_out && col + 4 <= N) {
-            epi.put4(erow + col, make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]));
+            epi.put4(erow + col, make_float4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]), n * (MF::REGS / 4) + g);
           } else {
 #pragma unroll
             for (int r = 0; r < 4; r++)
@@ -354,7 +357,7 @@ __device__ __forceinline__ void gemm_mfma_tile(const float* __restrict__ A, cons
         const uint64_t erow = (uint64_t)row * N;
         const int col = n0 + wn * WTN + TN * li;
         if (TN > 1 && vec_out && col + TN <= N) {
-          if constexpr (TN == 4) epi.put4(erow + col, make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]));
+          if constexpr (TN == 4) epi.put4(erow + col, make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]), 0);
           else if constexpr (TN == 2) epi.put2(erow + col, make_float2(acc[i][0][r], acc[i][1][r]));
         } else {
 #pragma unroll

@@ -181,13 +181,18 @@ std::string generate(const rgplan::Fused& f, const std::string& name, FusedKerne
 }
 
 std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, const ProductTile& t, const std::string& name,
-                          FusedKernel* k) {
+                          FusedKernel* k, int col_sum) {
   if (f.dtype != RG_F32) throw std::runtime_error("product epilogue: fp32 groups only");
   const std::string E = name + "_epi";
+  // Column sums (col_sum >= 0): a K-contiguous B's transposed form, where each lane stores runs
+  // of four columns, the same runs for every row (put4's slot: tile n across N, register group).
+  const int slots = (t.bn / t.wn / t.ms) * (t.ms / 16) * (t.ms == 32 ? 4 : 1);
+  if (col_sum >= 0 && (!t.tb || t.ms != 16)) throw std::runtime_error("product epilogue column sums: needs a K-contiguous B and 16x16 tiles");
   std::ostringstream s;
   s << "struct " << E << " {\n  float* c;\n";
   for (size_t j = 0; j < f.inputs.size(); j++) s << "  const float* in" << j << ";\n";
   for (size_t j = 0; j < f.outputs.size(); j++) s << "  float* out" << j << ";\n";
+  if (col_sum >= 0) s << "  float4 colacc[" << slots << "];\n";
   s << "  __device__ __forceinline__ void begin(unsigned int, unsigned int) {}\n";
   // The group's value of element e + v for v < W, from the product's outputs `a`.
   auto body = [&](int W) {
@@ -238,9 +243,15 @@ std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, 
     }
     return b.str();
   };
-  s << "  __device__ __forceinline__ void put4(unsigned long long e, float4 acc) {\n";
+  s << "  __device__ __forceinline__ void put4(unsigned long long e, float4 acc, int slot) {\n";
   if (store_c) s << "    *(float4*)(c + e) = acc;\n";
-  s << "    const float a[4] = {acc.x, acc.y, acc.z, acc.w};\n" << body(4) << "  }\n";
+  s << "    const float a[4] = {acc.x, acc.y, acc.z, acc.w};\n" << body(4);
+  if (col_sum >= 0) {
+    const std::string o = "o" + std::to_string(col_sum);
+    s << "    colacc[slot] = make_float4(colacc[slot].x + " << o << "[0], colacc[slot].y + " << o << "[1], colacc[slot].z + " << o
+      << "[2], colacc[slot].w + " << o << "[3]);\n";
+  }
+  s << "  }\n";
   s << "  __device__ __forceinline__ void put1(unsigned long long e, float acc) {\n";
   if (store_c) s << "    c[e] = acc;\n";
   s << "    const float a[1] = {acc};\n" << body(1) << "  }\n";
@@ -268,13 +279,37 @@ std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, 
     << R << "c";
   for (size_t j = 0; j < f.inputs.size(); j++) s << ", const float* " << R << "in" << j;
   for (size_t j = 0; j < f.outputs.size(); j++) s << ", float* " << R << "out" << j;
+  if (col_sum >= 0) s << ", float* __restrict__ colp";
   s << ") {\n  " << E << " epi{c";
   for (size_t j = 0; j < f.inputs.size(); j++) s << ", in" << j;
   for (size_t j = 0; j < f.outputs.size(); j++) s << ", out" << j;
   s << "};\n";
+  if (col_sum >= 0) s << "  for (int q = 0; q < " << slots << "; q++) epi.colacc[q] = make_float4(0.f, 0.f, 0.f, 0.f);\n";
   s << "  rgg::gemm_mfma_block<" << t.bm << ", " << t.bn << ", " << t.bk << ", " << t.wm << ", " << t.wn << ", " << (t.ta ? "true" : "false") << ", "
     << (t.tb ? "true" : "false") << ", " << t.mode << ", " << t.ms
-    << ">(A, B, M, N, K, a_off, b_off, a_stride, b_stride, splits, kps, bias, tiles_m, tiles_n, swizzle, epi);\n}\n";
+    << ">(A, B, M, N, K, a_off, b_off, a_stride, b_stride, splits, kps, bias, tiles_m, tiles_n, swizzle, epi);\n";
+  if (col_sum >= 0) {
+    // The tile's column sums of output col_sum from the lanes' register sums (each lane summed
+    // its rows in order): the 16 lanes holding the same columns combine by a fixed butterfly,
+    // then the WM waves along M in order, through LDS; one partial row per tile row. Lane l of
+    // wave (wm, wn) holds, in slot n, columns wn * WTN + 16 n + 4 (l / 16) .. + 3 of the tile.
+    const int wtn = t.bn / t.wn;
+    s << "  __shared__ float cs[" << t.wm << "][" << t.bn << "];\n";
+    s << "  {\n    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wmi = wave / " << t.wn << ", wni = wave % " << t.wn << ";\n";
+    s << "    for (int q = 0; q < " << slots << "; q++) {\n";
+    s << "      float4 v = epi.colacc[q];\n";
+    s << "      for (int x = 1; x < 16; x <<= 1) {\n";
+    s << "        v.x = v.x + __shfl_xor(v.x, x); v.y = v.y + __shfl_xor(v.y, x);\n";
+    s << "        v.z = v.z + __shfl_xor(v.z, x); v.w = v.w + __shfl_xor(v.w, x);\n      }\n";
+    s << "      if ((lane & 15) == 0) *(float4*)&cs[wmi][wni * " << wtn << " + 16 * q + 4 * (lane >> 4)] = v;\n    }\n  }\n";
+    s << "  __syncthreads();\n";
+    s << "  if (threadIdx.x < " << t.bn << ") {\n";
+    s << "    const rgg::TileIndex ti = rgg::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, swizzle);\n";
+    s << "    float v = cs[0][threadIdx.x];\n";
+    s << "    for (int w = 1; w < " << t.wm << "; w++) v = v + cs[w][threadIdx.x];\n";
+    s << "    colp[(rgg::uint64_t)ti.tm * N + ti.tn * " << t.bn << " + threadIdx.x] = v;\n  }\n";
+  }
+  s << "}\n";
   k->name = name;
   k->block = (uint32_t)nt;
   k->vec = 1;

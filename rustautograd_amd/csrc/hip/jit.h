@@ -65,9 +65,13 @@ struct ProductTile {
 // inputs at the output's position, applies its operations in its order (the values the plain
 // group kernel would compute) and stores its outputs, and the product itself when `store_c`.
 // The kernel's parameters are the tile kernel's, then the epilogue's pointers (product, the
-// group's inputs in order, its outputs in order).
+// group's inputs in order, its outputs in order). With `col_sum` >= 0 the kernel also sums
+// output `col_sum` over its tile's rows, column by column, once its outputs are stored, and
+// writes one partial row per tile row to a last pointer parameter: partial [tile row][N],
+// summed in tile-row order by a fold (a column sum that reads the group's output, computed here
+// instead of re-reading it).
 std::string generate_gemm(const rgplan::Fused& f, int64_t c_slot, bool store_c, const ProductTile& t, const std::string& name,
-                          FusedKernel* k);
+                          FusedKernel* k, int col_sum = -1);
 
 // Compiles all sources into one code object for gfx950 and resolves each kernel. Modules are
 // cached by source text for the life of the process. Throws std::runtime_error with the log.

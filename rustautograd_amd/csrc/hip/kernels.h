@@ -188,8 +188,10 @@ uint64_t gemm_workspace(int dtype, uint64_t m, uint64_t n, uint64_t k, uint64_t 
 
 // The MFMA tile of a single (unbatched) fp32 product whose operands are 16-byte aligned, as plan
 // slots are, when it runs unsplit on the tile kernel and each lane's finished outputs come in
-// runs of four adjacent columns (the form an elementwise epilogue takes): the shape arguments of
-// the tile kernel (gemm_mfma.h). False for any other product.
+// runs of two or four adjacent columns (the form an elementwise epilogue takes): the shape
+// arguments of the tile kernel (gemm_mfma.h). False for any other product. `mode` is the tile's
+// load mode, GEMM_WHOLE_TILES when M, N and K are multiples of the tile.
+constexpr int GEMM_WHOLE_TILES = 0;  // rgg::LOAD_EVEN
 struct GemmTile {
   int bm, bn, bk, wm, wn, ms, mode, kps;
   uint32_t tm, tn;

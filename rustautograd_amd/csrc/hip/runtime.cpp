@@ -120,6 +120,8 @@ struct Program {
   // Per step: for a product launched with others at another step (group_products), that step;
   // -1 otherwise.
   std::vector<int64_t> pair_of;
+  // Per step: for a column sum computed by a product epilogue's kernel, the step it runs at; -1.
+  std::vector<int64_t> absorbed_into;
   // Runs of consecutive small, independent fused groups launched as one kernel (merge_sets):
   // merged[m] replaces steps first..last when all of them run; merged_at[k] is the run starting
   // at step k, or -1. The single-step functions stay for partial ranges and per-step timing.
@@ -689,7 +691,8 @@ bool flat_product(const Instr& i, uint64_t* m, uint64_t* n, uint64_t* k, bool* t
 // Product `i` launched through `fk`, its kernel with group `f` as the epilogue (generate_gemm):
 // the tile kernel's arguments, then the pointers of the epilogue (the product's output when
 // `store_c`, else null; the group's inputs; its outputs), one kernel argument each.
-StepFn lower_product_epilogue(const Instr& i, const rgplan::Fused& f, const rgjit::FusedKernel* fk, bool store_c) {
+StepFn lower_product_epilogue(const Instr& i, const rgplan::Fused& f, const rgjit::FusedKernel* fk, bool store_c, const Program* pp,
+                              int64_t col_off) {
   uint64_t m, n, k;
   bool ta, tb;
   rgk::GemmTile t;
@@ -702,7 +705,7 @@ StepFn lower_product_epilogue(const Instr& i, const rgplan::Fused& f, const rgji
   if (ptr_slots.size() > 128) throw std::runtime_error("product epilogue with more than 127 operands");
   const int64_t as = i.args[0].slot, bs = i.args[1].slot, bias = i.args.size() == 3 ? i.args[2].slot : -1;
   const int M = (int)m, N = (int)n, K = (int)k;
-  return [fk, ptr_slots, as, bs, bias, t, M, N, K](hipStream_t s, void* const* sl, void*) {
+  return [fk, ptr_slots, as, bs, bias, t, M, N, K, pp, col_off](hipStream_t s, void* const* sl, void* ws) {
     const void* A = sl[as];
     const void* B = sl[bs];
     const void* bias_p = bias >= 0 ? sl[bias] : nullptr;
@@ -711,10 +714,15 @@ StepFn lower_product_epilogue(const Instr& i, const rgplan::Fused& f, const rgji
     const void* b_off = nullptr;
     uint64_t a_stride = 0, b_stride = 0;
     uint32_t tm = t.tm, tn = t.tn;
-    void* ptrs[128];
-    void* args[15 + 128] = {&A, &B, &mm, &nn, &kk, &a_off, &b_off, &a_stride, &b_stride, &splits, &kps, &bias_p, &tm, &tn, &swizzle};
-    for (size_t q = 0; q < ptr_slots.size(); q++) {
+    void* ptrs[129];
+    void* args[15 + 129] = {&A, &B, &mm, &nn, &kk, &a_off, &b_off, &a_stride, &b_stride, &splits, &kps, &bias_p, &tm, &tn, &swizzle};
+    size_t q = 0;
+    for (; q < ptr_slots.size(); q++) {
       ptrs[q] = ptr_slots[q] >= 0 ? sl[ptr_slots[q]] : nullptr;
+      args[15 + q] = &ptrs[q];
+    }
+    if (col_off >= 0) {  // the column sums' partial rows, in the fold area
+      ptrs[q] = (char*)ws + pp->fold_base() + col_off;
       args[15 + q] = &ptrs[q];
     }
     hipModuleLaunchKernel(fk->fn, tm * tn, 1, 1, fk->block, 1, 1, 0, s, args, nullptr);
@@ -793,12 +801,33 @@ bool product_output_needed(const Plan& plan, size_t k, size_t j) {
 struct Epilogues {
   std::vector<int64_t> at;  // per step: the product whose kernel computes this group, or -1
   std::vector<bool> sunk;   // per group step: the combined kernel runs at the group's step
+  // Per group step: the column sum the combined kernel also computes (a later sum over every
+  // axis but the last of one of the group's outputs), or -1; per step: the group whose kernel
+  // computes this sum, or -1.
+  std::vector<int64_t> sum_of, sum_in;
+  std::vector<int> sum_out;  // per group step: which of the group's outputs the sum reads
 };
+
+// Whether step s is an f32 sum over every axis but the last of the value in `slot`, shaped
+// [..., n] with `total` elements, into [1, ..., 1, n].
+bool column_sum_of(const Step& st, int64_t slot, uint64_t total, uint64_t n) {
+  if (st.kind != RG_STEP_INSTR || st.instr.op != RG_OP_REDUCE || st.instr.dtype != RG_F32 || st.instr.args.size() != 1) return false;
+  const Instr& i = st.instr;
+  const auto& in = i.args[0].shape;
+  if (i.args[0].slot != slot || in.empty() || (uint64_t)in.back() != n || prod(in) != total || (int)i.attr[0] != RG_REDUCE_SUM) return false;
+  const size_t n_axes = (size_t)i.attr[2];
+  std::vector<bool> red(in.size(), false);
+  for (size_t q = 0; q < n_axes; q++) red[(size_t)i.attr[3 + q]] = true;
+  for (size_t d = 0; d + 1 < in.size(); d++)
+    if (!red[d] && in[d] != 1) return false;
+  return !red[in.size() - 1] && (uint64_t)i.n == n;
+}
 
 Epilogues find_epilogues(const Plan& plan) {
   const auto& steps = plan.steps;
   const size_t n = steps.size();
-  Epilogues ep{std::vector<int64_t>(n, -1), std::vector<bool>(n, false)};
+  Epilogues ep{std::vector<int64_t>(n, -1), std::vector<bool>(n, false), std::vector<int64_t>(n, -1), std::vector<int64_t>(n, -1),
+               std::vector<int>(n, -1)};
   const char* env = getenv("RG_HIP_EPILOGUE");
   if (env && env[0] == '0') return ep;
   const bool every = env && std::string(env) == "all";
@@ -851,6 +880,28 @@ Epilogues find_epilogues(const Plan& plan) {
       ep.at[j] = k;
       ep.sunk[j] = !hoist;
       taken[(size_t)k] = true;
+      // A column sum of one of the group's outputs a few steps later, with nothing between the
+      // group and it overwriting that output: computed by the combined kernel from the values
+      // it stores, summed in registers (a K-contiguous B, whole 16x16-MFMA tiles: every output
+      // goes through put4). RG_HIP_EPILOGUE_SUMS=0 leaves it to its own kernel.
+      const char* sums = getenv("RG_HIP_EPILOGUE_SUMS");
+      if ((sums && sums[0] == '0') || !tb || tile.ms != 16 || tile.mode != rgk::GEMM_WHOLE_TILES) break;
+      for (size_t q = j + 1; q < n && q <= j + 4; q++) {
+        if (steps[q].kind == RG_STEP_INSTR && is_control(steps[q].instr.op)) break;
+        int out = -1;
+        for (size_t o = 0; o < f.outputs.size(); o++)
+          if (column_sum_of(steps[q], f.outputs[o].second, m * nn, nn)) out = (int)o;
+        if (out >= 0) {
+          bool clear = true;
+          for (size_t r = j + 1; r < q; r++) clear = clear && !has_slot(writes[r], f.outputs[(size_t)out].second);
+          if (clear) {
+            ep.sum_of[j] = (int64_t)q;
+            ep.sum_in[q] = (int64_t)j;
+            ep.sum_out[j] = out;
+          }
+          break;
+        }
+      }
       break;
     }
   }
@@ -863,7 +914,8 @@ void place_bodies(Program& prog);
 // Source of product `pk`'s kernel with fused step `j` as its epilogue (kernel `prefix`rge`pk`).
 // The product's own output is still stored (`*store_c`) when a later step or the host reads it
 // before it is next written.
-std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::string& prefix, bool* store_c, rgjit::FusedKernel* fk) {
+std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::string& prefix, bool* store_c, rgjit::FusedKernel* fk,
+                            int col_sum) {
   const Instr& pi = plan.steps[(size_t)pk].instr;
   const int64_t c = pi.dst;
   const bool keep = product_output_needed(plan, (size_t)pk, j);
@@ -874,7 +926,7 @@ std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::s
   if (!flat_product(pi, &m, &nn, &kk, &ta, &tb) || !rgk::gemm_epilogue_tile(RG_F32, m, nn, kk, ta, tb, &t))
     throw std::runtime_error("product epilogue: the product does not fit a single tile kernel");
   return rgjit::generate_gemm(plan.steps[j].fused, c, keep, rgjit::ProductTile{t.bm, t.bn, t.bk, t.wm, t.wn, t.ms, t.mode, ta, tb},
-                              prefix + "rge" + std::to_string(pk), fk);
+                              prefix + "rge" + std::to_string(pk), fk, col_sum);
 }
 
 // Independent products launched as one kernel (rgk::gemm_group): two adjacent plain products
@@ -886,7 +938,8 @@ std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::s
 // Step k launches them all, the others nothing; at run time a group whose operands turn out not
 // to fit (alignment) is launched as single kernels, at step k. The results are the single
 // launches'. RG_HIP_PAIR=0 turns this off.
-void group_products(Program& prog, const std::vector<GemmFill>& fills, const std::vector<rgk::GemmArgs>& base) {
+void group_products(Program& prog, const std::vector<GemmFill>& fills, const std::vector<rgk::GemmArgs>& base,
+                    std::vector<size_t>& fold_producer) {
   const size_t n = prog.plan.steps.size();
   prog.pair_of.assign(n, -1);
   const char* env = getenv("RG_HIP_PAIR");
@@ -942,6 +995,9 @@ void group_products(Program& prog, const std::vector<GemmFill>& fills, const std
       if (x != k) {
         prog.pair_of[x] = (int64_t)k;
         prog.steps[x] = [](hipStream_t, void* const*, void*) {};
+        // Its K-split partials are written at step k now: their fold is due after it.
+        for (auto& fp : fold_producer)
+          if (fp == x) fp = k;
       }
     }
     prog.steps[k] = [f](hipStream_t s, void* const* sl, void* wsp) {
@@ -974,6 +1030,7 @@ void build_program(Program& prog) {
   const Epilogues ep = find_epilogues(prog.plan);
   prog.epilogue_of = ep.at;
   prog.epilogue_sunk = ep.sunk;
+  prog.absorbed_into.assign(n_steps, -1);
   std::vector<int64_t> epilogue_at(n_steps, -1);  // product step -> the group it computes
   for (size_t j = 0; j < n_steps; j++)
     if (ep.at[j] >= 0) epilogue_at[(size_t)ep.at[j]] = (int64_t)j;
@@ -988,7 +1045,7 @@ void build_program(Program& prog) {
       const int64_t pk = prog.epilogue_of[k];
       if (pk >= 0) {
         bool keep = false;
-        src << epilogue_source(prog.plan, k, pk, "", &keep, fk.get());
+        src << epilogue_source(prog.plan, k, pk, "", &keep, fk.get(), ep.sum_out[k]);
         store_c[(size_t)pk] = keep;
       } else if (st.kind == RG_STEP_ROWS) {
         src << rgjit::generate_rows(st.fused, "rgr" + std::to_string(k), fk.get());
@@ -1033,18 +1090,42 @@ void build_program(Program& prog) {
   size_t fi = 0;
   for (size_t k = 0; k < prog.plan.steps.size(); k++) {
     const Step& st = prog.plan.steps[k];
+    // The combined kernel of product pk and group j, run at step k: with a column sum, its
+    // partial rows (one per tile row) go to the fold area, folded like a reduction's.
+    auto combined = [&](size_t pk, size_t j) {
+      int64_t col_off = -1;
+      if (ep.sum_of[j] >= 0) {
+        const size_t q = (size_t)ep.sum_of[j];
+        uint64_t m, nn, kk;
+        bool ta, tb;
+        rgk::GemmTile t;
+        if (!flat_product(prog.plan.steps[pk].instr, &m, &nn, &kk, &ta, &tb) || !rgk::gemm_epilogue_tile(RG_F32, m, nn, kk, ta, tb, &t))
+          throw std::runtime_error("product epilogue: the product no longer fits a single tile kernel");
+        col_off = (int64_t)prog.fold_bytes;
+        prog.folds.push_back({prog.fold_bytes, prog.plan.steps[q].instr.dst, t.tm, (uint32_t)nn, RG_REDUCE_SUM, RG_F32});
+        fold_producer.push_back(k);
+        prog.fold_bytes += ((uint64_t)t.tm * nn * 4 + 255) / 256 * 256;
+        prog.absorbed_into[q] = (int64_t)k;
+      }
+      return lower_product_epilogue(prog.plan.steps[pk].instr, prog.plan.steps[j].fused, kernel_of[j], store_c[pk], &prog, col_off);
+    };
     if ((st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) && ep.at[k] >= 0) {
       // Computed by its product's kernel, run here when the product waits for this step.
       fi++;
       const size_t pk = (size_t)ep.at[k];
-      if (ep.sunk[k]) prog.steps.push_back(lower_product_epilogue(prog.plan.steps[pk].instr, st.fused, kernel_of[k], store_c[pk]));
+      if (ep.sunk[k]) prog.steps.push_back(combined(pk, k));
       else prog.steps.push_back([](hipStream_t, void* const*, void*) {});
       continue;
     }
     if (st.kind == RG_STEP_INSTR && epilogue_at[k] >= 0) {
       const size_t j = (size_t)epilogue_at[k];
       if (ep.sunk[j]) prog.steps.push_back([](hipStream_t, void* const*, void*) {});
-      else prog.steps.push_back(lower_product_epilogue(st.instr, prog.plan.steps[j].fused, kernel_of[j], store_c[k]));
+      else prog.steps.push_back(combined(k, j));
+      continue;
+    }
+    if (st.kind == RG_STEP_INSTR && ep.sum_in[k] >= 0) {
+      // A column sum computed by the combined kernel of the group it reads.
+      prog.steps.push_back([](hipStream_t, void* const*, void*) {});
       continue;
     }
     if (st.kind == RG_STEP_FUSED || st.kind == RG_STEP_ROWS) {
@@ -1094,7 +1175,7 @@ void build_program(Program& prog) {
       while (fold_producer.size() < prog.folds.size()) fold_producer.push_back(k);
     }
   }
-  group_products(prog, gemm_fills, gemm_base);
+  group_products(prog, gemm_fills, gemm_base, fold_producer);
   for (auto& s : prog.plan.slots) prog.slot_bytes.push_back(std::max<uint64_t>((uint64_t)s.cap * esize(s.dtype), 4));
   place_bodies(prog);
   // Each fold runs before the first later step reading its output, or right after its producer.
@@ -1104,8 +1185,9 @@ void build_program(Program& prog) {
   // runs at.
   auto reads_at = [&](size_t j) {
     std::vector<int64_t> r;
-    // Products launched together read their operands at the step of the launch.
-    if (prog.pair_of[j] >= 0) return r;
+    // Products launched together read their operands at the step of the launch; a column sum
+    // computed by a combined kernel reads nothing at its own step.
+    if (prog.pair_of[j] >= 0 || prog.absorbed_into[j] >= 0) return r;
     bool grouped = false;
     for (size_t q = 0; q < n; q++)
       if (prog.pair_of[q] == (int64_t)j) {
@@ -1427,7 +1509,8 @@ void run_cond(hipStream_t s, const Program::Control& c, const Program& owner, co
 std::string plan_source(const Plan& root, int* count) {
   std::ostringstream src;
   std::function<void(const Plan&, const std::string&)> add = [&](const Plan& plan, const std::string& prefix) {
-    const std::vector<int64_t> epi = find_epilogues(plan).at;
+    const Epilogues eps = find_epilogues(plan);
+    const std::vector<int64_t>& epi = eps.at;
     for (size_t k = 0; k < plan.steps.size(); k++) {
       const auto& st = plan.steps[k];
       if (st.kind == RG_STEP_INSTR && is_control(st.instr.op)) {
@@ -1439,7 +1522,7 @@ std::string plan_source(const Plan& root, int* count) {
       if (st.kind != RG_STEP_FUSED && st.kind != RG_STEP_ROWS) continue;
       rgjit::FusedKernel fk;
       bool keep;
-      if (epi[k] >= 0) src << epilogue_source(plan, k, epi[k], prefix, &keep, &fk);
+      if (epi[k] >= 0) src << epilogue_source(plan, k, epi[k], prefix, &keep, &fk, eps.sum_out[k]);
       else if (st.kind == RG_STEP_ROWS) src << rgjit::generate_rows(st.fused, prefix + "rgr" + std::to_string(k), &fk);
       else src << rgjit::generate(st.fused, prefix + "rgf" + std::to_string(k), &fk);
       (*count)++;
@@ -1833,6 +1916,7 @@ int64_t rg_hip_program_step_runs_in(void* program, int64_t step) {
   if (step < 0 || (size_t)step >= p->plan.steps.size()) return -1;
   const size_t k = (size_t)step;
   if (p->pair_of[k] >= 0) return p->pair_of[k];
+  if (p->absorbed_into[k] >= 0) return p->absorbed_into[k];
   if (p->epilogue_of[k] >= 0) return p->epilogue_sunk[k] ? step : p->epilogue_of[k];
   for (size_t j = 0; j < p->epilogue_of.size(); j++)
     if (p->epilogue_of[j] == step && p->epilogue_sunk[j]) return (int64_t)j;

@@ -167,7 +167,19 @@ def test_product_epilogue_kernels_compile_for_gfx950(monkeypatch):
     z = g.un("tanh", g.bin("mul", y, y))
     words, _ = _rg.plan_words(g.g, [z], "hip", "standard")
     src = _kernel_source(words)
-    assert src.count("rgg::gemm_mfma_block<") == 1 and "amdgpu_waves_per_eu(2)" in src
+    assert src.count("rgg::gemm_mfma_block<") == 1 and "amdgpu_waves_per_eu(2)" in src and "colp" not in src
+    n, err = _compile_check(words)
+    assert n >= 1, err
+    # A column sum of the group's output (a bias gradient's shape) is computed by the same kernel
+    # when the product's right operand is K-contiguous (its lanes hold runs of four columns).
+    g = G()
+    x, w = g.input((8192, 256), "float32"), g.input((1024, 256), "float32")
+    y = g.op("matmul", [x, g.op("transpose", [w], perm=[1, 0])])
+    z = g.un("tanh", g.bin("mul", y, y))
+    zs = g.op("sum", [z], axes=[0], keepdims=False)
+    words, _ = _rg.plan_words(g.g, [z, zs], "hip", "standard")
+    src = _kernel_source(words)
+    assert src.count("rgg::gemm_mfma_block<") == 1 and "colp[" in src
     n, err = _compile_check(words)
     assert n >= 1, err
     monkeypatch.setenv("RG_HIP_EPILOGUE", "0")

@@ -1,6 +1,8 @@
-"""Kernels that compute two plan steps: elementwise groups computed in the epilogue of the product
-they read, against the same program with every group in its own kernel (RG_HIP_EPILOGUE=0), and
-pairs of independent products launched as one kernel, against single launches (RG_HIP_PAIR=0).
+"""Kernels that compute several plan steps: elementwise groups computed in the epilogue of the
+product they read, against the same program with every group in its own kernel
+(RG_HIP_EPILOGUE=0); column sums of such a group's output computed in the same kernel, against
+the reduction kernel (RG_HIP_EPILOGUE_SUMS=0); and independent products launched as one kernel,
+against single launches (RG_HIP_PAIR=0).
 
 The combined kernel applies the group's operations, in the group's order, to the product's
 finished outputs (the values the product's own kernel would have stored), so the two programs
@@ -36,7 +38,8 @@ def _bits(tree):
 def test_products_with_epilogues_match_separate_kernels_bit_for_bit(monkeypatch, name, mode, steps, pairs):
     step, state = workloads.mlp_train_step() if name == "C2" else workloads.gpt_train_step(workloads.GPT_CONFIGS[name])
     print(f"{name}: compile with and without product epilogues ({mode or 'default'}), {steps} device steps", flush=True)
-    monkeypatch.setenv("RG_HIP_PAIR", "0")  # pairs of products: the test below
+    monkeypatch.setenv("RG_HIP_PAIR", "0")  # pairs of products: a test below
+    monkeypatch.setenv("RG_HIP_EPILOGUE_SUMS", "0")  # column sums in the epilogue: a test below
     monkeypatch.setenv("RG_HIP_EPILOGUE", "0")
     plain = rg.compile(step, (state,), validate="none", device="hip")
     if mode:
@@ -80,3 +83,35 @@ def test_products_launched_together_match_single_launches_bit_for_bit(monkeypatc
     assert np.array_equal(np.array(r0.history["aux"]).view(np.uint64), np.array(r1.history["aux"]).view(np.uint64))
     for a, b in zip(_bits(r0.state), _bits(r1.state)):
         assert np.array_equal(a, b)
+
+
+def test_column_sums_in_product_epilogues_match_the_reduction_kernel(monkeypatch):
+    """Each C4 layer's fc1 bias gradient, the column sum of the GELU backward's output, is computed
+    by the product kernel that computes that output: each lane sums its rows in registers, the
+    tile's lanes and waves combine in a fixed order, and one partial row per 128-row tile goes to
+    the fold area (then folded in tile order). The sums' order differs from the reduction
+    kernel's (RG_HIP_EPILOGUE_SUMS=0), so after one step the bias gradients' leaves (the biases
+    and their AdamW moments) agree to rounding, within 1e-4 of each leaf's largest value (1.8e-5
+    measured on MI355X), and every other leaf and the loss bit for bit."""
+    step, state = workloads.gpt_train_step(workloads.GPT_CONFIGS["C4"])
+    print("C4: compile with and without column sums in product epilogues, 1 device step", flush=True)
+    monkeypatch.setenv("RG_HIP_EPILOGUE_SUMS", "0")
+    plain = rg.compile(step, (state,), validate="none", device="hip")
+    monkeypatch.delenv("RG_HIP_EPILOGUE_SUMS")
+    fused = rg.compile(step, (state,), validate="none", device="hip")
+    plan = fused.plan_summary()
+    absorbed = [(k, r) for k, r in enumerate(fused._n.step_runs_in()) if r != k and plan[k].get("op") == "sum"]
+    assert len(absorbed) == 6 and not [k for k, r in enumerate(plain._n.step_runs_in()) if r != k and plan[k].get("op") == "sum"]
+    r0 = rg.run(plain, state, steps=1)
+    r1 = rg.run(fused, state, steps=1)
+    assert r0.status == r1.status == "completed" and r0.history["aux"] == r1.history["aux"]
+    differing = 0
+    for a, b in zip(_pytree.leaves(r0.state), _pytree.leaves(r1.state)):
+        a, b = np.asarray(a.numpy()), np.asarray(b.numpy())
+        if np.array_equal(np.atleast_1d(a).view(np.uint8), np.atleast_1d(b).view(np.uint8)):
+            continue
+        differing += 1
+        assert a.shape == (1024,), a.shape
+        scale = max(float(np.abs(a).max()), 1e-30)
+        assert float(np.abs(a.astype(np.float64) - b).max()) <= 1e-4 * scale
+    assert 0 < differing <= 18, differing
