@@ -418,6 +418,28 @@ __device__ __forceinline__ void bwd_q_block(const AttnArgs& a, uint32_t bx, uint
 #pragma unroll
     for (int n = 0; n < ND; n++) drow[n * 16 + l16] = dacc[n][r];
   }
+  if (a.colp) {
+    // dq's column sums over the problem's rows (every wave holds 16 of them): each lane's four
+    // rows in order, the wave's four row groups by a fixed butterfly, then the waves in order
+    // through LDS (the K rows' space, every wave past its products).
+    float cs[ND];
+#pragma unroll
+    for (int n = 0; n < ND; n++) {
+      cs[n] = ((dacc[n][0] + dacc[n][1]) + dacc[n][2]) + dacc[n][3];
+      cs[n] = cs[n] + __shfl_xor(cs[n], 16);
+      cs[n] = cs[n] + __shfl_xor(cs[n], 32);
+    }
+    __syncthreads();
+    if (lane < 16)
+#pragma unroll
+      for (int n = 0; n < ND; n++) Ks[w * HD + n * 16 + l16] = cs[n];
+    __syncthreads();
+    if (tid < HD) {
+      float t = Ks[tid];
+      for (int q = 1; q < WAVES; q++) t = t + Ks[q * HD + tid];
+      a.colp[(uint64_t)(bh / a.heads) * a.col_len + a.col_q + (bh % a.heads) * a.dq.sh + tid] = t;
+    }
+  }
 }
 
 // Backward, key side: one block per 16 * WAVES keys; dv = P^T dO and dk = dS^T q over the query
@@ -574,6 +596,36 @@ __device__ __forceinline__ void bwd_kv_block(const AttnArgs& a, uint32_t bx, uin
       vrow[n * 16 + l16] = vacc[n][r];
     }
   }
+  if (a.colp) {
+    // dk's and dv's column sums over the problem's rows, as the query pass sums dq's (through the
+    // q rows' space): the stored values, each lane's four rows in order, a fixed butterfly over
+    // the wave's row groups, the waves in order.
+    float ck[ND], cv[ND];
+#pragma unroll
+    for (int n = 0; n < ND; n++) {
+      ck[n] = ((kacc[n][0] * rdiv + kacc[n][1] * rdiv) + kacc[n][2] * rdiv) + kacc[n][3] * rdiv;
+      cv[n] = ((vacc[n][0] + vacc[n][1]) + vacc[n][2]) + vacc[n][3];
+      ck[n] = ck[n] + __shfl_xor(ck[n], 16);
+      ck[n] = ck[n] + __shfl_xor(ck[n], 32);
+      cv[n] = cv[n] + __shfl_xor(cv[n], 16);
+      cv[n] = cv[n] + __shfl_xor(cv[n], 32);
+    }
+    __syncthreads();
+    if (lane < 16)
+#pragma unroll
+      for (int n = 0; n < ND; n++) {
+        Qs[w * 2 * HD + n * 16 + l16] = ck[n];
+        Qs[w * 2 * HD + HD + n * 16 + l16] = cv[n];
+      }
+    __syncthreads();
+    if (tid < 2 * HD) {
+      float t = Qs[tid];
+      for (int q = 1; q < WAVES; q++) t = t + Qs[q * 2 * HD + tid];
+      const uint32_t h = bh % a.heads;
+      const int64_t col = tid < HD ? a.col_k + h * a.dk.sh + tid : a.col_v + h * a.dv.sh + (tid - HD);
+      a.colp[(uint64_t)(bh / a.heads) * a.col_len + col] = t;
+    }
+  }
 }
 
 template <int HD, int WAVES>
@@ -665,7 +717,12 @@ void attention_forward(hipStream_t s, const AttnArgs& a, bool build_mask_bits) {
   else forward_hd<64>(s, a);
 }
 
+bool attention_backward_column_sums(const AttnArgs& a) {
+  return a.tq == a.tk && a.tq == 256 && a.bh >= 256 && a.bh % a.heads == 0;
+}
+
 void attention_backward(hipStream_t s, const AttnArgs& a) {
+  if (a.colp && !attention_backward_column_sums(a)) throw std::runtime_error("attention backward: column sums for these shapes");
   if (a.hd == 16) backward_hd<16>(s, a);
   else if (a.hd == 32) backward_hd<32>(s, a);
   else backward_hd<64>(s, a);

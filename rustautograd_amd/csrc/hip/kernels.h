@@ -170,12 +170,21 @@ struct AttnArgs {
   float *stat_m, *stat_z, *stat_dd;
   AttnOperand o_in, d_o;  // backward inputs: the forward output and its cotangent
   AttnOperand dq, dk, dv;
+  // Optional, backward: column sums of dq, dk and dv over each batch element's rows, as partial
+  // rows colp[b][col_len] (a bias gradient of the projection the three share: dq's column c of
+  // head h at col_q + h * dq.sh + c, dk's and dv's likewise), for a fold to sum over b. Only with
+  // attention_backward_column_sums.
+  float* colp = nullptr;
+  int64_t col_len = 0, col_q = 0, col_k = 0, col_v = 0;
 };
 bool attention_supported(int dtype, int64_t hd, int64_t tq, int64_t tk);
 uint64_t attention_mask_words(const AttnArgs& a);
 // `build_mask_bits`: pack the mask into `mask_bits` first (else they hold it already).
 void attention_forward(hipStream_t s, const AttnArgs& a, bool build_mask_bits = true);
 void attention_backward(hipStream_t s, const AttnArgs& a);
+// Whether the backward of these shapes can write column sums (AttnArgs::colp): one block per
+// problem for each pass, which holds all of the problem's rows.
+bool attention_backward_column_sums(const AttnArgs& a);
 
 // Whether the product runs through the bandwidth-bound skinny kernels (alignment aside: an
 // unaligned operand falls back to the general kernels at launch).

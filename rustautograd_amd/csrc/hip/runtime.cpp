@@ -551,7 +551,7 @@ StepFn lower_instr(Program& prog, const Instr& i) {
 
 // A fused attention step (attention.hip). The statistics slot holds the per-query max, sum and
 // rowsum(dO * O), then the packed mask bits.
-StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
+StepFn lower_attention(Program& prog, const rgplan::Attn& at, int64_t col_off = -1) {
   if (!rgk::attention_supported(at.dtype, at.hd, at.tq, at.tk))
     throw std::runtime_error("attention step of unsupported shape (hd " + std::to_string(at.hd) + ", t " + std::to_string(at.tq) + "x" +
                              std::to_string(at.tk) + ")");
@@ -585,7 +585,8 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
       if (v.offset % 4 || v.sb % 4 || v.sh % 4 || v.st % 4 || esize(prog.plan.slots[(size_t)v.slot].dtype) != 4)
         throw std::runtime_error("attention operand view is not 16-byte aligned");
   const bool bwd = at.backward;
-  return [=](hipStream_t s, void* const* sl, void*) {
+  const Program* pp = &prog;
+  return [=](hipStream_t s, void* const* sl, void* wsp) {
     rgk::AttnArgs a = base;
     auto op = [&](const rgplan::AttnView& v) {
       return rgk::AttnOperand{(const float*)sl[v.slot] + v.offset, v.sb, v.sh, v.st};
@@ -610,6 +611,13 @@ StepFn lower_attention(Program& prog, const rgplan::Attn& at) {
       a.dq = op(out[0]);
       a.dk = op(out[1]);
       a.dv = op(out[2]);
+      if (col_off >= 0) {  // column sums of dq, dk, dv: partial rows in the fold area
+        a.colp = (float*)((char*)wsp + pp->fold_base() + col_off);
+        a.col_len = out[0].st;
+        a.col_q = out[0].offset;
+        a.col_k = out[1].offset;
+        a.col_v = out[2].offset;
+      }
       rgk::attention_backward(s, a);
     }
   };
@@ -823,6 +831,49 @@ bool column_sum_of(const Step& st, int64_t slot, uint64_t total, uint64_t n) {
   return !red[in.size() - 1] && (uint64_t)i.n == n;
 }
 
+// The step q a few steps after attention backward step j that sums the three gradients' slot
+// over every axis but the last (a bias gradient of the projection q, k and v come from), when the
+// backward can write those sums itself: dq, dk and dv rows of one slot, L columns a row, the
+// views' heads covering every column once, and shapes for which the backward writes column sums
+// (rgk::attention_backward_column_sums). -1 otherwise, or with RG_HIP_EPILOGUE_SUMS=0.
+int64_t attention_column_sum(const Plan& plan, size_t j) {
+  const Step& sj = plan.steps[j];
+  if (sj.kind != RG_STEP_ATTN || !sj.attn.backward || sj.attn.out.size() != 3 || sj.attn.dtype != RG_F32) return -1;
+  const char* sums = getenv("RG_HIP_EPILOGUE_SUMS");
+  if (sums && sums[0] == '0') return -1;
+  const rgplan::Attn& at = sj.attn;
+  rgk::AttnArgs a{};
+  a.bh = (uint32_t)at.bh;
+  a.heads = (uint32_t)at.heads;
+  a.tq = (int)at.tq;
+  a.tk = (int)at.tk;
+  a.hd = (int)at.hd;
+  if (at.heads <= 0 || !rgk::attention_backward_column_sums(a)) return -1;
+  const int64_t slot = at.out[0].slot, L = at.out[0].st, B = at.bh / at.heads;
+  std::vector<int> seen((size_t)std::max<int64_t>(L, 0), 0);
+  for (const auto& v : at.out) {
+    if (v.slot != slot || v.st != L || v.sb != at.tq * L || v.offset < 0) return -1;
+    for (int64_t h = 0; h < at.heads; h++)
+      for (int64_t c = 0; c < at.hd; c++) {
+        const int64_t col = v.offset + h * v.sh + c;
+        if (col < 0 || col >= L || seen[(size_t)col]++) return -1;
+      }
+  }
+  for (int x : seen)
+    if (!x) return -1;
+  for (size_t q = j + 1; q < plan.steps.size() && q <= j + 4; q++) {
+    const Step& sq = plan.steps[q];
+    if (sq.kind == RG_STEP_INSTR && is_control(sq.instr.op)) return -1;
+    if (column_sum_of(sq, slot, (uint64_t)(B * at.tq * L), (uint64_t)L)) {
+      for (size_t r = j + 1; r < q; r++)
+        if (has_slot(step_writes(plan.steps[r]), slot)) return -1;
+      return (int64_t)q;
+    }
+  }
+  return -1;
+}
+
+
 Epilogues find_epilogues(const Plan& plan) {
   const auto& steps = plan.steps;
   const size_t n = steps.size();
@@ -1031,6 +1082,16 @@ void build_program(Program& prog) {
   prog.epilogue_of = ep.at;
   prog.epilogue_sunk = ep.sunk;
   prog.absorbed_into.assign(n_steps, -1);
+  // Column sums the attention backward computes (attention_column_sum): per attention step, the
+  // sum step; per sum step, the attention step.
+  std::vector<int64_t> attn_sum_of(n_steps, -1), attn_sum_in(n_steps, -1);
+  for (size_t j = 0; j < n_steps; j++) {
+    const int64_t q = attention_column_sum(prog.plan, j);
+    if (q >= 0 && ep.sum_in[(size_t)q] < 0) {
+      attn_sum_of[j] = q;
+      attn_sum_in[(size_t)q] = (int64_t)j;
+    }
+  }
   std::vector<int64_t> epilogue_at(n_steps, -1);  // product step -> the group it computes
   for (size_t j = 0; j < n_steps; j++)
     if (ep.at[j] >= 0) epilogue_at[(size_t)ep.at[j]] = (int64_t)j;
@@ -1123,8 +1184,9 @@ void build_program(Program& prog) {
       else prog.steps.push_back(combined(k, j));
       continue;
     }
-    if (st.kind == RG_STEP_INSTR && ep.sum_in[k] >= 0) {
-      // A column sum computed by the combined kernel of the group it reads.
+    if (st.kind == RG_STEP_INSTR && (ep.sum_in[k] >= 0 || attn_sum_in[k] >= 0)) {
+      // A column sum computed by the combined kernel of the group it reads, or by the attention
+      // backward whose gradients it reads.
       prog.steps.push_back([](hipStream_t, void* const*, void*) {});
       continue;
     }
@@ -1160,7 +1222,17 @@ void build_program(Program& prog) {
         hipModuleLaunchKernel(fk->fn, fk->grid, 1, 1, fk->block, 1, 1, 0, s, args, nullptr);
       });
     } else if (st.kind == RG_STEP_ATTN) {
-      prog.steps.push_back(lower_attention(prog, st.attn));
+      int64_t col_off = -1;
+      if (attn_sum_of[k] >= 0) {
+        const size_t q = (size_t)attn_sum_of[k];
+        const uint64_t rows = (uint64_t)(st.attn.bh / st.attn.heads), len = (uint64_t)st.attn.out[0].st;
+        col_off = (int64_t)prog.fold_bytes;
+        prog.folds.push_back({prog.fold_bytes, prog.plan.steps[q].instr.dst, (uint32_t)rows, (uint32_t)len, RG_REDUCE_SUM, RG_F32});
+        fold_producer.push_back(k);
+        prog.fold_bytes += (rows * len * 4 + 255) / 256 * 256;
+        prog.absorbed_into[q] = (int64_t)k;
+      }
+      prog.steps.push_back(lower_attention(prog, st.attn, col_off));
     } else if (is_control(st.instr.op)) {
       prog.steps.push_back(lower_control(prog, k));
     } else {

@@ -85,23 +85,28 @@ def test_products_launched_together_match_single_launches_bit_for_bit(monkeypatc
         assert np.array_equal(a, b)
 
 
-def test_column_sums_in_product_epilogues_match_the_reduction_kernel(monkeypatch):
-    """Each C4 layer's fc1 bias gradient, the column sum of the GELU backward's output, is computed
-    by the product kernel that computes that output: each lane sums its rows in registers, the
-    tile's lanes and waves combine in a fixed order, and one partial row per 128-row tile goes to
-    the fold area (then folded in tile order). The sums' order differs from the reduction
-    kernel's (RG_HIP_EPILOGUE_SUMS=0), so after one step the bias gradients' leaves (the biases
-    and their AdamW moments) agree to rounding, within 1e-4 of each leaf's largest value (1.8e-5
-    measured on MI355X), and every other leaf and the loss bit for bit."""
+def test_column_sums_in_their_producers_match_the_reduction_kernel(monkeypatch):
+    """Each C4 layer's two bias gradients that are column sums of a kernel's output are computed by
+    that kernel: the fc1 bias gradient by the product whose epilogue computes the GELU backward
+    (each lane sums its rows in registers, the tile's lanes and waves combine in a fixed order,
+    one partial row per 128-row tile), the q, k, v bias gradient by the attention backward (one
+    partial row per batch element); the fold area's partial rows are then folded in order. The
+    sums' order differs from the reduction kernel's (RG_HIP_EPILOGUE_SUMS=0), so after one step
+    the bias leaves (the biases and their AdamW moments) agree to rounding, within 1e-4 of each
+    leaf's largest value (7e-7 measured on MI355X), and every other leaf and the loss bit for bit.
+    The key third of the q, k, v bias is left out: its true gradient is exactly zero (softmax is
+    invariant to a per-row constant), so AdamW normalises rounding noise of either order to the
+    learning rate's size."""
     step, state = workloads.gpt_train_step(workloads.GPT_CONFIGS["C4"])
-    print("C4: compile with and without column sums in product epilogues, 1 device step", flush=True)
+    print("C4: compile with and without column sums in their producers, 1 device step", flush=True)
     monkeypatch.setenv("RG_HIP_EPILOGUE_SUMS", "0")
     plain = rg.compile(step, (state,), validate="none", device="hip")
     monkeypatch.delenv("RG_HIP_EPILOGUE_SUMS")
     fused = rg.compile(step, (state,), validate="none", device="hip")
     plan = fused.plan_summary()
     absorbed = [(k, r) for k, r in enumerate(fused._n.step_runs_in()) if r != k and plan[k].get("op") == "sum"]
-    assert len(absorbed) == 6 and not [k for k, r in enumerate(plain._n.step_runs_in()) if r != k and plan[k].get("op") == "sum"]
+    assert len(absorbed) == 12 and not [k for k, r in enumerate(plain._n.step_runs_in()) if r != k and plan[k].get("op") == "sum"]
+    assert sum(plan[r]["kind"] == "attention" for _, r in absorbed) == 6
     r0 = rg.run(plain, state, steps=1)
     r1 = rg.run(fused, state, steps=1)
     assert r0.status == r1.status == "completed" and r0.history["aux"] == r1.history["aux"]
@@ -111,7 +116,10 @@ def test_column_sums_in_product_epilogues_match_the_reduction_kernel(monkeypatch
         if np.array_equal(np.atleast_1d(a).view(np.uint8), np.atleast_1d(b).view(np.uint8)):
             continue
         differing += 1
-        assert a.shape == (1024,), a.shape
+        assert a.shape in ((1024,), (768,)), a.shape
         scale = max(float(np.abs(a).max()), 1e-30)
-        assert float(np.abs(a.astype(np.float64) - b).max()) <= 1e-4 * scale
-    assert 0 < differing <= 18, differing
+        keep = np.ones(a.shape, bool)
+        if a.shape == (768,):
+            keep[256:512] = False
+        assert float(np.abs(a.astype(np.float64) - b)[keep].max()) <= 1e-4 * scale
+    assert 0 < differing <= 36, differing
