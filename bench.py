@@ -43,7 +43,9 @@ def classify(plan, runs_in=None):
     with their flops, counted as one launch; a product with the elementwise group of its epilogue
     (and a column sum of that group's output) forms the class `gemm_mfma_epilogue`: the product's
     flops, the other steps' bytes beside the product's, one launch, so the combined kernel's time
-    is neither charged to the plain products nor counted as elementwise work done in no time."""
+    is neither charged to the plain products nor counted as elementwise work done in no time; an
+    attention backward with the column sum it computes stays in `attention`, the sum's bytes
+    beside its flops."""
     classes = {}
     runs_in = runs_in or list(range(len(plan)))
     members = {}
@@ -68,7 +70,9 @@ def classify(plan, runs_in=None):
         products_only = combined and all(is_product(q) for q in unit)
         launch = runs_in[k] == k
         if combined and not products_only:
-            add("gemm_mfma_epilogue", k, st if is_product(k) else dict(st, bound="hbm"), launch=launch)
+            attn = any(plan[q]["kind"] == "attention" for q in unit)
+            main = st["kind"] == "attention" if attn else is_product(k)
+            add("attention" if attn else "gemm_mfma_epilogue", k, st if main else dict(st, bound="hbm"), launch=launch)
         elif st["kind"] == "attention":
             add("attention", k, st)
         elif st["kind"] == "fused":
