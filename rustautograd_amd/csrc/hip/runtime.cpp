@@ -983,9 +983,11 @@ std::string epilogue_source(const Plan& plan, size_t j, int64_t pk, const std::s
 // Independent products launched as one kernel (rgk::gemm_group): two adjacent plain products
 // (no epilogue) k and k + 1, and with them, when it fits, the nearest earlier plain product j
 // moved down to step k (nothing between j and k writes j's operands or reads or writes its
-// output); then, for a plain product k left alone, the nearest earlier one left alone moved down
-// to it the same way. No member reads or writes what another writes, and the launches group at
-// program build (same MFMA tile shape, a sequence of operand layouts instantiated for groups).
+// output), or else the product k + 2 moved up to step k; then, for a plain product k left alone,
+// the nearest earlier one left alone moved down to it the same way. No member reads or writes
+// what another writes, and the launches group at program build (MFMA products of one tile shape
+// and a sequence of operand layouts instantiated for groups, or streamed products of at most
+// eight rows, any mix of the row, dot and outer-product kernels).
 // Step k launches them all, the others nothing; at run time a group whose operands turn out not
 // to fit (alignment) is launched as single kernels, at step k. The results are the single
 // launches'. RG_HIP_PAIR=0 turns this off.
@@ -1063,7 +1065,13 @@ void group_products(Program& prog, const std::vector<GemmFill>& fills, const std
     std::vector<size_t> members = {k, k + 1};
     if (!independent(members) || !compatible(members)) continue;
     const int64_t j = earlier(k, members);
-    if (j >= 0) members.insert(members.begin(), (size_t)j);
+    if (j >= 0) {
+      members.insert(members.begin(), (size_t)j);
+    } else if (k + 2 < n && fills[k + 2] && !used[k + 2]) {
+      // Or the product after the pair, which then runs two steps early.
+      std::vector<size_t> three = {k, k + 1, k + 2};
+      if (independent(three) && compatible(three)) members = three;
+    }
     launch_together(members, k);
   }
   for (size_t k = 0; k < n; k++) {

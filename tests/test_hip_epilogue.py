@@ -85,6 +85,26 @@ def test_products_launched_together_match_single_launches_bit_for_bit(monkeypatc
         assert np.array_equal(a, b)
 
 
+def test_streamed_products_launched_together_match_single_launches_bit_for_bit(monkeypatch):
+    """C5's chain ((8 x 4096) x 4096 x 4096 and its gradients) streams its products through the
+    row, dot and outer-product kernels. The forward product x W1 and the outer product of the
+    gradient run as one launch; the second forward product, the dot product that forms the
+    gradient of x W1 and the outer product that forms W2's gradient as another; and the last
+    forward product (8 x 8 outputs over K = 4096) with the outer product that forms W1's gradient
+    as a third. Each block runs its own product's block code (the 8-wave reduction of the last
+    forward product by 4 waves that each run two waves' lanes), so the results are the single
+    launches' bit for bit."""
+    program, inputs = workloads.matrix_chain()
+    print("C5: compile with and without grouped streamed products", flush=True)
+    monkeypatch.setenv("RG_HIP_PAIR", "0")
+    single = rg.compile(program, inputs, device="hip", validate="none")
+    monkeypatch.delenv("RG_HIP_PAIR")
+    grouped = rg.compile(program, inputs, device="hip", validate="none")
+    assert _pairs(single) == [] and _pairs(grouped) == [(1, 0), (3, 2), (4, 2), (6, 5)], _pairs(grouped)
+    for a, b in zip(single(*inputs), grouped(*inputs)):
+        assert np.array_equal(np.asarray(a.numpy()).view(np.uint32), np.asarray(b.numpy()).view(np.uint32))
+
+
 def test_column_sums_in_their_producers_match_the_reduction_kernel(monkeypatch):
     """Each C4 layer's two bias gradients that are column sums of a kernel's output are computed by
     that kernel: the fc1 bias gradient by the product whose epilogue computes the GELU backward

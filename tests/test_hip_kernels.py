@@ -418,3 +418,45 @@ def test_skinny_products_match_numpy_and_the_oracle(m, k, n, ta, tb):
     if m * k * n <= (1 << 27):
         cpu = run_graph("cpu", build, [t(a), t(b)], optimize="standard")[0]
         close(hip, cpu, 1e-4, "skinny vs oracle")
+
+
+# Independent streamed products of one program: rows and dot kernels (8 rows), outer products of
+# each operand layout and K of 8 and 4, and tiny outputs over K whose single kernel has 4, 8 and 16
+# waves.
+GROUPED_STREAMED = [
+    (8, 4096, 2048, False, False), (8, 4096, 1024, False, True), (2048, 8, 1024, True, False), (1024, 4, 2048, False, False),
+    (8, 2048, 8, False, False), (4, 8000, 4, True, False), (1024, 8, 1024, False, True), (8, 4096, 8, False, True),
+]
+
+
+def test_streamed_products_launched_together_match_single_launches(monkeypatch):
+    """Adjacent independent streamed products run as one launch of k_stream_group, each block
+    running its own product's block code: the outputs equal the single launches' (RG_HIP_PAIR=0)
+    bit for bit, and numpy's float64 products within 1e-4 of the largest value."""
+    rng = np.random.default_rng(11)
+    ops = []
+    for m, k, n, ta, tb in GROUPED_STREAMED:
+        ops.append(rng.normal(size=(k, m) if ta else (m, k)).astype(np.float32))
+        ops.append(rng.normal(size=(n, k) if tb else (k, n)).astype(np.float32))
+
+    def build(g, i):
+        return [_product_graph(None, None, ta, tb)(g, i[2 * q:2 * q + 2]) for q, (m, k, n, ta, tb) in enumerate(GROUPED_STREAMED)]
+
+    def compiled():
+        g = _rg.Graph()
+        ids = [g.input(list(x.shape), "float32") for x in ops]
+        return _rg.compile(g, build(g, ids), [t(x)._t for x in ops], "none", "hip", "standard")
+
+    monkeypatch.setenv("RG_HIP_PAIR", "0")
+    single = compiled()
+    monkeypatch.delenv("RG_HIP_PAIR")
+    grouped = compiled()
+    moved = [k for k, r in enumerate(grouped.step_runs_in()) if r != k]
+    assert all(r == k for k, r in enumerate(single.step_runs_in())) and len(moved) >= 3, grouped.step_runs_in()
+    out0 = [rg.Tensor(r).numpy() for r in single.call([t(x)._t for x in ops])]
+    out1 = [rg.Tensor(r).numpy() for r in grouped.call([t(x)._t for x in ops])]
+    for q, (m, k, n, ta, tb) in enumerate(GROUPED_STREAMED):
+        a, b = ops[2 * q], ops[2 * q + 1]
+        want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+        assert np.array_equal(out0[q].view(np.uint32), out1[q].view(np.uint32)), (m, k, n, ta, tb)
+        assert np.abs(out1[q] - want).max() <= 1e-4 * np.abs(want).max(), (m, k, n, ta, tb)
