@@ -842,8 +842,9 @@ void gemm(hipStream_t s, const GemmArgs& g) {
 namespace {
 
 // Product `g` as a part of a grouped streaming launch: the kernel gemm_skinny would launch for
-// it, when that is the row, dot or outer-product kernel for at most 8 rows (or K), its operands
-// aligned for it, and its K splits, if any, deferred to the fold area.
+// it, when that is the row, dot or outer-product kernel for at most 8 rows (or K), or the
+// tiny-output kernel of 4, 8 or 16 waves, its operands aligned for it, and its K splits, if any,
+// deferred to the fold area.
 bool stream_part_of(const GemmArgs& g, StreamPart* p) {
   if (g.m == 0 || g.n == 0 || g.batch != 1 || g.bias || g.a_off || g.b_off) return false;
   auto aligned = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
@@ -906,7 +907,7 @@ bool stream_part_of(const GemmArgs& g, StreamPart* p) {
 bool gemm_group(hipStream_t s, const GemmArgs* g, int count, bool launch) {
   if (count < 2 || count > GROUP_MAX) return false;
   {
-    // Streamed products (C5's chain): any mix of the row, dot and outer-product kernels.
+    // Streamed products (C5's chain): any mix of the row, dot, outer-product and tiny-output kernels.
     StreamParts parts{};
     uint32_t blocks = 0;
     bool all = true;
